@@ -1,0 +1,476 @@
+// dream_oracle.cpp -- CPU restatement of the Dream reference hot path.
+//
+// TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and bench.py's
+// cpu_baseline leg as the checker / CPU comparison.  The product never links it.
+//
+// Written from the reference's documented behaviour; each function names the
+// reference lines it restates.  Loop orders, blocking constants and the points
+// where "+=" accumulates are kept, because they fix the exact fp64 values the
+// reference produces (tests compare against its golden vectors at <=1e-12).
+#include "dream_oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <random>
+#include <vector>
+
+namespace {
+
+// One process-wide generator, like get_rng() (elementwise.inc:30-33).
+std::mt19937& rng() {
+    static std::mt19937 g(42u);
+    return g;
+}
+
+}  // namespace
+
+// The exported functions take C linkage from their declarations in dream_oracle.h.
+
+// ---------------------------------------------------------------------------
+// RNG: set_seed / randn (elementwise.inc:35-54), uniform draws of the selftests
+// (elementwise.inc:815, 897), kaiming_init (builtins.inc:511-519).
+// ---------------------------------------------------------------------------
+void orc_set_seed(unsigned int seed) { rng().seed(seed); }
+
+void orc_randn(double* out, long long n) {
+    std::normal_distribution<double> nd(0.0, 1.0);
+    for (long long i = 0; i < n; ++i) out[i] = nd(rng());
+}
+
+void orc_uniform(double* out, long long n, double lo, double hi) {
+    std::uniform_real_distribution<double> ud(lo, hi);
+    for (long long i = 0; i < n; ++i) out[i] = ud(rng());
+}
+
+void orc_uniform_f32(float* out, long long n, float lo, float hi) {
+    std::uniform_real_distribution<float> ud(lo, hi);
+    for (long long i = 0; i < n; ++i) out[i] = ud(rng());
+}
+
+void orc_kaiming(double* out, int rows, int cols) {
+    // std = sqrt(2 / cols): the reference treats the column count as fan_in.
+    std::normal_distribution<double> nd(0.0, std::sqrt(2.0 / cols));
+    long long n = (long long)rows * cols;
+    for (long long i = 0; i < n; ++i) out[i] = nd(rng());
+}
+
+// ---------------------------------------------------------------------------
+// GEMM
+// ---------------------------------------------------------------------------
+void orc_gemm_ref_d(const double* A, const double* B, double* C, int M, int K, int N) {
+    // elementwise.inc:878-886: one fp64 dot product per output, k ascending.
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            double s = 0.0;
+            for (int k = 0; k < K; ++k) s += A[(size_t)i * K + k] * B[(size_t)k * N + j];
+            C[(size_t)i * N + j] = s;
+        }
+}
+
+namespace {
+
+// Blocked GEMM skeleton shared by the fp64 and fp32 restatements.
+// Blocking (elementwise.inc:518-519, 645): NC columns of B per outer panel,
+// KC-deep slices of K (B packed once per slice), MC-row blocks of A handed to
+// OpenMP threads, and an MR x NR register tile whose per-k update is one fused
+// multiply-add per element.  Each C element therefore receives, per KC slice, an
+// FMA chain over that slice started from zero, added onto C once the slice ends.
+template <typename T, int MR, int NR>
+struct Blocked {
+    static constexpr int KC = 256, MC = 128, NC_CAP = 4096;
+
+    // [panel][k][MR], zero padded (elementwise.inc:522-532).
+    static void pack_a(const T* A, int lda, int mc, int kc, T* dst) {
+        for (int ir = 0; ir < mc; ir += MR) {
+            const int mr = std::min(MR, mc - ir);
+            for (int k = 0; k < kc; ++k, dst += MR)
+                for (int i = 0; i < MR; ++i)
+                    dst[i] = i < mr ? A[(size_t)(ir + i) * lda + k] : T(0);
+        }
+    }
+    // [panel][k][NR], zero padded (elementwise.inc:535-545).
+    static void pack_b(const T* B, int ldb, int kc, int nc, T* dst) {
+        for (int jr = 0; jr < nc; jr += NR) {
+            const int nr = std::min(NR, nc - jr);
+            for (int k = 0; k < kc; ++k, dst += NR)
+                for (int j = 0; j < NR; ++j)
+                    dst[j] = j < nr ? B[(size_t)k * ldb + jr + j] : T(0);
+        }
+    }
+    // Register tile: acc = fma chain over kc, then C(mr x nr) += acc
+    // (ukern_4x8 / ukern_edge, elementwise.inc:548-588; fgemm ukern 667-684).
+    static void tile(int kc, const T* Ap, const T* Bp, T* C, int ldc, int mr, int nr) {
+        T acc[MR][NR];
+        for (int i = 0; i < MR; ++i)
+            for (int j = 0; j < NR; ++j) acc[i][j] = T(0);
+        for (int k = 0; k < kc; ++k) {
+            const T* b = Bp + (size_t)k * NR;
+            const T* a = Ap + (size_t)k * MR;
+            for (int i = 0; i < MR; ++i)
+                for (int j = 0; j < NR; ++j) acc[i][j] = std::fma(a[i], b[j], acc[i][j]);
+        }
+        for (int i = 0; i < mr; ++i)
+            for (int j = 0; j < nr; ++j) C[(size_t)i * ldc + j] += acc[i][j];
+    }
+
+    static void run(const T* A, const T* B, T* C, int M, int K, int N) {
+        // C is zeroed first (elementwise.inc:595, 691).
+        std::fill(C, C + (size_t)M * N, T(0));
+        if (M <= 0 || K <= 0 || N <= 0) return;
+        const int ncb = std::min(N, NC_CAP);
+        std::vector<T> bpack((size_t)KC * ((ncb + NR - 1) / NR) * NR);
+        const bool par = (size_t)M * K * N >= 262144;   // elementwise.inc:606, 702
+        for (int jc = 0; jc < N; jc += ncb) {
+            const int nc = std::min(ncb, N - jc);
+            for (int pc = 0; pc < K; pc += KC) {
+                const int kc = std::min(KC, K - pc);
+                pack_b(B + (size_t)pc * N + jc, N, kc, nc, bpack.data());
+#pragma omp parallel for schedule(dynamic) if (par)
+                for (int ic = 0; ic < M; ic += MC) {
+                    const int mc = std::min(MC, M - ic);
+                    std::vector<T> apack((size_t)KC * ((MC + MR - 1) / MR) * MR);
+                    pack_a(A + (size_t)ic * K + pc, K, mc, kc, apack.data());
+                    for (int jr = 0; jr < nc; jr += NR) {
+                        const int nr = std::min(NR, nc - jr);
+                        const T* bp = bpack.data() + (size_t)(jr / NR) * kc * NR;
+                        for (int ir = 0; ir < mc; ir += MR) {
+                            const int mr = std::min(MR, mc - ir);
+                            const T* ap = apack.data() + (size_t)(ir / MR) * kc * MR;
+                            tile(kc, ap, bp, C + (size_t)(ic + ir) * N + jc + jr, N, mr, nr);
+                        }
+                    }
+                }
+            }
+        }
+    }
+};
+
+}  // namespace
+
+void orc_gemm_d(const double* A, const double* B, double* C, int M, int K, int N) {
+    Blocked<double, 4, 8>::run(A, B, C, M, K, N);
+}
+
+void orc_gemm_f32(const float* A, const float* B, float* C, int M, int K, int N) {
+    Blocked<float, 8, 16>::run(A, B, C, M, K, N);
+}
+
+void orc_gemm_general_d(int transA, int transB, int M, int N, int K,
+                        const double* A, int lda, const double* B, int ldb,
+                        double beta, double* C, int ldc) {
+#pragma omp parallel for schedule(static) if ((size_t)M * N * K >= 2097152)
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            double s = 0.0;
+            for (int k = 0; k < K; ++k) {
+                const double a = transA ? A[(size_t)k * lda + i] : A[(size_t)i * lda + k];
+                const double b = transB ? B[(size_t)j * ldb + k] : B[(size_t)k * ldb + j];
+                s += a * b;
+            }
+            double* c = C + (size_t)i * ldc + j;
+            *c = (beta == 0.0 ? 0.0 : beta * *c) + s;
+        }
+}
+
+void orc_matmul_bwd(const double* A, const double* B, const double* dY,
+                    double* dA, double* dB, int M, int K, int N) {
+    const bool par = (long long)M * K * N >= 2097152;   // autograd.inc:104, 117
+    // dA[i,k] += sum_j dY[i,j] * B[k,j]: dot over j, added once per (i,k) (autograd.inc:104-113).
+#pragma omp parallel for schedule(static) if (par)
+    for (int i = 0; i < M; ++i)
+        for (int k = 0; k < K; ++k) {
+            double acc = 0.0;
+            for (int j = 0; j < N; ++j) acc += dY[(size_t)i * N + j] * B[(size_t)k * N + j];
+            dA[(size_t)i * K + k] += acc;
+        }
+    // dB[k,j] += A[i,k] * dY[i,j], i ascending, axpy into the dB row (autograd.inc:116-124).
+#pragma omp parallel for schedule(static) if (par)
+    for (int k = 0; k < K; ++k) {
+        double* row = dB + (size_t)k * N;
+        for (int i = 0; i < M; ++i) {
+            const double a = A[(size_t)i * K + k];
+            const double* dy = dY + (size_t)i * N;
+            for (int j = 0; j < N; ++j) row[j] += a * dy[j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention forward
+// ---------------------------------------------------------------------------
+namespace {
+
+inline double dot(const double* a, const double* b, int n) {
+    double s = 0.0;
+    for (int k = 0; k < n; ++k) s += a[k] * b[k];
+    return s;
+}
+
+// Materialized SDPA for one slice: scores, row softmax (max-subtracted, divided by
+// the sum), then P @ V.  causal keeps j <= i only, masked entries stay 0
+// (training.inc:196-217 and 235-260).
+void sdpa_slice(const double* Q, const double* K, const double* V, double* O,
+                int S, int dk, bool causal, std::vector<double>& P) {
+    const double scale = 1.0 / std::sqrt((double)dk);
+    P.assign((size_t)S * S, 0.0);
+    for (int i = 0; i < S; ++i) {
+        const int jn = causal ? i + 1 : S;
+        double* p = &P[(size_t)i * S];
+        double mx = -1e30;
+        for (int j = 0; j < jn; ++j) {
+            p[j] = dot(Q + (size_t)i * dk, K + (size_t)j * dk, dk) * scale;
+            if (p[j] > mx) mx = p[j];
+        }
+        double sum = 0.0;
+        for (int j = 0; j < jn; ++j) { p[j] = std::exp(p[j] - mx); sum += p[j]; }
+        for (int j = 0; j < jn; ++j) p[j] /= sum;
+    }
+    for (int i = 0; i < S; ++i) {
+        const int jn = causal ? i + 1 : S;
+        for (int k = 0; k < dk; ++k) {
+            double s = 0.0;
+            for (int j = 0; j < jn; ++j) s += P[(size_t)i * S + j] * V[(size_t)j * dk + k];
+            O[(size_t)i * dk + k] = s;
+        }
+    }
+}
+
+}  // namespace
+
+void orc_attention(const double* Q, const double* K, const double* V, double* O,
+                   int B, int S, int dk) {
+    std::vector<double> P;
+    for (int b = 0; b < B; ++b) {
+        const size_t off = (size_t)b * S * dk;
+        sdpa_slice(Q + off, K + off, V + off, O + off, S, dk, false, P);
+    }
+}
+
+void orc_attention_causal(const double* Q, const double* K, const double* V, double* O,
+                          int B, int S, int dk) {
+    std::vector<double> P;
+    for (int b = 0; b < B; ++b) {
+        const size_t off = (size_t)b * S * dk;
+        sdpa_slice(Q + off, K + off, V + off, O + off, S, dk, true, P);
+    }
+}
+
+void orc_flash_fwd(const double* Q, const double* K, const double* V, double* O,
+                   int B, int S, int dk, int Bc) {
+    // training.inc:288-289, 366-399: causal online softmax over key blocks of Bc.
+    if (Bc < 1) Bc = 64;
+    const double scale = 1.0 / std::sqrt((double)dk);
+    std::vector<double> sc((size_t)Bc), acc((size_t)dk);
+    for (int b = 0; b < B; ++b) {
+        const size_t off = (size_t)b * S * dk;
+        const double *Qb = Q + off, *Kb = K + off, *Vb = V + off;
+        double* Ob = O + off;
+        for (int i = 0; i < S; ++i) {
+            double m = -1e30, l = 0.0;
+            std::fill(acc.begin(), acc.end(), 0.0);
+            for (int jb = 0; jb <= i; jb += Bc) {
+                const int je = std::min(i, jb + Bc - 1);
+                double mb = -1e30;
+                for (int j = jb; j <= je; ++j) {
+                    sc[j - jb] = dot(Qb + (size_t)i * dk, Kb + (size_t)j * dk, dk) * scale;
+                    mb = std::max(mb, sc[j - jb]);
+                }
+                const double mn = std::max(m, mb);
+                const double corr = std::exp(m - mn);   // rescale the running state
+                l *= corr;
+                for (int k = 0; k < dk; ++k) acc[k] *= corr;
+                for (int j = jb; j <= je; ++j) {
+                    const double p = std::exp(sc[j - jb] - mn);
+                    l += p;
+                    for (int k = 0; k < dk; ++k) acc[k] += p * Vb[(size_t)j * dk + k];
+                }
+                m = mn;
+            }
+            const double inv = l > 0.0 ? 1.0 / l : 0.0;
+            for (int k = 0; k < dk; ++k) Ob[(size_t)i * dk + k] = acc[k] * inv;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention backward ("+=" into dQ, dK, dV)
+// ---------------------------------------------------------------------------
+void orc_attention_bwd(const double* Q, const double* K, const double* V, const double* dO,
+                       double* dQ, double* dK, double* dV, int B, int S, int dk, int causal) {
+    // autograd.inc:675-778.  P recomputed; dV = P^T dO; dP = dO V^T;
+    // dS = P o (dP - rowsum(dP o P)); dQ += dS K * scale; dK += dS^T Q * scale.
+    const double scale = 1.0 / std::sqrt((double)dk);
+    std::vector<double> P, dP((size_t)S * S), dS((size_t)S * S), O((size_t)S * dk);
+    for (int b = 0; b < B; ++b) {
+        const size_t off = (size_t)b * S * dk;
+        const double *Qb = Q + off, *Kb = K + off, *Vb = V + off, *dOb = dO + off;
+        double *dQb = dQ + off, *dKb = dK + off, *dVb = dV + off;
+        sdpa_slice(Qb, Kb, Vb, O.data(), S, dk, causal != 0, P);
+        for (int j = 0; j < S; ++j)
+            for (int k = 0; k < dk; ++k) {
+                double s = 0.0;
+                for (int i = causal ? j : 0; i < S; ++i)
+                    s += P[(size_t)i * S + j] * dOb[(size_t)i * dk + k];
+                dVb[(size_t)j * dk + k] += s;
+            }
+        std::fill(dP.begin(), dP.end(), 0.0);
+        for (int i = 0; i < S; ++i) {
+            const int jn = causal ? i + 1 : S;
+            for (int j = 0; j < jn; ++j)
+                dP[(size_t)i * S + j] = dot(dOb + (size_t)i * dk, Vb + (size_t)j * dk, dk);
+        }
+        std::fill(dS.begin(), dS.end(), 0.0);
+        for (int i = 0; i < S; ++i) {
+            const int jn = causal ? i + 1 : S;
+            double rd = 0.0;
+            for (int j = 0; j < jn; ++j) rd += dP[(size_t)i * S + j] * P[(size_t)i * S + j];
+            for (int j = 0; j < jn; ++j)
+                dS[(size_t)i * S + j] = P[(size_t)i * S + j] * (dP[(size_t)i * S + j] - rd);
+        }
+        for (int i = 0; i < S; ++i)
+            for (int k = 0; k < dk; ++k) {
+                double s = 0.0;
+                const int jn = causal ? i + 1 : S;
+                for (int j = 0; j < jn; ++j) s += dS[(size_t)i * S + j] * Kb[(size_t)j * dk + k];
+                dQb[(size_t)i * dk + k] += s * scale;
+            }
+        for (int j = 0; j < S; ++j)
+            for (int k = 0; k < dk; ++k) {
+                double s = 0.0;
+                for (int i = causal ? j : 0; i < S; ++i)
+                    s += dS[(size_t)i * S + j] * Qb[(size_t)i * dk + k];
+                dKb[(size_t)j * dk + k] += s * scale;
+            }
+    }
+}
+
+namespace {
+
+// Pass 1 of the flash backward (autograd.inc:799-812): per-row running max m and
+// normalizer l over key blocks of Bc, same recurrence as the forward.
+void row_stats(const double* Qb, const double* Kb, int S, int dk, int Bc, bool causal,
+               double scale, std::vector<double>& sc, double* m_out, double* l_out) {
+    for (int i = 0; i < S; ++i) {
+        double m = -1e30, l = 0.0;
+        const int last = causal ? i : S - 1;
+        for (int jb = 0; jb <= last; jb += Bc) {
+            const int je = std::min(last, jb + Bc - 1);
+            double mb = -1e30;
+            for (int j = jb; j <= je; ++j) {
+                sc[j - jb] = dot(Qb + (size_t)i * dk, Kb + (size_t)j * dk, dk) * scale;
+                mb = std::max(mb, sc[j - jb]);
+            }
+            const double mn = std::max(m, mb);
+            l *= std::exp(m - mn);
+            for (int j = jb; j <= je; ++j) l += std::exp(sc[j - jb] - mn);
+            m = mn;
+        }
+        m_out[i] = m;
+        l_out[i] = l;
+    }
+}
+
+}  // namespace
+
+void orc_flash_bwd(const double* Q, const double* K, const double* V, const double* dO,
+                   double* dQ, double* dK, double* dV, int B, int S, int dk) {
+    // autograd.inc:779-840.
+    const double scale = 1.0 / std::sqrt((double)dk);
+    const int Bc = 64;
+    std::vector<double> sc(Bc), acc(dk), lrow(S), mrow(S), Drow(S);
+    for (int b = 0; b < B; ++b) {
+        const size_t off = (size_t)b * S * dk;
+        const double *Qb = Q + off, *Kb = K + off, *Vb = V + off, *dOb = dO + off;
+        double *dQb = dQ + off, *dKb = dK + off, *dVb = dV + off;
+        row_stats(Qb, Kb, S, dk, Bc, true, scale, sc, mrow.data(), lrow.data());
+        // pass 2 (813-820): D_i = dO_i . O_i with O_i recomputed from (m, l).
+        for (int i = 0; i < S; ++i) {
+            std::fill(acc.begin(), acc.end(), 0.0);
+            for (int j = 0; j <= i; ++j) {
+                const double s = dot(Qb + (size_t)i * dk, Kb + (size_t)j * dk, dk);
+                const double p = std::exp(s * scale - mrow[i]) / lrow[i];
+                for (int k = 0; k < dk; ++k) acc[k] += p * Vb[(size_t)j * dk + k];
+            }
+            Drow[i] = dot(dOb + (size_t)i * dk, acc.data(), dk);
+        }
+        // pass 3 (821-838): recompute a_ij, dS_ij = a_ij (dA_ij - D_i), scatter.
+        for (int i = 0; i < S; ++i) {
+            for (int j = 0; j <= i; ++j) {
+                const double s = dot(Qb + (size_t)i * dk, Kb + (size_t)j * dk, dk);
+                const double a = std::exp(s * scale - mrow[i]) / lrow[i];
+                const double dA = dot(dOb + (size_t)i * dk, Vb + (size_t)j * dk, dk);
+                const double ds = a * (dA - Drow[i]);
+                for (int k = 0; k < dk; ++k) {
+                    dVb[(size_t)j * dk + k] += a * dOb[(size_t)i * dk + k];
+                    dQb[(size_t)i * dk + k] += ds * Kb[(size_t)j * dk + k] * scale;
+                    dKb[(size_t)j * dk + k] += ds * Qb[(size_t)i * dk + k] * scale;
+                }
+            }
+        }
+    }
+}
+
+void orc_flash_lse(const double* Q, const double* K, double* lse, int B, int S, int dk,
+                   int causal) {
+    const double scale = 1.0 / std::sqrt((double)dk);
+    std::vector<double> sc(64), m(S), l(S);
+    for (int b = 0; b < B; ++b) {
+        const size_t off = (size_t)b * S * dk;
+        row_stats(Q + off, K + off, S, dk, 64, causal != 0, scale, sc, m.data(), l.data());
+        for (int i = 0; i < S; ++i) lse[(size_t)b * S + i] = m[i] + std::log(l[i]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Row reductions
+// ---------------------------------------------------------------------------
+void orc_softmax_rows(const double* X, double* Y, int R, int C) {
+    // elementwise.inc:346-356: max, exp(x - max) with running sum, divide.
+    for (int r = 0; r < R; ++r) {
+        const double* x = X + (size_t)r * C;
+        double* y = Y + (size_t)r * C;
+        double mx = x[0];
+        for (int j = 1; j < C; ++j) mx = std::max(mx, x[j]);
+        double s = 0.0;
+        for (int j = 0; j < C; ++j) { y[j] = std::exp(x[j] - mx); s += y[j]; }
+        for (int j = 0; j < C; ++j) y[j] /= s;
+    }
+}
+
+void orc_log_softmax_rows(const double* X, double* Y, int R, int C) {
+    // elementwise.inc:1557-1567: x - (max + log(sum exp(x - max))).
+    for (int r = 0; r < R; ++r) {
+        const double* x = X + (size_t)r * C;
+        double* y = Y + (size_t)r * C;
+        double mx = x[0];
+        for (int j = 1; j < C; ++j) mx = std::max(mx, x[j]);
+        double s = 0.0;
+        for (int j = 0; j < C; ++j) s += std::exp(x[j] - mx);
+        const double lse = mx + std::log(s);
+        for (int j = 0; j < C; ++j) y[j] = x[j] - lse;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 (training.inc:1969-1976)
+// ---------------------------------------------------------------------------
+float orc_to_bf16(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    u += 0x7FFFu + ((u >> 16) & 1u);   // bias so truncation rounds to nearest, ties to even
+    u &= 0xFFFF0000u;
+    float r;
+    std::memcpy(&r, &u, 4);
+    return r;
+}
+
+void orc_bf16_bits(const float* x, uint16_t* out, long long n) {
+    for (long long i = 0; i < n; ++i) {
+        const float r = orc_to_bf16(x[i]);
+        uint32_t u;
+        std::memcpy(&u, &r, 4);
+        out[i] = (uint16_t)(u >> 16);
+    }
+}
+

@@ -1,0 +1,100 @@
+/*
+ * dream_oracle.h -- CPU restatement of the Dream reference hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (dreamcompiler_amd/, include/)
+ * links, loads or calls this library.  Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may use it, and only as the checker / the timed
+ * CPU comparison, never as the thing measured on the GPU.
+ *
+ * Every function restates one reference function (file:line into
+ * heellowdsf/DreamCompiler).  All matrices are row-major and contiguous.
+ * Functions documented as "+=" accumulate into the output buffers exactly
+ * like the reference backward branches do.
+ *
+ * Pinning status (what checks each function, see tests/test_oracle.py):
+ *   orc_set_seed/orc_randn/orc_uniform/orc_kaiming   golden vectors from the reference build
+ *   orc_gemm_ref_d      closed forms (all-ones -> K), identity, brute-force fp64 sums via numpy
+ *   orc_gemm_d          golden vectors + gemm_ref_d (1e-11, the reference gate)
+ *   orc_gemm_f32        golden vectors + fp64 on the same fp32 inputs (2e-4, the reference gate)
+ *   orc_gemm_general_d  numpy fp64 einsum on random transposes / beta (independent code)
+ *   orc_matmul_bwd      golden vectors (reference backward) + finite differences
+ *   orc_attention*, orc_flash_fwd, orc_flash_bwd      golden vectors + special cases
+ *                       (S=1 -> O=V, constant K -> causal running mean) + finite differences
+ *   orc_flash_lse       closed form log-sum-exp (scipy.special.logsumexp)
+ *   orc_softmax_rows, orc_log_softmax_rows   scipy.special.softmax / log_softmax, rows sum to 1
+ *   orc_to_bf16         IEEE round-to-nearest-even (torch.bfloat16 cast) + hand-picked ties
+ */
+#ifndef DREAM_ORACLE_H
+#define DREAM_ORACLE_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* RNG (runtime/ops/elementwise.inc:30-54, runtime/io/builtins.inc:511-519).
+ * One global std::mt19937, seeded like set_seed(); draws are std::normal_distribution<double>
+ * (randn), std::uniform_real_distribution<double>(lo,hi) (selftests) and kaiming(rows, cols)
+ * = normal(0, sqrt(2/cols)). */
+void orc_set_seed(unsigned int seed);
+void orc_randn(double* out, long long n);
+void orc_uniform(double* out, long long n, double lo, double hi);
+void orc_uniform_f32(float* out, long long n, float lo, float hi);
+void orc_kaiming(double* out, int rows, int cols);
+
+/* GEMM, C = A(MxK) @ B(KxN).
+ * orc_gemm_ref_d : naive triple loop        (elementwise.inc:878-886)
+ * orc_gemm_d     : blocked fp64 4x8 kernel  (elementwise.inc:513-638)
+ * orc_gemm_f32   : blocked fp32 8x16 kernel (elementwise.inc:644-738) */
+void orc_gemm_ref_d(const double* A, const double* B, double* C, int M, int K, int N);
+void orc_gemm_d(const double* A, const double* B, double* C, int M, int K, int N);
+void orc_gemm_f32(const float* A, const float* B, float* C, int M, int K, int N);
+
+/* General fp64 GEMM used to check the GPU's transposed variants:
+ * C = op(A) @ op(B) + beta*C with op(X) = X or X^T (trans flags), leading dims in elements.
+ * The NT and TN shapes are the two matmul-backward products of autograd.inc:91-125. */
+void orc_gemm_general_d(int transA, int transB, int M, int N, int K,
+                        const double* A, int lda, const double* B, int ldb,
+                        double beta, double* C, int ldc);
+
+/* Matmul backward (autograd.inc:91-125): dA += dY @ B^T, dB += A^T @ dY. */
+void orc_matmul_bwd(const double* A, const double* B, const double* dY,
+                    double* dA, double* dB, int M, int K, int N);
+
+/* Attention forward; layout (B, S*dk): slice b starts at b*S*dk, scale 1/sqrt(dk).
+ * orc_attention        : training.inc:178-220 (non-causal)
+ * orc_attention_causal : training.inc:225-263
+ * orc_flash_fwd        : training.inc:284-401 CPU path (block Bc, online softmax) */
+void orc_attention(const double* Q, const double* K, const double* V, double* O,
+                   int B, int S, int dk);
+void orc_attention_causal(const double* Q, const double* K, const double* V, double* O,
+                          int B, int S, int dk);
+void orc_flash_fwd(const double* Q, const double* K, const double* V, double* O,
+                   int B, int S, int dk, int Bc);
+
+/* Attention backward, "+=" into dQ/dK/dV.
+ * orc_attention_bwd : autograd.inc:675-778 (causal selects the attention_causal branch)
+ * orc_flash_bwd     : autograd.inc:779-840 (3 passes, Bc = 64) */
+void orc_attention_bwd(const double* Q, const double* K, const double* V, const double* dO,
+                       double* dQ, double* dK, double* dV, int B, int S, int dk, int causal);
+void orc_flash_bwd(const double* Q, const double* K, const double* V, const double* dO,
+                   double* dQ, double* dK, double* dV, int B, int S, int dk);
+
+/* Per-row natural-log log-sum-exp of the scaled scores, lse[b*S+i] = m_i + log(l_i),
+ * from the (m, l) recurrence of pass 1 in autograd.inc:799-812 (causal) or the full row
+ * (non-causal).  This is the statistic the GPU forward saves for its backward. */
+void orc_flash_lse(const double* Q, const double* K, double* lse, int B, int S, int dk,
+                   int causal);
+
+/* Row reductions (elementwise.inc:338-358, 1550-1570): rows = R, cols = C. */
+void orc_softmax_rows(const double* X, double* Y, int R, int C);
+void orc_log_softmax_rows(const double* X, double* Y, int R, int C);
+
+/* bf16 rounding (training.inc:1969-1976): fp32 -> bf16 -> fp32, round to nearest even
+ * by the bias-and-truncate rule.  orc_bf16_bits returns the upper 16 bits. */
+float orc_to_bf16(float x);
+void orc_bf16_bits(const float* x, uint16_t* out, long long n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,222 @@
+"""ctypes wrapper around oracle/liboracle.so (the CPU restatement of the reference path).
+
+Test infrastructure: imported only by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg.  Every function returns fresh numpy arrays and never touches the GPU.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
+
+_dp = ctypes.POINTER(ctypes.c_double)
+_fp = ctypes.POINTER(ctypes.c_float)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_i = ctypes.c_int
+_ll = ctypes.c_longlong
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_set_seed": [ctypes.c_uint],
+            "orc_randn": [_dp, _ll],
+            "orc_uniform": [_dp, _ll, ctypes.c_double, ctypes.c_double],
+            "orc_uniform_f32": [_fp, _ll, ctypes.c_float, ctypes.c_float],
+            "orc_kaiming": [_dp, _i, _i],
+            "orc_gemm_ref_d": [_dp, _dp, _dp, _i, _i, _i],
+            "orc_gemm_d": [_dp, _dp, _dp, _i, _i, _i],
+            "orc_gemm_f32": [_fp, _fp, _fp, _i, _i, _i],
+            "orc_gemm_general_d": [_i, _i, _i, _i, _i, _dp, _i, _dp, _i, ctypes.c_double, _dp, _i],
+            "orc_matmul_bwd": [_dp, _dp, _dp, _dp, _dp, _i, _i, _i],
+            "orc_attention": [_dp, _dp, _dp, _dp, _i, _i, _i],
+            "orc_attention_causal": [_dp, _dp, _dp, _dp, _i, _i, _i],
+            "orc_flash_fwd": [_dp, _dp, _dp, _dp, _i, _i, _i, _i],
+            "orc_attention_bwd": [_dp] * 7 + [_i, _i, _i, _i],
+            "orc_flash_bwd": [_dp] * 7 + [_i, _i, _i],
+            "orc_flash_lse": [_dp, _dp, _dp, _i, _i, _i, _i],
+            "orc_softmax_rows": [_dp, _dp, _i, _i],
+            "orc_log_softmax_rows": [_dp, _dp, _i, _i],
+            "orc_to_bf16": [ctypes.c_float],
+            "orc_bf16_bits": [_fp, _u16p, _ll],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = None
+        L.orc_to_bf16.restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+def _d(a):
+    return np.ascontiguousarray(a, dtype=np.float64)
+
+
+def _ptr(a, t=_dp):
+    return a.ctypes.data_as(t)
+
+
+# --- RNG ---------------------------------------------------------------------
+def set_seed(seed):
+    lib().orc_set_seed(int(seed))
+
+
+def randn(*shape):
+    out = np.empty(int(np.prod(shape)), np.float64)
+    lib().orc_randn(_ptr(out), out.size)
+    return out.reshape(shape)
+
+
+def uniform(n, lo, hi):
+    out = np.empty(int(n), np.float64)
+    lib().orc_uniform(_ptr(out), out.size, lo, hi)
+    return out
+
+
+def uniform_f32(n, lo, hi):
+    out = np.empty(int(n), np.float32)
+    lib().orc_uniform_f32(_ptr(out, _fp), out.size, lo, hi)
+    return out
+
+
+def kaiming(rows, cols):
+    out = np.empty((rows, cols), np.float64)
+    lib().orc_kaiming(_ptr(out), rows, cols)
+    return out
+
+
+# --- GEMM ----------------------------------------------------------------------
+def gemm_ref_d(A, B):
+    A, B = _d(A), _d(B)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float64)
+    lib().orc_gemm_ref_d(_ptr(A), _ptr(B), _ptr(C), M, K, N)
+    return C
+
+
+def gemm_d(A, B):
+    A, B = _d(A), _d(B)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float64)
+    lib().orc_gemm_d(_ptr(A), _ptr(B), _ptr(C), M, K, N)
+    return C
+
+
+def gemm_f32(A, B):
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    lib().orc_gemm_f32(_ptr(A, _fp), _ptr(B, _fp), _ptr(C, _fp), M, K, N)
+    return C
+
+
+def gemm_general_d(transA, transB, A, B, beta=0.0, C=None):
+    """C = op(A) @ op(B) + beta*C in fp64; A/B given in their stored layout."""
+    A, B = _d(A), _d(B)
+    M = A.shape[1] if transA else A.shape[0]
+    K = A.shape[0] if transA else A.shape[1]
+    N = B.shape[0] if transB else B.shape[1]
+    out = np.zeros((M, N), np.float64) if C is None else _d(C).copy()
+    lib().orc_gemm_general_d(int(transA), int(transB), M, N, K, _ptr(A), A.shape[1],
+                             _ptr(B), B.shape[1], float(beta), _ptr(out), N)
+    return out
+
+
+def matmul_bwd(A, B, dY, dA=None, dB=None):
+    A, B, dY = _d(A), _d(B), _d(dY)
+    M, K = A.shape
+    N = B.shape[1]
+    dA = np.zeros((M, K)) if dA is None else _d(dA).copy()
+    dB = np.zeros((K, N)) if dB is None else _d(dB).copy()
+    lib().orc_matmul_bwd(_ptr(A), _ptr(B), _ptr(dY), _ptr(dA), _ptr(dB), M, K, N)
+    return dA, dB
+
+
+# --- attention (layout (B, S*dk)) ----------------------------------------------
+def _qkv(Q, K, V):
+    return _d(Q), _d(K), _d(V)
+
+
+def attention(Q, K, V, B, S, dk, causal):
+    Q, K, V = _qkv(Q, K, V)
+    O = np.empty_like(Q)
+    fn = lib().orc_attention_causal if causal else lib().orc_attention
+    fn(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), B, S, dk)
+    return O
+
+
+def flash_fwd(Q, K, V, B, S, dk, Bc=64):
+    Q, K, V = _qkv(Q, K, V)
+    O = np.empty_like(Q)
+    lib().orc_flash_fwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), B, S, dk, Bc)
+    return O
+
+
+def attention_bwd(Q, K, V, dO, B, S, dk, causal):
+    Q, K, V = _qkv(Q, K, V)
+    dO = _d(dO)
+    dQ, dK, dV = np.zeros_like(Q), np.zeros_like(Q), np.zeros_like(Q)
+    lib().orc_attention_bwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV),
+                            B, S, dk, int(causal))
+    return dQ, dK, dV
+
+
+def flash_bwd(Q, K, V, dO, B, S, dk):
+    Q, K, V = _qkv(Q, K, V)
+    dO = _d(dO)
+    dQ, dK, dV = np.zeros_like(Q), np.zeros_like(Q), np.zeros_like(Q)
+    lib().orc_flash_bwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV),
+                        B, S, dk)
+    return dQ, dK, dV
+
+
+def flash_lse(Q, K, B, S, dk, causal=True):
+    Q, K = _d(Q), _d(K)
+    lse = np.empty(B * S, np.float64)
+    lib().orc_flash_lse(_ptr(Q), _ptr(K), _ptr(lse), B, S, dk, int(causal))
+    return lse.reshape(B, S)
+
+
+# --- row reductions / bf16 -----------------------------------------------------
+def softmax_rows(X):
+    X = _d(X)
+    Y = np.empty_like(X)
+    lib().orc_softmax_rows(_ptr(X), _ptr(Y), X.shape[0], X.size // X.shape[0])
+    return Y
+
+
+def log_softmax_rows(X):
+    X = _d(X)
+    Y = np.empty_like(X)
+    lib().orc_log_softmax_rows(_ptr(X), _ptr(Y), X.shape[0], X.size // X.shape[0])
+    return Y
+
+
+def to_bf16(x):
+    return lib().orc_to_bf16(float(x))
+
+
+def bf16_bits(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_bf16_bits(_ptr(x, _fp), _ptr(out, _u16p), x.size)
+    return out
+
+
+def bf16_round(x):
+    """fp32 values rounded to bf16 (returned as fp32) by the reference's rule."""
+    bits = bf16_bits(x).astype(np.uint32) << 16
+    return bits.view(np.float32)

@@ -1,0 +1,93 @@
+"""Write tests/golden/ref_vectors.npz from the reference runtime built from source.
+
+Run in a container that has the reference tree (it builds oracle/_ref/ first):
+
+    make -C oracle ref && python tests/golden/gen_golden.py
+
+Every input is drawn by the reference's own RNG (set_seed + randn, elementwise.inc:35-54)
+and every output comes from the reference builtins through their C ABI:
+tensor_matmul (CPU dgemm / f32 fgemm), backward through "matmul", dream_attention,
+dream_attention_causal, dream_flash_attention and their backward branches,
+dream_softmax, dream_log_softmax, dream_kaiming_init.  The file holds data only
+(inputs and expected outputs, fp64).
+"""
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(HERE))
+from _ref_runtime import RefRuntime  # noqa: E402
+
+OUT = os.path.join(HERE, "ref_vectors.npz")
+
+
+def main():
+    R = RefRuntime()
+    v = {}
+    manifest = {}
+
+    # RNG: set_seed(42); randn(4, 250) and set_seed(7); kaiming_init(16, 10).
+    R.set_seed(42)
+    v["rng_randn_s42"] = R.randn(4, 250)
+    R.set_seed(7)
+    v["rng_kaiming_s7_16x10"] = R.kaiming(16, 10)
+    manifest["rng"] = "randn(4,250) after set_seed(42); kaiming_init(16,10) after set_seed(7)"
+
+    # fp64 dgemm via tensor_matmul.  K=300 crosses the KC=256 slice; M*K*N >= 262144
+    # takes the OpenMP branch.
+    R.set_seed(20260707)
+    for (M, K, N) in [(65, 63, 66), (33, 300, 35), (1, 7, 1), (5, 1, 9)]:
+        A, B = R.randn(M, K), R.randn(K, N)
+        key = f"gemm_d_{M}x{K}x{N}"
+        v[key + "_A"], v[key + "_B"], v[key + "_C"] = A, B, R.matmul(A, B)
+    manifest["gemm_d"] = "set_seed(20260707); per shape A=randn(M,K), B=randn(K,N); C=A@B (fp64)"
+
+    # fp32 fgemm via `as f32` operands.
+    for (M, K, N) in [(33, 31, 35), (40, 300, 37)]:
+        A, B = R.randn(M, K), R.randn(K, N)
+        key = f"gemm_f32_{M}x{K}x{N}"
+        v[key + "_A"], v[key + "_B"], v[key + "_C"] = A, B, R.matmul(A, B, f32=True)
+    manifest["gemm_f32"] = "continuing the stream: A,B randn; C = (A as f32) @ (B as f32)"
+
+    # matmul backward with a random upstream gradient W: backward(sum((A@B) * W)).
+    for (M, K, N) in [(65, 63, 66)]:
+        A, B, W = R.randn(M, K), R.randn(K, N), R.randn(M, N)
+        dA, dB = R.matmul_grads(A, B, W)
+        key = f"mmbwd_{M}x{K}x{N}"
+        v[key + "_A"], v[key + "_B"], v[key + "_W"] = A, B, W
+        v[key + "_dA"], v[key + "_dB"] = dA, dB
+    manifest["matmul_bwd"] = "A,B,W randn; dA,dB from backward(sum((A@B)*W))"
+
+    # Attention family.  One slice, S=100 (ragged against Bc=16 forward and the
+    # fixed Bc=64 backward), dk=24; plus S=64, dk=16, Bc=8.
+    R.set_seed(20260709)
+    for (B, S, dk, Bc) in [(1, 100, 24, 16), (2, 64, 16, 8)]:
+        Q, K, V, W = (R.randn(B, S * dk) for _ in range(4))
+        key = f"attn_B{B}_S{S}_dk{dk}_Bc{Bc}"
+        v[key + "_Q"], v[key + "_K"], v[key + "_V"], v[key + "_W"] = Q, K, V, W
+        for kind in ("plain", "causal", "flash"):
+            v[f"{key}_{kind}_O"] = R.attention(kind, Q, K, V, B, S, dk, Bc)
+            dQ, dK, dV = R.attention_grads(kind, Q, K, V, W, B, S, dk, Bc)
+            v[f"{key}_{kind}_dQ"], v[f"{key}_{kind}_dK"], v[f"{key}_{kind}_dV"] = dQ, dK, dV
+    manifest["attention"] = ("set_seed(20260709); Q,K,V,W = randn(B, S*dk); O from "
+                             "attention / attention_causal / flash_attention(Bc); grads from "
+                             "backward(sum(O*W))")
+
+    R.set_seed(11)
+    X = R.randn(7, 33)
+    v["softmax_X"], v["softmax_Y"], v["log_softmax_Y"] = X, R.softmax(X), R.softmax(X, log=True)
+    manifest["softmax"] = "set_seed(11); X=randn(7,33); softmax(X), log_softmax(X)"
+
+    np.savez_compressed(OUT, **v)
+    manifest["file"] = os.path.basename(OUT)
+    manifest["arrays"] = {k: list(a.shape) for k, a in v.items()}
+    with open(os.path.join(HERE, "manifest.json"), "w") as f:
+        json.dump(manifest, f, indent=1, sort_keys=True)
+    print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(v)} arrays)")
+
+
+if __name__ == "__main__":
+    main()
