@@ -1,0 +1,88 @@
+"""Build the HIP backend and the runtime library in-tree for gfx950.
+
+    python -m dreamcompiler_amd.build        (or __graft_entry__.build())
+
+Produces
+    dreamcompiler_amd/lib/libdream_hip.so   C ABI of include/dream_hip.h (HIP kernels)
+    dreamcompiler_amd/lib/libdream_rt.so    Dream builtins of include/dream_rt.h over it
+Objects go to dreamcompiler_amd/_build/.  hipcc cross-compiles, so no GPU is needed.
+"""
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+BUILD = os.path.join(PKG, "_build")
+LIBDIR = os.path.join(PKG, "lib")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+HIP_SOURCES = [
+    "dh_backend.hip",
+    "dh_gemm_f32.hip",
+    "dh_gemm_bf16.hip",
+    "dh_flash_fwd.hip",
+    "dh_flash_bwd.hip",
+]
+RT_SOURCES = ["dream_rt.cpp"]
+
+# Packed fp32 VALU forms are kept out of generated code (the device pass only).
+HIP_FLAGS = [
+    "-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument", "-I" + os.path.join(ROOT, "include"),
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out)
+
+
+def _compile(src, verbose):
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+    return obj
+
+
+def build(verbose=False, jobs=None):
+    os.makedirs(BUILD, exist_ok=True)
+    os.makedirs(LIBDIR, exist_ok=True)
+    srcs = [s for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    jobs = jobs or min(8, len(srcs))
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+    hip_so = os.path.join(LIBDIR, "libdream_hip.so")
+    tmp = hip_so + ".tmp"
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp], verbose)
+    os.replace(tmp, hip_so)
+    rt = [s for s in RT_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    if rt:
+        rt_so = os.path.join(LIBDIR, "libdream_rt.so")
+        tmp = rt_so + ".tmp"
+        _run([HIPCC, "-std=c++17", "-O2", "-fPIC", "-shared",
+              "-I" + os.path.join(ROOT, "include"),
+              *[os.path.join(CSRC, s) for s in rt], "-L" + LIBDIR, "-ldream_hip",
+              "-Wl,-rpath,$ORIGIN", "-o", tmp], verbose)
+        os.replace(tmp, rt_so)
+    return hip_so
+
+
+def clean():
+    shutil.rmtree(BUILD, ignore_errors=True)
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print("built", LIBDIR)

@@ -1,0 +1,134 @@
+// dh_common.hpp -- internal helpers shared by the HIP translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/dream_hip.h"
+
+namespace dh {
+
+// ---- status plumbing (defined in dh_backend.hip) --------------------------------
+int set_error(int code, const char* fmt, ...);
+int ensure_init();                 // DH_OK or DH_ERR_NO_DEVICE
+hipStream_t stream();
+int check_launch(const char* what);   // hipGetLastError after a launch
+int num_cus();
+
+#define DH_TRY(expr)                      \
+    do {                                  \
+        int _s = (expr);                  \
+        if (_s != DH_OK) return _s;       \
+    } while (0)
+
+// ---- vector types -------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---- bf16 bit helpers -----------------------------------------------------------
+// Round to nearest even by bias-and-truncate, the rule of dream_to_bf16
+// (runtime/nn/training.inc:1969-1976); NaN payloads follow the same arithmetic.
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float x) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t b) {
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+// Two fp32 -> packed bf16 pair (lo in bits 0-15).
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+// ---- 16-bit lane shuffles used by register transposes ------------------------------
+// lo16(a) | lo16(b) << 16 and hi16(a) | hi16(b) << 16 as single v_perm_b32 ops.
+__device__ inline uint32_t pack_lo16(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ inline uint32_t pack_hi16(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// ---- wavefront reductions (64 lanes) ----------------------------------------------
+// DPP for distances 1, 2 (quad permutes), 4 (half-row mirror), 8 (row mirror);
+// the 16- and 32-lane steps use the gfx950 permlane swaps.  Every lane ends
+// with the reduction over the full wave.
+__device__ inline float dpp_quad_xor1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ inline float dpp_quad_xor2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+__device__ inline float dpp_half_mirror(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+}
+__device__ inline float dpp_row_mirror(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+}
+// v_permlane32_swap with both operands = v returns {v[l & 31], v[(l & 31) + 32]}
+// in every lane, i.e. the lane's own value and its partner l ^ 32 in half order.
+// v_permlane16_swap does the same for partners l ^ 16 inside each 32-lane half.
+__device__ inline void halves32(float v, float& lo, float& hi) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    lo = __builtin_bit_cast(float, (uint32_t)r[0]);
+    hi = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ inline void halves16(float v, float& lo, float& hi) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    lo = __builtin_bit_cast(float, (uint32_t)r[0]);
+    hi = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+// Value held by lane l ^ 32.
+__device__ inline float xor32(float v) {
+    float lo, hi;
+    halves32(v, lo, hi);
+    return (__lane_id() & 32) ? lo : hi;
+}
+
+template <typename Op>
+__device__ inline float wave_reduce(float v, Op op) {
+    v = op(v, dpp_quad_xor1(v));
+    v = op(v, dpp_quad_xor2(v));
+    v = op(v, dpp_half_mirror(v));
+    v = op(v, dpp_row_mirror(v));
+    float lo, hi;
+    halves16(v, lo, hi);
+    v = op(lo, hi);
+    halves32(v, lo, hi);
+    return op(lo, hi);
+}
+struct OpMax { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpSum { __device__ float operator()(float a, float b) const { return a + b; } };
+
+// ---- XCD-aware tile order --------------------------------------------------------
+// Work-groups are dealt round-robin to the 8 XCDs (block b runs on XCD b % 8).
+// Remap so that each XCD receives a contiguous run of logical tiles, then walk
+// tiles in groups of `group_m` tile-rows so neighbouring tiles on one XCD share
+// A rows and B columns in that XCD's L2.
+__device__ inline void xcd_tile_order(int bid, int nblocks, int tiles_m, int tiles_n,
+                                      int group_m, int& tm, int& tn) {
+    int logical = bid;
+    if ((nblocks & 7) == 0) {
+        const int per = nblocks >> 3;
+        logical = (bid & 7) * per + (bid >> 3);
+    }
+    const int width = group_m * tiles_n;
+    const int group = logical / width;
+    const int first_m = group * group_m;
+    const int gsz = min(tiles_m - first_m, group_m);
+    const int in = logical - group * width;
+    tm = first_m + in % gsz;
+    tn = in / gsz;
+}
+
+}  // namespace dh

@@ -1,0 +1,206 @@
+// dh_gemm_f32.hip -- fp32 GEMM on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
+//
+// C[M x N] = op(A) @ op(B) + beta * C for the four storage layouts (NN, NT, TN, TT).
+// NN serves tensor_matmul's C = A @ B (runtime/ops/elementwise.inc:971-1213); NT and TN
+// with beta = 1 serve the matmul backward dA += dY B^T, dB += A^T dY
+// (runtime/ops/autograd.inc:91-125).
+//
+// Work decomposition
+//   work-group (256 threads = 4 wave64s) owns a 128 x 128 tile of C;
+//   wave w owns the 64 x 64 sub-tile (w / 2, w % 2): 2 x 2 MFMA blocks of 32 x 32,
+//   64 fp32 accumulators per lane.
+//   K advances in slices of 16: both operand slices are staged in LDS k-major
+//   (As[k][i], Bs[k][j]) and double-buffered; the next slice is fetched from global
+//   memory into registers while the matrix cores work on the current one.
+// MFMA operand layout (32x32x2): lane l supplies A[i = l % 32][k = l / 32] and
+//   B[k = l / 32][j = l % 32]; accumulator register r of lane l holds
+//   C[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
+// Edges: rows/cols beyond M, N and K are loaded as zeros and never stored, so any
+//   shape is exact.  When a matrix's leading dimension and base address allow it the
+//   contiguous dimension is fetched with 128-bit loads.
+#include "dh_common.hpp"
+
+namespace dh {
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 16, NTHREADS = 256;
+constexpr int LDS_A = BM + 4;   // padded k-major row strides (floats)
+constexpr int LDS_B = BN + 4;
+
+// Four consecutive elements of one row of a row-major matrix:
+// row r, columns c..c+3 of a rows x cols matrix with leading dimension ld.
+template <bool VEC>
+__device__ inline f32x4 load4(const float* __restrict__ p, int ld, int rows, int cols, int r,
+                              int c) {
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (r >= rows) return v;
+    const float* q = p + (size_t)r * ld + c;
+    if (VEC && c + 3 < cols) return *reinterpret_cast<const f32x4*>(q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (c + e < cols) v[e] = q[e];
+    return v;
+}
+
+// Operand slice loader.  "Contiguous-k" operands (A in NN/NT, B in NT/TT) are read
+// along k and transposed into the k-major LDS tile; the others are copied row by row.
+// TILE = tile extent along the non-k dimension (BM or BN).
+template <bool KCONTIG, bool VEC, int TILE>
+struct Slice {
+    f32x4 v[2];   // 2 x float4 per thread per slice (TILE * BK / 4 / NTHREADS)
+
+    // base/ld describe the stored matrix; t0 = first index along the tile dimension,
+    // k0 = first k; extent_t / extent_k bound the valid region.
+    __device__ void fetch(const float* __restrict__ base, int ld, int t0, int k0, int extent_t,
+                          int extent_k, int tid) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int f = tid + r * NTHREADS;
+            if (KCONTIG) {   // stored [t][k]: 4 k per float4
+                const int t = f / (BK / 4), kq = f % (BK / 4);
+                v[r] = load4<VEC>(base, ld, extent_t, extent_k, t0 + t, k0 + 4 * kq);
+            } else {         // stored [k][t]: 4 t per float4
+                const int k = f / (TILE / 4), tq = f % (TILE / 4);
+                v[r] = load4<VEC>(base, ld, extent_k, extent_t, k0 + k, t0 + 4 * tq);
+            }
+        }
+    }
+    __device__ void store(float* lds, int stride, int tid) const {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int f = tid + r * NTHREADS;
+            if (KCONTIG) {
+                const int t = f / (BK / 4), kq = f % (BK / 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) lds[(4 * kq + e) * stride + t] = v[r][e];
+            } else {
+                const int k = f / (TILE / 4), tq = f % (TILE / 4);
+                *reinterpret_cast<f32x4*>(&lds[k * stride + 4 * tq]) = v[r];
+            }
+        }
+    }
+};
+
+template <bool TA, bool TB, bool VA, bool VB>
+__global__ void __launch_bounds__(NTHREADS)
+gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
+                const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc) {
+    __shared__ __attribute__((aligned(16))) float As[2][BK * LDS_A];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDS_B];
+
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    int tm, tn;
+    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+
+    // A: op(A)[i][k]; stored [i][k] when !TA (k contiguous), [k][i] when TA.
+    Slice<!TA, VA, BM> sa;
+    // B: op(B)[k][j]; stored [k][j] when !TB (j contiguous), [j][k] when TB.
+    Slice<TB, VB, BN> sb;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    const int nk = (K + BK - 1) / BK;
+    if (nk > 0) {
+        sa.fetch(A, lda, m0, 0, M, K, tid);
+        sb.fetch(B, ldb, n0, 0, N, K, tid);
+        sa.store(As[0], LDS_A, tid);
+        sb.store(Bs[0], LDS_B, tid);
+        __syncthreads();
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            sa.fetch(A, lda, m0, (kt + 1) * BK, M, K, tid);
+            sb.fetch(B, ldb, n0, (kt + 1) * BK, N, K, tid);
+        }
+        const float* as = As[cur];
+        const float* bs = Bs[cur];
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            float a0 = as[(kk + h) * LDS_A + wm + l32];
+            float a1 = as[(kk + h) * LDS_A + wm + 32 + l32];
+            float b0 = bs[(kk + h) * LDS_B + wn + l32];
+            float b1 = bs[(kk + h) * LDS_B + wn + 32 + l32];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        if (more) {
+            sa.store(As[cur ^ 1], LDS_A, tid);
+            sb.store(Bs[cur ^ 1], LDS_B, tid);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue: lanes 0..31 of a register cover 32 consecutive columns of one row.
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int col = n0 + wn + 32 * b + l32;
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < M) {
+                    float* c = C + (size_t)row * ldc + col;
+                    *c = beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c;
+                }
+            }
+        }
+}
+
+template <bool TA, bool TB>
+int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
+           float* C, int ldc) {
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    // 128-bit loads need a 16-byte aligned base and a leading dimension divisible by 4.
+    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0);
+    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0);
+    dim3 grid(tiles), block(NTHREADS);
+    hipStream_t s = stream();
+    if (va && vb)
+        gemm_f32_kernel<TA, TB, true, true><<<grid, block, 0, s>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+    else if (va)
+        gemm_f32_kernel<TA, TB, true, false><<<grid, block, 0, s>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+    else if (vb)
+        gemm_f32_kernel<TA, TB, false, true><<<grid, block, 0, s>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+    else
+        gemm_f32_kernel<TA, TB, false, false><<<grid, block, 0, s>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+    return check_launch("dh_gemm_f32");
+}
+
+}  // namespace
+}  // namespace dh
+
+using namespace dh;
+
+extern "C" int dh_gemm_f32(int transA, int transB, int M, int N, int K, const float* A, int lda,
+                           const float* B, int ldb, float beta, float* C, int ldc) {
+    DH_TRY(ensure_init());
+    if (M < 0 || N < 0 || K < 0) return set_error(DH_ERR_INVALID, "dh_gemm_f32: negative shape");
+    if (M == 0 || N == 0) return DH_OK;
+    if (!C || (K > 0 && (!A || !B)))
+        return set_error(DH_ERR_INVALID, "dh_gemm_f32: null pointer");
+    // A and B are not read when K == 0, so only C's leading dimension matters then.
+    if (ldc < N || (K > 0 && (lda < (transA ? M : K) || ldb < (transB ? K : N))))
+        return set_error(DH_ERR_INVALID, "dh_gemm_f32: leading dimension too small");
+    if (transA)
+        return transB ? launch<true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc)
+                      : launch<true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+    return transB ? launch<false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc)
+                  : launch<false, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+}

@@ -1,0 +1,195 @@
+"""ctypes binding of libdream_hip.so (include/dream_hip.h) plus a small device-buffer type.
+
+The product path: every call goes to the HIP library.  There is no CPU fallback;
+if the library is missing or no GPU is usable the calls raise.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "lib", "libdream_hip.so")
+
+DH_OK, DH_ERR_NO_DEVICE, DH_ERR_INVALID, DH_ERR_OOM, DH_ERR_HIP, DH_ERR_UNSUPPORTED = range(6)
+F32, BF16, F64 = 0, 1, 2
+_DT = {np.dtype(np.float32): F32, np.dtype(np.uint16): BF16, np.dtype(np.float64): F64}
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name: (restype, argtypes) -- mirrors include/dream_hip.h
+_SIGS = {
+    "dh_init": (_i, []),
+    "dh_available": (_i, []),
+    "dh_device_info": (_i, [ctypes.c_char_p, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
+                            ctypes.POINTER(_i), ctypes.POINTER(ctypes.c_longlong)]),
+    "dh_last_error": (ctypes.c_char_p, []),
+    "dh_dispatch_threshold": (_sz, []),
+    "dh_matmul_eligible": (_i, [_i, _i]),
+    "dh_flash_eligible": (_i, [_i, _i, _i]),
+    "dh_malloc": (_vp, [_sz]),
+    "dh_free": (_i, [_vp]),
+    "dh_pool_release": (_i, []),
+    "dh_memcpy_h2d": (_i, [_vp, _vp, _sz]),
+    "dh_memcpy_d2h": (_i, [_vp, _vp, _sz]),
+    "dh_memcpy_d2d": (_i, [_vp, _vp, _sz]),
+    "dh_memset": (_i, [_vp, _i, _sz]),
+    "dh_sync": (_i, []),
+    "dh_get_stream": (_vp, []),
+    "dh_set_stream": (_i, [_vp]),
+    "dh_timer_start": (_i, []),
+    "dh_timer_stop": (_i, [ctypes.POINTER(_f)]),
+    "dh_convert": (_i, [_vp, _i, _vp, _i, _sz]),
+    "dh_gemm_f32": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i]),
+    "dh_gemm_bf16": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i]),
+    "dh_flash_fwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp]),
+    "dh_flash_bwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _vp,
+                          _vp, _vp, _vp, _i]),
+    "dh_row_softmax": (_i, [_vp, _vp, _i, _i, _i]),
+}
+
+EXPORTED = tuple(_SIGS)
+_lib = None
+
+
+class DreamHipError(RuntimeError):
+    pass
+
+
+def load():
+    """Load libdream_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise DreamHipError(
+                f"{LIB_PATH} is missing: build it with `python -m dreamcompiler_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status, what="dream_hip"):
+    if status != DH_OK:
+        msg = load().dh_last_error().decode(errors="replace")
+        raise DreamHipError(f"{what} failed with status {status}: {msg}")
+
+
+def available():
+    return load().dh_available() == 1
+
+
+def device_info():
+    L = load()
+    name = ctypes.create_string_buffer(256)
+    cus, xcds, clk = _i(), _i(), _i()
+    hbm = ctypes.c_longlong()
+    check(L.dh_device_info(name, 256, ctypes.byref(cus), ctypes.byref(xcds),
+                           ctypes.byref(clk), ctypes.byref(hbm)), "dh_device_info")
+    return {"name": name.value.decode(), "cus": cus.value, "xcds": xcds.value,
+            "sclk_mhz": clk.value, "hbm_bytes": hbm.value}
+
+
+def sync():
+    check(load().dh_sync(), "dh_sync")
+
+
+class DeviceBuffer:
+    """A device allocation from the library pool, with numpy upload/download."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = load().dh_malloc(max(self.nbytes, 1))
+        if not self.ptr:
+            check(DH_ERR_OOM, f"dh_malloc({self.nbytes})")
+
+    @classmethod
+    def from_numpy(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.dtype, buf.shape = arr.dtype, arr.shape
+        check(load().dh_memcpy_h2d(buf.ptr, arr.ctypes.data, arr.nbytes), "dh_memcpy_h2d")
+        sync()
+        return buf
+
+    @classmethod
+    def empty(cls, shape, dtype):
+        dtype = np.dtype(dtype)
+        buf = cls(int(np.prod(shape)) * dtype.itemsize)
+        buf.dtype, buf.shape = dtype, tuple(shape)
+        return buf
+
+    def numpy(self, shape=None, dtype=None):
+        dtype = np.dtype(dtype or self.dtype)
+        shape = tuple(shape or self.shape)
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        check(load().dh_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes), "dh_memcpy_d2h")
+        return out
+
+    def fill_zero(self):
+        check(load().dh_memset(self.ptr, 0, self.nbytes), "dh_memset")
+
+    def free(self):
+        if self.ptr:
+            load().dh_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _p(x):
+    return x.ptr if isinstance(x, DeviceBuffer) else x
+
+
+def convert(dst, dst_type, src, src_type, n):
+    check(load().dh_convert(_p(dst), dst_type, _p(src), src_type, int(n)), "dh_convert")
+
+
+def gemm_f32(transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc):
+    check(load().dh_gemm_f32(int(transA), int(transB), M, N, K, _p(A), lda, _p(B), ldb,
+                             float(beta), _p(C), ldc), "dh_gemm_f32")
+
+
+def gemm_bf16(transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc):
+    check(load().dh_gemm_bf16(int(transA), int(transB), M, N, K, _p(A), lda, _p(B), ldb,
+                              float(beta), _p(C), ldc), "dh_gemm_bf16")
+
+
+def flash_fwd(dtype, BH, S, D, scale, causal, Q, K, V, O, LSE):
+    check(load().dh_flash_fwd(dtype, BH, S, D, float(scale), int(causal), _p(Q), _p(K),
+                              _p(V), _p(O), _p(LSE)), "dh_flash_fwd")
+
+
+def flash_bwd(dtype, BH, S, D, scale, causal, Q, K, V, O, dO, LSE, dQ, dK, dV, accumulate):
+    check(load().dh_flash_bwd(dtype, BH, S, D, float(scale), int(causal), _p(Q), _p(K),
+                              _p(V), _p(O), _p(dO), _p(LSE), _p(dQ), _p(dK), _p(dV),
+                              int(accumulate)), "dh_flash_bwd")
+
+
+def row_softmax(X, Y, R, C, log=False):
+    check(load().dh_row_softmax(_p(X), _p(Y), R, C, int(log)), "dh_row_softmax")
+
+
+class Timer:
+    """HIP events on the library stream (the stream every kernel here runs on)."""
+
+    def __enter__(self):
+        check(load().dh_timer_start(), "dh_timer_start")
+        return self
+
+    def __exit__(self, *exc):
+        ms = _f()
+        check(load().dh_timer_stop(ctypes.byref(ms)), "dh_timer_stop")
+        self.ms = ms.value
+        return False

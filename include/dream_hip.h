@@ -1,0 +1,133 @@
+/*
+ * dream_hip.h -- C ABI of the MI355X (gfx950) backend for Dream's dense-tensor hot path.
+ *
+ * This library replaces the GPU half of the reference runtime's backend
+ * (runtime/backend/gpu.inc: the OpenCL/CUDA/cuBLAS loaders, DeviceMemPool, HostBuf
+ * staging and the OpenCL/cuBLAS GEMM and flash kernels).  Plain pointers and sizes
+ * only; no C++ or framework types cross this boundary.
+ *
+ * Conventions
+ *  - Every entry point returns an int status: DH_OK (0) or a DH_ERR_* code, with a
+ *    human-readable reason from dh_last_error().  Nothing here exits or throws; on
+ *    an error the caller decides what to do (the integrated runtime prints
+ *    "RUNTIME ERROR in <op>: ..." and keeps going, runtime/ops/elementwise.inc:972-989).
+ *  - Pointers named d_* are device pointers (from dh_malloc or any hipMalloc'd
+ *    buffer in the same process).  Pointers named h_* are host pointers.
+ *  - Matrices are row-major.  Leading dimensions are in elements.
+ *  - All work is enqueued on the library stream (dh_get_stream); calls return once
+ *    the work is queued, except where "synchronous" is stated.
+ *  - bf16 buffers hold the upper 16 bits of an IEEE fp32 value (uint16_t storage).
+ *  - Single device: the backend drives device 0 of the process (one process per GPU).
+ */
+#ifndef DREAM_HIP_H
+#define DREAM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    DH_OK = 0,
+    DH_ERR_NO_DEVICE = 1,   /* no usable HIP device / init failed      */
+    DH_ERR_INVALID = 2,     /* bad argument (shape, pointer, dtype)     */
+    DH_ERR_OOM = 3,         /* device allocation failed                 */
+    DH_ERR_HIP = 4,         /* a HIP runtime call or launch failed      */
+    DH_ERR_UNSUPPORTED = 5  /* valid request this build does not cover  */
+};
+
+enum { DH_F32 = 0, DH_BF16 = 1, DH_F64 = 2 };
+
+/* ---- device / init --------------------------------------------------------
+ * Replaces initBackend() (runtime/backend/gpu.inc:313-361): lazy, idempotent, logs
+ * "[dream] backend: HIP (device: ...)" once to stderr.  dh_init is also called
+ * implicitly by every other entry point. */
+int dh_init(void);
+/* 1 when a HIP device is usable (the replacement of the OpenCL/CUDA probe,
+ * gpu.inc:271-273, for the GEMM and flash builtins). */
+int dh_available(void);
+/* Device name, compute units, XCDs, max shader clock (MHz), HBM bytes. */
+int dh_device_info(char* name, int name_len, int* cus, int* xcds, int* sclk_mhz,
+                   long long* hbm_bytes);
+const char* dh_last_error(void);
+
+/* ---- dispatch policy (kept from the reference) -----------------------------
+ * gpu_dispatch_threshold() (gpu.inc:293-307): 262144 elements of M*N unless env
+ * DREAM_GPU_THRESHOLD overrides it.  dh_matmul_eligible: M*N >= threshold
+ * (elementwise.inc:1033).  dh_flash_eligible: B*S*S >= 262144 and dk <= 128
+ * (runtime/nn/training.inc:308, 336). */
+size_t dh_dispatch_threshold(void);
+int dh_matmul_eligible(int M, int N);
+int dh_flash_eligible(int B, int S, int dk);
+
+/* ---- memory (replaces DeviceMemPool, gpu.inc:372-420) ----------------------
+ * Exact-size buckets, at most 64 cached buffers per size; dh_free returns the
+ * buffer to its bucket.  dh_pool_release frees every cached buffer. */
+void* dh_malloc(size_t bytes);
+int dh_free(void* d_ptr);
+int dh_pool_release(void);
+int dh_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes);
+int dh_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes);
+int dh_memcpy_d2d(void* d_dst, const void* d_src, size_t bytes);
+int dh_memset(void* d_dst, int value, size_t bytes);
+int dh_sync(void);                         /* synchronous: waits for the stream */
+void* dh_get_stream(void);                 /* hipStream_t of the library        */
+int dh_set_stream(void* hip_stream);       /* NULL restores the library stream  */
+
+/* ---- timing on the library stream ----------------------------------------- */
+int dh_timer_start(void);
+int dh_timer_stop(float* ms);              /* synchronous */
+
+/* ---- conversions (replaces HostBuf fromDouble/toDouble, gpu.inc:177-196) ----
+ * dst[i] = convert(src[i]) for n elements.  Supported pairs: F64->F32, F32->F64,
+ * F64->BF16 (through fp32, then round to nearest even exactly as
+ * dream_to_bf16, runtime/nn/training.inc:1969-1976), F32->BF16, BF16->F32. */
+int dh_convert(void* d_dst, int dst_type, const void* d_src, int src_type, size_t n);
+
+/* ---- GEMM -------------------------------------------------------------------
+ * C[M x N] = op(A) @ op(B) + beta * C, fp32 accumulate, fp32 C.
+ * op(X) = X (trans = 0) or X^T (trans = 1) of the stored row-major matrix:
+ *   transA = 0: A is M x K (lda >= K);  transA = 1: A is stored K x M (lda >= M)
+ *   transB = 0: B is K x N (ldb >= N);  transB = 1: B is stored N x K (ldb >= K)
+ * NN is tensor_matmul's C = A @ B (elementwise.inc:971-1213, replacing the
+ * OpenCL matmul_tiled_wpt4 kernel and the cublasSgemm/GemmEx branch 1042-1212);
+ * NT with beta = 1 is the matmul backward's dA += dY @ B^T and TN with beta = 1
+ * its dB += A^T @ dY (runtime/ops/autograd.inc:91-125).
+ * beta = 0 never reads C.  M, N or K of 0 is a valid no-op (K = 0 scales C by beta). */
+int dh_gemm_f32(int transA, int transB, int M, int N, int K,
+                const float* d_A, int lda, const float* d_B, int ldb,
+                float beta, float* d_C, int ldc);
+/* Same contract with bf16 A and B (replaces the fp16 cublasGemmEx path,
+ * elementwise.inc:1046-1071; inputs are bf16 rather than truncated fp16). */
+int dh_gemm_bf16(int transA, int transB, int M, int N, int K,
+                 const uint16_t* d_A, int lda, const uint16_t* d_B, int ldb,
+                 float beta, float* d_C, int ldc);
+
+/* ---- FlashAttention -----------------------------------------------------------
+ * Q, K, V, O in the reference layout (B, S*dk): slice b (a batch x head pair)
+ * starts at b*S*D, rows of D contiguous.  dtype DH_F32 or DH_BF16 for Q/K/V/dO;
+ * O is written in the same dtype; LSE (fp32, B*S) receives m_i + ln(l_i) of the
+ * scaled scores (natural log).  Causal keeps key j <= query i
+ * (runtime/nn/training.inc:284-401, which replaces the OpenCL flash_attention_v1
+ * kernel 310-363).  D in {64, 128}.  scale is usually 1/sqrt(D). */
+int dh_flash_fwd(int dtype, int BH, int S, int D, float scale, int causal,
+                 const void* d_Q, const void* d_K, const void* d_V,
+                 void* d_O, float* d_LSE);
+/* Backward of dh_flash_fwd given its O and LSE (runtime/ops/autograd.inc:779-840).
+ * dQ, dK, dV are fp32 (B, S*D).  accumulate = 1 adds into them (the reference
+ * backward's "+="), 0 overwrites.  Deterministic: no floating-point atomics. */
+int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int causal,
+                 const void* d_Q, const void* d_K, const void* d_V,
+                 const void* d_O, const void* d_dO, const float* d_LSE,
+                 float* d_dQ, float* d_dK, float* d_dV, int accumulate);
+
+/* ---- row reductions (runtime/ops/elementwise.inc:338-358, 1550-1570) -----------
+ * Y = softmax or log_softmax over each of R rows of C contiguous fp32 values. */
+int dh_row_softmax(const float* d_X, float* d_Y, int R, int C, int log_softmax);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,186 @@
+"""GPU parity of dh_gemm_f32 / dh_gemm_bf16 against the fp64 oracle.
+
+Tolerances (stated per the contract of the north star):
+  fp32: max_ij |C - C64| / max_ij |C64| <= 1e-5 * sqrt(K), where C64 is the fp64 oracle
+        on the same fp64 inputs the fp32 operands were rounded from; the per-element
+        form |C - C64|_ij <= 1e-5 * sqrt(K) * (|A| |B|)_ij is checked as well.
+  bf16: max_ij |C - C64| / max_ij |C64| <= 2e-2, C64 = fp64 oracle on the bf16-rounded
+        (round-to-nearest-even) inputs.
+  The reference's own gates are also applied where they exist: gpu_selftest's
+  absolute sqrt(K) * 1e-4 (elementwise.inc:840-846) and gemm_selftest's f32 2e-4.
+"""
+import numpy as np
+import pytest
+
+import _oracle as O
+from _gpu import bf16_bits, bits_to_f32, elementwise_ratio, gemm, maxrel
+
+pytestmark = pytest.mark.gpu
+
+
+def f32(x):
+    return np.asarray(x, np.float32)
+
+
+def check_f32(got, A64, B64, K, transA=False, transB=False, beta=0.0, C0=None):
+    ref = O.gemm_general_d(transA, transB, A64, B64, beta, C0)
+    tol = 1e-5 * np.sqrt(max(K, 1))
+    e1 = maxrel(got, ref)
+    assert e1 <= tol, f"maxrel {e1:.3e} > {tol:.3e}"
+    if not beta:
+        opA = np.abs(A64.T if transA else A64)
+        opB = np.abs(B64.T if transB else B64)
+        e2 = elementwise_ratio(got, ref, opA, opB)
+        assert e2 <= tol, f"per-element {e2:.3e} > {tol:.3e}"
+    return e1
+
+
+def test_c1_fp32_1024_seed42():
+    # Config 1: set_seed(42); A = randn(1024,1024); B = randn(1024,1024); C = A @ B.
+    O.set_seed(42)
+    A, B = O.randn(1024, 1024), O.randn(1024, 1024)
+    got = gemm(f32(A), f32(B))
+    ref = O.gemm_d(A, B)                      # the reference's fp64 `@`
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(1024)
+    assert np.abs(got - ref).max() < np.sqrt(1024) * 1e-4   # gpu_selftest gate
+
+
+@pytest.mark.parametrize("shape", [
+    (1, 1, 1), (1, 7, 1), (5, 1, 9), (3, 4, 5), (7, 13, 17), (31, 33, 37), (64, 64, 64),
+    (65, 63, 66), (128, 100, 96), (200, 50, 300), (257, 129, 255),          # gemm_selftest
+    (32, 32, 32), (33, 31, 35), (256, 128, 256), (300, 200, 257), (100, 100, 100),
+    (1, 64, 1), (65, 1, 63),                                                 # kernel-sim shapes
+    (256, 128, 256), (300, 200, 257), (512, 64, 300),                        # gpu_selftest
+])
+def test_fp32_adversarial_shapes(shape):
+    M, K, N = shape
+    rng = np.random.default_rng(M * 1000 + K * 10 + N)
+    A, B = rng.uniform(-1, 1, (M, K)), rng.uniform(-1, 1, (K, N))
+    A, B = f32(A).astype(np.float64), f32(B).astype(np.float64)
+    got = gemm(f32(A), f32(B))
+    check_f32(got, A, B, K)
+    assert np.abs(got - O.gemm_ref_d(A, B)).max() < np.sqrt(K) * 1e-4
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("beta", [0.0, 1.0, -0.5])
+@pytest.mark.parametrize("ldpad", [0, 3, 4])
+def test_fp32_transposes_beta_strides(ta, tb, beta, ldpad):
+    M, N, K = 131, 67, 259
+    rng = np.random.default_rng(17 + ta + 2 * tb + int(4 * beta) + ldpad)
+    A = f32(rng.standard_normal((K, M) if ta else (M, K))).astype(np.float64)
+    B = f32(rng.standard_normal((N, K) if tb else (K, N))).astype(np.float64)
+    C0 = f32(rng.standard_normal((M, N))).astype(np.float64)
+    got = gemm(f32(A), f32(B), bool(ta), bool(tb), beta, f32(C0), ldpad=ldpad)
+    check_f32(got, A, B, K, ta, tb, beta, C0)
+
+
+def test_fp32_closed_forms_and_degenerate_shapes():
+    # ones(256,256) @ ones(256,256): every element is 256, sum 16777216 (gpu_diagnose).
+    C = gemm(np.ones((256, 256), np.float32), np.ones((256, 256), np.float32))
+    assert np.all(C == 256) and C.sum(dtype=np.float64) == 16777216
+    C = gemm(np.ones((2, 3), np.float32), np.ones((3, 2), np.float32))   # tests/09: "3 3"
+    assert np.all(C == 3)
+    # K = 0: C = beta * C
+    C0 = np.arange(12, dtype=np.float32).reshape(3, 4)
+    got = gemm(np.zeros((3, 0), np.float32), np.zeros((0, 4), np.float32), beta=2.0, C0=C0)
+    assert np.array_equal(got, 2 * C0)
+    # beta = 0 ignores NaN already in C
+    got = gemm(np.ones((5, 6), np.float32), np.ones((6, 7), np.float32), beta=0.0,
+               C0=np.full((5, 7), np.nan, np.float32))
+    assert np.all(got == 6)
+
+
+def _mlp_tensors():
+    # Config 2: X[4096x784] ~ U(0,1), W1 = kaiming_init(784, 257), W2 = kaiming_init(257, 10)
+    # (Dream's kaiming_init(r, c) draws N(0, sqrt(2/c)), builtins.inc:511-519); upstream
+    # gradients N(0,1); all from the reference RNG stream, seed 1234.
+    O.set_seed(1234)
+    X = O.uniform(4096 * 784, 0.0, 1.0).reshape(4096, 784)
+    W1, W2 = O.kaiming(784, 257), O.kaiming(257, 10)
+    dY = O.randn(4096, 10)
+    H = np.maximum(O.gemm_d(f32(X).astype(np.float64), f32(W1).astype(np.float64)), 0.0)
+    dZ1 = O.randn(4096, 257)
+    return [f32(t).astype(np.float64) for t in (X, W1, W2, dY, H, dZ1)]
+
+
+def test_c2_mlp_forward_backward_set():
+    X, W1, W2, dY, H, dZ1 = _mlp_tensors()
+    cases = [
+        ("X@W1", X, W1, 0, 0, 784),
+        ("H@W2", H, W2, 0, 0, 257),
+        ("dW1=X^T dZ1", X, dZ1, 1, 0, 4096),
+        ("dX=dZ1 W1^T", dZ1, W1, 0, 1, 257),
+        ("dW2=H^T dY", H, dY, 1, 0, 4096),
+        ("dH=dY W2^T", dY, W2, 0, 1, 10),
+    ]
+    for name, A, B, ta, tb, K in cases:
+        got = gemm(f32(A), f32(B), bool(ta), bool(tb))
+        check_f32(got, A, B, K, ta, tb)
+
+
+def _rowcol_sums_check(got, A64, B64, tol):
+    """Full-size property: row sums of C equal A @ (B 1) and column sums (1^T A) B."""
+    r_ref = A64 @ B64.sum(axis=1)
+    c_ref = A64.sum(axis=0) @ B64
+    r = got.sum(axis=1, dtype=np.float64)
+    c = got.sum(axis=0, dtype=np.float64)
+    assert np.abs(r - r_ref).max() <= tol * max(np.abs(r_ref).max(), 1.0)
+    assert np.abs(c - c_ref).max() <= tol * max(np.abs(c_ref).max(), 1.0)
+
+
+def test_c5_fp32_4096_full_size():
+    rng = np.random.default_rng(4096)
+    A = rng.standard_normal((4096, 4096), dtype=np.float32)
+    B = rng.standard_normal((4096, 4096), dtype=np.float32)
+    got = gemm(A, B)
+    A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    rows = np.sort(rng.choice(4096, 48, replace=False))
+    ref = O.gemm_d(A64[rows], B64)
+    assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(4096)
+    _rowcol_sums_check(got, A64, B64, 1e-5)
+
+
+@pytest.mark.parametrize("shape", [(1024, 1024, 1024), (257, 129, 255), (65, 63, 66),
+                                   (300, 200, 257), (1, 64, 1), (520, 8192, 264)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_bf16_parity(shape, ta, tb):
+    M, K, N = shape
+    rng = np.random.default_rng(M + K + N + 7 * ta + 13 * tb)
+    A = rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32)
+    B = rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32)
+    Ab, Bb = bf16_bits(A), bf16_bits(B)
+    got = gemm(Ab, Bb, bool(ta), bool(tb), dtype="bf16")
+    ref = O.gemm_general_d(ta, tb, bits_to_f32(Ab).astype(np.float64),
+                           bits_to_f32(Bb).astype(np.float64))
+    assert maxrel(got, ref) <= 2e-2
+    # fp32 accumulation of exact bf16 products is far tighter than the contract:
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_bf16_beta_and_padding():
+    M, N, K = 200, 136, 264
+    rng = np.random.default_rng(99)
+    A, B = rng.standard_normal((M, K), dtype=np.float32), rng.standard_normal((K, N), dtype=np.float32)
+    C0 = rng.standard_normal((M, N), dtype=np.float32)
+    for ldpad in (0, 3, 8):
+        Ab, Bb = bf16_bits(A), bf16_bits(B)
+        got = gemm(Ab, Bb, beta=1.0, C0=C0, dtype="bf16", ldpad=ldpad)
+        ref = O.gemm_general_d(0, 0, bits_to_f32(Ab).astype(np.float64),
+                               bits_to_f32(Bb).astype(np.float64), 1.0, C0.astype(np.float64))
+        assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_c5_bf16_8192_full_size():
+    # Config 5: A, B 8192^2 ~ N(0,1) rounded to bf16 (RNE), fp32 accumulate and output.
+    rng = np.random.default_rng(8192)
+    Ab = bf16_bits(rng.standard_normal((8192, 8192), dtype=np.float32))
+    Bb = bf16_bits(rng.standard_normal((8192, 8192), dtype=np.float32))
+    got = gemm(Ab, Bb, dtype="bf16")
+    A64 = bits_to_f32(Ab).astype(np.float64)
+    B64 = bits_to_f32(Bb).astype(np.float64)
+    rows = np.sort(rng.choice(8192, 24, replace=False))
+    ref = O.gemm_d(A64[rows], B64)
+    assert maxrel(got[rows], ref) <= 2e-2
+    assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(8192)
+    _rowcol_sums_check(got, A64, B64, 1e-5)

@@ -1,0 +1,296 @@
+"""Pins the CPU oracle (oracle/dream_oracle.cpp) before anything is checked against it.
+
+Three kinds of evidence, chosen so that a dropped term, a wrong sign or index or a
+transposed operand fails at least one check:
+  1. golden vectors written by the reference runtime itself (tests/golden/);
+  2. the reference build in oracle/_ref/, called on fresh inputs (skipped where the
+     reference tree was not available to build it, e.g. on the GPU box);
+  3. mathematics: closed forms, special cases, independent numpy/scipy/torch
+     computations and central finite differences.
+Runs on the CPU only.
+"""
+import os
+
+import numpy as np
+import pytest
+import scipy.special as sps
+
+import _oracle as O
+import _ref_runtime
+
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
+
+
+def rel(a, b):
+    return float(np.abs(np.asarray(a) - np.asarray(b)).max() / max(np.abs(b).max(), 1e-300))
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_built():
+    O.lib()
+
+
+# --------------------------------------------------------------------------- golden
+def test_rng_matches_reference_stream():
+    O.set_seed(42)
+    assert np.array_equal(O.randn(4, 250), GOLD["rng_randn_s42"])
+    O.set_seed(7)
+    assert np.array_equal(O.kaiming(16, 10), GOLD["rng_kaiming_s7_16x10"])
+
+
+@pytest.mark.parametrize("shape", [(65, 63, 66), (33, 300, 35), (1, 7, 1), (5, 1, 9)])
+def test_gemm_d_golden(shape):
+    key = "gemm_d_%dx%dx%d" % shape
+    A, B, C = GOLD[key + "_A"], GOLD[key + "_B"], GOLD[key + "_C"]
+    assert rel(O.gemm_d(A, B), C) <= 1e-12
+    assert rel(O.gemm_ref_d(A, B), C) <= 1e-11   # the reference's own selftest gate
+
+
+@pytest.mark.parametrize("shape", [(33, 31, 35), (40, 300, 37)])
+def test_gemm_f32_golden(shape):
+    key = "gemm_f32_%dx%dx%d" % shape
+    A, B, C = GOLD[key + "_A"], GOLD[key + "_B"], GOLD[key + "_C"]
+    got = O.gemm_f32(A.astype(np.float32), B.astype(np.float32))
+    assert rel(got, C) <= 1e-6
+
+
+def test_matmul_bwd_golden():
+    k = "mmbwd_65x63x66"
+    dA, dB = O.matmul_bwd(GOLD[k + "_A"], GOLD[k + "_B"], GOLD[k + "_W"])
+    assert rel(dA, GOLD[k + "_dA"]) <= 1e-12
+    assert rel(dB, GOLD[k + "_dB"]) <= 1e-12
+
+
+ATTN_CASES = [("attn_B1_S100_dk24_Bc16", 1, 100, 24, 16), ("attn_B2_S64_dk16_Bc8", 2, 64, 16, 8)]
+
+
+@pytest.mark.parametrize("key,B,S,dk,Bc", ATTN_CASES)
+def test_attention_family_golden(key, B, S, dk, Bc):
+    Q, K, V, W = (GOLD[f"{key}_{c}"] for c in "QKVW")
+    assert rel(O.attention(Q, K, V, B, S, dk, False), GOLD[key + "_plain_O"]) <= 1e-12
+    assert rel(O.attention(Q, K, V, B, S, dk, True), GOLD[key + "_causal_O"]) <= 1e-12
+    assert rel(O.flash_fwd(Q, K, V, B, S, dk, Bc), GOLD[key + "_flash_O"]) <= 1e-12
+    grads = {
+        "plain": O.attention_bwd(Q, K, V, W, B, S, dk, False),
+        "causal": O.attention_bwd(Q, K, V, W, B, S, dk, True),
+        "flash": O.flash_bwd(Q, K, V, W, B, S, dk),
+    }
+    for kind, g in grads.items():
+        for i, c in enumerate("QKV"):
+            assert rel(g[i], GOLD[f"{key}_{kind}_d{c}"]) <= 1e-12, (kind, c)
+
+
+def test_softmax_golden():
+    X = GOLD["softmax_X"]
+    assert rel(O.softmax_rows(X), GOLD["softmax_Y"]) <= 1e-14
+    assert rel(O.log_softmax_rows(X), GOLD["log_softmax_Y"]) <= 1e-14
+
+
+# --------------------------------------------------------------------------- mathematics
+def test_gemm_closed_forms():
+    # all-ones M x K @ K x N is exactly K everywhere (tests/09, 10, 13; gpu_diagnose 256^2).
+    for M, K, N in [(2, 3, 2), (256, 256, 256), (7, 300, 5)]:
+        C = O.gemm_d(np.ones((M, K)), np.ones((K, N)))
+        assert np.all(C == K)
+        assert np.all(O.gemm_f32(np.ones((M, K)), np.ones((K, N))) == K)
+    A = np.random.default_rng(1).standard_normal((37, 41))
+    assert np.array_equal(O.gemm_ref_d(A, np.eye(41)), A)
+    assert np.array_equal(O.gemm_d(np.eye(37), A), A)
+
+
+def test_gemm_against_independent_numpy():
+    rng = np.random.default_rng(2)
+    for M, K, N in [(65, 63, 66), (130, 513, 67), (1, 1, 1), (9, 1000, 3)]:
+        A, B = rng.standard_normal((M, K)), rng.standard_normal((K, N))
+        ref = A @ B
+        assert rel(O.gemm_ref_d(A, B), ref) <= 1e-13
+        assert rel(O.gemm_d(A, B), ref) <= 1e-13
+        assert rel(O.gemm_f32(A, B), A.astype(np.float32).astype(np.float64)
+                   @ B.astype(np.float32).astype(np.float64)) <= 2e-6 * np.sqrt(K)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_general_transposes_and_beta(ta, tb):
+    rng = np.random.default_rng(3 + 2 * ta + tb)
+    M, N, K = 23, 17, 29
+    A = rng.standard_normal((K, M) if ta else (M, K))
+    B = rng.standard_normal((N, K) if tb else (K, N))
+    C0 = rng.standard_normal((M, N))
+    opA = A.T if ta else A
+    opB = B.T if tb else B
+    for beta in (0.0, 1.0, -0.5):
+        got = O.gemm_general_d(ta, tb, A, B, beta, C0)
+        assert rel(got, opA @ opB + beta * C0) <= 1e-13
+    # beta = 0 must ignore C, even NaN
+    got = O.gemm_general_d(ta, tb, A, B, 0.0, np.full((M, N), np.nan))
+    assert np.isfinite(got).all()
+
+
+def test_matmul_bwd_is_nt_tn_and_accumulates():
+    rng = np.random.default_rng(4)
+    A, B, dY = rng.standard_normal((13, 7)), rng.standard_normal((7, 11)), rng.standard_normal((13, 11))
+    dA0, dB0 = rng.standard_normal((13, 7)), rng.standard_normal((7, 11))
+    dA, dB = O.matmul_bwd(A, B, dY, dA0, dB0)
+    assert rel(dA, dA0 + dY @ B.T) <= 1e-13
+    assert rel(dB, dB0 + A.T @ dY) <= 1e-13
+
+
+def _fd_grad(f, X, eps=1e-6):
+    g = np.zeros_like(X)
+    flat, gf = X.reshape(-1), g.reshape(-1)
+    for i in range(flat.size):
+        h = eps * max(1.0, abs(flat[i]))
+        old = flat[i]
+        flat[i] = old + h
+        fp = f()
+        flat[i] = old - h
+        fm = f()
+        flat[i] = old
+        gf[i] = (fp - fm) / (2 * h)
+    return g
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_bwd_finite_differences(causal):
+    # gradcheck pattern of training.inc:3856-3907: loss = sum(O * W) with random W.
+    rng = np.random.default_rng(5)
+    B, S, dk = 2, 5, 3
+    Q, K, V, W = (rng.standard_normal((B, S * dk)) for _ in range(4))
+    loss = lambda: float((O.attention(Q, K, V, B, S, dk, causal) * W).sum())  # noqa: E731
+    dQ, dK, dV = O.attention_bwd(Q, K, V, W, B, S, dk, causal)
+    for X, g in ((Q, dQ), (K, dK), (V, dV)):
+        assert rel(g, _fd_grad(loss, X)) <= 1e-6
+    if causal:
+        fQ, fK, fV = O.flash_bwd(Q, K, V, W, B, S, dk)
+        for a, b in ((fQ, dQ), (fK, dK), (fV, dV)):
+            assert rel(a, b) <= 1e-12
+
+
+def test_flash_special_cases():
+    rng = np.random.default_rng(6)
+    # S = 1: the only key is the query's own -> O = V.
+    Q, K, V = (rng.standard_normal((3, 8)) for _ in range(3))
+    assert rel(O.flash_fwd(Q, K, V, 3, 1, 8), V) <= 1e-15
+    # Constant keys: uniform weights over j <= i -> causal running mean of V.
+    S, dk = 37, 4
+    Q = rng.standard_normal((1, S * dk))
+    K = np.tile(rng.standard_normal(dk), S)[None, :]
+    V = rng.standard_normal((1, S * dk))
+    Vm = V.reshape(S, dk)
+    mean = np.cumsum(Vm, axis=0) / np.arange(1, S + 1)[:, None]
+    for Bc in (1, 5, 64):
+        assert rel(O.flash_fwd(Q, K, V, 1, S, dk, Bc).reshape(S, dk), mean) <= 1e-13
+    # flash == standard causal at the reference's own selftest gate (1e-9).
+    for S, dk, Bc in [(64, 16, 8), (64, 16, 16), (128, 32, 32), (100, 24, 16)]:
+        Q, K, V = (rng.standard_normal((1, S * dk)) for _ in range(3))
+        assert rel(O.flash_fwd(Q, K, V, 1, S, dk, Bc), O.attention(Q, K, V, 1, S, dk, True)) < 1e-9
+
+
+def test_attention_against_independent_numpy():
+    rng = np.random.default_rng(7)
+    B, S, dk = 3, 19, 6
+    Q, K, V = (rng.standard_normal((B, S * dk)) for _ in range(3))
+    for causal in (False, True):
+        q, k, v = (x.reshape(B, S, dk) for x in (Q, K, V))
+        s = q @ k.transpose(0, 2, 1) / np.sqrt(dk)
+        if causal:
+            s = np.where(np.tril(np.ones((S, S), bool)), s, -np.inf)
+        ref = (sps.softmax(s, axis=-1) @ v).reshape(B, S * dk)
+        assert rel(O.attention(Q, K, V, B, S, dk, causal), ref) <= 1e-13
+        lse = sps.logsumexp(s, axis=-1)
+        assert rel(O.flash_lse(Q, K, B, S, dk, causal), lse) <= 1e-13
+
+
+def test_attention_bwd_invariants():
+    # sum_j dS_ij = 0 per row  <=>  sum over keys of dK contributions is consistent;
+    # checked through the identity D_i = dO_i . O_i = sum_j P_ij dP_ij.
+    rng = np.random.default_rng(8)
+    B, S, dk = 1, 9, 4
+    Q, K, V, dO = (rng.standard_normal((B, S * dk)) for _ in range(4))
+    O_ = O.attention(Q, K, V, B, S, dk, True).reshape(S, dk)
+    q, k, v, do = (x.reshape(S, dk) for x in (Q, K, V, dO))
+    s = np.where(np.tril(np.ones((S, S), bool)), q @ k.T / np.sqrt(dk), -np.inf)
+    P = sps.softmax(s, axis=-1)
+    dP = do @ v.T
+    assert np.allclose((do * O_).sum(1), (P * dP).sum(1), rtol=1e-12, atol=1e-12)
+    # shifting every key by the same vector c adds q_i . c to a whole score row, which
+    # the row softmax removes: O is unchanged.
+    K2 = (k + rng.standard_normal(dk)[None, :]).reshape(1, -1)
+    assert rel(O.attention(Q, K2, V, B, S, dk, True).reshape(S, dk), O_) <= 1e-13
+
+
+def test_softmax_math():
+    rng = np.random.default_rng(9)
+    X = rng.standard_normal((11, 257)) * 5
+    Y = O.softmax_rows(X)
+    assert np.allclose(Y.sum(1), 1.0, atol=1e-14)
+    assert rel(Y, sps.softmax(X, axis=1)) <= 1e-14
+    assert rel(O.softmax_rows(X + 3.0), Y) <= 1e-13          # shift invariance
+    assert rel(O.log_softmax_rows(X), sps.log_softmax(X, axis=1)) <= 1e-14
+
+
+def test_bf16_round_to_nearest_even():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(10)
+    x = np.concatenate([
+        rng.standard_normal(100000).astype(np.float32) * np.float32(10) ** rng.integers(
+            -30, 30, 100000).astype(np.float32),
+        np.array([0.0, -0.0, 1.0, -1.0, 3.4e38, 1e-40, -1e-40], np.float32),
+        # exact ties: 1 + 2^-8 (even below), 1 + 3*2^-8 (even above)
+        np.array([1.00390625, 1.01171875, -1.00390625], np.float32),
+    ])
+    x = x[np.isfinite(x)]
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.bf16_bits(x), ref)
+    assert O.to_bf16(1.00390625) == 1.0
+    assert O.to_bf16(1.01171875) == 1.015625
+
+
+def test_planted_mistakes_are_caught():
+    """Mutations of the oracle's outputs that a plausible bug would produce fail the gates."""
+    k = "attn_B1_S100_dk24_Bc16"
+    Q, K, V, W = (GOLD[f"{k}_{c}"] for c in "QKVW")
+    good = O.flash_fwd(Q, K, V, 1, 100, 24, 16)
+    # dropped scale (1/sqrt(dk) missing) -> reference mismatch
+    bad = O.flash_fwd(Q * np.sqrt(24), K, V, 1, 100, 24, 16)
+    assert rel(good, GOLD[k + "_flash_O"]) <= 1e-12 and rel(bad, GOLD[k + "_flash_O"]) > 1e-3
+    # swapped Q and K -> mismatch
+    assert rel(O.flash_fwd(K, Q, V, 1, 100, 24, 16), GOLD[k + "_flash_O"]) > 1e-3
+    # non-causal instead of causal -> mismatch
+    assert rel(O.attention(Q, K, V, 1, 100, 24, False), GOLD[k + "_flash_O"]) > 1e-3
+    # transposed B in the GEMM -> mismatch
+    g = "gemm_d_65x63x66"
+    A, B = GOLD[g + "_A"], GOLD[g + "_B"]
+    assert rel(O.gemm_d(A, B[::-1]), GOLD[g + "_C"]) > 1e-3
+
+
+# --------------------------------------------------------------------------- reference build
+needs_ref = pytest.mark.skipif(not _ref_runtime.available(),
+                               reason="oracle/_ref not built (no reference tree on this host)")
+
+
+@pytest.fixture(scope="module")
+def ref():
+    return _ref_runtime.RefRuntime()
+
+
+@needs_ref
+@pytest.mark.parametrize("shape", [(257, 129, 255), (64, 64, 64), (7, 13, 17), (300, 200, 257)])
+def test_gemm_against_reference_build(ref, shape):
+    M, K, N = shape
+    rng = np.random.default_rng(M * 7 + K)
+    A, B = rng.standard_normal((M, K)), rng.standard_normal((K, N))
+    assert rel(O.gemm_d(A, B), ref.matmul(A, B)) <= 1e-12
+    assert rel(O.gemm_f32(A, B), ref.matmul(A, B, f32=True)) <= 1e-6
+
+
+@needs_ref
+def test_flash_against_reference_build(ref):
+    rng = np.random.default_rng(12)
+    B, S, dk, Bc = 2, 130, 32, 64
+    Q, K, V, W = (rng.standard_normal((B, S * dk)) for _ in range(4))
+    assert rel(O.flash_fwd(Q, K, V, B, S, dk, Bc), ref.attention("flash", Q, K, V, B, S, dk, Bc)) <= 1e-12
+    got = O.flash_bwd(Q, K, V, W, B, S, dk)
+    want = ref.attention_grads("flash", Q, K, V, W, B, S, dk, Bc)
+    for a, b in zip(got, want):
+        assert rel(a, b) <= 1e-12
