@@ -59,3 +59,34 @@ def elementwise_ratio(got, ref, absA, absB):
     """max_ij |got - ref| / (|A| |B|)_ij: error against the per-element product scale."""
     scale = absA @ absB
     return float((np.abs(got - ref) / np.maximum(scale, 1e-30)).max())
+
+
+def flash_fwd(Q, K, V, BH, S, D, causal=True, dtype="f32", scale=None):
+    """dh_flash_fwd on host arrays of shape (BH, S*D).  Q/K/V fp32 (dtype f32) or bf16
+    bits (dtype bf16).  Returns (O as fp32, LSE)."""
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    dt = hip.BF16 if dtype == "bf16" else hip.F32
+    np_t = np.uint16 if dtype == "bf16" else np.float32
+    dQ, dK, dV = (DB.from_numpy(np.ascontiguousarray(x, np_t)) for x in (Q, K, V))
+    dO_ = DB.empty((BH, S * D), np_t)
+    dL = DB.empty((BH, S), np.float32)
+    hip.flash_fwd(dt, BH, S, D, scale, causal, dQ, dK, dV, dO_, dL)
+    O = dO_.numpy()
+    O = bits_to_f32(O) if dtype == "bf16" else O
+    return O, dL.numpy()
+
+
+def flash_bwd(Q, K, V, O, dO, LSE, BH, S, D, causal=True, dtype="f32", scale=None,
+              accumulate=False, init=None):
+    """dh_flash_bwd; O/dO in the input dtype (bf16 bits for bf16).  Returns fp32 grads."""
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    dt = hip.BF16 if dtype == "bf16" else hip.F32
+    np_t = np.uint16 if dtype == "bf16" else np.float32
+    bufs = [DB.from_numpy(np.ascontiguousarray(x, np_t)) for x in (Q, K, V, O, dO)]
+    dL = DB.from_numpy(np.ascontiguousarray(LSE, np.float32))
+    if init is None:
+        grads = [DB.empty((BH, S * D), np.float32) for _ in range(3)]
+    else:
+        grads = [DB.from_numpy(np.ascontiguousarray(g, np.float32)) for g in init]
+    hip.flash_bwd(dt, BH, S, D, scale, causal, *bufs, dL, *grads, int(accumulate))
+    return tuple(g.numpy() for g in grads)
