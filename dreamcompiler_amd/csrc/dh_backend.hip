@@ -98,7 +98,7 @@ int check_launch(const char* what) {
 }
 
 // ---------------------------------------------------------------------------
-// Conversion kernels: grid-stride, 4 elements per thread per step.
+// Conversion kernels: grid-stride loop, one element per thread per step.
 // ---------------------------------------------------------------------------
 template <typename S, typename D>
 __device__ inline D cvt(S x);
@@ -113,6 +113,7 @@ template <> __device__ inline uint16_t cvt<float, uint16_t>(float x) {
 template <> __device__ inline float cvt<uint16_t, float>(uint16_t x) {
     return bf16_bits_to_f32(x);
 }
+template <> __device__ inline float cvt<float, float>(float x) { return x; }
 
 template <typename S, typename D>
 __global__ void __launch_bounds__(256) convert_kernel(D* __restrict__ dst,
@@ -340,6 +341,7 @@ int dh_convert(void* dst, int dt, const void* src, int stype, size_t n) {
     if (stype == DH_F64 && dt == DH_BF16) return launch_convert<double, uint16_t>(dst, src, n);
     if (stype == DH_F32 && dt == DH_BF16) return launch_convert<float, uint16_t>(dst, src, n);
     if (stype == DH_BF16 && dt == DH_F32) return launch_convert<uint16_t, float>(dst, src, n);
+    if (stype == DH_F32 && dt == DH_F32) return launch_convert<float, float>(dst, src, n);
     return set_error(DH_ERR_UNSUPPORTED, "dh_convert: unsupported pair %d -> %d", stype, dt);
 }
 

@@ -83,7 +83,8 @@ int dh_timer_stop(float* ms);              /* synchronous */
 /* ---- conversions (replaces HostBuf fromDouble/toDouble, gpu.inc:177-196) ----
  * dst[i] = convert(src[i]) for n elements.  Supported pairs: F64->F32, F32->F64,
  * F64->BF16 (through fp32, then round to nearest even exactly as
- * dream_to_bf16, runtime/nn/training.inc:1969-1976), F32->BF16, BF16->F32. */
+ * dream_to_bf16, runtime/nn/training.inc:1969-1976), F32->BF16, BF16->F32, and F32->F32
+ * (a plain device copy). */
 int dh_convert(void* d_dst, int dst_type, const void* d_src, int src_type, size_t n);
 
 /* ---- GEMM -------------------------------------------------------------------
