@@ -1,0 +1,708 @@
+// dream_rt.cpp -- Dream runtime builtins of the dense-tensor hot path over the HIP C ABI.
+//
+// Mirrors the reference runtime's builtin interface (names, argument meaning, +1
+// ownership, "RUNTIME ERROR in <op>" error behaviour); see include/dream_rt.h.  Every
+// GEMM and attention computation goes through include/dream_hip.h.  Tensors are host
+// fp64 (optionally with an fp32 mirror); each hot-path op stages its operands to the
+// device, runs the kernels and copies the result back, the same contract as the
+// reference's GPU branch (HostBuf + cuBLAS/OpenCL, runtime/ops/elementwise.inc:1042-1212).
+#include "../../include/dream_rt.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <unordered_set>
+#include <vector>
+
+#include "../../include/dream_hip.h"
+
+namespace {
+
+bool g_bf16 = false;   // dream_enable_fp16(): reduced-precision `@`
+
+std::mt19937& rng() {
+    static std::mt19937 g(std::random_device{}());
+    return g;
+}
+
+void rt_error(const char* op, const char* fmt, ...) {
+    std::fprintf(stderr, "RUNTIME ERROR in %s: ", op);
+    va_list ap;
+    va_start(ap, fmt);
+    std::vfprintf(stderr, fmt, ap);
+    va_end(ap);
+    std::fprintf(stderr, "\n");
+    std::fflush(stderr);
+}
+
+// Device buffer from the backend pool, returned on scope exit.
+struct Dev {
+    void* p = nullptr;
+    explicit Dev(size_t bytes) : p(dh_malloc(bytes ? bytes : 1)) {}
+    ~Dev() { if (p) dh_free(p); }
+    Dev(const Dev&) = delete;
+    Dev& operator=(const Dev&) = delete;
+    bool ok() const { return p != nullptr; }
+    float* f() const { return static_cast<float*>(p); }
+    uint16_t* h() const { return static_cast<uint16_t*>(p); }
+    double* d() const { return static_cast<double*>(p); }
+};
+
+struct Failure {};   // thrown internally by need(), caught at the builtin boundary
+
+void need(int status) {
+    if (status != DH_OK) throw Failure{};
+}
+
+Tensor* incref(Tensor* t) {
+    if (t) ++t->refcount;
+    return t;
+}
+
+bool hip_ready(const char* op) {
+    if (dh_available()) return true;
+    rt_error(op, "HIP backend unavailable (%s)", dh_last_error());
+    return false;
+}
+
+// Upload n fp64 host values as fp32 (dt = DH_F32) or bf16 (dt = DH_BF16) on the device.
+void upload(const double* h, size_t n, int dt, const Dev& out) {
+    Dev tmp(n * sizeof(double));
+    if (!tmp.ok()) throw Failure{};
+    need(dh_memcpy_h2d(tmp.p, h, n * sizeof(double)));
+    need(dh_convert(out.p, dt, tmp.p, DH_F64, n));
+}
+
+// Operand of a matmul: the live fp32 mirror when the tensor carries one.
+void upload_operand(const Tensor* t, int dt, const Dev& out) {
+    if (t->dtype == 1 && t->fdata) {
+        if (dt == DH_F32) {
+            need(dh_memcpy_h2d(out.p, t->fdata, (size_t)t->size * sizeof(float)));
+        } else {
+            Dev tmp((size_t)t->size * sizeof(float));
+            need(dh_memcpy_h2d(tmp.p, t->fdata, (size_t)t->size * sizeof(float)));
+            need(dh_convert(out.p, dt, tmp.p, DH_F32, t->size));
+        }
+    } else {
+        upload(t->data, t->size, dt, out);
+    }
+}
+
+void download_f64(const Dev& src_f32, double* h, size_t n) {
+    Dev tmp(n * sizeof(double));
+    if (!tmp.ok()) throw Failure{};
+    need(dh_convert(tmp.p, DH_F64, src_f32.p, DH_F32, n));
+    need(dh_memcpy_d2h(h, tmp.p, n * sizeof(double)));
+}
+
+void set_graph(Tensor* c, Tensor* l, Tensor* r, int op) {
+    c->is_leaf = 0;
+    c->op = op;
+    c->lhs = incref(l);
+    c->rhs = incref(r);
+}
+
+int padded_dim(int dk) { return dk <= 32 ? 32 : dk <= 64 ? 64 : dk <= 128 ? 128 : -1; }
+
+// (B*S, dk) fp64 rows -> (B*S, Dp) fp32 rows with zero padding, uploaded as dt.
+void upload_rows(const double* h, size_t rows, int dk, int Dp, int dt, const Dev& out) {
+    std::vector<float> buf(rows * Dp, 0.f);
+    for (size_t r = 0; r < rows; ++r)
+        for (int k = 0; k < dk; ++k) buf[r * Dp + k] = (float)h[r * dk + k];
+    if (dt == DH_F32) {
+        need(dh_memcpy_h2d(out.p, buf.data(), buf.size() * sizeof(float)));
+    } else {
+        Dev tmp(buf.size() * sizeof(float));
+        need(dh_memcpy_h2d(tmp.p, buf.data(), buf.size() * sizeof(float)));
+        need(dh_convert(out.p, dt, tmp.p, DH_F32, buf.size()));
+    }
+}
+
+std::vector<float> download_rows_f32(const Dev& d, size_t rows, int Dp, int dt) {
+    std::vector<float> buf(rows * Dp);
+    if (dt == DH_F32) {
+        need(dh_memcpy_d2h(buf.data(), d.p, buf.size() * sizeof(float)));
+    } else {
+        Dev tmp(buf.size() * sizeof(float));
+        need(dh_convert(tmp.p, DH_F32, d.p, dt, buf.size()));
+        need(dh_memcpy_d2h(buf.data(), tmp.p, buf.size() * sizeof(float)));
+    }
+    return buf;
+}
+
+Tensor* attention_impl(const char* name, int op, bool causal, Tensor* Q, Tensor* K, Tensor* V,
+                       Tensor* bt, Tensor* st, Tensor* dt_) {
+    if (!Q || !K || !V || !bt || !st || !dt_) return create_scalar(0.0);
+    const int B = (int)bt->data[0], S = (int)st->data[0], dk = (int)dt_->data[0];
+    if (B <= 0 || S <= 0 || dk <= 0 || Q->size != B * S * dk || K->size != Q->size ||
+        V->size != Q->size) {
+        rt_error(name, "Q/K/V must hold batch*seq*dk = %d*%d*%d values (got %d, %d, %d)", B, S,
+                 dk, Q->size, K->size, V->size);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    const int Dp = padded_dim(dk);
+    if (Dp < 0) {
+        rt_error(name, "head dim dk=%d above the 128 the GPU kernels hold", dk);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    if (!hip_ready(name)) return alloc_tensor(1, 1, 1, 1);
+    Tensor* out = alloc_tensor(B, S * dk, 1, 1);
+    out->is_leaf = 0;
+    out->op = op;
+    out->parents[0] = incref(Q);
+    out->parents[1] = incref(K);
+    out->parents[2] = incref(V);
+    out->num_parents = 3;
+    out->attn_B = B;
+    out->attn_S = S;
+    out->attn_dk = dk;
+    const size_t rows = (size_t)B * S;
+    const int dt = g_bf16 ? DH_BF16 : DH_F32;
+    const size_t esz = dt == DH_BF16 ? 2 : 4;
+    try {
+        Dev q(rows * Dp * esz), k(rows * Dp * esz), v(rows * Dp * esz), o(rows * Dp * esz);
+        Dev lse(rows * sizeof(float));
+        if (!q.ok() || !k.ok() || !v.ok() || !o.ok() || !lse.ok()) throw Failure{};
+        upload_rows(Q->data, rows, dk, Dp, dt, q);
+        upload_rows(K->data, rows, dk, Dp, dt, k);
+        upload_rows(V->data, rows, dk, Dp, dt, v);
+        need(dh_flash_fwd(dt, B, S, Dp, (float)(1.0 / std::sqrt((double)dk)), causal ? 1 : 0,
+                          q.p, k.p, v.p, o.p, lse.f()));
+        std::vector<float> ob = download_rows_f32(o, rows, Dp, dt);
+        for (size_t r = 0; r < rows; ++r)
+            for (int c = 0; c < dk; ++c) out->data[r * dk + c] = (double)ob[r * Dp + c];
+        out->lse = (float*)std::malloc(rows * sizeof(float));
+        need(dh_memcpy_d2h(out->lse, lse.p, rows * sizeof(float)));
+    } catch (const Failure&) {
+        rt_error(name, "%s", dh_last_error());
+        tensor_decref(out);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    return out;
+}
+
+void attention_backward(Tensor* t, bool causal) {
+    Tensor *Q = t->parents[0], *K = t->parents[1], *V = t->parents[2];
+    const int B = t->attn_B, S = t->attn_S, dk = t->attn_dk, Dp = padded_dim(dk);
+    const size_t rows = (size_t)B * S;
+    const int dt = g_bf16 ? DH_BF16 : DH_F32;
+    const size_t esz = dt == DH_BF16 ? 2 : 4;
+    Dev q(rows * Dp * esz), k(rows * Dp * esz), v(rows * Dp * esz), o(rows * Dp * esz),
+        g(rows * Dp * esz), lse(rows * sizeof(float)), dq(rows * Dp * 4), dkk(rows * Dp * 4),
+        dv(rows * Dp * 4);
+    if (!q.ok() || !k.ok() || !v.ok() || !o.ok() || !g.ok() || !lse.ok() || !dq.ok() ||
+        !dkk.ok() || !dv.ok())
+        throw Failure{};
+    upload_rows(Q->data, rows, dk, Dp, dt, q);
+    upload_rows(K->data, rows, dk, Dp, dt, k);
+    upload_rows(V->data, rows, dk, Dp, dt, v);
+    upload_rows(t->data, rows, dk, Dp, dt, o);
+    upload_rows(t->grad, rows, dk, Dp, dt, g);
+    need(dh_memcpy_h2d(lse.p, t->lse, rows * sizeof(float)));
+    need(dh_flash_bwd(dt, B, S, Dp, (float)(1.0 / std::sqrt((double)dk)), causal ? 1 : 0, q.p,
+                      k.p, v.p, o.p, g.p, lse.f(), dq.f(), dkk.f(), dv.f(), 0));
+    Tensor* dst[3] = {Q, K, V};
+    const Dev* src[3] = {&dq, &dkk, &dv};
+    for (int x = 0; x < 3; ++x) {
+        std::vector<float> h = download_rows_f32(*src[x], rows, Dp, DH_F32);
+        for (size_t r = 0; r < rows; ++r)
+            for (int c = 0; c < dk; ++c) dst[x]->grad[r * dk + c] += (double)h[r * Dp + c];
+    }
+}
+
+void matmul_backward(Tensor* t) {
+    // dA += dY B^T (NT), dB += A^T dY (TN), in fp32 on the GPU, accumulated into the fp64
+    // gradients on the host (runtime/ops/autograd.inc:91-125).
+    Tensor *A = t->lhs, *B = t->rhs;
+    const int M = A->d0, K = A->d1, N = B->d1;
+    Dev a((size_t)M * K * 4), b((size_t)K * N * 4), dy((size_t)M * N * 4), da((size_t)M * K * 4),
+        db((size_t)K * N * 4);
+    if (!a.ok() || !b.ok() || !dy.ok() || !da.ok() || !db.ok()) throw Failure{};
+    upload(A->data, (size_t)M * K, DH_F32, a);
+    upload(B->data, (size_t)K * N, DH_F32, b);
+    upload(t->grad, (size_t)M * N, DH_F32, dy);
+    need(dh_gemm_f32(0, 1, M, K, N, dy.f(), N, b.f(), N, 0.f, da.f(), K));
+    need(dh_gemm_f32(1, 0, K, N, M, a.f(), K, dy.f(), N, 0.f, db.f(), N));
+    std::vector<float> ha((size_t)M * K), hb((size_t)K * N);
+    need(dh_memcpy_d2h(ha.data(), da.p, ha.size() * 4));
+    need(dh_memcpy_d2h(hb.data(), db.p, hb.size() * 4));
+    for (size_t x = 0; x < ha.size(); ++x) A->grad[x] += (double)ha[x];
+    for (size_t x = 0; x < hb.size(); ++x) B->grad[x] += (double)hb[x];
+}
+
+void topo_sort(Tensor* root, std::vector<Tensor*>& order) {
+    // Iterative post-order DFS over lhs, rhs and parents (runtime/backend/gpu.inc:742-779).
+    std::unordered_set<Tensor*> seen;
+    std::vector<std::pair<Tensor*, int>> stack{{root, 0}};
+    seen.insert(root);
+    while (!stack.empty()) {
+        auto& [t, i] = stack.back();
+        Tensor* kids[5] = {t->lhs, t->rhs, t->parents[0], t->parents[1], t->parents[2]};
+        if (i < 5) {
+            Tensor* k = kids[i++];
+            if (k && !seen.count(k)) {
+                seen.insert(k);
+                stack.push_back({k, 0});
+            }
+        } else {
+            order.push_back(t);
+            stack.pop_back();
+        }
+    }
+}
+
+// Naive fp64 references used by the selftests only.
+void ref_gemm(const double* A, const double* B, double* C, int M, int K, int N) {
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            double s = 0.0;
+            for (int k = 0; k < K; ++k) s += A[(size_t)i * K + k] * B[(size_t)k * N + j];
+            C[(size_t)i * N + j] = s;
+        }
+}
+
+void ref_causal_attention(const double* Q, const double* K, const double* V, double* O, int S,
+                          int dk) {
+    const double scale = 1.0 / std::sqrt((double)dk);
+    std::vector<double> p(S);
+    for (int i = 0; i < S; ++i) {
+        double mx = -1e300, sum = 0.0;
+        for (int j = 0; j <= i; ++j) {
+            double s = 0.0;
+            for (int k = 0; k < dk; ++k) s += Q[i * dk + k] * K[j * dk + k];
+            p[j] = s * scale;
+            mx = std::max(mx, p[j]);
+        }
+        for (int j = 0; j <= i; ++j) sum += (p[j] = std::exp(p[j] - mx));
+        for (int k = 0; k < dk; ++k) {
+            double s = 0.0;
+            for (int j = 0; j <= i; ++j) s += p[j] * V[j * dk + k];
+            O[i * dk + k] = s / sum;
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+// ----------------------------------------------------------------------------- tensors
+Tensor* alloc_tensor(int d0, int d1, int d2, int d3) {
+    if (d0 < 0 || d1 < 0 || d2 < 0 || d3 < 0) {
+        std::fprintf(stderr, "RUNTIME ERROR: negative tensor dimension (%d,%d,%d,%d)\n", d0, d1,
+                     d2, d3);
+        d0 = d1 = d2 = d3 = 1;
+    }
+    long long n = (long long)d0 * d1 * d2 * d3;
+    if (n > 500000000LL) {
+        std::fprintf(stderr, "RUNTIME ERROR: tensor too large (%lld elements)\n", n);
+        d0 = d1 = d2 = d3 = 1;
+        n = 1;
+    }
+    const int size = n <= 0 ? 1 : (int)n;
+    Tensor* t = (Tensor*)std::calloc(1, sizeof(Tensor));
+    t->data = (double*)std::calloc(size, sizeof(double));
+    t->grad = (double*)std::calloc(size, sizeof(double));
+    t->size = size;
+    t->d0 = d0;
+    t->d1 = d1;
+    t->d2 = d2;
+    t->d3 = d3;
+    t->refcount = 1;
+    t->is_leaf = 1;
+    return t;
+}
+
+Tensor* create_scalar(double v) {
+    Tensor* t = alloc_tensor(1, 1, 1, 1);
+    t->data[0] = v;
+    return t;
+}
+
+Tensor* tensor_incref(Tensor* t) { return incref(t); }
+
+Tensor* tensor_decref(Tensor* t) {
+    if (!t || --t->refcount > 0) return nullptr;
+    tensor_decref(t->lhs);
+    tensor_decref(t->rhs);
+    for (int i = 0; i < t->num_parents; ++i) tensor_decref(t->parents[i]);
+    std::free(t->data);
+    std::free(t->grad);
+    std::free(t->fdata);
+    std::free(t->fgrad);
+    std::free(t->lse);
+    std::free(t);
+    return nullptr;
+}
+
+Tensor* ones(Tensor* d0, Tensor* d1) {
+    Tensor* t = alloc_tensor((int)d0->data[0], (int)d1->data[0], 1, 1);
+    std::fill(t->data, t->data + t->size, 1.0);
+    return t;
+}
+
+Tensor* dream_set_seed(Tensor* s) {
+    const unsigned seed = s ? (unsigned)s->data[0] : 42u;
+    rng().seed(seed);
+    std::fprintf(stderr, "[seed] RNG seeded with %u\n", seed);
+    return create_scalar((double)seed);
+}
+
+Tensor* dream_randn(Tensor* d0, Tensor* d1) {
+    Tensor* t = alloc_tensor((int)d0->data[0], (int)d1->data[0], 1, 1);
+    std::normal_distribution<double> nd(0.0, 1.0);
+    for (int i = 0; i < t->size; ++i) t->data[i] = nd(rng());
+    return t;
+}
+
+Tensor* sum(Tensor* a) {
+    Tensor* c = alloc_tensor(1, 1, 1, 1);
+    double s = 0.0;
+    for (int i = 0; i < a->size; ++i) s += a->data[i];
+    c->data[0] = s;
+    set_graph(c, a, nullptr, DREAM_OP_SUM);
+    return c;
+}
+
+static Tensor* binary(Tensor* a, Tensor* b, int op) {
+    Tensor* c = alloc_tensor(std::max(a->d0, b->d0), std::max(a->d1, b->d1), a->d2, a->d3);
+    for (int i = 0; i < c->size; ++i) {
+        const double x = a->data[i % a->size], y = b->data[i % b->size];
+        c->data[i] = op == DREAM_OP_MUL ? x * y : x + y;
+    }
+    set_graph(c, a, b, op);
+    return c;
+}
+
+Tensor* tensor_add(Tensor* a, Tensor* b) { return binary(a, b, DREAM_OP_ADD); }
+Tensor* tensor_mul(Tensor* a, Tensor* b) { return binary(a, b, DREAM_OP_MUL); }
+
+Tensor* tensor_get_grad(Tensor* t) {
+    if (!t) {
+        rt_error("grad()", "argument is null");
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    Tensor* g = alloc_tensor(t->d0, t->d1, t->d2, t->d3);
+    std::copy(t->grad, t->grad + t->size, g->data);
+    return g;
+}
+
+Tensor* zero_grad(Tensor* t) {
+    if (!t) {
+        rt_error("zero_grad", "tensor is null");
+        return nullptr;
+    }
+    std::fill(t->grad, t->grad + t->size, 0.0);
+    Tensor *l = t->lhs, *r = t->rhs;
+    t->lhs = t->rhs = nullptr;
+    tensor_decref(l);
+    tensor_decref(r);
+    for (int i = 0; i < t->num_parents; ++i) tensor_decref(t->parents[i]);
+    t->num_parents = 0;
+    return incref(t);
+}
+
+// ----------------------------------------------------------------------------- precision
+Tensor* dream_set_precision(Tensor* t, int code) {
+    if (!t) return nullptr;
+    if (code == 1) {
+        if (t->dtype != 1 || !t->fdata) {
+            if (!t->fdata) t->fdata = (float*)std::calloc(t->size, sizeof(float));
+            if (!t->fgrad) t->fgrad = (float*)std::calloc(t->size, sizeof(float));
+            for (int i = 0; i < t->size; ++i) t->fdata[i] = (float)t->data[i];
+            t->dtype = 1;
+        }
+    } else {
+        if (t->dtype == 1 && t->fdata)
+            for (int i = 0; i < t->size; ++i) t->data[i] = (double)t->fdata[i];
+        t->dtype = 0;
+    }
+    return incref(t);
+}
+
+Tensor* dream_to_float32(Tensor* t) {
+    if (!t || t->dtype == 1) return incref(t);
+    if (!t->fdata) t->fdata = (float*)std::calloc(t->size, sizeof(float));
+    if (!t->fgrad) t->fgrad = (float*)std::calloc(t->size, sizeof(float));
+    for (int i = 0; i < t->size; ++i) {
+        t->fdata[i] = (float)t->data[i];
+        t->data[i] = (double)t->fdata[i];
+        t->fgrad[i] = (float)t->grad[i];
+    }
+    t->dtype = 1;
+    return incref(t);
+}
+
+Tensor* dream_enable_fp16(void) {
+    g_bf16 = true;
+    std::fprintf(stderr, "[dream] reduced-precision matmul enabled (bf16 operands, fp32 accumulate)\n");
+    return create_scalar(1.0);
+}
+
+Tensor* dream_disable_fp16(void) {
+    g_bf16 = false;
+    return create_scalar(1.0);
+}
+
+// ----------------------------------------------------------------------------- hot path
+Tensor* tensor_matmul(Tensor* a, Tensor* b) {
+    if (!a || !b) {
+        rt_error("matmul (@)", "null operand%s%s", a ? "" : " (left=null)", b ? "" : " (right=null)");
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    if (!a->data || !b->data) {
+        rt_error("matmul (@)", "null data pointer left=%dx%d right=%dx%d", a->d0, a->d1, b->d0, b->d1);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    if (a->d1 != b->d0) {
+        rt_error("matmul (@)", "shape mismatch (%dx%d @ %dx%d) \xe2\x80\x94 inner dimensions must match",
+                 a->d0, a->d1, b->d0, b->d1);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    if (!hip_ready("matmul (@)")) return alloc_tensor(1, 1, 1, 1);
+    const int M = a->d0, K = a->d1, N = b->d1;
+    Tensor* c = alloc_tensor(M, N, 1, 1);
+    set_graph(c, a, b, DREAM_OP_MATMUL);
+    const bool f32 = a->dtype == 1 && b->dtype == 1 && a->fdata && b->fdata;
+    try {
+        const size_t mk = (size_t)M * K, kn = (size_t)K * N, mn = (size_t)M * N;
+        Dev dc(mn * 4);
+        if (!dc.ok()) throw Failure{};
+        if (g_bf16 && !f32) {
+            Dev da(mk * 2), db(kn * 2);
+            if (!da.ok() || !db.ok()) throw Failure{};
+            upload_operand(a, DH_BF16, da);
+            upload_operand(b, DH_BF16, db);
+            need(dh_gemm_bf16(0, 0, M, N, K, da.h(), K, db.h(), N, 0.f, dc.f(), N));
+        } else {
+            Dev da(mk * 4), db(kn * 4);
+            if (!da.ok() || !db.ok()) throw Failure{};
+            upload_operand(a, DH_F32, da);
+            upload_operand(b, DH_F32, db);
+            need(dh_gemm_f32(0, 0, M, N, K, da.f(), K, db.f(), N, 0.f, dc.f(), N));
+        }
+        if (f32) {
+            // fp32 result: fdata is the live copy, data its fp64 mirror (elementwise.inc:1000-1017)
+            c->fdata = (float*)std::calloc(c->size, sizeof(float));
+            c->fgrad = (float*)std::calloc(c->size, sizeof(float));
+            c->dtype = 1;
+            need(dh_memcpy_d2h(c->fdata, dc.p, mn * 4));
+            for (size_t i = 0; i < mn; ++i) c->data[i] = (double)c->fdata[i];
+        } else {
+            download_f64(dc, c->data, mn);
+        }
+    } catch (const Failure&) {
+        rt_error("matmul (@)", "%s", dh_last_error());
+        tensor_decref(c);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    return c;
+}
+
+Tensor* dream_flash_attention(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq,
+                              Tensor* dk, Tensor* block) {
+    (void)block;   // the key-block size is a CPU tiling knob; the GPU kernels fix their own
+    return attention_impl("flash_attention", DREAM_OP_FLASH, true, Q, K, V, batch, seq, dk);
+}
+
+Tensor* dream_attention(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq, Tensor* dk) {
+    return attention_impl("attention", DREAM_OP_ATTN, false, Q, K, V, batch, seq, dk);
+}
+
+Tensor* dream_attention_causal(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq,
+                               Tensor* dk) {
+    return attention_impl("attention_causal", DREAM_OP_ATTN_CAUSAL, true, Q, K, V, batch, seq, dk);
+}
+
+Tensor* backward(Tensor* root) {
+    if (!root) {
+        std::fprintf(stderr, "error: backward(null)\n");
+        return create_scalar(0);
+    }
+    std::fill(root->grad, root->grad + root->size, 1.0);
+    std::vector<Tensor*> order;
+    topo_sort(root, order);
+    for (int x = (int)order.size() - 1; x >= 0; --x) {
+        Tensor* t = order[x];
+        try {
+            switch (t->op) {
+                case DREAM_OP_MATMUL:
+                    if (!hip_ready("backward(matmul)")) break;
+                    matmul_backward(t);
+                    break;
+                case DREAM_OP_FLASH:
+                case DREAM_OP_ATTN_CAUSAL:
+                case DREAM_OP_ATTN:
+                    if (!t->lse || !hip_ready("backward(attention)")) break;
+                    attention_backward(t, t->op != DREAM_OP_ATTN);
+                    break;
+                case DREAM_OP_SUM:
+                    for (int j = 0; j < t->lhs->size; ++j) t->lhs->grad[j] += t->grad[0];
+                    break;
+                case DREAM_OP_MUL:
+                    for (int j = 0; j < t->size; ++j) {
+                        const double g = t->grad[j];
+                        t->lhs->grad[j % t->lhs->size] += g * t->rhs->data[j % t->rhs->size];
+                        t->rhs->grad[j % t->rhs->size] += g * t->lhs->data[j % t->lhs->size];
+                    }
+                    break;
+                case DREAM_OP_ADD:
+                    for (int j = 0; j < t->size; ++j) {
+                        t->lhs->grad[j % t->lhs->size] += t->grad[j];
+                        t->rhs->grad[j % t->rhs->size] += t->grad[j];
+                    }
+                    break;
+                default:
+                    break;
+            }
+        } catch (const Failure&) {
+            rt_error("backward", "%s", dh_last_error());
+        }
+    }
+    return create_scalar(1.0);
+}
+
+// ----------------------------------------------------------------------------- queries
+int dream_gpu_available(void) { return 0; }
+
+int dream_hip_available(void) { return dh_available(); }
+
+Tensor* gpu_selftest(void) {
+    if (!dh_available()) {
+        std::printf("=== gpu_selftest: no HIP device -- skipped ===\n");
+        std::printf("  GPU: SKIP (CPU-only host; GPU kernels not exercised)\n");
+        return create_scalar(1.0);
+    }
+    rng().seed(20260708);
+    std::printf("=== gpu_selftest: GPU kernels vs fp64 reference ===\n");
+    std::uniform_real_distribution<double> dist(-1.0, 1.0);
+    int pass = 0, total = 0;
+    double worst = 0.0;
+    const int shapes[3][3] = {{256, 128, 256}, {300, 200, 257}, {512, 64, 300}};
+    for (const auto& s : shapes) {
+        Tensor* A = alloc_tensor(s[0], s[1], 1, 1);
+        Tensor* B = alloc_tensor(s[1], s[2], 1, 1);
+        for (int i = 0; i < A->size; ++i) A->data[i] = dist(rng());
+        for (int i = 0; i < B->size; ++i) B->data[i] = dist(rng());
+        Tensor* Cg = tensor_matmul(A, B);
+        std::vector<double> Cc((size_t)s[0] * s[2]);
+        ref_gemm(A->data, B->data, Cc.data(), s[0], s[1], s[2]);
+        double max_abs = 0.0;
+        for (size_t i = 0; i < Cc.size() && Cg->size == (int)Cc.size(); ++i)
+            max_abs = std::max(max_abs, std::fabs(Cg->data[i] - Cc[i]));
+        const double tol = std::sqrt((double)s[1]) * 1e-4;   // elementwise.inc:843-845
+        const bool ok = Cg->size == (int)Cc.size() && max_abs < tol;
+        std::printf("  matmul %dx%dx%d  max_abs=%.2e (tol %.1e)  %s\n", s[0], s[1], s[2], max_abs,
+                    tol, ok ? "PASS" : "FAIL");
+        worst = std::max(worst, max_abs);
+        ++total;
+        pass += ok;
+        tensor_decref(A);
+        tensor_decref(B);
+        tensor_decref(Cg);
+    }
+    {   // causal flash attention on one slice, S=256, dk=64, against fp64
+        const int S = 256, dkk = 64;
+        Tensor* Q = alloc_tensor(1, S * dkk, 1, 1);
+        Tensor* Kt = alloc_tensor(1, S * dkk, 1, 1);
+        Tensor* Vt = alloc_tensor(1, S * dkk, 1, 1);
+        for (Tensor* t : {Q, Kt, Vt})
+            for (int i = 0; i < t->size; ++i) t->data[i] = dist(rng());
+        Tensor *b1 = create_scalar(1), *s1 = create_scalar(S), *d1 = create_scalar(dkk);
+        Tensor* Og = dream_flash_attention(Q, Kt, Vt, b1, s1, d1, nullptr);
+        std::vector<double> Oc((size_t)S * dkk);
+        ref_causal_attention(Q->data, Kt->data, Vt->data, Oc.data(), S, dkk);
+        double max_abs = 0.0;
+        for (size_t i = 0; i < Oc.size() && Og->size == (int)Oc.size(); ++i)
+            max_abs = std::max(max_abs, std::fabs(Og->data[i] - Oc[i]));
+        const bool ok = Og->size == (int)Oc.size() && max_abs < 1e-4;
+        std::printf("  flash_attention S=%d dk=%d  max_abs=%.2e (tol 1.0e-04)  %s\n", S, dkk,
+                    max_abs, ok ? "PASS" : "FAIL");
+        worst = std::max(worst, max_abs);
+        ++total;
+        pass += ok;
+        for (Tensor* t : {Q, Kt, Vt, b1, s1, d1, Og}) tensor_decref(t);
+    }
+    std::printf("  GPU: %d/%d PASS (worst abs err %.2e)\n", pass, total, worst);
+    std::fflush(stdout);
+    return create_scalar(pass == total ? 1.0 : 0.0);
+}
+
+Tensor* dream_gpu_warmup(void) {
+    const auto t0 = std::chrono::steady_clock::now();
+    if (!dh_available()) {
+        std::printf("[gpu_warmup] no GPU; nothing to warm up\n");
+        return create_scalar(0.0);
+    }
+    const int n = 768;
+    Tensor* a = alloc_tensor(n, n, 1, 1);
+    Tensor* b = alloc_tensor(n, n, 1, 1);
+    for (int i = 0; i < a->size; ++i) {
+        a->data[i] = 0.01 * (i % 7);
+        b->data[i] = 0.01 * (i % 5);
+    }
+    tensor_decref(tensor_matmul(a, b));
+    const int S = 512, dkk = 64;
+    Tensor* Q = alloc_tensor(1, S * dkk, 1, 1);
+    for (int i = 0; i < Q->size; ++i) Q->data[i] = 0.01 * (i % 11);
+    Tensor *bt = create_scalar(1), *st = create_scalar(S), *dt = create_scalar(dkk);
+    tensor_decref(dream_flash_attention(Q, Q, Q, bt, st, dt, nullptr));
+    for (Tensor* t : {a, b, Q, bt, st, dt}) tensor_decref(t);
+    const double s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    std::printf("[gpu_warmup] GPU ready (init + first launches took %.3f s)\n", s);
+    std::fflush(stdout);
+    return create_scalar(s);
+}
+
+Tensor* flash_attention_selftest(void) {
+    std::printf("=== flash_attention_selftest: GPU flash == fp64 standard attention ===\n");
+    if (!dh_available()) {
+        std::printf("  FLASH_ATTN: SKIP (no HIP device)\n");
+        return create_scalar(1.0);
+    }
+    rng().seed(20260709);
+    std::normal_distribution<double> nd(0.0, 1.0);
+    int pass = 0, total = 0;
+    double worst = 0.0;
+    const int cfgs[4][3] = {{64, 16, 8}, {64, 16, 16}, {128, 32, 32}, {100, 24, 16}};
+    for (const auto& c : cfgs) {
+        const int S = c[0], dkk = c[1];
+        Tensor* Q = alloc_tensor(1, S * dkk, 1, 1);
+        Tensor* K = alloc_tensor(1, S * dkk, 1, 1);
+        Tensor* V = alloc_tensor(1, S * dkk, 1, 1);
+        for (int i = 0; i < Q->size; ++i) {
+            Q->data[i] = nd(rng());
+            K->data[i] = nd(rng());
+            V->data[i] = nd(rng());
+        }
+        Tensor *bt = create_scalar(1), *st = create_scalar(S), *dt = create_scalar(dkk),
+               *blk = create_scalar(c[2]);
+        Tensor* fla = dream_flash_attention(Q, K, V, bt, st, dt, blk);
+        std::vector<double> ref((size_t)S * dkk);
+        ref_causal_attention(Q->data, K->data, V->data, ref.data(), S, dkk);
+        double num = 0.0, den = 0.0;
+        for (size_t i = 0; i < ref.size() && fla->size == (int)ref.size(); ++i) {
+            num = std::max(num, std::fabs(fla->data[i] - ref[i]));
+            den = std::max(den, std::fabs(ref[i]));
+        }
+        const double mr = den > 0 ? num / den : num;
+        // fp32 GPU against fp64: normwise max relative error within 1e-5 * sqrt(S)
+        const bool ok = fla->size == (int)ref.size() && mr < 1e-5 * std::sqrt((double)S);
+        std::printf("  S=%d dk=%d block=%d: max_rel=%.2e  %s\n", S, dkk, c[2], mr,
+                    ok ? "PASS" : "FAIL");
+        worst = std::max(worst, mr);
+        ++total;
+        pass += ok;
+        for (Tensor* t : {Q, K, V, bt, st, dt, blk, fla}) tensor_decref(t);
+    }
+    std::printf("  FLASH_ATTN: %d/%d PASS (worst rel err %.2e)\n", pass, total, worst);
+    std::fflush(stdout);
+    return create_scalar(pass == total ? 1.0 : 0.0);
+}
+
+}  // extern "C"

@@ -1,0 +1,101 @@
+/*
+ * dream_rt.h -- Dream runtime builtins of the dense-tensor hot path, over the HIP backend.
+ *
+ * Same names, argument meaning, ownership and error behaviour as the reference runtime's
+ * builtins (runtime/runtime.h, runtime/ops/elementwise.inc, runtime/ops/autograd.inc,
+ * runtime/nn/training.inc), so compiled .dream programs and C callers bind unchanged:
+ *   - every Tensor* returned is a +1 reference owned by the caller; arguments are never
+ *     stolen (interop/dream.h:13-16);
+ *   - errors print "RUNTIME ERROR in <op>: ..." to stderr and return a fresh 1x1 tensor
+ *     (runtime/ops/elementwise.inc:972-989); nothing exits.
+ * The GEMM and attention builtins compute on the GPU through include/dream_hip.h; this
+ * runtime has no CPU GEMM or CPU attention.  Host-side builtins kept only to build
+ * programs around the hot path (ones, randn, sum, tensor_mul, ...) run on the host, as
+ * the reference's own elementwise ops do.
+ *
+ * Tensor: fields 0-6 (data, grad, size, d0..d3) are the layout generated code reads
+ * (runtime/runtime.h:49-55); all later fields belong to this runtime.
+ */
+#ifndef DREAM_RT_H
+#define DREAM_RT_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct Tensor {
+    /* ---- IR-visible, fixed order (runtime/runtime.h:49-55) ---- */
+    double* data;
+    double* grad;
+    int size;
+    int d0, d1, d2, d3;
+    /* ---- runtime-only ---- */
+    int refcount;
+    int is_leaf;
+    int op;                    /* graph node kind (DREAM_OP_*)                     */
+    struct Tensor* lhs;
+    struct Tensor* rhs;
+    struct Tensor* parents[3];
+    int num_parents;
+    int attn_B, attn_S, attn_dk;   /* "B,S,dk" of an attention node (bwd_name)    */
+    int dtype;                 /* 0 = fp64 storage, 1 = live fp32 mirror (as f32)  */
+    float* fdata;              /* fp32 mirror when dtype == 1                      */
+    float* fgrad;
+    float* lse;                /* attention nodes: per-row log-sum-exp (B*S)       */
+} Tensor;
+
+enum {
+    DREAM_OP_LEAF = 0, DREAM_OP_MATMUL, DREAM_OP_FLASH, DREAM_OP_ATTN, DREAM_OP_ATTN_CAUSAL,
+    DREAM_OP_SUM, DREAM_OP_MUL, DREAM_OP_ADD
+};
+
+/* ---- tensors (runtime/core/tensor.inc:143-303) ---- */
+Tensor* alloc_tensor(int d0, int d1, int d2, int d3);
+Tensor* create_scalar(double v);
+Tensor* tensor_incref(Tensor* t);
+Tensor* tensor_decref(Tensor* t);
+Tensor* ones(Tensor* d0, Tensor* d1);                      /* elementwise.inc:2     */
+Tensor* dream_set_seed(Tensor* seed);                      /* elementwise.inc:35-40 */
+Tensor* dream_randn(Tensor* d0, Tensor* d1);               /* elementwise.inc:48-54 */
+Tensor* sum(Tensor* a);                                    /* elementwise.inc:56    */
+Tensor* tensor_add(Tensor* a, Tensor* b);
+Tensor* tensor_mul(Tensor* a, Tensor* b);
+Tensor* tensor_get_grad(Tensor* t);                        /* autograd.inc:1-14     */
+Tensor* zero_grad(Tensor* t);                              /* autograd.inc:15-24    */
+
+/* ---- precision (runtime/io/builtins.inc:1168-1184, 380-394, 465-475) ---- */
+Tensor* dream_set_precision(Tensor* t, int code);          /* `as f32` (1) / `as f64` (0) */
+Tensor* dream_to_float32(Tensor* t);
+Tensor* dream_enable_fp16(void);   /* reduced-precision `@`: bf16 operands, fp32 accumulate */
+Tensor* dream_disable_fp16(void);
+
+/* ---- the hot path ---- */
+/* C = A @ B (runtime/ops/elementwise.inc:971-1213), graph node "matmul". */
+Tensor* tensor_matmul(Tensor* a, Tensor* b);
+/* Causal FlashAttention (runtime/nn/training.inc:284-401); block_t may be NULL. */
+Tensor* dream_flash_attention(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq,
+                              Tensor* dk, Tensor* block);
+/* Standard attention, non-causal and causal (training.inc:178-263), computed by the
+ * same FlashAttention kernels instead of materialising S x S scores. */
+Tensor* dream_attention(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq, Tensor* dk);
+Tensor* dream_attention_causal(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq,
+                               Tensor* dk);
+/* Reverse sweep from root (runtime/ops/autograd.inc:26-887) for the node kinds above;
+ * gradients accumulate ("+=") into grad buffers like the reference. */
+Tensor* backward(Tensor* root);
+
+/* ---- backend queries, selftests (runtime/backend/gpu.inc:271-273,
+ *      runtime/ops/elementwise.inc:759-875, runtime/nn/training.inc:405-435) ---- */
+/* 0: the OpenCL fused-expression path does not exist, so generated code keeps fused
+ * elementwise expressions on its CPU branch (src/AST.cpp:1053-1076). */
+int dream_gpu_available(void);
+/* 1 when the HIP backend can run the GEMM and attention builtins. */
+int dream_hip_available(void);
+Tensor* gpu_selftest(void);
+Tensor* dream_gpu_warmup(void);
+Tensor* flash_attention_selftest(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,57 @@
+"""Runtime builtins on the CPU: argument checks and error convention (no GPU work).
+
+Mirrors tests/08_shape_mismatch.dream and the error rules of the reference
+(runtime/ops/elementwise.inc:972-989): print "RUNTIME ERROR in matmul (@): ..." and
+return a fresh 1x1 tensor; never exit.
+"""
+import numpy as np
+
+from dreamcompiler_amd import runtime as rt
+
+
+def test_shape_mismatch_error_and_1x1_result(capfd):
+    L = rt.load()
+    a, b = rt.tensor(np.ones((2, 3))), rt.tensor(np.ones((2, 3)))
+    c = L.tensor_matmul(a, b)
+    err = capfd.readouterr().err
+    assert "RUNTIME ERROR in matmul (@): shape mismatch (2x3 @ 2x3)" in err
+    assert (c.contents.d0, c.contents.d1, c.contents.size) == (1, 1, 1)
+    rt.release(a, b, c)
+
+
+def test_null_operand_error(capfd):
+    L = rt.load()
+    a = rt.tensor(np.ones((2, 2)))
+    c = L.tensor_matmul(a, None)
+    assert "null operand (right=null)" in capfd.readouterr().err
+    assert c.contents.size == 1
+    rt.release(a, c)
+
+
+def test_fused_expressions_stay_on_cpu_branch():
+    # Generated code asks dream_gpu_available() before JIT-ing OpenCL fused kernels
+    # (src/AST.cpp:1053-1076); that path does not exist here, so it must answer 0.
+    assert rt.load().dream_gpu_available() == 0
+
+
+def test_attention_argument_check(capfd):
+    L = rt.load()
+    q = rt.tensor(np.ones((1, 10)))
+    o = L.dream_flash_attention(q, q, q, rt.scalar(1), rt.scalar(4), rt.scalar(3), None)
+    assert "Q/K/V must hold batch*seq*dk" in capfd.readouterr().err
+    assert o.contents.size == 1
+
+
+def test_host_builtins_and_refcounts():
+    L = rt.load()
+    L.dream_set_seed(rt.scalar(5))
+    r1 = rt.read(L.dream_randn(rt.scalar(1), rt.scalar(512)))
+    L.dream_set_seed(rt.scalar(5))
+    r2 = rt.read(L.dream_randn(rt.scalar(1), rt.scalar(512)))
+    assert np.array_equal(r1, r2) and r1.shape == (1, 512)
+    o = L.ones(rt.scalar(2), rt.scalar(3))
+    assert np.all(rt.read(o) == 1.0)
+    s = L.sum(L.tensor_mul(o, o))
+    assert rt.read(s)[0, 0] == 6.0
+    L.backward(s)
+    assert np.all(rt.read(o, grad=True) == 2.0)   # d/do sum(o*o) = 2o
