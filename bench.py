@@ -236,7 +236,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--workload", default="gemm_bf16_8192", choices=sorted(WORKLOADS))
     ap.add_argument("--only", action="store_true",
                     help="time only --workload (for profiling runs); no extra metrics")
