@@ -17,6 +17,8 @@
 // Operands stored with k as the slow (row) index -- B in NN, A in TN -- are fetched
 // as 4 (k) x 8 (i or j) blocks and transposed in registers with v_perm_b32 before
 // the LDS write.
+#include <cstdlib>
+
 #include "dh_common.hpp"
 
 namespace dh {
@@ -214,11 +216,250 @@ int launch_vec(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* 
     return launch_cfg<128, 128, 64, 2, TA, TB, VA, VB>(M, N, K, A, lda, B, ldb, beta, C, ldc);
 }
 
+// ---------------------------------------------------------------------------------
+// Fast path for tile-aligned shapes (M, N multiples of 256, K of 32, leading dims of 8,
+// 16-byte aligned operands): both operands travel global -> LDS by direct-to-LDS DMA
+// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), so no registers or
+// LDS-write instructions are spent on staging.  LDS tiles keep the global orientation:
+//   k-contiguous operand  : [256 rows][32 k],  16-byte chunk c of row r at position
+//                           c ^ (r / 4 % 4)  -> MFMA fragment = one ds_read_b128
+//   mn-contiguous operand : [32 k][256 cols], chunk c of row k at c ^ 4 (k % 4)
+//                           -> MFMA fragment = two ds_read_b64_tr_b16
+// ds_read_b64_tr_b16 semantics (measured on gfx950): in each 16-lane group, lane i names
+// a row R_i of 4 consecutive 16-bit values; lane j receives R_{j/4 + 4e}[j % 4] for
+// e = 0..3.  Pointing lane i at [kb + i/4][nb + 4 (i % 4)] therefore hands lane j the 4
+// values [kb .. kb + 3][nb + j], the MFMA operand layout.  The LDS serves 64 banks of
+// 4 bytes (16 lanes of a b128 read, 32 lanes of a b64 read per pass); both swizzles make
+// the fragment reads conflict free under that model.  Two LDS stages (128 KB); fragments of the next
+// k-step are read while the matrix cores run the current one.
+// ---------------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline s16x4 ds_read_tr(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (s16x4 __attribute__((address_space(3)))*)(p));
+}
+
+// 16-byte direct-to-LDS load.  Issued as inline assembly so that the compiler's wait
+// insertion, which cannot tell the DMA target from the stage being read, does not
+// serialise every LDS read behind it; the kernel waits (vmcnt) itself before each
+// barrier.  m0 holds the wave's LDS base; one wait state separates the m0 write from
+// the DMA, as the hardware requires.
+__device__ inline void lds_dma16(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds_base), "v"(g)
+                 : "memory", "m0");
+}
+
+__device__ inline uint32_t lds_addr(const uint16_t* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
+}
+
+template <bool KCONTIG, int WAVES>
+struct FastOperand {
+    // One 32-k stage of a 256-wide operand tile is 16 KB = 16 DMA blocks of 1 KB; wave w
+    // issues blocks PER*w .. PER*w + PER-1.  Per-lane element offsets at k0 = 0 and the
+    // per-stage step.
+    static constexpr int PER = 16 / WAVES;
+    uint32_t off[PER];
+    uint32_t step;
+
+    __device__ void init(int ld, int t0, int wave, int lane) {
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int b = PER * wave + t;
+            if (KCONTIG) {                     // block b = rows 16b .. 16b+15 of [t][32 k]
+                const int row = 16 * b + (lane >> 2);
+                const int c = (lane & 3) ^ ((lane >> 4) & 3);   // = p ^ ((row >> 2) & 3)
+                off[t] = (uint32_t)(t0 + row) * ld + 8 * c;
+            } else {                           // block b = k rows 2b, 2b+1 of [32 k][t]
+                const int k = 2 * b + (lane >> 5);
+                const int c = (lane & 31) ^ (4 * (k & 3));
+                off[t] = (uint32_t)k * ld + t0 + 8 * c;
+            }
+        }
+        step = KCONTIG ? 32u : 32u * (uint32_t)ld;
+    }
+    __device__ void issue(const uint16_t* __restrict__ g, int kt, uint16_t* lds, int wave) const {
+        const uint32_t adv = (uint32_t)kt * step;
+        const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds) + 1024u * PER * wave);
+#pragma unroll
+        for (int t = 0; t < PER; ++t) lds_dma16(g + (off[t] + adv), base + 1024u * t);
+    }
+    // MFMA operand for tile rows/cols o .. o+31, k-step kk (16 k) of the stage.
+    __device__ static bf16x8 frag(const uint16_t* lds, int o, int kk, int lane) {
+        const int h = lane >> 5;
+        if (KCONTIG) {                         // [256][32]: chunk c of row r at c ^ (r/4 % 4)
+            const int row = o + (lane & 31);
+            const int p = (2 * kk + h) ^ ((row >> 2) & 3);
+            return *reinterpret_cast<const bf16x8*>(lds + row * 32 + 8 * p);
+        } else {                               // [32][256]: chunk c of row k at c ^ 4 (k % 4)
+            const int G = (lane & 31) >> 4, i = lane & 15;
+            const int n = o + 16 * G + 4 * (i & 3);
+            s16x4 r[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int k = 16 * kk + 8 * h + 4 * q + (i >> 2);
+                const int p = (n >> 3) ^ (4 * (k & 3));
+                r[q] = ds_read_tr(lds + k * 256 + 8 * p + 4 * ((n >> 2) & 1));
+            }
+            return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    }
+};
+
+constexpr int FAST_TILE = 256 * 32;   // elements of one operand stage (32 k)
+constexpr int FAST_NSTAGE = 4;        // LDS ring: 4 x (A + B) x 16 KB = 128 KB
+
+// Fragments of one 16-k step for the wave's FM x FN block of 32 x 32 MFMA tiles.
+template <typename OA, typename OB, int FM, int FN>
+__device__ inline void load_frags(const uint16_t* st, int kk, int wm, int wn, int lane,
+                                  bf16x8 (&fa)[FM], bf16x8 (&fb)[FN]) {
+#pragma unroll
+    for (int x = 0; x < FM; ++x) fa[x] = OA::frag(st, wm + 32 * x, kk, lane);
+#pragma unroll
+    for (int x = 0; x < FN; ++x) fb[x] = OB::frag(st + FAST_TILE, wn + 32 * x, kk, lane);
+}
+
+template <int FM, int FN>
+__device__ inline void mfma_block(const bf16x8 (&fa)[FM], const bf16x8 (&fb)[FN],
+                                  f32x16 (&acc)[FM][FN]) {
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+}
+
+// Wait until at most n of this wave's DMA stages (2 * PER loads each) are in flight.
+template <int PER2>
+__device__ inline void wait_dma_stages(int n) {
+    if (PER2 == 8) {
+        if (n >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (n == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+        if (n >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else if (n == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+}
+
+// WAVES = 4: 2 x 2 waves of 128 x 128 (one wave per SIMD, 256 accumulators);
+// WAVES = 8: 2 x 4 waves of 128 x 64 (two waves per SIMD, 128 accumulators each, so one
+// wave's MFMAs cover the other's barrier and LDS-read gaps).
+template <bool TA, bool TB, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
+gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
+                      const uint16_t* __restrict__ B, int ldb, float beta, float* __restrict__ C,
+                      int ldc) {
+    using OA = FastOperand<!TA, WAVES>;
+    using OB = FastOperand<TB, WAVES>;
+    constexpr int WN_CNT = WAVES / 2;                 // waves along N
+    constexpr int FM = 4, FN = 4 / (WAVES / 4);       // 128 x (128 or 64) per wave
+    // Ring of FAST_NSTAGE stages, each an A tile then a B tile.  Stage kt + 3 is fetched
+    // while stage kt is consumed, so every DMA has three stages of MFMA work to land.
+    __shared__ __attribute__((aligned(16))) uint16_t ring[FAST_NSTAGE * 2 * FAST_TILE];
+
+    const int tiles_m = M / 256, tiles_n = N / 256;
+    int tm, tn;
+    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
+    const int m0 = tm * 256, n0 = tn * 256;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm = (wave / WN_CNT) * 128, wn = (wave % WN_CNT) * (256 / WN_CNT);
+
+    OA oa;
+    OB ob;
+    oa.init(lda, m0, wave, lane);
+    ob.init(ldb, n0, wave, lane);
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    const int nk = K / 32;
+    auto issue = [&](int kt) {
+        uint16_t* st = ring + (kt % FAST_NSTAGE) * 2 * FAST_TILE;
+        oa.issue(A, kt, st, wave);
+        ob.issue(B, kt, st + FAST_TILE, wave);
+    };
+    auto stage_ptr = [&](int kt) { return ring + (kt % FAST_NSTAGE) * 2 * FAST_TILE; };
+    const int pre = nk < FAST_NSTAGE - 1 ? nk : FAST_NSTAGE - 1;
+    for (int s = 0; s < pre; ++s) issue(s);
+    wait_dma_stages<2 * OA::PER>(pre - 1);
+    __syncthreads();
+    // Software pipeline per 32-k stage kt (fragments of k-step 0 already in f0):
+    //   DMA stage kt+3 | read k-step 1 -> f1 | MFMA f0 | wait LDS reads + DMA of kt+1 |
+    //   barrier | read k-step 0 of kt+1 -> f0 | MFMA f1
+    // The matrix cores run f0 across the barrier wait and f1 across the next reads.  A
+    // ring slot is refilled (DMA kt+3 -> slot of kt-1) only after the barrier that follows
+    // every wave's last read of it.
+    bf16x8 f0a[FM], f0b[FN], f1a[FM], f1b[FN];
+    load_frags<OA, OB, FM, FN>(stage_ptr(0), 0, wm, wn, lane, f0a, f0b);
+    for (int kt = 0; kt < nk; ++kt) {
+        if (kt + FAST_NSTAGE - 1 < nk) issue(kt + FAST_NSTAGE - 1);
+        load_frags<OA, OB, FM, FN>(stage_ptr(kt), 1, wm, wn, lane, f1a, f1b);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_block<FM, FN>(f0a, f0b, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + 1 < nk) {
+            const int ahead = min(nk - 1, kt + FAST_NSTAGE - 1) - (kt + 1);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            wait_dma_stages<2 * OA::PER>(ahead);
+            __syncthreads();
+            load_frags<OA, OB, FM, FN>(stage_ptr(kt + 1), 0, wm, wn, lane, f0a, f0b);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_block<FM, FN>(f1a, f1b, acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b) {
+            const int col = n0 + wn + 32 * b + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
+                float* c = C + (size_t)row * ldc + col;
+                *c = beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c;
+            }
+        }
+}
+
+template <bool TA, bool TB>
+int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
+                float beta, float* C, int ldc) {
+    static const int waves = [] {
+        const char* e = std::getenv("DH_GEMM_BF16_WAVES");   // tuning knob: 4 or 8
+        return (e && std::atoi(e) == 4) ? 4 : 8;
+    }();
+    if (waves == 4)
+        gemm_bf16_fast_kernel<TA, TB, 4><<<(M / 256) * (N / 256), 256, 0, stream()>>>(
+            M, N, K, A, lda, B, ldb, beta, C, ldc);
+    else
+        gemm_bf16_fast_kernel<TA, TB, 8><<<(M / 256) * (N / 256), 512, 0, stream()>>>(
+            M, N, K, A, lda, B, ldb, beta, C, ldc);
+    return check_launch("dh_gemm_bf16(fast)");
+}
+
 template <bool TA, bool TB>
 int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
            float beta, float* C, int ldc) {
     const bool va = ((uintptr_t)A % 16 == 0) && (lda % 8 == 0);
     const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 8 == 0);
+    const long long a_elems = (long long)(TA ? K : M) * lda, b_elems = (long long)(TB ? N : K) * ldb;
+    if (va && vb && M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K > 0 &&
+        (M / 256) * (N / 256) >= num_cus() && a_elems < (1LL << 31) && b_elems < (1LL << 31))
+        return launch_fast<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc);
     if (va && vb) return launch_vec<TA, TB, true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc);
     if (va) return launch_vec<TA, TB, true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
     if (vb) return launch_vec<TA, TB, false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc);

@@ -184,3 +184,22 @@ def test_c5_bf16_8192_full_size():
     assert maxrel(got[rows], ref) <= 2e-2
     assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(8192)
     _rowcol_sums_check(got, A64, B64, 1e-5)
+
+
+@pytest.mark.parametrize("K", [64, 256, 320])          # 1, 4 (even) and 5 (odd) LDS stages
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_tile_aligned_fast_path(K, ta, tb):
+    # M = N = 4096 gives 256 tiles of 256 x 256, the direct-to-LDS path.
+    M = N = 4096
+    rng = np.random.default_rng(K + 10 * ta + 20 * tb)
+    A = bf16_bits(rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32))
+    C0 = rng.standard_normal((M, N), dtype=np.float32)
+    got = gemm(A, B, bool(ta), bool(tb), beta=0.5, C0=C0, dtype="bf16")
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    opA = A64.T if ta else A64
+    opB = B64.T if tb else B64
+    rows = np.sort(rng.choice(M, 64, replace=False))
+    ref = opA[rows] @ opB + 0.5 * C0[rows].astype(np.float64)
+    assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(K)
+    _rowcol_sums_check(got - 0.5 * C0, A64.T if ta else A64, B64.T if tb else B64, 1e-5)
