@@ -47,23 +47,23 @@ struct Bf16Stage {
     u32x4 k[KCH];
     u32x4 v[4];
 
+    // Rows at or beyond S read row S - 1 instead: finite data for keys that are masked
+    // out, and no divergent branches around the loads.
     __device__ void fetch(const uint16_t* __restrict__ Kg, const uint16_t* __restrict__ Vg,
                           int j0, int S, int tid) {
 #pragma unroll
         for (int c = 0; c < KCH; ++c) {
             const int f = tid + c * NT;
             const int key = f / (D / 8), dq = f % (D / 8);
-            const int j = j0 + key;
-            k[c] = j < S ? *reinterpret_cast<const u32x4*>(Kg + (size_t)j * D + 8 * dq)
-                         : u32x4{0u, 0u, 0u, 0u};
+            const int j = min(j0 + key, S - 1);
+            k[c] = *reinterpret_cast<const u32x4*>(Kg + (size_t)j * D + 8 * dq);
         }
         if (tid < VBLK) {
             const int kq = tid % (BN / 4), db = tid / (BN / 4);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int j = j0 + 4 * kq + r;
-                v[r] = j < S ? *reinterpret_cast<const u32x4*>(Vg + (size_t)j * D + 8 * db)
-                             : u32x4{0u, 0u, 0u, 0u};
+                const int j = min(j0 + 4 * kq + r, S - 1);
+                v[r] = *reinterpret_cast<const u32x4*>(Vg + (size_t)j * D + 8 * db);
             }
         }
     }
@@ -92,6 +92,91 @@ __device__ inline uint32_t cvt_pk_bf16(float a, float b) {
            ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
 }
 
+// Lazy rescaling: a row keeps exponentiating against the max it already uses (m) until a
+// block's max exceeds it by more than RESCALE_TH (log2 units).  Then p <= 2^RESCALE_TH,
+// harmless for fp32 sums and bf16 P, and the 128-register output accumulator is rescaled
+// only when some row of the wave actually needs it -- after the first blocks, almost never.
+constexpr float RESCALE_TH = 8.0f;
+
+// Scores S^T of one 64-key stage for one 32-row sub-block: sacc[kb] = K[32 kb ..] Q^T.
+template <int D>
+__device__ inline void scores(const uint16_t* ks, const bf16x8 (&qf)[D / 16], int l32, int h,
+                              f32x16 (&sacc)[2]) {
+    using St = Bf16Stage<D>;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) {
+            const bf16x8 kf = *reinterpret_cast<const bf16x8*>(
+                &ks[(32 * kb + l32) * St::KS + 16 * t + 8 * h]);
+            sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], sacc[kb], 0, 0, 0);
+        }
+    }
+}
+
+// Online-softmax update of one 32-row sub-block for one stage, then O^T += V^T P^T.
+// Keys j > lim (this lane's causal diagonal / the end of the sequence) are masked.
+template <int D>
+__device__ inline void softmax_pv(const uint16_t* vt, f32x16 (&sacc)[2], float scale_log2,
+                                  int j0, int lim, int l32, int h, float& m, float& l,
+                                  f32x16 (&oacc)[D / 32]) {
+    using St = Bf16Stage<D>;
+    constexpr int ND = D / 32;
+    float mx = NEG;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int j = j0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+            const float s = j > lim ? NEG : sacc[kb][r] * scale_log2;
+            sacc[kb][r] = s;
+            mx = fmaxf(mx, s);
+        }
+    mx = fmaxf(mx, xor32(mx));
+    if (__any(mx > m + RESCALE_TH)) {      // wave-uniform: rare after the first blocks
+        const float m_new = fmaxf(m, mx);
+        const float corr = fast_exp2(m - m_new);
+        m = m_new;
+        l *= corr;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+    }
+    float sum = 0.f;
+    uint32_t pk[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            const float p0 = fast_exp2(sacc[kb][r] - m);
+            const float p1 = fast_exp2(sacc[kb][r + 1] - m);
+            sum += p0 + p1;
+            pk[kb][r >> 1] = cvt_pk_bf16(p0, p1);
+        }
+    l += sum + xor32(sum);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const bf16x8 pf = __builtin_bit_cast(
+                bf16x8, u32x4{pk[kb][4 * kk], pk[kb][4 * kk + 1], pk[kb][4 * kk + 2],
+                              pk[kb][4 * kk + 3]});
+            const int key = 32 * kb + 16 * kk + 4 * h;
+#pragma unroll
+            for (int d = 0; d < ND; ++d) {
+                const uint16_t* row = &vt[(32 * d + l32) * St::VS + key];
+                const u32x2 a = *reinterpret_cast<const u32x2*>(row);
+                const u32x2 b = *reinterpret_cast<const u32x2*>(row + 8);
+                oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8, u32x4{a[0], a[1], b[0], b[1]}), pf, oacc[d], 0, 0,
+                    0);
+            }
+        }
+}
+
 template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(NT)
 flash_fwd_bf16_kernel(int BH, int S, float scale_log2, const uint16_t* __restrict__ Q,
@@ -113,7 +198,8 @@ flash_fwd_bf16_kernel(int BH, int S, float scale_log2, const uint16_t* __restric
     const uint16_t* Kg = K + base;
     const uint16_t* Vg = V + base;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, h = lane >> 5;
     const int wrow = q0 + 64 * wave;               // first row of this wave
 
@@ -121,13 +207,11 @@ flash_fwd_bf16_kernel(int BH, int S, float scale_log2, const uint16_t* __restric
     bf16x8 qf[2][NTK];
 #pragma unroll
     for (int rs = 0; rs < 2; ++rs) {
-        const int i = wrow + 32 * rs + l32;
+        const int i = min(wrow + 32 * rs + l32, S - 1);
 #pragma unroll
-        for (int t = 0; t < NTK; ++t) {
-            u32x4 x = i < S ? *reinterpret_cast<const u32x4*>(Qg + (size_t)i * D + 16 * t + 8 * h)
-                            : u32x4{0u, 0u, 0u, 0u};
-            qf[rs][t] = __builtin_bit_cast(bf16x8, x);
-        }
+        for (int t = 0; t < NTK; ++t)
+            qf[rs][t] = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4*>(Qg + (size_t)i * D + 16 * t + 8 * h));
     }
 
     f32x16 oacc[2][ND];
@@ -154,85 +238,16 @@ flash_fwd_bf16_kernel(int BH, int S, float scale_log2, const uint16_t* __restric
         const uint16_t* ks = kbuf + cur * St::K_ELEMS;
         const uint16_t* vt = vbuf + cur * St::V_ELEMS;
         const int j0 = st * BN;
-
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            const int r0 = wrow + 32 * rs;           // first query row of the sub-block
-            const int i = r0 + l32;                  // this lane's query row
-            // Causal: a sub-block whose rows all precede this stage has nothing to add.
+            const int r0 = wrow + 32 * rs;
+            // causal: a sub-block whose rows all precede this stage has nothing to add
             if (CAUSAL && j0 > r0 + 31) continue;
+            // keys above lim are masked: the causal diagonal and the end of the sequence
+            const int lim = CAUSAL ? min(r0 + l32, S - 1) : S - 1;
             f32x16 sacc[2];
-            bool act[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const int kb0 = j0 + 32 * kb;
-                act[kb] = kb0 < S && (!CAUSAL || kb0 <= r0 + 31);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-                if (act[kb]) {
-#pragma unroll
-                    for (int t = 0; t < NTK; ++t) {
-                        bf16x8 kf = *reinterpret_cast<const bf16x8*>(
-                            &ks[(32 * kb + l32) * St::KS + 16 * t + 8 * h]);
-                        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[rs][t],
-                                                                          sacc[kb], 0, 0, 0);
-                    }
-                }
-            }
-            // scale to log2 units, mask, block row max
-            float mx = NEG;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int j = j0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                    float s = sacc[kb][r] * scale_log2;
-                    if (!act[kb] || j >= S || (CAUSAL && j > i)) s = NEG;
-                    sacc[kb][r] = s;
-                    mx = fmaxf(mx, s);
-                }
-            mx = fmaxf(mx, xor32(mx));
-            const float m_new = fmaxf(m[rs], mx);
-            const float corr = fast_exp2(m[rs] - m_new);
-            m[rs] = m_new;
-            float sum = 0.f;
-            uint32_t pk[2][8];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    const float p0 = fast_exp2(sacc[kb][r] - m_new);
-                    const float p1 = fast_exp2(sacc[kb][r + 1] - m_new);
-                    sum += p0 + p1;
-                    pk[kb][r >> 1] = cvt_pk_bf16(p0, p1);
-                }
-            sum += xor32(sum);
-            l[rs] = l[rs] * corr + sum;
-#pragma unroll
-            for (int d = 0; d < ND; ++d)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[rs][d][r] *= corr;
-            // O^T += V^T P^T over the 64 keys: per 32-key sub-block two k-steps of 16.
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                if (!act[kb]) continue;
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    u32x4 pw = {pk[kb][4 * kk], pk[kb][4 * kk + 1], pk[kb][4 * kk + 2],
-                                pk[kb][4 * kk + 3]};
-                    const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
-                    const int key = 32 * kb + 16 * kk + 4 * h;
-#pragma unroll
-                    for (int d = 0; d < ND; ++d) {
-                        const uint16_t* row = &vt[(32 * d + l32) * St::VS + key];
-                        u32x2 a = *reinterpret_cast<const u32x2*>(row);
-                        u32x2 b = *reinterpret_cast<const u32x2*>(row + 8);
-                        u32x4 w = {a[0], a[1], b[0], b[1]};
-                        oacc[rs][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            __builtin_bit_cast(bf16x8, w), pf, oacc[rs][d], 0, 0, 0);
-                    }
-                }
-            }
+            scores<D>(ks, qf[rs], l32, h, sacc);
+            softmax_pv<D>(vt, sacc, scale_log2, j0, lim, l32, h, m[rs], l[rs], oacc[rs]);
         }
         if (more) stage.store(kbuf + (cur ^ 1) * St::K_ELEMS, vbuf + (cur ^ 1) * St::V_ELEMS, tid);
         __syncthreads();
