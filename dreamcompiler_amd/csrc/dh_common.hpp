@@ -110,6 +110,39 @@ __device__ inline float wave_reduce(float v, Op op) {
 struct OpMax { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
 struct OpSum { __device__ float operator()(float a, float b) const { return a + b; } };
 
+// ---- LDS transfer primitives -------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+// ds_read_b64_tr_b16.  Within each group of 16 lanes, lane i supplies the address of 4
+// consecutive 16-bit values R_i; lane j receives R_{j/4 + 4e}[j % 4] for e = 0..3.
+__device__ inline s16x4 ds_read_tr(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (s16x4 __attribute__((address_space(3)))*)(p));
+}
+
+// 16-byte direct-to-LDS load: lane l's 16 bytes land at lds_base + 16 l.  Issued as
+// inline assembly so that the compiler's wait insertion, which cannot tell the DMA
+// target from the stage being read, does not serialise every LDS read behind it; the
+// kernel waits (vmcnt) itself before each barrier.  m0 holds the wave's LDS base; one
+// wait state separates the m0 write from the DMA, as the hardware requires.
+__device__ inline void lds_dma16(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds_base), "v"(g)
+                 : "memory", "m0");
+}
+
+__device__ inline uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Wait until at most N of this wave's vector-memory operations are in flight.
+template <int N>
+__device__ inline void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // ---- XCD-aware tile order --------------------------------------------------------
 // Work-groups are dealt round-robin to the 8 XCDs (block b runs on XCD b % 8).
 // Remap so that each XCD receives a contiguous run of logical tiles, then walk

@@ -233,28 +233,6 @@ int launch_vec(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* 
 // the fragment reads conflict free under that model.  Two LDS stages (128 KB); fragments of the next
 // k-step are read while the matrix cores run the current one.
 // ---------------------------------------------------------------------------------
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-__device__ inline s16x4 ds_read_tr(const uint16_t* p) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (s16x4 __attribute__((address_space(3)))*)(p));
-}
-
-// 16-byte direct-to-LDS load.  Issued as inline assembly so that the compiler's wait
-// insertion, which cannot tell the DMA target from the stage being read, does not
-// serialise every LDS read behind it; the kernel waits (vmcnt) itself before each
-// barrier.  m0 holds the wave's LDS base; one wait state separates the m0 write from
-// the DMA, as the hardware requires.
-__device__ inline void lds_dma16(const void* g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(lds_base), "v"(g)
-                 : "memory", "m0");
-}
-
-__device__ inline uint32_t lds_addr(const uint16_t* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
-}
 
 template <bool KCONTIG, int WAVES>
 struct FastOperand {
