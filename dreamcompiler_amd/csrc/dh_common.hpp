@@ -125,11 +125,30 @@ __device__ inline s16x4 ds_read_tr(const uint16_t* p) {
 // inline assembly so that the compiler's wait insertion, which cannot tell the DMA
 // target from the stage being read, does not serialise every LDS read behind it; the
 // kernel waits (vmcnt) itself before each barrier.  m0 holds the wave's LDS base; one
-// wait state separates the m0 write from the DMA, as the hardware requires.
+// wait state separates the m0 write from the DMA, as the hardware requires.  The
+// compiler treats m0 as reserved and does not see this write: that is safe only while
+// no compiler-generated instruction of the calling kernels reads m0 (none does in the
+// gfx950 code of this library; LDS instructions there do not use it).
 __device__ inline void lds_dma16(const void* g, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                  :
                  : "s"(lds_base), "v"(g)
+                 : "memory", "m0");
+}
+
+// Raw buffer resource (gfx9 family): 48-bit base, no stride, `bytes` addressable; loads
+// beyond `bytes` (checked per dword) return zero.
+__device__ inline u32x4 make_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+
+// 16-byte direct-to-LDS buffer load: lane l's 16 bytes at rsrc base + voff land at
+// lds_base + 16 l (zeros past the resource's range).  Same waiting rules as lds_dma16.
+__device__ inline void lds_dma16_buf(uint32_t voff, u32x4 rsrc, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(rsrc)
                  : "memory", "m0");
 }
 

@@ -81,6 +81,29 @@ __device__ inline float dot2_bf16(uint32_t p, uint32_t q, float acc) {
                                            acc, false);
 }
 
+// Work-group -> (slice bh, q-tile rank rr; rank 0 = longest causal key range).  Work-groups
+// are dealt round-robin to the 8 XCDs.  When the slices split evenly, XCD x takes the
+// slices bh = x (mod 8) in groups of G and finishes one group before the next, heaviest
+// q-tile first within a group: the few slices in flight keep their K and V in the XCD's
+// L2, and G = 4 causal slices hold enough work that the last, longest tiles of a group
+// do not trail.  Otherwise: heaviest q-tile of every slice first.
+template <bool CAUSAL>
+__device__ inline void bf_order(int BH, int n_qt, int& bh, int& rr) {
+    const int bid = blockIdx.x;
+    if (BH & 7) {
+        bh = bid % BH;
+        rr = bid / BH;
+        return;
+    }
+    constexpr int G = CAUSAL ? 4 : 1;
+    const int x = bid & 7, k = bid >> 3, spx = BH >> 3;
+    const int g = k / (G * n_qt);
+    const int gsz = min(G, spx - g * G);
+    const int w = k - g * G * n_qt;
+    rr = w / gsz;
+    bh = 8 * (g * G + w % gsz) + x;
+}
+
 // One work-group = 8 waves x 32 query rows.  Per stage of 64 keys a wave computes
 // S^T = K Q^T (2 x D/16 MFMAs, K from LDS, Q from registers), the online softmax on its
 // 32 scores per lane, and O^T += V^T P^T (2 x 2 x D/32 MFMAs, V through transpose reads,
@@ -98,8 +121,8 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
     const int n_qt = (S + BF_ROWS - 1) / BF_ROWS;
-    const int bh = blockIdx.x % BH;
-    const int rr = blockIdx.x / BH;
+    int bh, rr;
+    bf_order<CAUSAL>(BH, n_qt, bh, rr);
     const int qt = CAUSAL ? n_qt - 1 - rr : rr;
     const int q0 = qt * BF_ROWS;
     const size_t base = (size_t)bh * S * D;
@@ -113,9 +136,13 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     const int r0 = q0 + 32 * wave;                 // first query row of this wave
     const uint32_t ring_lds = lds_addr(ring);
 
+    const int kend = CAUSAL ? min(S, q0 + BF_ROWS) : S;
+    const int nst = (kend + BN - 1) / BN;
     // DMA work of this wave: blocks wave, wave + 8, ... of the stage (K tile first).
-    uint32_t dlds[T::PER];
-    int drow[T::PER], dcol[T::PER];
+    // Loads go through a buffer resource per stage (base = key row j0, range = the rows
+    // left in the slice), so each lane's byte offset is loop-invariant and rows at or past
+    // S arrive as zeros (masked keys; zero V rows meet p = 0).
+    uint32_t dlds[T::PER], dvoff[T::PER];
     bool dk[T::PER];
 #pragma unroll
     for (int q = 0; q < T::PER; ++q) {
@@ -124,17 +151,20 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
         const int row = b * T::RPB + lane / T::CH, pos = lane % T::CH;
         dk[q] = tile == 0;
         dlds[q] = tile * T::TILE + b * 1024;
-        drow[q] = row;
-        dcol[q] = 8 * (pos ^ (tile == 0 ? T::kswz(row) : T::vswz(row)));
+        dvoff[q] = row * T::ROWB + 16 * (pos ^ (tile == 0 ? T::kswz(row) : T::vswz(row)));
     }
-    auto issue = [&](int st) {
-        const int j0 = st * BN;
+    // DMA block q of stage st into ring slot st % BF_NSTAGE.  A stage at or past nst is
+    // never computed: its slot is free, and the load re-reads key rows from 0 (in bounds,
+    // cached) so that callers need no branch.
+    auto issue_one = [&](int st, int q) {
+        const int j0 = st < nst ? st * BN : 0;
         const uint32_t sb = ring_lds + (st % BF_NSTAGE) * T::STAGE;
+        const u32x4 rs = make_rsrc((dk[q] ? Kg : Vg) + (size_t)j0 * D, (uint32_t)(S - j0) * T::ROWB);
+        lds_dma16_buf(dvoff[q], rs, __builtin_amdgcn_readfirstlane(sb + dlds[q]));
+    };
+    auto issue = [&](int st) {
 #pragma unroll
-        for (int q = 0; q < T::PER; ++q) {
-            const size_t off = (size_t)min(j0 + drow[q], S - 1) * D + dcol[q];
-            lds_dma16((dk[q] ? Kg : Vg) + off, __builtin_amdgcn_readfirstlane(sb + dlds[q]));
-        }
+        for (int q = 0; q < T::PER; ++q) issue_one(st, q);
     };
 
     // Q fragments (B operand of S^T = K Q^T): lane (i, h) holds Q[i][16t + 8h .. +7].
@@ -172,38 +202,28 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     float m = -INFINITY, l = 0.f;
     const int lim = CAUSAL ? min(r0 + l32, S - 1) : S - 1;   // last key this row sees
 
-    const int kend = CAUSAL ? min(S, q0 + BF_ROWS) : S;
-    const int nst = (kend + BN - 1) / BN;
     // stages this wave computes: none if all its rows are padding, else up to its diagonal
     const int wlast = r0 >= S ? 0 : CAUSAL ? min(S - 1, r0 + 31) / BN + 1 : nst;
 
-#pragma unroll
-    for (int st = 0; st < BF_NSTAGE - 1; ++st)
-        if (st < nst) issue(st);
-    for (int st = 0; st < nst; ++st) {
-        // stage st has landed once at most (stages issued after it) x PER loads remain
-        const int ahead = min(nst - 1 - st, BF_NSTAGE - 2);
-        if (ahead >= 2) wait_vmcnt<2 * T::PER>();
-        else if (ahead == 1) wait_vmcnt<T::PER>();
+    // Software pipeline, per wave and stage st (scores of st already in `cur`, masked,
+    // with their row max):
+    //   A  lazy-rescale decision for st (rarely taken branch);
+    //   B  S(st+1) = K(st+1) Q^T on the matrix cores while the VALU exponentiates st;
+    //   C  O^T += V^T P^T for st, then the mask and row max of st+1 (whose VALU work
+    //      overlaps the last PV MFMAs in flight).  B and C form one basic block.
+    // Stage st+1 must therefore be in LDS at barrier st; the DMA stays 3 stages ahead in
+    // the 4-slot ring (the slot refilled after barrier st last held stage st-1).  B and C
+    // run unconditionally: past the last stage they read a stale, in-bounds ring slot and
+    // the result is discarded.
+    auto sync = [&](int st) {
+        // stages <= st + 1 must have landed; st + 2 may still be in flight
+        if (st + 2 < nst) wait_vmcnt<T::PER>();
         else wait_vmcnt<0>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
-        if (st + BF_NSTAGE - 1 < nst) issue(st + BF_NSTAGE - 1);
-        if (st >= wlast) continue;
-
+    };
+    auto scores = [&](int st, f32x16 (&sacc)[2]) {
         const uint8_t* kt = ring + (st % BF_NSTAGE) * T::STAGE;
-        const uint8_t* vt = kt + T::TILE;
-        const int j0 = st * BN;
-        // All K fragments of the stage are read up front so that the LDS latency overlaps
-        // the MFMAs; the two 32-key chains alternate.
-        bf16x8 kf[2][NTK];
-#pragma unroll
-        for (int t = 0; t < NTK; ++t)
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-                kf[kb][t] = *reinterpret_cast<const bf16x8*>(kt + kofs[t] + 32 * kb * T::ROWB);
-        __builtin_amdgcn_sched_barrier(0);
-        f32x16 sacc[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -211,9 +231,14 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
 #pragma unroll
         for (int t = 0; t < NTK; ++t)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb][t], qf[t], sacc[kb], 0, 0, 0);
-        // sacc[kb][r] = S^T[key j0 + 32 kb + 8 (r / 4) + 4 h + r % 4][row r0 + l32]
+            for (int kb = 0; kb < 2; ++kb) {
+                const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kt + kofs[t] + 32 * kb * T::ROWB);
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], sacc[kb], 0, 0, 0);
+            }
+    };
+    // sacc[kb][r] = S^T[key st*BN + 32 kb + 8 (r / 4) + 4 h + r % 4][row r0 + l32]
+    auto mask = [&](int st, f32x16 (&sacc)[2]) {
+        const int j0 = st * BN;
         if (j0 + BN - 1 > (CAUSAL ? r0 : S - 1)) {        // wave-uniform: diagonal or tail
             const int rel = lim - j0 - 4 * h;             // mask offsets above rel
 #pragma unroll
@@ -222,11 +247,19 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
                 for (int r = 0; r < 16; ++r)
                     if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) sacc[kb][r] = -INFINITY;
         }
-        float mx = -INFINITY;
+    };
+    auto rowmax = [&](const f32x16 (&sacc)[2]) {      // max over this lane's 32 scores
+        float t8[8];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+        for (int q = 0; q < 8; ++q) {
+            const f32x16& a = sacc[q >> 2];
+            const int o = 4 * (q & 3);
+            t8[q] = fmaxf(fmaxf(a[o], a[o + 1]), fmaxf(a[o + 2], a[o + 3]));
+        }
+        return fmaxf(fmaxf(fmaxf(t8[0], t8[1]), fmaxf(t8[2], t8[3])),
+                     fmaxf(fmaxf(t8[4], t8[5]), fmaxf(t8[6], t8[7])));
+    };
+    auto rescale = [&](float mx) {
         if (__any((mx - m) * sl2 > RESCALE_TH)) {      // wave-uniform: rare after the start
             mx = fmaxf(mx, xor32(mx));
             const float m_new = fmaxf(m, mx);
@@ -238,37 +271,133 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
 #pragma unroll
                 for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
         }
+    };
+    // B and C for stage st, interleaved by hand: sched_barrier(0) between chunks fixes
+    // the issue order, and fragment reads are issued ahead of their MFMA by hand.  An MFMA
+    // holds the SIMD's issue port about as long as two VALU ops and an exponential as
+    // long as two, so the VALU work is spread to keep each chunk near one MFMA's time:
+    //   B: chunk i issues score MFMA i of stage st+1 (i = 2 t + kb), the exponentials of
+    //      pairs [QB i / NS, QB (i+1) / NS) of stage st, and this wave's DMA share of stage
+    //      st+3 (one block every other chunk);
+    //   C: chunk j issues PV MFMA j of stage st (j = (2 kb + kk) ND + d); its first chunks
+    //      exponentiate the remaining pairs (each before the PV MFMA that consumes it), the
+    //      later ones take the bf16 row sums (dot2) and, after the mask of st+1, the row max
+    //      of st+1, which is returned.
+    auto overlap = [&](int st, const f32x16 (&cur)[2], f32x16 (&nxt)[2]) -> float {
+        constexpr int NS = 2 * NTK;            // score MFMAs per stage
+        constexpr int NP = 4 * ND;             // PV MFMAs per stage
+        constexpr int QB = D == 128 ? 10 : D == 64 ? 12 : 16;   // pairs exponentiated in B
+        constexpr int J0 = 16 - QB;            // first C chunk free of exponentials
+        constexpr int KPF = 4;                 // K fragments in flight
+        const uint8_t* kt = ring + ((st + 1) % BF_NSTAGE) * T::STAGE;
+        const uint8_t* vt = ring + (st % BF_NSTAGE) * T::STAGE + T::TILE;
+        auto kfrag = [&](int i) {
+            return *reinterpret_cast<const bf16x8*>(kt + kofs[i >> 1] + 32 * (i & 1) * T::ROWB);
+        };
+        // V fragment of PV MFMA j: keys 32 kb + 16 kk + 4 h + (0..3) and + 8 (see vofs).
+        auto vread = [&](int j, s16x4 (&a)[2]) {
+            const int d = j % ND, kk = (j / ND) & 1, kb = j / (2 * ND);
+            const uint8_t* vk = vt + (32 * kb + 16 * kk) * T::ROWB + vofs[d];
+            a[0] = ds_read_tr(reinterpret_cast<const uint16_t*>(vk));
+            a[1] = ds_read_tr(reinterpret_cast<const uint16_t*>(vk + 8 * T::ROWB));
+        };
         const float mb = m * sl2;
-        uint32_t pk[2][8];
+        uint32_t pk[16];                       // pk[8 kb + r / 2] = bf16 pair (r, r + 1) of cur[kb]
+        auto expo = [&](int q) {
+            const f32x16& c = cur[q >> 3];
+            const int r = 2 * (q & 7);
+            const float p0 = fast_exp2(__builtin_fmaf(c[r], sl2, -mb));
+            const float p1 = fast_exp2(__builtin_fmaf(c[r + 1], sl2, -mb));
+            pk[q] = cvt_pk_bf16(p0, p1);
+            asm volatile("" : "+v"(pk[q]));    // keep it in this chunk (no sinking)
+        };
+        bf16x8 kf[KPF];
+        s16x4 va[3][2];
+#pragma unroll
+        for (int i = 0; i < KPF; ++i) kf[i] = kfrag(i);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                const float p0 = fast_exp2(__builtin_fmaf(sacc[kb][r], sl2, -mb));
-                const float p1 = fast_exp2(__builtin_fmaf(sacc[kb][r + 1], sl2, -mb));
-                pk[kb][r >> 1] = cvt_pk_bf16(p0, p1);
-                l = dot2_bf16(pk[kb][r >> 1], 0x3F803F80u, l);
+            for (int r = 0; r < 16; ++r) nxt[kb][r] = 0.f;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            nxt[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i % KPF], qf[i >> 1],
+                                                                 nxt[i & 1], 0, 0, 0);
+            if (i + KPF < NS) kf[i % KPF] = kfrag(i + KPF);
+            else if (i + KPF - NS < 2) vread(i + KPF - NS, va[i + KPF - NS]);
+#pragma unroll
+            for (int q = QB * i / NS; q < QB * (i + 1) / NS; ++q) expo(q);
+            if ((i & 1) && (i >> 1) < T::PER) issue_one(st + BF_NSTAGE - 1, i >> 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int q = NS / 2; q < T::PER; ++q) issue_one(st + BF_NSTAGE - 1, q);
+        float tmax[8];
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            if (j == NP / 2) {
+                mask(st + 1, nxt);
+                __builtin_amdgcn_sched_barrier(0);
             }
-        // O^T += V^T P^T.  k-step kk of key block kb pairs keys 16 kk + 4 h + (0..3) and
-        // 16 kk + 8 + 4 h + (0..3): the score registers 8 kk .. 8 kk + 7 of this lane.
+            const int d = j % ND, q0 = 4 * (j / ND);
+            const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[q0], pk[q0 + 1], pk[q0 + 2], pk[q0 + 3]});
+            const s16x4(&a)[2] = va[j % 3];
+            const bf16x8 vf = __builtin_bit_cast(
+                bf16x8, s16x8{a[0][0], a[0][1], a[0][2], a[0][3], a[1][0], a[1][1], a[1][2], a[1][3]});
+            oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[d], 0, 0, 0);
+            if (j + 2 < NP) vread(j + 2, va[(j + 2) % 3]);
+            if (j < J0) expo(QB + j);
+            if (j >= J0) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+                for (int q = 16 * (j - J0) / (NP - J0); q < 16 * (j - J0 + 1) / (NP - J0); ++q)
+                    l = dot2_bf16(pk[q], 0x3F803F80u, l);
+                asm volatile("" : "+v"(l));
+            }
+            if (j >= NP / 2) {
+                constexpr int MPC = 8 / (NP / 2);     // partial maxima per chunk
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const bf16x8 pf = __builtin_bit_cast(
-                    bf16x8, u32x4{pk[kb][4 * kk], pk[kb][4 * kk + 1], pk[kb][4 * kk + 2],
-                                  pk[kb][4 * kk + 3]});
-                const uint8_t* vk = vt + (32 * kb + 16 * kk) * T::ROWB;
-#pragma unroll
-                for (int d = 0; d < ND; ++d) {
-                    const s16x4 a0 = ds_read_tr(reinterpret_cast<const uint16_t*>(vk + vofs[d]));
-                    const s16x4 a1 = ds_read_tr(
-                        reinterpret_cast<const uint16_t*>(vk + vofs[d] + 8 * T::ROWB));
-                    const bf16x8 vf = __builtin_bit_cast(
-                        bf16x8, s16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]});
-                    oacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, oacc[d], 0, 0, 0);
+                for (int u = 0; u < MPC; ++u) {
+                    const int q = (j - NP / 2) * MPC + u;
+                    const f32x16& a4 = nxt[q >> 2];
+                    const int o = 4 * (q & 3);
+                    tmax[q] = fmaxf(fmaxf(a4[o], a4[o + 1]), fmaxf(a4[o + 2], a4[o + 3]));
+                    asm volatile("" : "+v"(tmax[q]));
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return fmaxf(fmaxf(fmaxf(tmax[0], tmax[1]), fmaxf(tmax[2], tmax[3])),
+                     fmaxf(fmaxf(tmax[4], tmax[5]), fmaxf(tmax[6], tmax[7])));
+    };
+    auto step = [&](int st, f32x16 (&cur)[2], f32x16 (&nxt)[2], float mx_cur) -> float {
+        sync(st);
+        if (st >= wlast) {                     // no rows left here: only the DMA share
+            issue(st + BF_NSTAGE - 1);
+            return 0.f;
+        }
+        rescale(mx_cur);
+        return overlap(st, cur, nxt);
+    };
+
+#pragma unroll
+    for (int st = 0; st < BF_NSTAGE - 1; ++st)
+        if (st < nst) issue(st);
+    // prologue: S(0) and its max
+    if (nst > 2) wait_vmcnt<2 * T::PER>();              // stage 0 landed, 1 and 2 may fly
+    else if (nst == 2) wait_vmcnt<T::PER>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    f32x16 sa[2], sb[2];
+    float mx = 0.f;
+    if (wlast > 0) {
+        scores(0, sa);
+        mask(0, sa);
+        mx = rowmax(sa);
+    }
+    for (int st = 0; st < nst; st += 2) {
+        mx = step(st, sa, sb, mx);
+        if (st + 1 < nst) mx = step(st + 1, sb, sa, mx);
     }
 
     // Epilogue: lane (i, h) holds O^T[d][i] for d = 32 dt + 8 q + 4 h + (0..3).
