@@ -226,6 +226,9 @@ def measure(name, steps, warmup):
     res = {"workload": name, "desc": desc, "ms": round(ms, 5), "tflops": round(tflops, 2),
            "frac_peak": round(tflops / PEAK[prec], 4), "peak_tflops": PEAK[prec],
            "alg_bytes": alg_bytes, "wall_s": round(wall, 4)}
+    traffic = load_traffic().get(name)
+    if traffic:
+        res["hbm_bytes_measured"] = traffic["bytes_per_launch"]
     for b in bufs:
         b.free()
     hip.load().dh_pool_release()
@@ -266,9 +269,11 @@ def main():
     head = measure(args.workload, args.steps, args.warmup)
     metrics = {}
     if not args.only:
+        # Every workload gets the same warm-up: MI355X clocks settle only after some tens
+        # of launches (power management), and the first launches run at a transient clock.
         for name in WORKLOADS:
             if name != args.workload:
-                metrics[name] = measure(name, max(3, args.steps // 2), 2)
+                metrics[name] = measure(name, args.steps, args.warmup)
         metrics["mlp_c2"] = mlp_metrics(max(5, args.steps), 3)
 
     traffic = load_traffic().get(args.workload)
