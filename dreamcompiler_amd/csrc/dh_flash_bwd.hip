@@ -11,8 +11,10 @@
 // MFMA layouts: in launch 2 the scores are formed as S = Q K^T so the lane index is the
 // key (the row of dK / dV); in launch 3 as S^T = K Q^T so the lane index is the query.
 // Either way the product that consumes P or dS takes it straight from the score
-// registers (the same interleaved-key trick as the forward), and the second operand
-// is read from an LDS tile staged transposed ([d][row]) for bf16 or row-major for fp32.
+// registers (the same interleaved-key trick as the forward).  bf16: the streamed tiles
+// (Q, dO in launch 2; K, V in launch 3) arrive by direct-to-LDS DMA in 4-deep rings and
+// the transposed operands come from the same tiles through transpose reads; fp32: tiles
+// are staged through registers into row-major LDS.
 #include "dh_common.hpp"
 
 namespace dh {
@@ -24,8 +26,9 @@ constexpr int RB = 32;   // rows (queries or keys) per LDS stage
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ inline uint32_t cvt_pk_bf16(float a, float b) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));   // RNE
 }
 
 template <typename T> __device__ inline float to_f(T x);
@@ -37,7 +40,8 @@ template <> __device__ inline float to_f<uint16_t>(uint16_t x) { return bf16_bit
 // ---------------------------------------------------------------------------------
 template <typename T, int D>
 __global__ void __launch_bounds__(NT)
-dvec_kernel(int rows, const T* __restrict__ O, const T* __restrict__ dO, float* __restrict__ Dv) {
+dvec_kernel(int rows, const T* __restrict__ O, const T* __restrict__ dO, float* __restrict__ Dv,
+            const float* __restrict__ LSE, float* __restrict__ L2) {
     const int row = blockIdx.x * (NT / 16) + (threadIdx.x >> 4);
     const int sub = threadIdx.x & 15;
     float acc = 0.f;
@@ -51,93 +55,154 @@ dvec_kernel(int rows, const T* __restrict__ O, const T* __restrict__ dO, float* 
     acc += dpp_quad_xor2(acc);
     acc += dpp_half_mirror(acc);
     acc += dpp_row_mirror(acc);
-    if (row < rows && sub == 0) Dv[row] = acc;
+    if (row < rows && sub == 0) {
+        Dv[row] = acc;
+        if (L2) L2[row] = LSE[row] * 1.4426950408889634f;   // log2-domain LSE (bf16 kernels)
+    }
 }
 
 // ---------------------------------------------------------------------------------
-// bf16 staging: a 32-row x D tile fetched as 4-row x 8-column blocks, written to LDS
-// row-major ([row][d], stride D + 8) and optionally transposed ([d][row], stride 36).
+// bf16 kernels.  Tiles stream through LDS rings filled by direct-to-LDS buffer loads
+// (rows at or past S arrive as zeros).  A tile read both as b128 row fragments (MFMA A
+// operand, one row per lane) and through ds_read_b64_tr_b16 (the transposed operand)
+// keeps the 16-byte chunk c of row r at position c ^ dswz(r), conflict-free for both
+// access patterns; a tile read only as rows uses kswz.
 // ---------------------------------------------------------------------------------
-template <int D>
-struct Tile16 {
-    static constexpr int NS = D + 8;          // natural row stride (bf16)
-    static constexpr int TS = RB + 4;         // transposed row stride (bf16)
-    static constexpr int NAT = RB * NS;       // elements of a natural tile
-    static constexpr int TRN = D * TS;        // elements of a transposed tile
-    static constexpr int NB = (RB / 4) * (D / 8);   // blocks per tile
-
-    u32x4 v[4];
-
-    __device__ void fetch(const uint16_t* __restrict__ g, int r0, int S, int b) {
-        const int kq = b % (RB / 4), db = b / (RB / 4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = r0 + 4 * kq + r;
-            v[r] = row < S ? *reinterpret_cast<const u32x4*>(g + (size_t)row * D + 8 * db)
-                           : u32x4{0u, 0u, 0u, 0u};
-        }
+template <int D, int ROWS>
+struct BwTile {
+    static constexpr int CH = D / 8;              // 16-byte chunks per row
+    static constexpr int ROWB = 2 * D;            // bytes per row
+    static constexpr int TILE = ROWS * ROWB;      // bytes per tile
+    static constexpr int NBLK = TILE / 1024;      // 1 KB DMA blocks per tile
+    static constexpr int RPB = 1024 / ROWB;       // rows per DMA block
+    static constexpr int RW = 256 / ROWB;         // rows per 256-byte bank sweep
+    __device__ static int kswz(int r) { return (r * CH / 16) % CH; }
+    __device__ static int dswz(int r) { return 4 * ((r / RW) % (4 / RW)) + ((r >> 2) & 3); }
+    __device__ static uint32_t rowfrag(int r, int c, bool dual) {
+        return r * ROWB + 16 * (c ^ (dual ? dswz(r) : kswz(r)));
     }
-    __device__ void store(uint16_t* nat, uint16_t* trn, int b) const {
-        const int kq = b % (RB / 4), db = b / (RB / 4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            *reinterpret_cast<u32x4*>(&nat[(4 * kq + r) * NS + 8 * db]) = v[r];
-        if (trn) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                u32x2 lo = {pack_lo16(v[0][q], v[1][q]), pack_lo16(v[2][q], v[3][q])};
-                u32x2 hi = {pack_hi16(v[0][q], v[1][q]), pack_hi16(v[2][q], v[3][q])};
-                *reinterpret_cast<u32x2*>(&trn[(8 * db + 2 * q) * TS + 4 * kq]) = lo;
-                *reinterpret_cast<u32x2*>(&trn[(8 * db + 2 * q + 1) * TS + 4 * kq]) = hi;
-            }
-        }
+    // Transpose-read address of row r, columns n .. n + 3 (n a multiple of 4).
+    __device__ static uint32_t trfrag(int r, int n) {
+        return r * ROWB + 16 * ((n >> 3) ^ dswz(r)) + 8 * ((n >> 2) & 1);
+    }
+    // DMA lane mapping: lane l of block b carries row b RPB + l / CH, stored at position
+    // l % CH of that row, so it loads chunk (l % CH) ^ swz(row) of the row.
+    __device__ static uint32_t dma_voff(int b, int lane, bool dual) {
+        const int row = b * RPB + lane / CH, pos = lane % CH;
+        return row * ROWB + 16 * (pos ^ (dual ? dswz(row) : kswz(row)));
     }
 };
 
-// MFMA operand of 8 interleaved rows (4h + 16kk + {0..3} and +8) from a transposed tile.
-__device__ inline bf16x8 trn_frag(const uint16_t* trn_row, int kk, int h) {
-    const uint16_t* p = trn_row + 16 * kk + 4 * h;
-    u32x2 a = *reinterpret_cast<const u32x2*>(p);
-    u32x2 b = *reinterpret_cast<const u32x2*>(p + 8);
-    return __builtin_bit_cast(bf16x8, u32x4{a[0], a[1], b[0], b[1]});
+// Transposed MFMA A operand: 8 rows (r0 + 4h + i/4 and + 8, through the two offsets)
+// by 32 columns, see the ds_read_tr lane rule.
+__device__ inline bf16x8 tr_operand(const uint8_t* p, uint32_t o0, uint32_t o1) {
+    const s16x4 a0 = ds_read_tr(reinterpret_cast<const uint16_t*>(p + o0));
+    const s16x4 a1 = ds_read_tr(reinterpret_cast<const uint16_t*>(p + o1));
+    return __builtin_bit_cast(bf16x8, s16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]});
+}
+
+template <int PER>
+__device__ inline void wait_dma(int ahead) {     // at most `ahead` stages of PER loads in flight
+    if (ahead >= 2) wait_vmcnt<2 * PER>();
+    else if (ahead == 1) wait_vmcnt<PER>();
+    else wait_vmcnt<0>();
 }
 
 // ---------------------------------------------------------------------------------
-// 2. dK, dV (bf16).  Work-group: 128 keys (wave w owns keys k0 + 32w .. +31); loops
-//    over 32-query stages.  S[i][j] and dP[i][j] come out with lane = key j and
-//    register r = query 8(r/4) + 4h + r%4.
+// 2. dK, dV (bf16).  Work-group: 4 waves x 32 keys (one wave per SIMD: K, V fragments
+//    and both accumulators stay in registers); 32-query stages of Q, dO and the stage's
+//    LSE*log2(e) and Dvec through a 4-deep LDS ring.  S = Q K^T and dP = dO V^T come out
+//    with lane = key j and register r = query 8 (r / 4) + 4 h + r % 4; P and dS feed
+//    dV^T += dO^T P and dK^T += Q^T dS straight from those registers.
 // ---------------------------------------------------------------------------------
+constexpr int KV_WAVES = 4;
+constexpr int KV_NT = 64 * KV_WAVES;
+constexpr int KV_KEYS = 32 * KV_WAVES;
+constexpr int KV_BQ = 32;
+constexpr int KV_NSTAGE = 4;
+
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(NT)
+__global__ void __launch_bounds__(KV_NT)
 bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __restrict__ Q,
                      const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-                     const uint16_t* __restrict__ dO, const float* __restrict__ LSE,
+                     const uint16_t* __restrict__ dO, const float* __restrict__ L2,
                      const float* __restrict__ Dv, float* __restrict__ dK,
                      float* __restrict__ dV, int accumulate) {
-    using Tl = Tile16<D>;
+    using T = BwTile<D, KV_BQ>;
     constexpr int ND = D / 32, NTK = D / 16;
-    constexpr int STAGE = 2 * Tl::NAT + 2 * Tl::TRN;     // bf16 elements per stage
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    __shared__ __attribute__((aligned(16))) float s_lse[2][RB], s_dv[2][RB];
+    constexpr int VEC = 2 * T::TILE;                 // 1 KB of LSE*log2(e), then 1 KB of Dvec
+    constexpr int STAGE = VEC + 2048;
+    constexpr int PER = 2 * T::NBLK / KV_WAVES;      // tile blocks per wave per stage
+    constexpr int PERV = PER + 1;                    // + one vector block
+    static_assert(PER >= 1 && PER * KV_WAVES == 2 * T::NBLK, "stage must split over the waves");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
     const int bh = blockIdx.x % BH;
     const int kt = blockIdx.x / BH;      // causal: small kt = longest query range, first
-    const int kbase = kt * 128;
+    const int kbase = kt * KV_KEYS;
     const size_t base = (size_t)bh * S * D;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, h = lane >> 5;
     const int k0 = kbase + 32 * wave;
     const int j = k0 + l32;
+    const uint32_t ring_lds = lds_addr(ring);
+
+    const int qstart = CAUSAL ? kbase : 0;
+    const int nst = qstart < S ? (S - qstart + KV_BQ - 1) / KV_BQ : 0;
+    // first stage with a query at or after this wave's first key; none if no valid key
+    const int wfirst = k0 >= S ? nst : CAUSAL ? (k0 - qstart) / KV_BQ : 0;
+
+    uint32_t dlds[PER], dvoff[PER];
+    bool dq_[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int gb = wave + KV_WAVES * q;
+        const int tile = gb / T::NBLK, b = gb % T::NBLK;
+        dq_[q] = tile == 0;
+        dlds[q] = tile * T::TILE + b * 1024;
+        dvoff[q] = T::dma_voff(b, lane, true);
+    }
+    auto issue = [&](int st) {
+        const int i0 = qstart + st * KV_BQ;
+        const uint32_t sb = ring_lds + (st % KV_NSTAGE) * STAGE;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const u32x4 rs = make_rsrc((dq_[q] ? Q : dO) + base + (size_t)i0 * D,
+                                       (uint32_t)(S - i0) * T::ROWB);
+            lds_dma16_buf(dvoff[q], rs, __builtin_amdgcn_readfirstlane(sb + dlds[q]));
+        }
+        // the stage's LSE*log2(e) (waves 0, 2) or Dvec (waves 1, 3): 256 floats from i0
+        const bool lse = (wave & 1) == 0;
+        const u32x4 rv = make_rsrc((lse ? L2 : Dv) + (size_t)bh * S + i0, (uint32_t)(S - i0) * 4);
+        lds_dma16_buf(16 * lane, rv, __builtin_amdgcn_readfirstlane(sb + VEC + (lse ? 0 : 1024)));
+    };
 
     // K and V rows of this lane's key as B operands: K[j][16t + 8h .. +7].
     bf16x8 kf[NTK], vf[NTK];
+    {
+        const int jc = min(j, S - 1);
 #pragma unroll
-    for (int t = 0; t < NTK; ++t) {
-        const size_t off = base + (size_t)j * D + 16 * t + 8 * h;
-        kf[t] = __builtin_bit_cast(bf16x8, j < S ? *reinterpret_cast<const u32x4*>(K + off)
-                                                 : u32x4{0u, 0u, 0u, 0u});
-        vf[t] = __builtin_bit_cast(bf16x8, j < S ? *reinterpret_cast<const u32x4*>(V + off)
-                                                 : u32x4{0u, 0u, 0u, 0u});
+        for (int t = 0; t < NTK; ++t) {
+            const size_t off = base + (size_t)jc * D + 16 * t + 8 * h;
+            kf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(K + off));
+            vf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(V + off));
+        }
+#pragma unroll
+        for (int t = 0; t < NTK; ++t)
+            asm volatile("" ::"v"(__builtin_bit_cast(u32x4, kf[t])), "v"(__builtin_bit_cast(u32x4, vf[t])));
+    }
+    uint32_t rofs[NTK], tofs0[ND], tofs1[ND];
+#pragma unroll
+    for (int t = 0; t < NTK; ++t) rofs[t] = T::rowfrag(l32, 2 * t + h, true);
+    {
+        const int ii = lane & 15, g = (lane >> 4) & 1, vr = 4 * h + (ii >> 2);
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+            const int n = 32 * dt + 16 * g + 4 * (ii & 3);
+            tofs0[dt] = T::trfrag(vr, n);
+            tofs1[dt] = T::trfrag(vr + 8, n);
+        }
     }
     f32x16 dkacc[ND], dvacc[ND];
 #pragma unroll
@@ -145,95 +210,85 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
 #pragma unroll
         for (int r = 0; r < 16; ++r) dkacc[d][r] = dvacc[d][r] = 0.f;
 
-    const int qstart = CAUSAL ? kbase : 0;
-    const int nst = qstart < S ? (S - qstart + RB - 1) / RB : 0;
-    Tl tq, tg;
-    float pre_lse = 0.f, pre_dv = 0.f;
-    auto fetch = [&](int st) {
-        const int r0 = qstart + st * RB;
-        if (tid < Tl::NB) tq.fetch(Q + base, r0, S, tid);
-        else if (tid < 2 * Tl::NB) tg.fetch(dO + base, r0, S, tid - Tl::NB);
-        if (tid < RB) {
-            const int row = r0 + tid;
-            pre_lse = row < S ? LSE[(size_t)bh * S + row] * 1.4426950408889634f : 0.f;
-            pre_dv = row < S ? Dv[(size_t)bh * S + row] : 0.f;
-        }
-    };
-    auto store = [&](int buf) {
-        uint16_t* sb = smem + buf * STAGE;
-        if (tid < Tl::NB) tq.store(sb, sb + 2 * Tl::NAT, tid);
-        else if (tid < 2 * Tl::NB)
-            tg.store(sb + Tl::NAT, sb + 2 * Tl::NAT + Tl::TRN, tid - Tl::NB);
-        if (tid < RB) {
-            s_lse[buf][tid] = pre_lse;
-            s_dv[buf][tid] = pre_dv;
-        }
-    };
-    if (nst > 0) {
-        fetch(0);
-        store(0);
-        __syncthreads();
-    }
+#pragma unroll
+    for (int st = 0; st < KV_NSTAGE - 1; ++st)
+        if (st < nst) issue(st);
     for (int st = 0; st < nst; ++st) {
-        const int cur = st & 1;
-        const bool more = st + 1 < nst;
-        if (more) fetch(st + 1);
-        const int i0 = qstart + st * RB;
-        // causal: queries i0..i0+31 all precede this wave's first key -> nothing to add
-        if (!(CAUSAL && i0 + RB - 1 < k0)) {
-            const uint16_t* qs = smem + cur * STAGE;
-            const uint16_t* gs = qs + Tl::NAT;
-            const uint16_t* qt = qs + 2 * Tl::NAT;
-            const uint16_t* gt = qt + Tl::TRN;
-            f32x16 s, dp;
+        wait_dma<PERV>(min(nst - 1 - st, KV_NSTAGE - 2));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        if (st + KV_NSTAGE - 1 < nst) issue(st + KV_NSTAGE - 1);
+        if (st < wfirst) continue;
+
+        const uint8_t* qt = ring + (st % KV_NSTAGE) * STAGE;
+        const uint8_t* gt = qt + T::TILE;
+        const float* vec = reinterpret_cast<const float*>(qt + VEC);
+        const int i0 = qstart + st * KV_BQ;
+        f32x16 sc, dp;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+        for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
 #pragma unroll
-            for (int t = 0; t < NTK; ++t) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&qs[l32 * Tl::NS + 16 * t + 8 * h]);
-                const bf16x8 g = *reinterpret_cast<const bf16x8*>(&gs[l32 * Tl::NS + 16 * t + 8 * h]);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kf[t], s, 0, 0, 0);
-                dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(g, vf[t], dp, 0, 0, 0);
-            }
-            uint32_t pk[8], dk[8];
+        for (int t = 0; t < NTK; ++t) {
+            const bf16x8 a = *reinterpret_cast<const bf16x8*>(qt + rofs[t]);
+            const bf16x8 g = *reinterpret_cast<const bf16x8*>(gt + rofs[t]);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kf[t], sc, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(g, vf[t], dp, 0, 0, 0);
+        }
+        // Phase fences keep the scheduler from hoisting every fragment read of the stage
+        // (one wave per SIMD: registers, not latency, are the limit here).
+        __builtin_amdgcn_sched_barrier(0);
+        // P; queries past S and (causal) keys after the query are dropped.  Register r
+        // holds query i0 + 4 h + o(r), o(r) = 8 (r / 4) + r % 4.
+        float p[16];
 #pragma unroll
-            for (int r = 0; r < 16; r += 4) {
-                const int il = 8 * (r >> 2) + 4 * h;             // local query of reg r
-                const f32x4 lse4 = *reinterpret_cast<const f32x4*>(&s_lse[cur][il]);
-                const f32x4 dv4 = *reinterpret_cast<const f32x4*>(&s_dv[cur][il]);
-                float p[4], ds[4];
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(vec + 8 * q + 4 * h);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int i = i0 + il + e;
-                    const bool ok = i < S && j < S && (!CAUSAL || j <= i);
-                    p[e] = ok ? fast_exp2(s[r + e] * sl2 - lse4[e]) : 0.f;
-                    ds[e] = p[e] * (dp[r + e] - dv4[e]);
-                }
-                pk[r / 2] = cvt_pk_bf16(p[0], p[1]);
-                pk[r / 2 + 1] = cvt_pk_bf16(p[2], p[3]);
-                dk[r / 2] = cvt_pk_bf16(ds[0], ds[1]);
-                dk[r / 2 + 1] = cvt_pk_bf16(ds[2], ds[3]);
-            }
+            for (int e = 0; e < 4; ++e) p[4 * q + e] = fast_exp2(__builtin_fmaf(sc[4 * q + e], sl2, -l4[e]));
+        }
+        if (i0 + KV_BQ > S || (CAUSAL && i0 < k0 + 31)) {   // wave-uniform: tail or diagonal
+            const int lo = CAUSAL ? j - i0 - 4 * h : -KV_BQ;   // keep o >= lo (key <= query)
+            const int hi = S - i0 - 4 * h;                      // keep o < hi (query < S)
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const bf16x8 pf = __builtin_bit_cast(
-                    bf16x8, u32x4{pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]});
-                const bf16x8 sf = __builtin_bit_cast(
-                    bf16x8, u32x4{dk[4 * kk], dk[4 * kk + 1], dk[4 * kk + 2], dk[4 * kk + 3]});
-#pragma unroll
-                for (int d = 0; d < ND; ++d) {
-                    dvacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        trn_frag(&gt[(32 * d + l32) * Tl::TS], kk, h), pf, dvacc[d], 0, 0, 0);
-                    dkacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        trn_frag(&qt[(32 * d + l32) * Tl::TS], kk, h), sf, dkacc[d], 0, 0, 0);
-                }
+            for (int r = 0; r < 16; ++r) {
+                const int o = 8 * (r >> 2) + (r & 3);
+                if (o < lo || o >= hi) p[r] = 0.f;
             }
         }
-        if (more) store(cur ^ 1);
-        __syncthreads();
+        // dS = P o (dP - Dvec), both packed to bf16 pairs
+        uint32_t pk[8], pd[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(vec + 256 + 8 * q + 4 * h);
+            float ds[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ds[e] = p[4 * q + e] * (dp[4 * q + e] - d4[e]);
+            pk[2 * q] = cvt_pk_bf16(p[4 * q], p[4 * q + 1]);
+            pk[2 * q + 1] = cvt_pk_bf16(p[4 * q + 2], p[4 * q + 3]);
+            pd[2 * q] = cvt_pk_bf16(ds[0], ds[1]);
+            pd[2 * q + 1] = cvt_pk_bf16(ds[2], ds[3]);
+        }
+        // k-step kk pairs queries 16 kk + 4 h + (0..3) and + 8: score registers 8 kk .. + 7
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            __builtin_amdgcn_sched_barrier(0);
+            const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]});
+            const bf16x8 sf = __builtin_bit_cast(bf16x8, u32x4{pd[4 * kk], pd[4 * kk + 1], pd[4 * kk + 2], pd[4 * kk + 3]});
+            const uint8_t* gk = gt + 16 * kk * T::ROWB;
+            const uint8_t* qk = qt + 16 * kk * T::ROWB;
+#pragma unroll
+            for (int d = 0; d < ND; ++d) {
+                dvacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_operand(gk, tofs0[d], tofs1[d]), pf, dvacc[d], 0, 0, 0);
+                dkacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_operand(qk, tofs0[d], tofs1[d]), sf, dkacc[d], 0, 0, 0);
+            }
+        }
+        // The accumulators are only touched by the matrix cores: keep them in AGPRs across
+        // iterations (otherwise the allocator copies them between register files per stage).
+#pragma unroll
+        for (int d = 0; d < ND; ++d) asm volatile("" : "+a"(dkacc[d]), "+a"(dvacc[d]));
     }
     if (j >= S) return;
-    // lane (j, h) holds dK^T[d][j], dV^T[d][j] for d = 32*db + 8q + 4h + (0..3)
+    // lane (j, h) holds dK^T[d][j], dV^T[d][j] for d = 32 dt + 8 q + 4 h + (0..3)
     float* dkr = dK + base + (size_t)j * D;
     float* dvr = dV + base + (size_t)j * D;
 #pragma unroll
@@ -243,8 +298,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
             const int col = 32 * d + 8 * q + 4 * h;
             f32x4 a = {dkacc[d][4 * q] * scale, dkacc[d][4 * q + 1] * scale,
                        dkacc[d][4 * q + 2] * scale, dkacc[d][4 * q + 3] * scale};
-            f32x4 b = {dvacc[d][4 * q], dvacc[d][4 * q + 1], dvacc[d][4 * q + 2],
-                       dvacc[d][4 * q + 3]};
+            f32x4 b = {dvacc[d][4 * q], dvacc[d][4 * q + 1], dvacc[d][4 * q + 2], dvacc[d][4 * q + 3]};
             if (accumulate) {
                 a += *reinterpret_cast<const f32x4*>(dkr + col);
                 b += *reinterpret_cast<const f32x4*>(dvr + col);
@@ -255,109 +309,161 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
 }
 
 // ---------------------------------------------------------------------------------
-// 3. dQ (bf16).  Work-group: 128 queries (wave w owns queries q0 + 32w .. +31); loops
-//    over 32-key stages.  S^T and dP^T come out with lane = query.
+// 3. dQ (bf16).  Work-group: 8 waves x 32 queries (two waves per SIMD); 64-key stages of
+//    K and V through a 4-deep LDS ring.  S^T = K Q^T and dP^T = V dO^T come out with
+//    lane = query; dS^T feeds dQ^T += K^T dS^T straight from the registers, K^T through
+//    transpose reads of the same K tile.
 // ---------------------------------------------------------------------------------
+constexpr int DQ_WAVES = 8;
+constexpr int DQ_NT = 64 * DQ_WAVES;
+constexpr int DQ_ROWS = 32 * DQ_WAVES;
+constexpr int DQ_BN = 64;
+constexpr int DQ_NSTAGE = 4;
+
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(NT)
+__global__ void __launch_bounds__(DQ_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __restrict__ Q,
                    const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-                   const uint16_t* __restrict__ dO, const float* __restrict__ LSE,
+                   const uint16_t* __restrict__ dO, const float* __restrict__ L2,
                    const float* __restrict__ Dv, float* __restrict__ dQ, int accumulate) {
-    using Tl = Tile16<D>;
+    using T = BwTile<D, DQ_BN>;
     constexpr int ND = D / 32, NTK = D / 16;
-    constexpr int STAGE = 2 * Tl::NAT + Tl::TRN;     // K natural, V natural, K^T
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    constexpr int STAGE = 2 * T::TILE;               // K tile, then V tile
+    constexpr int PER = 2 * T::NBLK / DQ_WAVES;
+    static_assert(PER >= 1 && PER * DQ_WAVES == 2 * T::NBLK, "stage must split over the waves");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
-    const int n_qt = (S + 127) / 128;
+    const int n_qt = (S + DQ_ROWS - 1) / DQ_ROWS;
     const int bh = blockIdx.x % BH;
     const int rr = blockIdx.x / BH;
     const int qt = CAUSAL ? n_qt - 1 - rr : rr;
-    const int qbase = qt * 128;
+    const int q0 = qt * DQ_ROWS;
     const size_t base = (size_t)bh * S * D;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, h = lane >> 5;
-    const int r0 = qbase + 32 * wave;
+    const int r0 = q0 + 32 * wave;
     const int i = r0 + l32;
+    const uint32_t ring_lds = lds_addr(ring);
+    const int kend = CAUSAL ? min(S, q0 + DQ_ROWS) : S;
+    const int nst = (kend + DQ_BN - 1) / DQ_BN;
+    const int wlast = r0 >= S ? 0 : CAUSAL ? min(S - 1, r0 + 31) / DQ_BN + 1 : nst;
 
+    uint32_t dlds[PER], dvoff[PER];
+    bool dk_[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int gb = wave + DQ_WAVES * q;
+        const int tile = gb / T::NBLK, b = gb % T::NBLK;
+        dk_[q] = tile == 0;
+        dlds[q] = tile * T::TILE + b * 1024;
+        dvoff[q] = T::dma_voff(b, lane, tile == 0);
+    }
+    auto issue = [&](int st) {
+        const int j0 = st * DQ_BN;
+        const uint32_t sb = ring_lds + (st % DQ_NSTAGE) * STAGE;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const u32x4 rs = make_rsrc((dk_[q] ? K : V) + base + (size_t)j0 * D,
+                                       (uint32_t)(S - j0) * T::ROWB);
+            lds_dma16_buf(dvoff[q], rs, __builtin_amdgcn_readfirstlane(sb + dlds[q]));
+        }
+    };
+
+    // Q and dO rows of this lane's query as B operands: Q[i][16t + 8h .. +7].
     bf16x8 qf[NTK], gf[NTK];
+    float lse2, dvi;
+    {
+        const int ic = min(i, S - 1);
+#pragma unroll
+        for (int t = 0; t < NTK; ++t) {
+            const size_t off = base + (size_t)ic * D + 16 * t + 8 * h;
+            qf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(Q + off));
+            gf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(dO + off));
+        }
+        lse2 = L2[(size_t)bh * S + ic];
+        dvi = Dv[(size_t)bh * S + ic];
+#pragma unroll
+        for (int t = 0; t < NTK; ++t)
+            asm volatile("" ::"v"(__builtin_bit_cast(u32x4, qf[t])), "v"(__builtin_bit_cast(u32x4, gf[t])));
+        asm volatile("" ::"v"(lse2), "v"(dvi));
+    }
+    uint32_t kofs[NTK], vofs[NTK], tofs0[ND], tofs1[ND];
 #pragma unroll
     for (int t = 0; t < NTK; ++t) {
-        const size_t off = base + (size_t)i * D + 16 * t + 8 * h;
-        qf[t] = __builtin_bit_cast(bf16x8, i < S ? *reinterpret_cast<const u32x4*>(Q + off)
-                                                 : u32x4{0u, 0u, 0u, 0u});
-        gf[t] = __builtin_bit_cast(bf16x8, i < S ? *reinterpret_cast<const u32x4*>(dO + off)
-                                                 : u32x4{0u, 0u, 0u, 0u});
+        kofs[t] = T::rowfrag(l32, 2 * t + h, true);
+        vofs[t] = T::rowfrag(l32, 2 * t + h, false);
     }
-    const float lse2 = i < S ? LSE[(size_t)bh * S + i] * 1.4426950408889634f : 0.f;
-    const float dvi = i < S ? Dv[(size_t)bh * S + i] : 0.f;
+    {
+        const int ii = lane & 15, g = (lane >> 4) & 1, vr = 4 * h + (ii >> 2);
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+            const int n = 32 * dt + 16 * g + 4 * (ii & 3);
+            tofs0[dt] = T::trfrag(vr, n);
+            tofs1[dt] = T::trfrag(vr + 8, n);
+        }
+    }
     f32x16 dqacc[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dqacc[d][r] = 0.f;
+    const int lim = CAUSAL ? min(i, S - 1) : S - 1;   // last key this query sees
 
-    const int kend = CAUSAL ? min(S, qbase + 128) : S;
-    const int nst = (kend + RB - 1) / RB;
-    Tl tk, tv;
-    auto fetch = [&](int st) {
-        if (tid < Tl::NB) tk.fetch(K + base, st * RB, S, tid);
-        else if (tid < 2 * Tl::NB) tv.fetch(V + base, st * RB, S, tid - Tl::NB);
-    };
-    auto store = [&](int buf) {
-        uint16_t* sb = smem + buf * STAGE;
-        if (tid < Tl::NB) tk.store(sb, sb + 2 * Tl::NAT, tid);
-        else if (tid < 2 * Tl::NB) tv.store(sb + Tl::NAT, nullptr, tid - Tl::NB);
-    };
-    if (nst > 0) {
-        fetch(0);
-        store(0);
-        __syncthreads();
-    }
+#pragma unroll
+    for (int st = 0; st < DQ_NSTAGE - 1; ++st)
+        if (st < nst) issue(st);
     for (int st = 0; st < nst; ++st) {
-        const int cur = st & 1;
-        const bool more = st + 1 < nst;
-        if (more) fetch(st + 1);
-        const int j0 = st * RB;
-        if (!(CAUSAL && j0 > r0 + 31)) {
-            const uint16_t* ks = smem + cur * STAGE;
-            const uint16_t* vs = ks + Tl::NAT;
-            const uint16_t* kt = ks + 2 * Tl::NAT;
-            f32x16 s, dp;
+        wait_dma<PER>(min(nst - 1 - st, DQ_NSTAGE - 2));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        if (st + DQ_NSTAGE - 1 < nst) issue(st + DQ_NSTAGE - 1);
+        if (st >= wlast) continue;
+
+        const uint8_t* kt = ring + (st % DQ_NSTAGE) * STAGE;
+        const uint8_t* vt = kt + T::TILE;
+        const int j0 = st * DQ_BN;
+        f32x16 sc[2], dp[2];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int t = 0; t < NTK; ++t) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&ks[l32 * Tl::NS + 16 * t + 8 * h]);
-                const bf16x8 v = *reinterpret_cast<const bf16x8*>(&vs[l32 * Tl::NS + 16 * t + 8 * h]);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[t], s, 0, 0, 0);
-                dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, gf[t], dp, 0, 0, 0);
+            for (int r = 0; r < 16; ++r) sc[kb][r] = dp[kb][r] = 0.f;
+#pragma unroll
+        for (int t = 0; t < NTK; ++t)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + kofs[t] + 32 * kb * T::ROWB);
+                const bf16x8 v = *reinterpret_cast<const bf16x8*>(vt + vofs[t] + 32 * kb * T::ROWB);
+                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[t], sc[kb], 0, 0, 0);
+                dp[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, gf[t], dp[kb], 0, 0, 0);
             }
-            uint32_t dk[8];
+        // dS^T[key][i]; keys after the query (causal) or past S are dropped
+        const bool msk = j0 + DQ_BN - 1 > (CAUSAL ? r0 : S - 1);   // wave-uniform
+        const int rel = lim - j0 - 4 * h;
+        uint32_t pd[16];
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                float ds[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int jj = j0 + 8 * ((r + e) >> 2) + 4 * h + ((r + e) & 3);
-                    const bool ok = i < S && jj < S && (!CAUSAL || jj <= i);
-                    const float p = ok ? fast_exp2(s[r + e] * sl2 - lse2) : 0.f;
-                    ds[e] = p * (dp[r + e] - dvi);
-                }
-                dk[r / 2] = cvt_pk_bf16(ds[0], ds[1]);
+        for (int q = 0; q < 16; ++q) {
+            const int kb = q >> 3, r = 2 * (q & 7);
+            float p0 = fast_exp2(__builtin_fmaf(sc[kb][r], sl2, -lse2));
+            float p1 = fast_exp2(__builtin_fmaf(sc[kb][r + 1], sl2, -lse2));
+            if (msk) {
+                const int o = 32 * kb + 8 * (r >> 2) + (r & 3);
+                if (o > rel) p0 = 0.f;
+                if (o + 1 > rel) p1 = 0.f;
             }
+            pd[q] = cvt_pk_bf16(p0 * (dp[kb][r] - dvi), p1 * (dp[kb][r + 1] - dvi));
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-                const bf16x8 sf = __builtin_bit_cast(
-                    bf16x8, u32x4{dk[4 * kk], dk[4 * kk + 1], dk[4 * kk + 2], dk[4 * kk + 3]});
+                const int q0p = 8 * kb + 4 * kk;
+                const bf16x8 sf = __builtin_bit_cast(bf16x8, u32x4{pd[q0p], pd[q0p + 1], pd[q0p + 2], pd[q0p + 3]});
+                const uint8_t* kk_ = kt + (32 * kb + 16 * kk) * T::ROWB;
 #pragma unroll
                 for (int d = 0; d < ND; ++d)
-                    dqacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        trn_frag(&kt[(32 * d + l32) * Tl::TS], kk, h), sf, dqacc[d], 0, 0, 0);
+                    dqacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_operand(kk_, tofs0[d], tofs1[d]), sf, dqacc[d], 0, 0, 0);
             }
-        }
-        if (more) store(cur ^ 1);
-        __syncthreads();
     }
     if (i >= S) return;
     float* dqr = dQ + base + (size_t)i * D;
@@ -652,29 +758,29 @@ int set_lds(Kern kern, size_t bytes, bool& done) {
 
 template <int D, bool CAUSAL>
 int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const void* V,
-             const void* dO, const float* LSE, const float* Dv, float* dQ, float* dK, float* dV,
+             const void* dO, const float* L2, const float* Dv, float* dQ, float* dK, float* dV,
              int acc) {
-    using Tl = Tile16<D>;
     const float sl2 = scale * 1.4426950408889634f;
-    const int tiles = (S + 127) / 128;
     {
         auto kern = bwd_dkdv_bf16_kernel<D, CAUSAL>;
-        const size_t lds = 2 * (2 * Tl::NAT + 2 * Tl::TRN) * sizeof(uint16_t);
+        const size_t lds = (size_t)KV_NSTAGE * (2 * BwTile<D, KV_BQ>::TILE + 2048);
         static bool done = false;
         DH_TRY(set_lds(kern, lds, done));
-        kern<<<BH * tiles, NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
-                                                (const uint16_t*)K, (const uint16_t*)V,
-                                                (const uint16_t*)dO, LSE, Dv, dK, dV, acc);
+        const int grid = BH * ((S + KV_KEYS - 1) / KV_KEYS);
+        kern<<<grid, KV_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
+                                             (const uint16_t*)K, (const uint16_t*)V,
+                                             (const uint16_t*)dO, L2, Dv, dK, dV, acc);
         DH_TRY(check_launch("dh_flash_bwd(dK,dV bf16)"));
     }
     {
         auto kern = bwd_dq_bf16_kernel<D, CAUSAL>;
-        const size_t lds = 2 * (2 * Tl::NAT + Tl::TRN) * sizeof(uint16_t);
+        const size_t lds = (size_t)DQ_NSTAGE * 2 * BwTile<D, DQ_BN>::TILE;
         static bool done = false;
         DH_TRY(set_lds(kern, lds, done));
-        kern<<<BH * tiles, NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
-                                                (const uint16_t*)K, (const uint16_t*)V,
-                                                (const uint16_t*)dO, LSE, Dv, dQ, acc);
+        const int grid = BH * ((S + DQ_ROWS - 1) / DQ_ROWS);
+        kern<<<grid, DQ_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
+                                             (const uint16_t*)K, (const uint16_t*)V,
+                                             (const uint16_t*)dO, L2, Dv, dQ, acc);
         DH_TRY(check_launch("dh_flash_bwd(dQ bf16)"));
     }
     return DH_OK;
@@ -710,8 +816,9 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
 }
 
 template <typename T, int D>
-int run_dvec(int rows, const void* O, const void* dO, float* Dv) {
-    dvec_kernel<T, D><<<(rows + 15) / 16, NT, 0, stream()>>>(rows, (const T*)O, (const T*)dO, Dv);
+int run_dvec(int rows, const void* O, const void* dO, float* Dv, const float* LSE, float* L2) {
+    dvec_kernel<T, D><<<(rows + 15) / 16, NT, 0, stream()>>>(rows, (const T*)O, (const T*)dO, Dv,
+                                                             LSE, L2);
     return check_launch("dh_flash_bwd(Dvec)");
 }
 
@@ -721,11 +828,12 @@ int dispatch(int dtype, int causal, int BH, int S, float scale, const void* Q, c
              float* dQ, float* dK, float* dV, int acc) {
     const int rows = BH * S;
     if (dtype == DH_BF16) {
-        DH_TRY((run_dvec<uint16_t, D>(rows, O, dO, Dv)));
-        return causal ? run_bf16<D, true>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc)
-                      : run_bf16<D, false>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc);
+        float* L2 = Dv + rows;                       // second half of the scratch
+        DH_TRY((run_dvec<uint16_t, D>(rows, O, dO, Dv, LSE, L2)));
+        return causal ? run_bf16<D, true>(BH, S, scale, Q, K, V, dO, L2, Dv, dQ, dK, dV, acc)
+                      : run_bf16<D, false>(BH, S, scale, Q, K, V, dO, L2, Dv, dQ, dK, dV, acc);
     }
-    DH_TRY((run_dvec<float, D>(rows, O, dO, Dv)));
+    DH_TRY((run_dvec<float, D>(rows, O, dO, Dv, LSE, nullptr)));
     return causal ? run_f32<D, true>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc)
                   : run_f32<D, false>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc);
 }
@@ -750,9 +858,10 @@ extern "C" int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int ca
         return set_error(DH_ERR_UNSUPPORTED, "dh_flash_bwd: dtype %d", dtype);
     for (const void* p : {Q, K, V, O, dO, (const void*)dQ, (const void*)dK, (const void*)dV})
         if ((uintptr_t)p % 16) return set_error(DH_ERR_INVALID, "dh_flash_bwd: 16-byte alignment");
-    // Dvec scratch (BH*S floats) from the pool; returned to it once the work is queued
-    // (later users of the buffer are ordered after these kernels on the same stream).
-    float* Dv = (float*)dh_malloc((size_t)BH * S * sizeof(float));
+    // Scratch from the pool: Dvec (BH*S floats) and, for bf16, LSE*log2(e) (BH*S floats);
+    // returned to the pool once the work is queued (later users of the buffer are ordered
+    // after these kernels on the same stream).
+    float* Dv = (float*)dh_malloc((size_t)BH * S * sizeof(float) * (dtype == DH_BF16 ? 2 : 1));
     if (!Dv) return DH_ERR_OOM;
     int st;
     if (D == 128) st = dispatch<128>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV, accumulate);
