@@ -53,7 +53,11 @@ def _run(cmd, verbose):
 # Per-source additions.  dh_flash_fwd: the softmax takes row maxima of matrix-core
 # results; with NaNs honoured, IEEE-mode max first quiets each operand (one extra VALU
 # op per score).  The reference runtime itself is built with -ffast-math.
-SRC_FLAGS = {"dh_flash_fwd.hip": ["-fno-honor-nans"]}
+# dh_flash_bwd: matrix-core results in arch VGPRs.  The kernels fit there (<= 236), and
+# the accumulator-register form made the allocator shuttle the dK/dV accumulators
+# between register files every stage.
+SRC_FLAGS = {"dh_flash_fwd.hip": ["-fno-honor-nans"],
+             "dh_flash_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
 
 
 def _compile(src, verbose):

@@ -109,8 +109,8 @@ __device__ inline void wait_dma(int ahead) {     // at most `ahead` stages of PE
 }
 
 // ---------------------------------------------------------------------------------
-// 2. dK, dV (bf16).  Work-group: 4 waves x 32 keys (one wave per SIMD: K, V fragments
-//    and both accumulators stay in registers); 32-query stages of Q, dO and the stage's
+// 2. dK, dV (bf16).  Work-group: 4 waves x 32 keys (one wave per SIMD: both accumulators
+//    stay in registers, K and V of the 128 keys in LDS); 32-query stages of Q, dO and the stage's
 //    LSE*log2(e) and Dvec through a 4-deep LDS ring.  S = Q K^T and dP = dO V^T come out
 //    with lane = key j and register r = query 8 (r / 4) + 4 h + r % 4; P and dS feed
 //    dV^T += dO^T P and dK^T += Q^T dS straight from those registers.
@@ -122,16 +122,19 @@ constexpr int KV_BQ = 32;
 constexpr int KV_NSTAGE = 4;
 
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(KV_NT)
+__global__ void __launch_bounds__(KV_NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
 bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __restrict__ Q,
                      const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                      const uint16_t* __restrict__ dO, const float* __restrict__ L2,
                      const float* __restrict__ Dv, float* __restrict__ dK,
                      float* __restrict__ dV, int accumulate) {
     using T = BwTile<D, KV_BQ>;
+    using R = BwTile<D, KV_KEYS>;                    // resident K, V of the work-group's keys
     constexpr int ND = D / 32, NTK = D / 16;
     constexpr int VEC = 2 * T::TILE;                 // 1 KB of LSE*log2(e), then 1 KB of Dvec
     constexpr int STAGE = VEC + 2048;
+    constexpr int KVRES = KV_NSTAGE * STAGE;         // K tile, then V tile, after the ring
+    constexpr int PERR = 2 * R::NBLK / KV_WAVES;     // resident blocks per wave
     constexpr int PER = 2 * T::NBLK / KV_WAVES;      // tile blocks per wave per stage
     constexpr int PERV = PER + 1;                    // + one vector block
     static_assert(PER >= 1 && PER * KV_WAVES == 2 * T::NBLK, "stage must split over the waves");
@@ -178,23 +181,25 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
         lds_dma16_buf(16 * lane, rv, __builtin_amdgcn_readfirstlane(sb + VEC + (lse ? 0 : 1024)));
     };
 
-    // K and V rows of this lane's key as B operands: K[j][16t + 8h .. +7].
-    bf16x8 kf[NTK], vf[NTK];
-    {
-        const int jc = min(j, S - 1);
+    // K and V of the work-group's keys stay in LDS for the whole kernel (loaded first, so
+    // the stage waits below also cover them); lane (j, h) reads K[j][16t + 8h .. +7] as the
+    // B operand.
 #pragma unroll
-        for (int t = 0; t < NTK; ++t) {
-            const size_t off = base + (size_t)jc * D + 16 * t + 8 * h;
-            kf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(K + off));
-            vf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(V + off));
-        }
-#pragma unroll
-        for (int t = 0; t < NTK; ++t)
-            asm volatile("" ::"v"(__builtin_bit_cast(u32x4, kf[t])), "v"(__builtin_bit_cast(u32x4, vf[t])));
+    for (int q = 0; q < PERR; ++q) {
+        const int gb = wave + KV_WAVES * q;
+        const int tile = gb / R::NBLK, b = gb % R::NBLK;
+        const u32x4 rs = make_rsrc((tile == 0 ? K : V) + base + (size_t)kbase * D,
+                                   (uint32_t)max(S - kbase, 0) * R::ROWB);
+        lds_dma16_buf(R::dma_voff(b, lane, false), rs,
+                      __builtin_amdgcn_readfirstlane(ring_lds + KVRES + tile * R::TILE + b * 1024));
     }
-    uint32_t rofs[NTK], tofs0[ND], tofs1[ND];
+    uint32_t rofs[NTK], kofs[NTK];
 #pragma unroll
-    for (int t = 0; t < NTK; ++t) rofs[t] = T::rowfrag(l32, 2 * t + h, true);
+    for (int t = 0; t < NTK; ++t) {
+        rofs[t] = T::rowfrag(l32, 2 * t + h, true);
+        kofs[t] = KVRES + R::rowfrag(32 * wave + l32, 2 * t + h, false);
+    }
+    uint32_t tofs0[ND], tofs1[ND];
     {
         const int ii = lane & 15, g = (lane >> 4) & 1, vr = 4 * h + (ii >> 2);
 #pragma unroll
@@ -213,13 +218,17 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
 #pragma unroll
     for (int st = 0; st < KV_NSTAGE - 1; ++st)
         if (st < nst) issue(st);
-    for (int st = 0; st < nst; ++st) {
+    auto sync = [&](int st) {
         wait_dma<PERV>(min(nst - 1 - st, KV_NSTAGE - 2));
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         if (st + KV_NSTAGE - 1 < nst) issue(st + KV_NSTAGE - 1);
-        if (st < wfirst) continue;
-
+    };
+    // Stages before this wave's first useful one: barriers and DMA share only.  Two loops
+    // keep the compute loop free of branches around the accumulators.
+    for (int st = 0; st < wfirst; ++st) sync(st);
+    for (int st = wfirst; st < nst; ++st) {
+        sync(st);
         const uint8_t* qt = ring + (st % KV_NSTAGE) * STAGE;
         const uint8_t* gt = qt + T::TILE;
         const float* vec = reinterpret_cast<const float*>(qt + VEC);
@@ -231,8 +240,10 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
         for (int t = 0; t < NTK; ++t) {
             const bf16x8 a = *reinterpret_cast<const bf16x8*>(qt + rofs[t]);
             const bf16x8 g = *reinterpret_cast<const bf16x8*>(gt + rofs[t]);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kf[t], sc, 0, 0, 0);
-            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(g, vf[t], dp, 0, 0, 0);
+            const bf16x8 kb = *reinterpret_cast<const bf16x8*>(ring + kofs[t]);
+            const bf16x8 vb = *reinterpret_cast<const bf16x8*>(ring + kofs[t] + R::TILE);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kb, sc, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(g, vb, dp, 0, 0, 0);
         }
         // Phase fences keep the scheduler from hoisting every fragment read of the stage
         // (one wave per SIMD: registers, not latency, are the limit here).
@@ -282,10 +293,6 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
                 dkacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_operand(qk, tofs0[d], tofs1[d]), sf, dkacc[d], 0, 0, 0);
             }
         }
-        // The accumulators are only touched by the matrix cores: keep them in AGPRs across
-        // iterations (otherwise the allocator copies them between register files per stage).
-#pragma unroll
-        for (int d = 0; d < ND; ++d) asm volatile("" : "+a"(dkacc[d]), "+a"(dvacc[d]));
     }
     if (j >= S) return;
     // lane (j, h) holds dK^T[d][j], dV^T[d][j] for d = 32 dt + 8 q + 4 h + (0..3)
@@ -763,7 +770,8 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
     const float sl2 = scale * 1.4426950408889634f;
     {
         auto kern = bwd_dkdv_bf16_kernel<D, CAUSAL>;
-        const size_t lds = (size_t)KV_NSTAGE * (2 * BwTile<D, KV_BQ>::TILE + 2048);
+        const size_t lds = (size_t)KV_NSTAGE * (2 * BwTile<D, KV_BQ>::TILE + 2048) +
+                           2 * BwTile<D, KV_KEYS>::TILE;
         static bool done = false;
         DH_TRY(set_lds(kern, lds, done));
         const int grid = BH * ((S + KV_KEYS - 1) / KV_KEYS);
