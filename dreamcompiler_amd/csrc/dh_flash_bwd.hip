@@ -109,20 +109,24 @@ __device__ inline void wait_dma(int ahead) {     // at most `ahead` stages of PE
 }
 
 // ---------------------------------------------------------------------------------
-// 2. dK, dV (bf16).  Work-group: 4 waves x 32 keys (one wave per SIMD: both accumulators
-//    stay in registers, K and V of the 128 keys in LDS); 32-query stages of Q, dO and the stage's
-//    LSE*log2(e) and Dvec through a 4-deep LDS ring.  S = Q K^T and dP = dO V^T come out
-//    with lane = key j and register r = query 8 (r / 4) + 4 h + r % 4; P and dS feed
-//    dV^T += dO^T P and dK^T += Q^T dS straight from those registers.
+// 2. dK, dV (bf16).  Work-group: 128 keys, 8 waves (two per SIMD).  Waves w and w + 4 own
+//    the same 32 keys (group w % 4) and take alternate 32-query stages (parity w / 4): each
+//    step of the loop consumes two stages, and at the end the odd-stage waves hand their
+//    partial dK, dV to their partner through LDS, which adds and stores them (a fixed
+//    order: results stay bit-identical run to run).  K and V of the 128 keys stay in LDS;
+//    Q, dO and each stage's LSE*log2(e) and Dvec stream through a 4-stage ring (two
+//    steps).  S = Q K^T and dP = dO V^T come out with lane = key j and register r = query
+//    8 (r / 4) + 4 h + r % 4; P and dS feed dV^T += dO^T P and dK^T += Q^T dS straight from
+//    those registers.
 // ---------------------------------------------------------------------------------
-constexpr int KV_WAVES = 4;
+constexpr int KV_WAVES = 8;
 constexpr int KV_NT = 64 * KV_WAVES;
-constexpr int KV_KEYS = 32 * KV_WAVES;
+constexpr int KV_KEYS = 128;
 constexpr int KV_BQ = 32;
 constexpr int KV_NSTAGE = 4;
 
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(KV_NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(KV_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __restrict__ Q,
                      const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                      const uint16_t* __restrict__ dO, const float* __restrict__ L2,
@@ -135,9 +139,10 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
     constexpr int STAGE = VEC + 2048;
     constexpr int KVRES = KV_NSTAGE * STAGE;         // K tile, then V tile, after the ring
     constexpr int PERR = 2 * R::NBLK / KV_WAVES;     // resident blocks per wave
-    constexpr int PER = 2 * T::NBLK / KV_WAVES;      // tile blocks per wave per stage
-    constexpr int PERV = PER + 1;                    // + one vector block
-    static_assert(PER >= 1 && PER * KV_WAVES == 2 * T::NBLK, "stage must split over the waves");
+    constexpr int PER = 4 * T::NBLK / KV_WAVES;      // tile blocks per wave per step
+    static_assert(PERR >= 1 && PERR * KV_WAVES == 2 * R::NBLK, "resident tiles must split");
+    static_assert(PER >= 1 && PER * KV_WAVES == 4 * T::NBLK, "a step must split over the waves");
+    static_assert(KV_WAVES * 64 * 32 * ND * 4 / 2 <= KVRES + 2 * R::TILE, "reduction fits LDS");
     extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
     const int bh = blockIdx.x % BH;
@@ -146,44 +151,58 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
     const size_t base = (size_t)bh * S * D;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave & 3, par = wave >> 2;
     const int l32 = lane & 31, h = lane >> 5;
-    const int k0 = kbase + 32 * wave;
+    const int k0 = kbase + 32 * grp;
     const int j = k0 + l32;
     const uint32_t ring_lds = lds_addr(ring);
 
     const int qstart = CAUSAL ? kbase : 0;
     const int nst = qstart < S ? (S - qstart + KV_BQ - 1) / KV_BQ : 0;
-    // first stage with a query at or after this wave's first key; none if no valid key
+    const int nsteps = (nst + 1) / 2;
+    // first stage with a query at or after this group's first key; none if no valid key
     const int wfirst = k0 >= S ? nst : CAUSAL ? (k0 - qstart) / KV_BQ : 0;
+    // steps whose stage of this wave's parity lies in [wfirst, nst)
+    const int s_end = (nst - par + 1) >> 1;
+    const int s_first = min((wfirst - par + 1) >> 1, s_end);
 
+    // DMA share per step: tile blocks w + 8 q over (stage in step, tile, block), plus one
+    // vector block (waves w and w + 4 load the same one).
     uint32_t dlds[PER], dvoff[PER];
+    int dsis[PER];
     bool dq_[PER];
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
         const int gb = wave + KV_WAVES * q;
-        const int tile = gb / T::NBLK, b = gb % T::NBLK;
+        const int sis = gb / (2 * T::NBLK), rem = gb % (2 * T::NBLK);
+        const int tile = rem / T::NBLK, b = rem % T::NBLK;
+        dsis[q] = sis;
         dq_[q] = tile == 0;
-        dlds[q] = tile * T::TILE + b * 1024;
+        dlds[q] = sis * STAGE + tile * T::TILE + b * 1024;
         dvoff[q] = T::dma_voff(b, lane, true);
     }
-    auto issue = [&](int st) {
-        const int i0 = qstart + st * KV_BQ;
-        const uint32_t sb = ring_lds + (st % KV_NSTAGE) * STAGE;
+    const int vsis = (wave & 3) >> 1;
+    const bool vlse = (wave & 1) == 0;
+    auto issue_step = [&](int sp) {
+        const uint32_t sb = ring_lds + ((2 * sp) % KV_NSTAGE) * STAGE;
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-            const u32x4 rs = make_rsrc((dq_[q] ? Q : dO) + base + (size_t)i0 * D,
-                                       (uint32_t)(S - i0) * T::ROWB);
+            const int i0 = qstart + (2 * sp + dsis[q]) * KV_BQ;
+            const u32x4 rs = make_rsrc((dq_[q] ? Q : dO) + base + (size_t)min(i0, S) * D,
+                                       (uint32_t)max(S - i0, 0) * T::ROWB);
             lds_dma16_buf(dvoff[q], rs, __builtin_amdgcn_readfirstlane(sb + dlds[q]));
         }
-        // the stage's LSE*log2(e) (waves 0, 2) or Dvec (waves 1, 3): 256 floats from i0
-        const bool lse = (wave & 1) == 0;
-        const u32x4 rv = make_rsrc((lse ? L2 : Dv) + (size_t)bh * S + i0, (uint32_t)(S - i0) * 4);
-        lds_dma16_buf(16 * lane, rv, __builtin_amdgcn_readfirstlane(sb + VEC + (lse ? 0 : 1024)));
+        // 256 floats of LSE*log2(e) or Dvec from the stage's first query
+        const int i0 = qstart + (2 * sp + vsis) * KV_BQ;
+        const u32x4 rv = make_rsrc((vlse ? L2 : Dv) + (size_t)bh * S + min(i0, S),
+                                   (uint32_t)max(S - i0, 0) * 4);
+        lds_dma16_buf(16 * lane, rv,
+                      __builtin_amdgcn_readfirstlane(sb + vsis * STAGE + VEC + (vlse ? 0 : 1024)));
     };
 
     // K and V of the work-group's keys stay in LDS for the whole kernel (loaded first, so
-    // the stage waits below also cover them); lane (j, h) reads K[j][16t + 8h .. +7] as the
-    // B operand.
+    // the first step's wait also covers them); lane (j, h) reads K[j][16t + 8h .. +7] as
+    // the B operand.
 #pragma unroll
     for (int q = 0; q < PERR; ++q) {
         const int gb = wave + KV_WAVES * q;
@@ -197,7 +216,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
 #pragma unroll
     for (int t = 0; t < NTK; ++t) {
         rofs[t] = T::rowfrag(l32, 2 * t + h, true);
-        kofs[t] = KVRES + R::rowfrag(32 * wave + l32, 2 * t + h, false);
+        kofs[t] = KVRES + R::rowfrag(32 * grp + l32, 2 * t + h, false);
     }
     uint32_t tofs0[ND], tofs1[ND];
     {
@@ -215,20 +234,14 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
 #pragma unroll
         for (int r = 0; r < 16; ++r) dkacc[d][r] = dvacc[d][r] = 0.f;
 
-#pragma unroll
-    for (int st = 0; st < KV_NSTAGE - 1; ++st)
-        if (st < nst) issue(st);
-    auto sync = [&](int st) {
-        wait_dma<PERV>(min(nst - 1 - st, KV_NSTAGE - 2));
+    if (nsteps > 0) issue_step(0);
+    auto sync = [&](int sp) {
+        wait_vmcnt<0>();                             // this step's stages (issued a step ago)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
-        if (st + KV_NSTAGE - 1 < nst) issue(st + KV_NSTAGE - 1);
+        if (sp + 1 < nsteps) issue_step(sp + 1);     // into the slots of step sp - 1
     };
-    // Stages before this wave's first useful one: barriers and DMA share only.  Two loops
-    // keep the compute loop free of branches around the accumulators.
-    for (int st = 0; st < wfirst; ++st) sync(st);
-    for (int st = wfirst; st < nst; ++st) {
-        sync(st);
+    auto compute = [&](int st) {
         const uint8_t* qt = ring + (st % KV_NSTAGE) * STAGE;
         const uint8_t* gt = qt + T::TILE;
         const float* vec = reinterpret_cast<const float*>(qt + VEC);
@@ -245,8 +258,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kb, sc, 0, 0, 0);
             dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(g, vb, dp, 0, 0, 0);
         }
-        // Phase fences keep the scheduler from hoisting every fragment read of the stage
-        // (one wave per SIMD: registers, not latency, are the limit here).
+        // Phase fences keep the scheduler from hoisting every fragment read of the stage.
         __builtin_amdgcn_sched_barrier(0);
         // P; queries past S and (causal) keys after the query are dropped.  Register r
         // holds query i0 + 4 h + o(r), o(r) = 8 (r / 4) + r % 4.
@@ -293,8 +305,38 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
                 dkacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_operand(qk, tofs0[d], tofs1[d]), sf, dkacc[d], 0, 0, 0);
             }
         }
+    };
+    // Three loops (steps before this wave's first stage, steps with a stage, the rest) keep
+    // the compute loop free of branches around the accumulators.
+    for (int sp = 0; sp < s_first; ++sp) sync(sp);
+    for (int sp = s_first; sp < s_end; ++sp) {
+        sync(sp);
+        compute(2 * sp + par);
     }
-    if (j >= S) return;
+    for (int sp = s_end; sp < nsteps; ++sp) sync(sp);
+
+    // Odd-stage partials to LDS (lane-major, conflict free), then the partner adds them.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(ring) + grp * (64 * 32 * ND);
+    if (par == 1) {
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                red[((2 * d) * 16 + r) * 64 + lane] = dkacc[d][r];
+                red[((2 * d + 1) * 16 + r) * 64 + lane] = dvacc[d][r];
+            }
+    }
+    __syncthreads();
+    if (par == 1 || j >= S) return;
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            dkacc[d][r] += red[((2 * d) * 16 + r) * 64 + lane];
+            dvacc[d][r] += red[((2 * d + 1) * 16 + r) * 64 + lane];
+        }
     // lane (j, h) holds dK^T[d][j], dV^T[d][j] for d = 32 dt + 8 q + 4 h + (0..3)
     float* dkr = dK + base + (size_t)j * D;
     float* dvr = dV + base + (size_t)j * D;
