@@ -114,7 +114,8 @@ int dh_gemm_bf16(int transA, int transB, int M, int N, int K,
  * (runtime/nn/training.inc:284-401, which replaces the OpenCL flash_attention_v1
  * kernel 310-363).  D in {32, 64, 128} (callers zero-pad other head dims: zero columns
  * of Q and K leave Q K^T unchanged and zero columns of V give zero columns of O).
- * scale is usually 1/sqrt(dk) of the unpadded head dim. */
+ * scale is usually 1/sqrt(dk) of the unpadded head dim (the reference always passes
+ * that, training.inc:292); it must be finite and > 0, else DH_ERR_INVALID. */
 int dh_flash_fwd(int dtype, int BH, int S, int D, float scale, int causal,
                  const void* d_Q, const void* d_K, const void* d_V,
                  void* d_O, float* d_LSE);

@@ -12,6 +12,7 @@ import pytest
 
 import _oracle as O
 from _gpu import bf16_bits, bits_to_f32, flash_bwd, flash_fwd, maxrel
+from dreamcompiler_amd import hip
 
 pytestmark = pytest.mark.gpu
 
@@ -107,6 +108,19 @@ def test_bf16_bwd(S, D, causal):
     refs = _bwd_ref(*(bits_to_f32(x) for x in (Q, K, V, G)), BH, S, D, causal)
     for name, g, r in zip("QKV", grads, refs):
         assert maxrel(g, r) <= 2e-2, name
+
+
+def test_fwd_rejects_non_positive_scale():
+    # The forward keeps its running max on raw scores, which needs scale > 0; the
+    # reference always passes 1/sqrt(dk) (runtime/nn/training.inc:292).
+    BH, S, D = 1, 64, 32
+    bufs = [hip.DeviceBuffer.from_numpy(x) for x in inputs(BH, S, D, 3, n=3)]
+    out = hip.DeviceBuffer.empty((BH, S * D), np.float32)
+    lse = hip.DeviceBuffer.empty((BH, S), np.float32)
+    for bad in (0.0, -0.125, float("inf"), float("nan")):
+        st = hip.load().dh_flash_fwd(hip.F32, BH, S, D, bad, 1, *(b.ptr for b in bufs), out.ptr, lse.ptr)
+        assert st == hip.DH_ERR_INVALID, bad
+        assert b"scale" in hip.load().dh_last_error()
 
 
 def test_bwd_accumulate_and_determinism():
