@@ -152,6 +152,14 @@ __device__ inline void lds_dma16_buf(uint32_t voff, u32x4 rsrc, uint32_t lds_bas
                  : "memory", "m0");
 }
 
+// As lds_dma16_buf with a wave-uniform byte offset soff added to every lane's address.
+__device__ inline void lds_dma16_buf_so(uint32_t voff, u32x4 rsrc, uint32_t soff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+
 __device__ inline uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }

@@ -219,7 +219,7 @@ int launch_vec(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* 
 // ---------------------------------------------------------------------------------
 // Fast path for tile-aligned shapes (M, N multiples of 256, K of 32, leading dims of 8,
 // 16-byte aligned operands): both operands travel global -> LDS by direct-to-LDS DMA
-// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), so no registers or
+// (buffer_load_dwordx4 ... lds: lane l's 16 bytes land at base + 16 l), so no registers or
 // LDS-write instructions are spent on staging.  LDS tiles keep the global orientation:
 //   k-contiguous operand  : [256 rows][32 k],  16-byte chunk c of row r at position
 //                           c ^ (r / 4 % 4)  -> MFMA fragment = one ds_read_b128
@@ -230,8 +230,8 @@ int launch_vec(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* 
 // e = 0..3.  Pointing lane i at [kb + i/4][nb + 4 (i % 4)] therefore hands lane j the 4
 // values [kb .. kb + 3][nb + j], the MFMA operand layout.  The LDS serves 64 banks of
 // 4 bytes (16 lanes of a b128 read, 32 lanes of a b64 read per pass); both swizzles make
-// the fragment reads conflict free under that model.  Two LDS stages (128 KB); fragments of the next
-// k-step are read while the matrix cores run the current one.
+// the fragment reads conflict free under that model.  A ring of four LDS stages (128 KB);
+// fragments of the next k-step are read while the matrix cores run the current one.
 // ---------------------------------------------------------------------------------
 
 template <bool KCONTIG, int WAVES>
@@ -240,30 +240,35 @@ struct FastOperand {
     // issues blocks PER*w .. PER*w + PER-1.  Per-lane element offsets at k0 = 0 and the
     // per-stage step.
     static constexpr int PER = 16 / WAVES;
-    uint32_t off[PER];
-    uint32_t step;
+    uint32_t off[PER];     // byte offsets from the operand base at stage 0
+    uint32_t step;         // bytes per stage
+    uint32_t bytes;        // operand extent (rows x ld x 2 < 2^32, checked by the host)
 
-    __device__ void init(int ld, int t0, int wave, int lane) {
+    __device__ void init(int ld, int rows, int t0, int wave, int lane) {
 #pragma unroll
         for (int t = 0; t < PER; ++t) {
             const int b = PER * wave + t;
             if (KCONTIG) {                     // block b = rows 16b .. 16b+15 of [t][32 k]
                 const int row = 16 * b + (lane >> 2);
                 const int c = (lane & 3) ^ ((lane >> 4) & 3);   // = p ^ ((row >> 2) & 3)
-                off[t] = (uint32_t)(t0 + row) * ld + 8 * c;
+                off[t] = 2u * ((uint32_t)(t0 + row) * ld + 8 * c);
             } else {                           // block b = k rows 2b, 2b+1 of [32 k][t]
                 const int k = 2 * b + (lane >> 5);
                 const int c = (lane & 31) ^ (4 * (k & 3));
-                off[t] = (uint32_t)k * ld + t0 + 8 * c;
+                off[t] = 2u * ((uint32_t)k * ld + t0 + 8 * c);
             }
         }
-        step = KCONTIG ? 32u : 32u * (uint32_t)ld;
+        step = KCONTIG ? 64u : 64u * (uint32_t)ld;
+        bytes = 2u * (uint32_t)rows * (uint32_t)ld;
     }
+    // Buffer-resource DMA: the per-lane offsets stay in VGPRs for the whole loop and the
+    // stage advance is a scalar offset, so an issue costs no vector instructions.
     __device__ void issue(const uint16_t* __restrict__ g, int kt, uint16_t* lds, int wave) const {
-        const uint32_t adv = (uint32_t)kt * step;
+        const uint32_t soff = __builtin_amdgcn_readfirstlane((uint32_t)kt * step);
         const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds) + 1024u * PER * wave);
+        const u32x4 rs = make_rsrc(g, bytes);
 #pragma unroll
-        for (int t = 0; t < PER; ++t) lds_dma16(g + (off[t] + adv), base + 1024u * t);
+        for (int t = 0; t < PER; ++t) lds_dma16_buf_so(off[t], rs, soff, base + 1024u * t);
     }
     // MFMA operand for tile rows/cols o .. o+31, k-step kk (16 k) of the stage.
     __device__ static bf16x8 frag(const uint16_t* lds, int o, int kk, int lane) {
@@ -351,8 +356,8 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 
     OA oa;
     OB ob;
-    oa.init(lda, m0, wave, lane);
-    ob.init(ldb, n0, wave, lane);
+    oa.init(lda, TA ? K : M, m0, wave, lane);
+    ob.init(ldb, TB ? N : K, n0, wave, lane);
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -379,38 +384,59 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     // The matrix cores run f0 across the barrier wait and f1 across the next reads.  A
     // ring slot is refilled (DMA kt+3 -> slot of kt-1) only after the barrier that follows
     // every wave's last read of it.
+    // The last stage is peeled off the loop: with it inside, the compiler's wait before
+    // the f1 block has to cover a path without the trailing reads and waits for those
+    // reads too, so they would no longer overlap the f1 MFMAs.
+    // The epilogue's kernel arguments are fetched here: a scalar load still in flight at
+    // the loop entry would make every LDS wait in the loop a full lgkmcnt(0).
+    asm volatile("" ::"s"(C), "s"(ldc), "s"(beta));
     bf16x8 f0a[FM], f0b[FN], f1a[FM], f1b[FN];
     load_frags<OA, OB, FM, FN>(stage_ptr(0), 0, wm, wn, lane, f0a, f0b);
-    for (int kt = 0; kt < nk; ++kt) {
+    for (int kt = 0; kt < nk - 1; ++kt) {
         if (kt + FAST_NSTAGE - 1 < nk) issue(kt + FAST_NSTAGE - 1);
         load_frags<OA, OB, FM, FN>(stage_ptr(kt), 1, wm, wn, lane, f1a, f1b);
         __builtin_amdgcn_sched_barrier(0);
         mfma_block<FM, FN>(f0a, f0b, acc);
         __builtin_amdgcn_sched_barrier(0);
-        if (kt + 1 < nk) {
-            const int ahead = min(nk - 1, kt + FAST_NSTAGE - 1) - (kt + 1);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            wait_dma_stages<2 * OA::PER>(ahead);
-            __syncthreads();
-            load_frags<OA, OB, FM, FN>(stage_ptr(kt + 1), 0, wm, wn, lane, f0a, f0b);
-        }
+        const int ahead = min(nk - 1, kt + FAST_NSTAGE - 1) - (kt + 1);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wait_dma_stages<2 * OA::PER>(ahead);
+        __syncthreads();
+        load_frags<OA, OB, FM, FN>(stage_ptr(kt + 1), 0, wm, wn, lane, f0a, f0b);
         __builtin_amdgcn_sched_barrier(0);
         mfma_block<FM, FN>(f1a, f1b, acc);
         __builtin_amdgcn_sched_barrier(0);
     }
+    load_frags<OA, OB, FM, FN>(stage_ptr(nk - 1), 1, wm, wn, lane, f1a, f1b);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_block<FM, FN>(f0a, f0b, acc);
+    mfma_block<FM, FN>(f1a, f1b, acc);
 
+    // Register r of block (a, b) is C[32 a + 8 (r / 4) + 4 (lane / 32) + r % 4][32 b + lane % 32]
+    // (relative to the wave's tile): each store instruction writes two 128-byte row pieces.
+    // One uniform branch on beta keeps both forms straight-line code.
+    float* cw = C + (size_t)(m0 + wm + 4 * h) * ldc + n0 + wn + l32;
+    auto at = [&](int a, int b, int r) {
+        return cw + (size_t)(32 * a + 8 * (r >> 2) + (r & 3)) * ldc + 32 * b;
+    };
+    if (beta == 0.f) {
 #pragma unroll
-    for (int a = 0; a < FM; ++a)
+        for (int a = 0; a < FM; ++a)
 #pragma unroll
-        for (int b = 0; b < FN; ++b) {
-            const int col = n0 + wn + 32 * b + l32;
+            for (int b = 0; b < FN; ++b)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
-                float* c = C + (size_t)row * ldc + col;
-                *c = beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c;
-            }
-        }
+                for (int r = 0; r < 16; ++r) *at(a, b, r) = acc[a][b][r];
+    } else {
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float* c = at(a, b, r);
+                    *c = acc[a][b][r] + beta * *c;
+                }
+    }
 }
 
 template <bool TA, bool TB>

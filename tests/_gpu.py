@@ -20,31 +20,34 @@ def bits_to_f32(b):
     return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
-def gemm(A, B, transA=False, transB=False, beta=0.0, C0=None, dtype="f32", ldpad=0):
+def gemm(A, B, transA=False, transB=False, beta=0.0, C0=None, dtype="f32", ldpad=0,
+         ldcpad=None):
     """Run dh_gemm_{f32,bf16} on host arrays given in their stored layout.
 
     A, B: fp32 arrays (stored layout), or uint16 bf16 bits for dtype="bf16".
     ldpad: extra columns of padding on every stored matrix (exercises lda > K etc.).
+    ldcpad: padding of C alone when given (overrides ldpad for C).
     """
     M = A.shape[1] if transA else A.shape[0]
     K = A.shape[0] if transA else A.shape[1]
     N = B.shape[0] if transB else B.shape[1]
     np_t = np.uint16 if dtype == "bf16" else np.float32
 
-    def padded(X, t):
+    def padded(X, t, pad):
         X = np.ascontiguousarray(X, t)
-        if not ldpad:
+        if not pad:
             return X
-        P = np.zeros((X.shape[0], X.shape[1] + ldpad), t)
+        P = np.zeros((X.shape[0], X.shape[1] + pad), t)
         P[:, :X.shape[1]] = X
         return P
 
-    Ap, Bp = padded(A, np_t), padded(B, np_t)
-    Cp = padded(np.zeros((M, N), np.float32) if C0 is None else C0, np.float32)
+    cpad = ldpad if ldcpad is None else ldcpad
+    Ap, Bp = padded(A, np_t, ldpad), padded(B, np_t, ldpad)
+    Cp = padded(np.zeros((M, N), np.float32) if C0 is None else C0, np.float32, cpad)
     dA, dB, dC = DB.from_numpy(Ap), DB.from_numpy(Bp), DB.from_numpy(Cp)
     fn = hip.gemm_bf16 if dtype == "bf16" else hip.gemm_f32
     fn(transA, transB, M, N, K, dA, Ap.shape[1], dB, Bp.shape[1], beta, dC, Cp.shape[1])
-    out = dC.numpy((M, N + ldpad), np.float32)[:, :N]
+    out = dC.numpy((M, N + cpad), np.float32)[:, :N]
     for b in (dA, dB, dC):
         b.free()
     return out

@@ -203,3 +203,22 @@ def test_bf16_tile_aligned_fast_path(K, ta, tb):
     ref = opA[rows] @ opB + 0.5 * C0[rows].astype(np.float64)
     assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(K)
     _rowcol_sums_check(got - 0.5 * C0, A64.T if ta else A64, B64.T if tb else B64, 1e-5)
+
+
+@pytest.mark.parametrize("ldcpad", [1, 2, 4])
+@pytest.mark.parametrize("beta", [0.0, -0.5])
+def test_bf16_fast_path_c_strides(ldcpad, beta):
+    # Fast-path operands (lda, ldb multiples of 8) with C rows that are not 16-byte
+    # aligned (ldc = N + 1, N + 2) take the per-element store form; ldc = N + 4 the
+    # 16-byte form at a padded stride.
+    M = N = 4096
+    K = 64
+    rng = np.random.default_rng(ldcpad + 100 * (beta != 0))
+    A = bf16_bits(rng.standard_normal((M, K), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((K, N), dtype=np.float32))
+    C0 = rng.standard_normal((M, N), dtype=np.float32)
+    got = gemm(A, B, beta=beta, C0=C0, dtype="bf16", ldpad=8, ldcpad=ldcpad)
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    rows = np.sort(rng.choice(M, 64, replace=False))
+    ref = A64[rows] @ B64 + beta * C0[rows].astype(np.float64)
+    assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(K)
