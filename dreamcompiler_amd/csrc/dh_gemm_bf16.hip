@@ -290,6 +290,30 @@ struct FastOperand {
             return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7));
         }
     }
+    // The same fragment as PARTS separate LDS instructions (one b128 read, or two
+    // transposing b64 reads), so that a schedule can place each between matrix-core ops.
+    static constexpr int PARTS = KCONTIG ? 1 : 2;
+    __device__ static void part(const uint16_t* lds, int o, int kk, int lane, int q,
+                                s16x4 (&f)[2]) {
+        const int h = lane >> 5;
+        if (KCONTIG) {
+            const int row = o + (lane & 31);
+            const int p = (2 * kk + h) ^ ((row >> 2) & 3);
+            const s16x8 v = *reinterpret_cast<const s16x8*>(lds + row * 32 + 8 * p);
+            f[0] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+            f[1] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+        } else {
+            const int G = (lane & 31) >> 4, i = lane & 15;
+            const int n = o + 16 * G + 4 * (i & 3);
+            const int k = 16 * kk + 8 * h + 4 * q + (i >> 2);
+            const int p = (n >> 3) ^ (4 * (k & 3));
+            f[q] = ds_read_tr(lds + k * 256 + 8 * p + 4 * ((n >> 2) & 1));
+        }
+    }
+    // DMA block t of this wave's share of a stage (see issue()).
+    __device__ void issue_one(u32x4 rs, uint32_t soff, uint32_t base, int t) const {
+        lds_dma16_buf_so(off[t], rs, soff, base + 1024u * t);
+    }
 };
 
 constexpr int FAST_TILE = 256 * 32;   // elements of one operand stage (32 k)
@@ -315,6 +339,48 @@ __device__ inline void mfma_block(const bf16x8 (&fa)[FM], const bf16x8 (&fb)[FN]
             acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
 }
 
+__device__ inline bf16x8 cat8(const s16x4 (&f)[2]) {
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(f[0], f[1], 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// One 16-k step of a one-wave-per-SIMD schedule: the FM x FN matrix-core ops on the
+// current fragments (ca, cb), with the LDS reads of the next fragments (na, nb, from stage
+// `nst`, k-step nkk) and, when DMA, this wave's 2 x PER DMA blocks of a later stage placed
+// one per op.  A single wave per SIMD issues at most one instruction every few cycles, so
+// grouped reads or DMA issues would leave the matrix core idle; spread out, each hides
+// under the op before it.
+template <typename OA, typename OB, int FM, int FN, bool DMA>
+__device__ inline void step_interleaved(const s16x4 (&ca)[FM][2], const s16x4 (&cb)[FN][2],
+                                        f32x16 (&acc)[FM][FN], const uint16_t* nst, int nkk,
+                                        int wm, int wn, int lane, s16x4 (&na)[FM][2],
+                                        s16x4 (&nb)[FN][2], const OA& oa, const OB& ob,
+                                        u32x4 rsa, u32x4 rsb, uint32_t soa, uint32_t sob,
+                                        uint32_t basea, uint32_t baseb) {
+    constexpr int NRA = FM * OA::PARTS, NR = NRA + FN * OB::PARTS;
+    constexpr int NDMA = DMA ? OA::PER + OB::PER : 0;
+    static_assert(NR <= FM * FN && NDMA <= FM * FN, "schedule slots");
+#pragma unroll
+    for (int i = 0; i < FM * FN; ++i) {
+        const int a = i / FN, b = i % FN;
+        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat8(ca[a]), cat8(cb[b]), acc[a][b],
+                                                            0, 0, 0);
+        if (i < NRA) {
+            OA::part(nst, wm + 32 * (i / OA::PARTS), nkk, lane, i % OA::PARTS, na[i / OA::PARTS]);
+        } else if (i < NR) {
+            const int j = i - NRA;
+            OB::part(nst + FAST_TILE, wn + 32 * (j / OB::PARTS), nkk, lane, j % OB::PARTS,
+                     nb[j / OB::PARTS]);
+        }
+        // DMA blocks go after the later ops, once the reads are under way.
+        const int d = i - (FM * FN - NDMA);
+        if (d >= 0) {
+            if (d < OA::PER) oa.issue_one(rsa, soa, basea, d);
+            else ob.issue_one(rsb, sob, baseb, d - OA::PER);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // Wait until at most n of this wave's DMA stages (2 * PER loads each) are in flight.
 template <int PER2>
 __device__ inline void wait_dma_stages(int n) {
@@ -329,9 +395,12 @@ __device__ inline void wait_dma_stages(int n) {
     }
 }
 
-// WAVES = 4: 2 x 2 waves of 128 x 128 (one wave per SIMD, 256 accumulators);
+// WAVES = 4 (default): 2 x 2 waves of 128 x 128 (one wave per SIMD, 256 accumulators in
+// AGPRs), reads and DMA issues interleaved op by op.  Under the chip's power cap it runs
+// 2-3% faster than
 // WAVES = 8: 2 x 4 waves of 128 x 64 (two waves per SIMD, 128 accumulators each, so one
-// wave's MFMAs cover the other's barrier and LDS-read gaps).
+// wave's MFMAs cover the other's barrier and LDS-read gaps), which reads 1.5x the LDS
+// fragment bytes per matrix-core op.
 template <bool TA, bool TB, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES)
 gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
@@ -368,6 +437,74 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
     const int nk = K / 32;
+    if constexpr (WAVES == 4) {
+        // One wave per SIMD, 128 x 128 each: half the LDS fragment traffic per matrix-core op
+        // of the two-wave form, with the reads and DMA issues interleaved op by op.  Stage
+        // indices past the last stage are clamped (the last stage is fetched again into a
+        // slot nobody reads any more), so every stage issues the same DMA count and the
+        // waits are constants: before the barrier of stage kt, stage kt+1 must have landed
+        // while kt+2 and kt+3 may still be in flight.
+        const u32x4 rsa = make_rsrc(A, oa.bytes), rsb = make_rsrc(B, ob.bytes);
+        auto slot_bases = [&](int s, uint32_t& ba, uint32_t& bb) {
+            const uint32_t st = lds_addr(ring + (s % FAST_NSTAGE) * 2 * FAST_TILE);
+            ba = __builtin_amdgcn_readfirstlane(st + 1024u * OA::PER * wave);
+            bb = __builtin_amdgcn_readfirstlane(st + 2u * FAST_TILE + 1024u * OB::PER * wave);
+        };
+        auto soffs = [&](int s, uint32_t& sa, uint32_t& sb) {
+            const uint32_t k = (uint32_t)min(s, nk - 1);
+            sa = __builtin_amdgcn_readfirstlane(k * oa.step);
+            sb = __builtin_amdgcn_readfirstlane(k * ob.step);
+        };
+        for (int s = 0; s < FAST_NSTAGE - 1; ++s) {
+            uint32_t ba, bb, sa, sb;
+            slot_bases(s, ba, bb);
+            soffs(s, sa, sb);
+#pragma unroll
+            for (int t = 0; t < OA::PER; ++t) oa.issue_one(rsa, sa, ba, t);
+#pragma unroll
+            for (int t = 0; t < OB::PER; ++t) ob.issue_one(rsb, sb, bb, t);
+        }
+        static_assert(2 * (OA::PER + OB::PER) == 16, "vmcnt below assumes 8 DMAs per stage");
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        __syncthreads();
+        asm volatile("" ::"s"(C), "s"(ldc), "s"(beta));
+        s16x4 f0a[FM][2], f0b[FN][2], f1a[FM][2], f1b[FN][2];
+#pragma unroll
+        for (int x = 0; x < FM; ++x)
+#pragma unroll
+            for (int q = 0; q < OA::PARTS; ++q) OA::part(ring, wm + 32 * x, 0, lane, q, f0a[x]);
+#pragma unroll
+        for (int x = 0; x < FN; ++x)
+#pragma unroll
+            for (int q = 0; q < OB::PARTS; ++q)
+                OB::part(ring + FAST_TILE, wn + 32 * x, 0, lane, q, f0b[x]);
+        for (int kt = 0; kt < nk - 1; ++kt) {
+            uint32_t ba, bb, sa, sb;
+            slot_bases(kt + FAST_NSTAGE - 1, ba, bb);
+            soffs(kt + FAST_NSTAGE - 1, sa, sb);
+            step_interleaved<OA, OB, FM, FN, true>(f0a, f0b, acc, ring + (kt % FAST_NSTAGE) * 2 * FAST_TILE,
+                                                   1, wm, wn, lane, f1a, f1b, oa, ob, rsa, rsb,
+                                                   sa, sb, ba, bb);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(16)" ::: "memory");
+            __syncthreads();
+            step_interleaved<OA, OB, FM, FN, false>(
+                f1a, f1b, acc, ring + ((kt + 1) % FAST_NSTAGE) * 2 * FAST_TILE, 0, wm, wn, lane,
+                f0a, f0b, oa, ob, rsa, rsb, 0u, 0u, 0u, 0u);
+        }
+        step_interleaved<OA, OB, FM, FN, false>(f0a, f0b, acc,
+                                                ring + ((nk - 1) % FAST_NSTAGE) * 2 * FAST_TILE, 1,
+                                                wm, wn, lane, f1a, f1b, oa, ob, rsa, rsb, 0u, 0u,
+                                                0u, 0u);
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat8(f1a[a]), cat8(f1b[b]),
+                                                                    acc[a][b], 0, 0, 0);
+        // The clamped refetches may still be landing in free slots: drain them before the
+        // work-group can end and its LDS be handed to another.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
     auto issue = [&](int kt) {
         uint16_t* st = ring + (kt % FAST_NSTAGE) * 2 * FAST_TILE;
         oa.issue(A, kt, st, wave);
@@ -411,6 +548,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     __builtin_amdgcn_sched_barrier(0);
     mfma_block<FM, FN>(f0a, f0b, acc);
     mfma_block<FM, FN>(f1a, f1b, acc);
+    }
 
     // Register r of block (a, b) is C[32 a + 8 (r / 4) + 4 (lane / 32) + r % 4][32 b + lane % 32]
     // (relative to the wave's tile): each store instruction writes two 128-byte row pieces.
@@ -444,7 +582,7 @@ int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t*
                 float beta, float* C, int ldc) {
     static const int waves = [] {
         const char* e = std::getenv("DH_GEMM_BF16_WAVES");   // tuning knob: 4 or 8
-        return (e && std::atoi(e) == 4) ? 4 : 8;
+        return (e && std::atoi(e) == 8) ? 8 : 4;
     }();
     if (waves == 4)
         gemm_bf16_fast_kernel<TA, TB, 4><<<(M / 256) * (N / 256), 256, 0, stream()>>>(

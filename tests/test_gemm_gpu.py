@@ -222,3 +222,36 @@ def test_bf16_fast_path_c_strides(ldcpad, beta):
     rows = np.sort(rng.choice(M, 64, replace=False))
     ref = A64[rows] @ B64 + beta * C0[rows].astype(np.float64)
     assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(K)
+
+
+_TWO_WAVE_SCRIPT = r"""
+import sys, numpy as np
+sys.path[:0] = [{tests!r}, {root!r}]
+from _gpu import bf16_bits, bits_to_f32, gemm, maxrel
+for ta, tb in [(0, 0), (0, 1), (1, 0), (1, 1)]:
+    M = N = 4096; K = 320
+    rng = np.random.default_rng(7 + 10 * ta + 20 * tb)
+    A = bf16_bits(rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32))
+    got = gemm(A, B, bool(ta), bool(tb), dtype="bf16")
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    opA, opB = (A64.T if ta else A64), (B64.T if tb else B64)
+    rows = np.sort(rng.choice(M, 64, replace=False))
+    e = maxrel(got[rows], opA[rows] @ opB)
+    print("two-wave variant", ta, tb, e, flush=True)
+    assert e <= 1e-5 * np.sqrt(K), e
+"""
+
+
+def test_bf16_fast_path_two_wave_variant():
+    # The fast path's 8-wave form (two waves per SIMD, DH_GEMM_BF16_WAVES=8) is chosen once
+    # per process, so it runs in a child process of its own.
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = _TWO_WAVE_SCRIPT.format(tests=here, root=os.path.dirname(here))
+    r = subprocess.run([sys.executable, "-c", code], env={**os.environ, "DH_GEMM_BF16_WAVES": "8"},
+                       capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.count("two-wave variant") == 4, r.stdout
