@@ -27,6 +27,7 @@ HIP_SOURCES = [
     "dh_gemm_bf16.hip",
     "dh_flash_fwd.hip",
     "dh_flash_bwd.hip",
+    "dh_rows.hip",
 ]
 RT_SOURCES = ["dream_rt.cpp"]
 

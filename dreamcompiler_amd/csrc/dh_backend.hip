@@ -133,35 +133,6 @@ int launch_convert(void* dst, const void* src, size_t n) {
     return check_launch("dh_convert");
 }
 
-// ---------------------------------------------------------------------------
-// Row softmax / log-softmax: one wavefront per row, three passes over the row
-// (max, sum of exp(x - max), normalise) with DPP / permlane reductions.
-// Matches dream_softmax (elementwise.inc:346-356) and dream_log_softmax
-// (elementwise.inc:1557-1567) in fp32.
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) row_softmax_kernel(const float* __restrict__ X,
-                                                          float* __restrict__ Y, int R, int C,
-                                                          int log_softmax) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= R) return;
-    const float* x = X + (size_t)row * C;
-    float* y = Y + (size_t)row * C;
-    float mx = -INFINITY;
-    for (int j = lane; j < C; j += 64) mx = fmaxf(mx, x[j]);
-    mx = wave_reduce(mx, OpMax());
-    float s = 0.f;
-    for (int j = lane; j < C; j += 64) s += __expf(x[j] - mx);
-    s = wave_reduce(s, OpSum());
-    if (log_softmax) {
-        const float lse = mx + __logf(s);
-        for (int j = lane; j < C; j += 64) y[j] = x[j] - lse;
-    } else {
-        const float inv = 1.f / s;
-        for (int j = lane; j < C; j += 64) y[j] = __expf(x[j] - mx) * inv;
-    }
-}
-
 }  // namespace dh
 
 using namespace dh;
@@ -345,13 +316,5 @@ int dh_convert(void* dst, int dt, const void* src, int stype, size_t n) {
     return set_error(DH_ERR_UNSUPPORTED, "dh_convert: unsupported pair %d -> %d", stype, dt);
 }
 
-int dh_row_softmax(const float* X, float* Y, int R, int C, int log_softmax) {
-    DH_TRY(ensure_init());
-    if (R < 0 || C < 0) return set_error(DH_ERR_INVALID, "dh_row_softmax: negative shape");
-    if (R == 0 || C == 0) return DH_OK;
-    if (!X || !Y) return set_error(DH_ERR_INVALID, "dh_row_softmax: null pointer");
-    row_softmax_kernel<<<(R + 3) / 4, 256, 0, stream()>>>(X, Y, R, C, log_softmax);
-    return check_launch("dh_row_softmax");
-}
 
 }  // extern "C"

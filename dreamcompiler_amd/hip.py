@@ -49,6 +49,9 @@ _SIGS = {
     "dh_flash_bwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp, _vp, _vp, _i]),
     "dh_row_softmax": (_i, [_vp, _vp, _i, _i, _i]),
+    "dh_row_softmax_bwd": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "dh_layer_norm": (_i, [_vp, _vp, _i, _i]),
+    "dh_layer_norm_bwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -179,6 +182,20 @@ def flash_bwd(dtype, BH, S, D, scale, causal, Q, K, V, O, dO, LSE, dQ, dK, dV, a
 
 def row_softmax(X, Y, R, C, log=False):
     check(load().dh_row_softmax(_p(X), _p(Y), R, C, int(log)), "dh_row_softmax")
+
+
+def row_softmax_bwd(Y, G, GX, R, C, log=False, accumulate=False):
+    check(load().dh_row_softmax_bwd(_p(Y), _p(G), _p(GX), R, C, int(log), int(accumulate)),
+          "dh_row_softmax_bwd")
+
+
+def layer_norm(X, Y, R, C):
+    check(load().dh_layer_norm(_p(X), _p(Y), R, C), "dh_layer_norm")
+
+
+def layer_norm_bwd(X, Y, DY, GX, R, C, accumulate=False):
+    check(load().dh_layer_norm_bwd(_p(X), _p(Y), _p(DY), _p(GX), R, C, int(accumulate)),
+          "dh_layer_norm_bwd")
 
 
 class Timer:

@@ -127,9 +127,23 @@ int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int causal,
                  const void* d_O, const void* d_dO, const float* d_LSE,
                  float* d_dQ, float* d_dK, float* d_dV, int accumulate);
 
-/* ---- row reductions (runtime/ops/elementwise.inc:338-358, 1550-1570) -----------
- * Y = softmax or log_softmax over each of R rows of C contiguous fp32 values. */
+/* ---- row-wise ops: fp32, R rows of C contiguous values -------------------------
+ * accumulate = 1 adds into GX (the reference backward's "+="), 0 overwrites it.
+ * Y = softmax or log_softmax of every row (dream_softmax, elementwise.inc:338-358;
+ * dream_log_softmax, elementwise.inc:1550-1570). */
 int dh_row_softmax(const float* d_X, float* d_Y, int R, int C, int log_softmax);
+/* Their backward from the forward OUTPUT Y: softmax GX (+)= Y (G - rowsum(G Y))
+ * (autograd.inc:396-409); log_softmax GX (+)= G - exp(Y) rowsum(G), exp(Y) being the softmax
+ * the reference recomputes from its input (autograd.inc:212-233). */
+int dh_row_softmax_bwd(const float* d_Y, const float* d_G, float* d_GX, int R, int C,
+                       int log_softmax, int accumulate);
+/* Row layer norm without affine terms: Y = (X - mean) / sqrt(var + 1e-5), biased variance
+ * (dream_layer_norm, runtime/io/builtins.inc:167-188). */
+int dh_layer_norm(const float* d_X, float* d_Y, int R, int C);
+/* Its backward, inv_std recomputed from X (autograd.inc:453-471):
+ * GX (+)= inv_std / C (C DY - rowsum(DY) - Y rowsum(DY Y)). */
+int dh_layer_norm_bwd(const float* d_X, const float* d_Y, const float* d_DY, float* d_GX,
+                      int R, int C, int accumulate);
 
 #ifdef __cplusplus
 }

@@ -452,6 +452,166 @@ void orc_log_softmax_rows(const double* X, double* Y, int R, int C) {
     }
 }
 
+void orc_softmax_bwd(const double* Y, const double* G, double* GX, int R, int C) {
+    // autograd.inc:396-409: per row dot = sum_j g_j y_j, then gx_j += y_j (g_j - dot).
+    for (int r = 0; r < R; ++r) {
+        const double* y = Y + (size_t)r * C;
+        const double* g = G + (size_t)r * C;
+        double* gx = GX + (size_t)r * C;
+        double dot = 0.0;
+        for (int j = 0; j < C; ++j) dot += g[j] * y[j];
+        for (int j = 0; j < C; ++j) gx[j] += y[j] * (g[j] - dot);
+    }
+}
+
+void orc_log_softmax_bwd(const double* X, const double* G, double* GX, int N, int C) {
+    // autograd.inc:212-233: softmax recomputed from x (max, exp, normalise), then
+    // dx_j += dy_j - sm_j * sum_k dy_k.
+    std::vector<double> sm(C > 0 ? C : 1);
+    for (int n = 0; n < N; ++n) {
+        const double* x = X + (size_t)n * C;
+        const double* g = G + (size_t)n * C;
+        double* gx = GX + (size_t)n * C;
+        double mx = x[0];
+        for (int j = 1; j < C; ++j) if (x[j] > mx) mx = x[j];
+        double s = 0.0;
+        for (int j = 0; j < C; ++j) { sm[j] = std::exp(x[j] - mx); s += sm[j]; }
+        for (int j = 0; j < C; ++j) sm[j] /= s;
+        double gs = 0.0;
+        for (int j = 0; j < C; ++j) gs += g[j];
+        for (int j = 0; j < C; ++j) gx[j] += g[j] - sm[j] * gs;
+    }
+}
+
+void orc_layer_norm(const double* X, double* Y, int R, int C) {
+    // builtins.inc:167-188: per row mean, biased variance, y = (x - mu) / sqrt(var + 1e-5).
+    for (int r = 0; r < R; ++r) {
+        const double* x = X + (size_t)r * C;
+        double* y = Y + (size_t)r * C;
+        double mu = 0.0;
+        for (int j = 0; j < C; ++j) mu += x[j];
+        mu /= C;
+        double var = 0.0;
+        for (int j = 0; j < C; ++j) { const double d = x[j] - mu; var += d * d; }
+        var /= C;
+        const double inv_std = 1.0 / std::sqrt(var + 1e-5);
+        for (int j = 0; j < C; ++j) y[j] = (x[j] - mu) * inv_std;
+    }
+}
+
+void orc_layer_norm_bwd(const double* X, const double* Y, const double* DY, double* GX, int R,
+                        int C) {
+    // autograd.inc:453-471: inv_std recomputed from x; per row
+    // gx_j += inv_std / C * (C dy_j - sum dy - y_j sum(dy y)).
+    for (int r = 0; r < R; ++r) {
+        const double* x = X + (size_t)r * C;
+        const double* y = Y + (size_t)r * C;
+        const double* dy = DY + (size_t)r * C;
+        double* gx = GX + (size_t)r * C;
+        double mu = 0.0;
+        for (int j = 0; j < C; ++j) mu += x[j];
+        mu /= C;
+        double var = 0.0;
+        for (int j = 0; j < C; ++j) { const double d = x[j] - mu; var += d * d; }
+        var /= C;
+        const double inv_std = 1.0 / std::sqrt(var + 1e-5);
+        double sdy = 0.0, sdyy = 0.0;
+        for (int j = 0; j < C; ++j) { sdy += dy[j]; sdyy += dy[j] * y[j]; }
+        for (int j = 0; j < C; ++j) gx[j] += inv_std / C * (C * dy[j] - sdy - y[j] * sdyy);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Linear layers and batched matmul
+// ---------------------------------------------------------------------------
+void orc_linear(const double* X, const double* W, const double* b, double* Y, int N, int in_dim,
+                int out_dim, int relu) {
+    // elementwise.inc:1432-1510: Y = bias (broadcast), then Y[i,:] += X[i,k] * W^T[k,:] in
+    // (i, k, j) order over an explicit transpose of W; linear_relu clamps Y < 0 to 0.
+    std::vector<double> Wt((size_t)in_dim * out_dim);
+    for (int j = 0; j < out_dim; ++j)
+        for (int k = 0; k < in_dim; ++k) Wt[(size_t)k * out_dim + j] = W[(size_t)j * in_dim + k];
+    for (int i = 0; i < N; ++i) {
+        double* y = Y + (size_t)i * out_dim;
+        for (int j = 0; j < out_dim; ++j) y[j] = b[j];
+        for (int k = 0; k < in_dim; ++k) {
+            const double xik = X[(size_t)i * in_dim + k];
+            const double* wt = &Wt[(size_t)k * out_dim];
+            for (int j = 0; j < out_dim; ++j) y[j] += xik * wt[j];
+        }
+    }
+    if (relu)
+        for (size_t i = 0; i < (size_t)N * out_dim; ++i) if (Y[i] < 0) Y[i] = 0;
+}
+
+void orc_linear_bwd(const double* X, const double* W, const double* Y, double* dY, double* dX,
+                    double* dW, double* db, int N, int in_dim, int out_dim, int relu) {
+    // autograd.inc:156-205.  linear_relu first zeroes dY where Y <= 0 -- in place, as the
+    // reference does to the node's own gradient -- then db += column sums of dY,
+    // dX += dY W (i, j, k order), dW += dY^T X (j, i, k order).
+    if (relu)
+        for (size_t i = 0; i < (size_t)N * out_dim; ++i) if (Y[i] <= 0) dY[i] = 0;
+    for (int j = 0; j < out_dim; ++j) {
+        double s = 0.0;
+        for (int i = 0; i < N; ++i) s += dY[(size_t)i * out_dim + j];
+        db[j] += s;
+    }
+    for (int i = 0; i < N; ++i)
+        for (int j = 0; j < out_dim; ++j) {
+            const double dy = dY[(size_t)i * out_dim + j];
+            const double* w = W + (size_t)j * in_dim;
+            double* dx = dX + (size_t)i * in_dim;
+            for (int k = 0; k < in_dim; ++k) dx[k] += dy * w[k];
+        }
+    for (int j = 0; j < out_dim; ++j) {
+        double* dw = dW + (size_t)j * in_dim;
+        for (int i = 0; i < N; ++i) {
+            const double dy = dY[(size_t)i * out_dim + j];
+            const double* x = X + (size_t)i * in_dim;
+            for (int k = 0; k < in_dim; ++k) dw[k] += dy * x[k];
+        }
+    }
+}
+
+void orc_bmm(const double* A, const double* B, double* C, int Bt, int M, int K, int N) {
+    // elementwise.inc:1218-1252: per batch, C[r][c] = sum_k A[r][k] B[k][c] (dot order k).
+    for (int bi = 0; bi < Bt; ++bi) {
+        const double* a = A + (size_t)bi * M * K;
+        const double* b = B + (size_t)bi * K * N;
+        double* c = C + (size_t)bi * M * N;
+        for (int r = 0; r < M; ++r)
+            for (int cc = 0; cc < N; ++cc) {
+                double s = 0.0;
+                for (int k = 0; k < K; ++k) s += a[(size_t)r * K + k] * b[(size_t)k * N + cc];
+                c[(size_t)r * N + cc] = s;
+            }
+    }
+}
+
+void orc_bmm_bwd(const double* A, const double* B, const double* G, double* gA, double* gB,
+                 int Bt, int M, int K, int N) {
+    // autograd.inc:549-574: gA += G B^T, gB += A^T G per batch, each entry one dot product.
+    for (int bi = 0; bi < Bt; ++bi) {
+        const double* go = G + (size_t)bi * M * N;
+        const double* a = A + (size_t)bi * M * K;
+        const double* b = B + (size_t)bi * K * N;
+        double* ga = gA + (size_t)bi * M * K;
+        double* gb = gB + (size_t)bi * K * N;
+        for (int r = 0; r < M; ++r)
+            for (int k = 0; k < K; ++k) {
+                double s = 0.0;
+                for (int c = 0; c < N; ++c) s += go[(size_t)r * N + c] * b[(size_t)k * N + c];
+                ga[(size_t)r * K + k] += s;
+            }
+        for (int k = 0; k < K; ++k)
+            for (int c = 0; c < N; ++c) {
+                double s = 0.0;
+                for (int r = 0; r < M; ++r) s += a[(size_t)r * K + k] * go[(size_t)r * N + c];
+                gb[(size_t)k * N + c] += s;
+            }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // bf16 (training.inc:1969-1976)
 // ---------------------------------------------------------------------------

@@ -88,6 +88,28 @@ void orc_flash_lse(const double* Q, const double* K, double* lse, int B, int S, 
 /* Row reductions (elementwise.inc:338-358, 1550-1570): rows = R, cols = C. */
 void orc_softmax_rows(const double* X, double* Y, int R, int C);
 void orc_log_softmax_rows(const double* X, double* Y, int R, int C);
+/* Their backward, "+=" into GX: softmax from its output Y (autograd.inc:396-409),
+ * log_softmax from its input X (autograd.inc:212-233). */
+void orc_softmax_bwd(const double* Y, const double* G, double* GX, int R, int C);
+void orc_log_softmax_bwd(const double* X, const double* G, double* GX, int N, int C);
+/* Row-wise layer norm without affine terms, eps 1e-5 (builtins.inc:167-188), and its
+ * backward "+=" into GX (autograd.inc:453-471). */
+void orc_layer_norm(const double* X, double* Y, int R, int C);
+void orc_layer_norm_bwd(const double* X, const double* Y, const double* DY, double* GX, int R,
+                        int C);
+
+/* Fused linear layer Y = X W^T + b (W stored out_dim x in_dim), relu != 0 for
+ * linear_relu (elementwise.inc:1432-1510), and its backward (autograd.inc:156-205):
+ * relu masks dY in place (Y <= 0 -> 0), then db, dX, dW "+=". */
+void orc_linear(const double* X, const double* W, const double* b, double* Y, int N, int in_dim,
+                int out_dim, int relu);
+void orc_linear_bwd(const double* X, const double* W, const double* Y, double* dY, double* dX,
+                    double* dW, double* db, int N, int in_dim, int out_dim, int relu);
+/* Batched matmul C[b] = A[b] B[b] (elementwise.inc:1218-1252) and its backward
+ * gA += G B^T, gB += A^T G (autograd.inc:549-574); A is (Bt, M*K), B (Bt, K*N). */
+void orc_bmm(const double* A, const double* B, double* C, int Bt, int M, int K, int N);
+void orc_bmm_bwd(const double* A, const double* B, const double* G, double* gA, double* gB,
+                 int Bt, int M, int K, int N);
 
 /* bf16 rounding (training.inc:1969-1976): fp32 -> bf16 -> fp32, round to nearest even
  * by the bias-and-truncate rule.  orc_bf16_bits returns the upper 16 bits. */

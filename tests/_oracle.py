@@ -45,6 +45,14 @@ def lib():
             "orc_flash_lse": [_dp, _dp, _dp, _i, _i, _i, _i],
             "orc_softmax_rows": [_dp, _dp, _i, _i],
             "orc_log_softmax_rows": [_dp, _dp, _i, _i],
+            "orc_softmax_bwd": [_dp, _dp, _dp, _i, _i],
+            "orc_log_softmax_bwd": [_dp, _dp, _dp, _i, _i],
+            "orc_layer_norm": [_dp, _dp, _i, _i],
+            "orc_layer_norm_bwd": [_dp, _dp, _dp, _dp, _i, _i],
+            "orc_linear": [_dp, _dp, _dp, _dp, _i, _i, _i, _i],
+            "orc_linear_bwd": [_dp] * 7 + [_i, _i, _i, _i],
+            "orc_bmm": [_dp, _dp, _dp, _i, _i, _i, _i],
+            "orc_bmm_bwd": [_dp] * 5 + [_i, _i, _i, _i],
             "orc_to_bf16": [ctypes.c_float],
             "orc_bf16_bits": [_fp, _u16p, _ll],
         }
@@ -203,6 +211,74 @@ def log_softmax_rows(X):
     Y = np.empty_like(X)
     lib().orc_log_softmax_rows(_ptr(X), _ptr(Y), X.shape[0], X.size // X.shape[0])
     return Y
+
+
+def _rows(X):
+    R = X.shape[0] if X.ndim > 1 else 1
+    return R, X.size // R
+
+
+def softmax_bwd(Y, G, GX=None):
+    """gx += y (g - sum(g y)) per row (softmax backward from its output)."""
+    Y, G = _d(Y), _d(G)
+    GX = np.zeros_like(Y) if GX is None else _d(GX).copy()
+    lib().orc_softmax_bwd(_ptr(Y), _ptr(G), _ptr(GX), *_rows(Y))
+    return GX
+
+
+def log_softmax_bwd(X, G, GX=None):
+    """gx += g - softmax(x) sum(g) per row (log_softmax backward from its input)."""
+    X, G = _d(X), _d(G)
+    GX = np.zeros_like(X) if GX is None else _d(GX).copy()
+    lib().orc_log_softmax_bwd(_ptr(X), _ptr(G), _ptr(GX), *_rows(X))
+    return GX
+
+
+def layer_norm(X):
+    X = _d(X)
+    Y = np.empty_like(X)
+    lib().orc_layer_norm(_ptr(X), _ptr(Y), *_rows(X))
+    return Y
+
+
+def layer_norm_bwd(X, Y, DY, GX=None):
+    X, Y, DY = _d(X), _d(Y), _d(DY)
+    GX = np.zeros_like(X) if GX is None else _d(GX).copy()
+    lib().orc_layer_norm_bwd(_ptr(X), _ptr(Y), _ptr(DY), _ptr(GX), *_rows(X))
+    return GX
+
+
+def linear(X, W, b, relu=False):
+    """Y = X W^T + b (W is out x in), optionally ReLU."""
+    X, W, b = _d(X), _d(W), _d(b).ravel()
+    Y = np.empty((X.shape[0], W.shape[0]), np.float64)
+    lib().orc_linear(_ptr(X), _ptr(W), _ptr(b), _ptr(Y), X.shape[0], X.shape[1], W.shape[0],
+                     int(relu))
+    return Y
+
+
+def linear_bwd(X, W, Y, dY, relu=False):
+    """Returns (dY after the ReLU mask, dX, dW, db), accumulated from zero."""
+    X, W, Y = _d(X), _d(W), _d(Y)
+    dY = _d(dY).copy()
+    dX, dW, db = np.zeros_like(X), np.zeros_like(W), np.zeros(W.shape[0], np.float64)
+    lib().orc_linear_bwd(_ptr(X), _ptr(W), _ptr(Y), _ptr(dY), _ptr(dX), _ptr(dW), _ptr(db),
+                         X.shape[0], X.shape[1], W.shape[0], int(relu))
+    return dY, dX, dW, db
+
+
+def bmm(A, B, Bt, M, K, N):
+    A, B = _d(A), _d(B)
+    C = np.empty((Bt, M * N), np.float64)
+    lib().orc_bmm(_ptr(A), _ptr(B), _ptr(C), Bt, M, K, N)
+    return C
+
+
+def bmm_bwd(A, B, G, Bt, M, K, N):
+    A, B, G = _d(A), _d(B), _d(G)
+    gA, gB = np.zeros((Bt, M * K), np.float64), np.zeros((Bt, K * N), np.float64)
+    lib().orc_bmm_bwd(_ptr(A), _ptr(B), _ptr(G), _ptr(gA), _ptr(gB), Bt, M, K, N)
+    return gA, gB
 
 
 def to_bf16(x):

@@ -43,6 +43,8 @@ class RefRuntime:
                             ("backward", 1), ("dream_flash_attention", 7),
                             ("dream_attention", 6), ("dream_attention_causal", 6),
                             ("dream_softmax", 1), ("dream_log_softmax", 1),
+                            ("dream_layer_norm", 1), ("dream_linear", 3),
+                            ("dream_linear_relu", 3), ("dream_bmm", 6),
                             ("dream_set_seed", 1), ("dream_randn", 2),
                             ("dream_kaiming_init", 2), ("gemm_selftest", 0),
                             ("flash_attention_selftest", 0), ("tensor_decref", 1)]:
@@ -124,3 +126,38 @@ class RefRuntime:
     def softmax(self, X, log=False):
         fn = self.L.dream_log_softmax if log else self.L.dream_softmax
         return self.read(fn(self.tensor(X)))
+
+    def _grads(self, out, W, *ins):
+        """backward(sum(out * W)) -> the .grad of each input tensor and of out."""
+        w = self.tensor(W)
+        self.L.backward(self.L.sum(self.L.tensor_mul(out, w)))
+        return tuple(self.read(t, grad=True) for t in ins) + (self.read(out, grad=True),)
+
+    def softmax_grads(self, X, W, log=False):
+        x = self.tensor(X)
+        y = (self.L.dream_log_softmax if log else self.L.dream_softmax)(x)
+        return self._grads(y, W, x)[0]
+
+    def layer_norm(self, X):
+        return self.read(self.L.dream_layer_norm(self.tensor(X)))
+
+    def layer_norm_grads(self, X, W):
+        x = self.tensor(X)
+        return self._grads(self.L.dream_layer_norm(x), W, x)[0]
+
+    def linear(self, X, Wt, b, relu=False):
+        fn = self.L.dream_linear_relu if relu else self.L.dream_linear
+        return self.read(fn(self.tensor(X), self.tensor(Wt), self.tensor(b)))
+
+    def linear_grads(self, X, Wt, b, G, relu=False):
+        """(dX, dW, db, dY of the node after backward) for backward(sum(Y * G))."""
+        fn = self.L.dream_linear_relu if relu else self.L.dream_linear
+        x, w, bb = self.tensor(X), self.tensor(Wt), self.tensor(b)
+        return self._grads(fn(x, w, bb), G, x, w, bb)
+
+    def bmm(self, A, B, Bt, M, K, N, grads_W=None):
+        a, b = self.tensor(A), self.tensor(B)
+        c = self.L.dream_bmm(a, b, *(self.scalar(v) for v in (Bt, M, K, N)))
+        if grads_W is None:
+            return self.read(c)
+        return self._grads(c, grads_W, a, b)[:2]

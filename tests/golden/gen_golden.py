@@ -81,6 +81,34 @@ def main():
     v["softmax_X"], v["softmax_Y"], v["log_softmax_Y"] = X, R.softmax(X), R.softmax(X, log=True)
     manifest["softmax"] = "set_seed(11); X=randn(7,33); softmax(X), log_softmax(X)"
 
+    # Row ops, linear layers and bmm with their backward (upstream gradient W through
+    # backward(sum(Y * W))).
+    R.set_seed(13)
+    G = R.randn(7, 33)
+    v["softmax_G"] = G
+    v["softmax_dX"] = R.softmax_grads(X, G)
+    v["log_softmax_dX"] = R.softmax_grads(X, G, log=True)
+    LX, LG = R.randn(6, 50) * 3.0 + 1.5, R.randn(6, 50)
+    v["layer_norm_X"], v["layer_norm_G"] = LX, LG
+    v["layer_norm_Y"], v["layer_norm_dX"] = R.layer_norm(LX), R.layer_norm_grads(LX, LG)
+    manifest["rows"] = ("set_seed(13); G=randn(7,33) on softmax_X: dX of softmax / log_softmax; "
+                        "layer_norm_X = 3*randn(6,50)+1.5, G=randn(6,50): Y and dX")
+    LinX, LinW, Linb, LinG = R.randn(9, 13), R.randn(11, 13), R.randn(1, 11), R.randn(9, 11)
+    v["linear_X"], v["linear_W"], v["linear_b"], v["linear_G"] = LinX, LinW, Linb, LinG
+    for relu in (False, True):
+        key = "linear_relu" if relu else "linear"
+        v[key + "_Y"] = R.linear(LinX, LinW, Linb, relu)
+        dX, dW, db, dY = R.linear_grads(LinX, LinW, Linb, LinG, relu)
+        v[key + "_dX"], v[key + "_dW"], v[key + "_db"], v[key + "_dY"] = dX, dW, db, dY
+    manifest["linear"] = ("X=randn(9,13), W=randn(11,13) (out x in), b=randn(1,11), "
+                          "G=randn(9,11); Y of linear / linear_relu; dX, dW, db and the node's "
+                          "own grad dY (ReLU-masked in place) after backward(sum(Y*G))")
+    BA, BB, BG = R.randn(3, 5 * 7), R.randn(3, 7 * 6), R.randn(3, 5 * 6)
+    v["bmm_A"], v["bmm_B"], v["bmm_G"] = BA, BB, BG
+    v["bmm_C"] = R.bmm(BA, BB, 3, 5, 7, 6)
+    v["bmm_dA"], v["bmm_dB"] = R.bmm(BA, BB, 3, 5, 7, 6, grads_W=BG)
+    manifest["bmm"] = "A=randn(3,35), B=randn(3,42), G=randn(3,30); bmm(B=3,M=5,K=7,N=6), grads"
+
     np.savez_compressed(OUT, **v)
     manifest["file"] = os.path.basename(OUT)
     manifest["arrays"] = {k: list(a.shape) for k, a in v.items()}

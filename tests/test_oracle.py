@@ -294,3 +294,116 @@ def test_flash_against_reference_build(ref):
     want = ref.attention_grads("flash", Q, K, V, W, B, S, dk, Bc)
     for a, b in zip(got, want):
         assert rel(a, b) <= 1e-12
+
+
+# --------------------------------------------------------------------------- row ops, linear, bmm
+def _fd_sumgrad(f, X, W, h=1e-6):
+    """Central differences of sum(f(X) * W) with respect to every entry of X."""
+    g = np.zeros_like(X)
+    for idx in np.ndindex(X.shape):
+        Xp, Xm = X.copy(), X.copy()
+        Xp[idx] += h
+        Xm[idx] -= h
+        g[idx] = ((f(Xp) * W).sum() - (f(Xm) * W).sum()) / (2 * h)
+    return g
+
+
+def test_row_ops_golden():
+    X, G = GOLD["softmax_X"], GOLD["softmax_G"]
+    assert rel(O.softmax_bwd(O.softmax_rows(X), G), GOLD["softmax_dX"]) <= 1e-12
+    assert rel(O.log_softmax_bwd(X, G), GOLD["log_softmax_dX"]) <= 1e-12
+    LX, LG = GOLD["layer_norm_X"], GOLD["layer_norm_G"]
+    Y = O.layer_norm(LX)
+    assert rel(Y, GOLD["layer_norm_Y"]) <= 1e-12
+    assert rel(O.layer_norm_bwd(LX, Y, LG), GOLD["layer_norm_dX"]) <= 1e-12
+
+
+def test_row_ops_math():
+    rng = np.random.default_rng(31)
+    X, W = rng.standard_normal((4, 9)) * 2, rng.standard_normal((4, 9))
+    # backward = finite differences of the forward (independent of the closed forms)
+    assert rel(O.softmax_bwd(O.softmax_rows(X), W), _fd_sumgrad(O.softmax_rows, X, W)) <= 1e-7
+    assert rel(O.log_softmax_bwd(X, W), _fd_sumgrad(O.log_softmax_rows, X, W)) <= 1e-7
+    assert rel(O.layer_norm_bwd(X, O.layer_norm(X), W), _fd_sumgrad(O.layer_norm, X, W)) <= 1e-6
+    # layer norm: rows have mean 0 and variance var / (var + eps); affine invariance
+    Xl = rng.standard_normal((6, 300)) * 4 + 2
+    Y = O.layer_norm(Xl)
+    var = Xl.var(axis=1)
+    assert np.abs(Y.mean(1)).max() <= 1e-13
+    assert rel(Y.var(axis=1), var / (var + 1e-5)) <= 1e-12
+    assert rel(O.layer_norm(Xl * 3 - 7), O.layer_norm(Xl)) <= 1e-5   # eps breaks exactness
+    # softmax backward rows sum to zero; log_softmax backward of a constant gradient too
+    assert np.abs(O.softmax_bwd(O.softmax_rows(X), W).sum(1)).max() <= 1e-14
+    assert np.abs(O.log_softmax_bwd(X, np.ones_like(X)).sum(1)).max() <= 1e-13
+    # "+=" semantics
+    base = rng.standard_normal(X.shape)
+    assert rel(O.softmax_bwd(O.softmax_rows(X), W, base),
+               base + O.softmax_bwd(O.softmax_rows(X), W)) <= 1e-14
+
+
+def test_linear_golden():
+    X, W, b, G = (GOLD["linear_" + c] for c in "XWbG")
+    for relu, key in ((False, "linear"), (True, "linear_relu")):
+        Y = O.linear(X, W, b, relu)
+        assert rel(Y, GOLD[key + "_Y"]) <= 1e-12
+        dY, dX, dW, db = O.linear_bwd(X, W, Y, G, relu)
+        for got, name in ((dY, "dY"), (dX, "dX"), (dW, "dW"), (db.reshape(1, -1), "db")):
+            assert rel(got, GOLD[f"{key}_{name}"]) <= 1e-12, name
+
+
+def test_linear_math():
+    rng = np.random.default_rng(32)
+    X, W, b = rng.standard_normal((6, 5)), rng.standard_normal((4, 5)), rng.standard_normal(4)
+    Y = O.linear(X, W, b)
+    assert rel(Y, X @ W.T + b) <= 1e-14                                   # independent numpy
+    assert rel(O.linear(X, W, b, relu=True), np.maximum(X @ W.T + b, 0)) <= 1e-14
+    G = rng.standard_normal(Y.shape)
+    for relu in (False, True):
+        dY, dX, dW, db = O.linear_bwd(X, W, O.linear(X, W, b, relu), G, relu)
+        f = lambda x: O.linear(x, W, b, relu)   # noqa: E731
+        assert rel(dX, _fd_sumgrad(f, X, G)) <= 1e-6
+        assert rel(dW, _fd_sumgrad(lambda w: O.linear(X, w, b, relu), W, G)) <= 1e-6
+        assert rel(db, _fd_sumgrad(lambda bb: O.linear(X, W, bb, relu), b, G)) <= 1e-6
+
+
+def test_bmm_golden_and_math():
+    A, B, G = GOLD["bmm_A"], GOLD["bmm_B"], GOLD["bmm_G"]
+    assert rel(O.bmm(A, B, 3, 5, 7, 6), GOLD["bmm_C"]) <= 1e-12
+    gA, gB = O.bmm_bwd(A, B, G, 3, 5, 7, 6)
+    assert rel(gA, GOLD["bmm_dA"]) <= 1e-12 and rel(gB, GOLD["bmm_dB"]) <= 1e-12
+    # independent numpy batched product, and its adjoint identities
+    A3, B3, G3 = A.reshape(3, 5, 7), B.reshape(3, 7, 6), G.reshape(3, 5, 6)
+    assert rel(O.bmm(A, B, 3, 5, 7, 6).reshape(3, 5, 6), A3 @ B3) <= 1e-14
+    assert rel(gA.reshape(3, 5, 7), G3 @ B3.transpose(0, 2, 1)) <= 1e-14
+    assert rel(gB.reshape(3, 7, 6), A3.transpose(0, 2, 1) @ G3) <= 1e-14
+
+
+def test_planted_mistakes_in_new_rows_are_caught():
+    # log_softmax backward with the softmax form (wrong formula) -> golden mismatch
+    X, G = GOLD["softmax_X"], GOLD["softmax_G"]
+    assert rel(O.softmax_bwd(O.log_softmax_rows(X), G), GOLD["log_softmax_dX"]) > 1e-3
+    # linear with W instead of W^T (square case would hide it: use the transposed shape)
+    X, W, b = GOLD["linear_X"], GOLD["linear_W"], GOLD["linear_b"]
+    assert rel(O.linear(X, W, np.zeros_like(b)), GOLD["linear_Y"]) > 1e-3   # dropped bias
+    # bmm operands of different batches paired (batch index off by one)
+    A, B = GOLD["bmm_A"], GOLD["bmm_B"]
+    assert rel(O.bmm(A, np.roll(B, 1, axis=0), 3, 5, 7, 6), GOLD["bmm_C"]) > 1e-3
+
+
+@needs_ref
+def test_new_rows_against_reference_build(ref):
+    rng = np.random.default_rng(33)
+    X, W = rng.standard_normal((17, 129)) * 2, rng.standard_normal((17, 129))
+    assert rel(O.softmax_bwd(O.softmax_rows(X), W), ref.softmax_grads(X, W)) <= 1e-12
+    assert rel(O.log_softmax_bwd(X, W), ref.softmax_grads(X, W, log=True)) <= 1e-12
+    assert rel(O.layer_norm(X), ref.layer_norm(X)) <= 1e-12
+    assert rel(O.layer_norm_bwd(X, O.layer_norm(X), W), ref.layer_norm_grads(X, W)) <= 1e-12
+    Xl, Wl, bl = rng.standard_normal((40, 33)), rng.standard_normal((21, 33)), rng.standard_normal((1, 21))
+    Gl = rng.standard_normal((40, 21))
+    for relu in (False, True):
+        Y = O.linear(Xl, Wl, bl, relu)
+        assert rel(Y, ref.linear(Xl, Wl, bl, relu)) <= 1e-12
+        got = O.linear_bwd(Xl, Wl, Y, Gl, relu)
+        dX, dW, db, dY = ref.linear_grads(Xl, Wl, bl, Gl, relu)
+        for a, b in zip(got, (dY, dX, dW, db.ravel())):
+            assert rel(a, b) <= 1e-12
