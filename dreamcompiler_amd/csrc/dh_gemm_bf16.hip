@@ -1,7 +1,7 @@
 // dh_gemm_bf16.hip -- bf16 x bf16 -> fp32 GEMM on gfx950 (v_mfma_f32_32x32x16_bf16).
 //
-// Same contract as dh_gemm_f32 (NN / NT / TN / TT, beta), with bf16 operands and fp32
-// accumulation and output.  Replaces the reference's fp16 cublasGemmEx branch
+// Same contract as dh_gemm_f32 (NN / NT / TN / TT, beta, batch strides, bias + ReLU epilogue),
+// with bf16 operands and fp32 accumulation and output.  Replaces the reference's fp16 cublasGemmEx branch
 // (runtime/ops/elementwise.inc:1046-1071) for tensor_matmul in reduced-precision mode.
 //
 // Work decomposition
@@ -97,7 +97,11 @@ template <int BM, int BN, int BK, int WAVES_M, bool TA, bool TB, bool VA, bool V
 __global__ void __launch_bounds__(NTHREADS)
 gemm_bf16_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
                  const uint16_t* __restrict__ B, int ldb, float beta, float* __restrict__ C,
-                 int ldc) {
+                 int ldc, long long sA, long long sB, long long sC,
+                 const float* __restrict__ bias, int relu) {
+    A += blockIdx.y * sA;   // batch member blockIdx.y
+    B += blockIdx.y * sB;
+    C += blockIdx.y * sC;
     constexpr int WAVES_N = 4 / WAVES_M;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -177,20 +181,30 @@ gemm_bf16_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
         for (int b = 0; b < FN; ++b) {
             const int col = n0 + wn + 32 * b + l32;
             if (col >= N) continue;
+            const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (row < M) {
                     float* c = C + (size_t)row * ldc + col;
-                    *c = beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c;
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) + bv;
+                    if (relu) v = v < 0.f ? 0.f : v;
+                    *c = v;
                 }
             }
         }
 }
 
+struct Batch {
+    long long sA, sB, sC;   // element strides between batch members (0 for one product)
+    int count;
+    const float* bias;      // per-column bias of the epilogue, or null
+    int relu;
+};
+
 template <int BM, int BN, int BK, int WAVES_M, bool TA, bool TB, bool VA, bool VB>
 int launch_cfg(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
-               float beta, float* C, int ldc) {
+               float beta, float* C, int ldc, const Batch& bt) {
     auto kern = gemm_bf16_kernel<BM, BN, BK, WAVES_M, TA, TB, VA, VB>;
     const size_t lds = (size_t)2 * (BM + BN) * (BK + 8) * sizeof(uint16_t);
     static bool attr_set = false;
@@ -202,18 +216,24 @@ int launch_cfg(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* 
         attr_set = true;
     }
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    kern<<<tiles, NTHREADS, lds, stream()>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    return check_launch("dh_gemm_bf16");
+    for (int b0 = 0; b0 < bt.count; b0 += 65535) {   // gridDim.y = batch member
+        const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
+        kern<<<dim3(tiles, nb), NTHREADS, lds, stream()>>>(
+            M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB, ldb, beta, C + b0 * bt.sC, ldc, bt.sA,
+            bt.sB, bt.sC, bt.bias, bt.relu);
+        DH_TRY(check_launch("dh_gemm_bf16"));
+    }
+    return DH_OK;
 }
 
 template <bool TA, bool TB, bool VA, bool VB>
 int launch_vec(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
-               float beta, float* C, int ldc) {
+               float beta, float* C, int ldc, const Batch& bt) {
     // The 256 x 256 tile needs enough tiles to cover the chip; otherwise use 128 x 128.
-    const long long big_tiles = (long long)((M + 255) / 256) * ((N + 255) / 256);
+    const long long big_tiles = (long long)((M + 255) / 256) * ((N + 255) / 256) * bt.count;
     if (M >= 256 && N >= 256 && big_tiles >= num_cus())
-        return launch_cfg<256, 256, 64, 2, TA, TB, VA, VB>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    return launch_cfg<128, 128, 64, 2, TA, TB, VA, VB>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+        return launch_cfg<256, 256, 64, 2, TA, TB, VA, VB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    return launch_cfg<128, 128, 64, 2, TA, TB, VA, VB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 
 // ---------------------------------------------------------------------------------
@@ -405,7 +425,11 @@ template <bool TA, bool TB, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES)
 gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
                       const uint16_t* __restrict__ B, int ldb, float beta, float* __restrict__ C,
-                      int ldc) {
+                      int ldc, long long sA, long long sB, long long sC,
+                      const float* __restrict__ bias, int relu) {
+    A += blockIdx.y * sA;   // batch member blockIdx.y
+    B += blockIdx.y * sB;
+    C += blockIdx.y * sC;
     using OA = FastOperand<!TA, WAVES>;
     using OB = FastOperand<TB, WAVES>;
     constexpr int WN_CNT = WAVES / 2;                 // waves along N
@@ -467,7 +491,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
         static_assert(2 * (OA::PER + OB::PER) == 16, "vmcnt below assumes 8 DMAs per stage");
         asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         __syncthreads();
-        asm volatile("" ::"s"(C), "s"(ldc), "s"(beta));
+        asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(relu));
         s16x4 f0a[FM][2], f0b[FN][2], f1a[FM][2], f1b[FN][2];
 #pragma unroll
         for (int x = 0; x < FM; ++x)
@@ -526,7 +550,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     // reads too, so they would no longer overlap the f1 MFMAs.
     // The epilogue's kernel arguments are fetched here: a scalar load still in flight at
     // the loop entry would make every LDS wait in the loop a full lgkmcnt(0).
-    asm volatile("" ::"s"(C), "s"(ldc), "s"(beta));
+    asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(relu));
     bf16x8 f0a[FM], f0b[FN], f1a[FM], f1b[FN];
     load_frags<OA, OB, FM, FN>(stage_ptr(0), 0, wm, wn, lane, f0a, f0b);
     for (int kt = 0; kt < nk - 1; ++kt) {
@@ -552,12 +576,12 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 
     // Register r of block (a, b) is C[32 a + 8 (r / 4) + 4 (lane / 32) + r % 4][32 b + lane % 32]
     // (relative to the wave's tile): each store instruction writes two 128-byte row pieces.
-    // One uniform branch on beta keeps both forms straight-line code.
+    // One uniform branch on the epilogue form keeps each form straight-line code.
     float* cw = C + (size_t)(m0 + wm + 4 * h) * ldc + n0 + wn + l32;
     auto at = [&](int a, int b, int r) {
         return cw + (size_t)(32 * a + 8 * (r >> 2) + (r & 3)) * ldc + 32 * b;
     };
-    if (beta == 0.f) {
+    if (beta == 0.f && !bias && !relu) {
 #pragma unroll
         for (int a = 0; a < FM; ++a)
 #pragma unroll
@@ -565,6 +589,10 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 #pragma unroll
                 for (int r = 0; r < 16; ++r) *at(a, b, r) = acc[a][b][r];
     } else {
+        // C = acc + beta C + bias[col], then max(., 0) when relu (NaN passes).
+        float bv[FN];
+#pragma unroll
+        for (int b = 0; b < FN; ++b) bv[b] = bias ? bias[n0 + wn + 32 * b + l32] : 0.f;
 #pragma unroll
         for (int a = 0; a < FM; ++a)
 #pragma unroll
@@ -572,40 +600,47 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     float* c = at(a, b, r);
-                    *c = acc[a][b][r] + beta * *c;
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) + bv[b];
+                    if (relu) v = v < 0.f ? 0.f : v;
+                    *c = v;
                 }
     }
 }
 
 template <bool TA, bool TB>
 int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
-                float beta, float* C, int ldc) {
+                float beta, float* C, int ldc, const Batch& bt) {
     static const int waves = [] {
         const char* e = std::getenv("DH_GEMM_BF16_WAVES");   // tuning knob: 4 or 8
         return (e && std::atoi(e) == 8) ? 8 : 4;
     }();
-    if (waves == 4)
-        gemm_bf16_fast_kernel<TA, TB, 4><<<(M / 256) * (N / 256), 256, 0, stream()>>>(
-            M, N, K, A, lda, B, ldb, beta, C, ldc);
-    else
-        gemm_bf16_fast_kernel<TA, TB, 8><<<(M / 256) * (N / 256), 512, 0, stream()>>>(
-            M, N, K, A, lda, B, ldb, beta, C, ldc);
-    return check_launch("dh_gemm_bf16(fast)");
+    auto kern = waves == 4 ? gemm_bf16_fast_kernel<TA, TB, 4> : gemm_bf16_fast_kernel<TA, TB, 8>;
+    for (int b0 = 0; b0 < bt.count; b0 += 65535) {   // gridDim.y = batch member
+        const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
+        kern<<<dim3((M / 256) * (N / 256), nb), 64 * waves, 0, stream()>>>(
+            M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB, ldb, beta, C + b0 * bt.sC, ldc, bt.sA,
+            bt.sB, bt.sC, bt.bias, bt.relu);
+        DH_TRY(check_launch("dh_gemm_bf16(fast)"));
+    }
+    return DH_OK;
 }
 
 template <bool TA, bool TB>
 int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
-           float beta, float* C, int ldc) {
-    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 8 == 0);
-    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 8 == 0);
+           float beta, float* C, int ldc, const Batch& bt) {
+    // 16-byte operand rows: aligned bases, leading dimensions and batch strides in multiples
+    // of 8 elements.
+    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 8 == 0) && (bt.sA % 8 == 0);
+    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 8 == 0) && (bt.sB % 8 == 0);
     const long long a_elems = (long long)(TA ? K : M) * lda, b_elems = (long long)(TB ? N : K) * ldb;
     if (va && vb && M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K > 0 &&
-        (M / 256) * (N / 256) >= num_cus() && a_elems < (1LL << 31) && b_elems < (1LL << 31))
-        return launch_fast<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    if (va && vb) return launch_vec<TA, TB, true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    if (va) return launch_vec<TA, TB, true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    if (vb) return launch_vec<TA, TB, false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    return launch_vec<TA, TB, false, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+        (long long)(M / 256) * (N / 256) * bt.count >= num_cus() && a_elems < (1LL << 31) &&
+        b_elems < (1LL << 31))
+        return launch_fast<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    if (va && vb) return launch_vec<TA, TB, true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    if (va) return launch_vec<TA, TB, true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    if (vb) return launch_vec<TA, TB, false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    return launch_vec<TA, TB, false, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 
 }  // namespace
@@ -613,19 +648,32 @@ int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, i
 
 using namespace dh;
 
-extern "C" int dh_gemm_bf16(int transA, int transB, int M, int N, int K, const uint16_t* A,
-                            int lda, const uint16_t* B, int ldb, float beta, float* C, int ldc) {
+extern "C" int dh_gemm_bf16_ex(int transA, int transB, int M, int N, int K, const uint16_t* A,
+                               int lda, long long strideA, const uint16_t* B, int ldb,
+                               long long strideB, float beta, float* C, int ldc,
+                               long long strideC, int batch, const float* bias, int relu) {
     DH_TRY(ensure_init());
-    if (M < 0 || N < 0 || K < 0) return set_error(DH_ERR_INVALID, "dh_gemm_bf16: negative shape");
-    if (M == 0 || N == 0) return DH_OK;
+    if (M < 0 || N < 0 || K < 0 || batch < 0)
+        return set_error(DH_ERR_INVALID, "dh_gemm_bf16: negative shape");
+    if (M == 0 || N == 0 || batch == 0) return DH_OK;
     if (!C || (K > 0 && (!A || !B)))
         return set_error(DH_ERR_INVALID, "dh_gemm_bf16: null pointer");
     // A and B are not read when K == 0, so only C's leading dimension matters then.
     if (ldc < N || (K > 0 && (lda < (transA ? M : K) || ldb < (transB ? K : N))))
         return set_error(DH_ERR_INVALID, "dh_gemm_bf16: leading dimension too small");
+    if (batch > 1 && (strideA < 0 || strideB < 0 || strideC < (long long)(M - 1) * ldc + N))
+        return set_error(DH_ERR_INVALID, "dh_gemm_bf16: batch strides overlap C or are negative");
+    const Batch bt{batch > 1 ? strideA : 0, batch > 1 ? strideB : 0, batch > 1 ? strideC : 0,
+                   batch, bias, relu};
     if (transA)
-        return transB ? launch<true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc)
-                      : launch<true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    return transB ? launch<false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc)
-                  : launch<false, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+        return transB ? launch<true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt)
+                      : launch<true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    return transB ? launch<false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt)
+                  : launch<false, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+}
+
+extern "C" int dh_gemm_bf16(int transA, int transB, int M, int N, int K, const uint16_t* A,
+                            int lda, const uint16_t* B, int ldb, float beta, float* C, int ldc) {
+    return dh_gemm_bf16_ex(transA, transB, M, N, K, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1,
+                           nullptr, 0);
 }

@@ -1,9 +1,12 @@
 // dh_gemm_f32.hip -- fp32 GEMM on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
 //
-// C[M x N] = op(A) @ op(B) + beta * C for the four storage layouts (NN, NT, TN, TT).
+// C[M x N] = op(A) @ op(B) + beta * C for the four storage layouts (NN, NT, TN, TT), optionally
+// batched (strided operands, gridDim.y = batch member) and with a bias + ReLU epilogue.
 // NN serves tensor_matmul's C = A @ B (runtime/ops/elementwise.inc:971-1213); NT and TN
 // with beta = 1 serve the matmul backward dA += dY B^T, dB += A^T dY
-// (runtime/ops/autograd.inc:91-125).
+// (runtime/ops/autograd.inc:91-125).  NT with the bias (+ ReLU) epilogue is dream_linear /
+// linear_relu's Y = X W^T + b (elementwise.inc:1432-1516); batched NN is dream_bmm
+// (elementwise.inc:1218-1252).
 //
 // Work decomposition
 //   work-group (256 threads = 4 wave64s) owns a 128 x 128 tile of C;
@@ -84,7 +87,13 @@ struct Slice {
 template <bool TA, bool TB, bool VA, bool VB>
 __global__ void __launch_bounds__(NTHREADS)
 gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
-                const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc) {
+                const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
+                long long sA, long long sB, long long sC, const float* __restrict__ bias,
+                int relu) {
+    // Batch member blockIdx.y (strides in elements; 0 for a single product).
+    A += blockIdx.y * sA;
+    B += blockIdx.y * sB;
+    C += blockIdx.y * sC;
     __shared__ __attribute__((aligned(16))) float As[2][BK * LDS_A];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDS_B];
 
@@ -146,41 +155,56 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     }
 
     // Epilogue: lanes 0..31 of a register cover 32 consecutive columns of one row.
+    // C = acc + beta C + bias[col], then max(., 0) when relu (NaN passes, like `y < 0 ? 0 : y`).
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int col = n0 + wn + 32 * b + l32;
             if (col >= N) continue;
+            const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (row < M) {
                     float* c = C + (size_t)row * ldc + col;
-                    *c = beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c;
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) + bv;
+                    if (relu) v = v < 0.f ? 0.f : v;
+                    *c = v;
                 }
             }
         }
 }
 
+struct Batch {
+    long long sA, sB, sC;
+    int count;
+    const float* bias;
+    int relu;
+};
+
 template <bool TA, bool TB>
 int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
-           float* C, int ldc) {
+           float* C, int ldc, const Batch& bt) {
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    // 128-bit loads need a 16-byte aligned base and a leading dimension divisible by 4.
-    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0);
-    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0);
-    dim3 grid(tiles), block(NTHREADS);
+    // 128-bit loads need 16-byte aligned bases and leading dimensions and batch strides
+    // divisible by 4.
+    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0) && (bt.sA % 4 == 0);
+    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0) && (bt.sB % 4 == 0);
     hipStream_t s = stream();
-    if (va && vb)
-        gemm_f32_kernel<TA, TB, true, true><<<grid, block, 0, s>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    else if (va)
-        gemm_f32_kernel<TA, TB, true, false><<<grid, block, 0, s>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    else if (vb)
-        gemm_f32_kernel<TA, TB, false, true><<<grid, block, 0, s>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    else
-        gemm_f32_kernel<TA, TB, false, false><<<grid, block, 0, s>>>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    return check_launch("dh_gemm_f32");
+    auto kern = va && vb ? gemm_f32_kernel<TA, TB, true, true>
+              : va       ? gemm_f32_kernel<TA, TB, true, false>
+              : vb       ? gemm_f32_kernel<TA, TB, false, true>
+                         : gemm_f32_kernel<TA, TB, false, false>;
+    // gridDim.y carries the batch member; chunks of 65535 keep it within the y limit.
+    for (int b0 = 0; b0 < bt.count; b0 += 65535) {
+        const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
+        kern<<<dim3(tiles, nb), NTHREADS, 0, s>>>(M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB,
+                                                  ldb, beta, C + b0 * bt.sC, ldc, bt.sA, bt.sB,
+                                                  bt.sC, bt.bias, bt.relu);
+        DH_TRY(check_launch("dh_gemm_f32"));
+    }
+    return DH_OK;
 }
 
 }  // namespace
@@ -188,19 +212,32 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
 
 using namespace dh;
 
-extern "C" int dh_gemm_f32(int transA, int transB, int M, int N, int K, const float* A, int lda,
-                           const float* B, int ldb, float beta, float* C, int ldc) {
+extern "C" int dh_gemm_f32_ex(int transA, int transB, int M, int N, int K, const float* A,
+                              int lda, long long strideA, const float* B, int ldb,
+                              long long strideB, float beta, float* C, int ldc,
+                              long long strideC, int batch, const float* bias, int relu) {
     DH_TRY(ensure_init());
-    if (M < 0 || N < 0 || K < 0) return set_error(DH_ERR_INVALID, "dh_gemm_f32: negative shape");
-    if (M == 0 || N == 0) return DH_OK;
+    if (M < 0 || N < 0 || K < 0 || batch < 0)
+        return set_error(DH_ERR_INVALID, "dh_gemm_f32: negative shape");
+    if (M == 0 || N == 0 || batch == 0) return DH_OK;
     if (!C || (K > 0 && (!A || !B)))
         return set_error(DH_ERR_INVALID, "dh_gemm_f32: null pointer");
     // A and B are not read when K == 0, so only C's leading dimension matters then.
     if (ldc < N || (K > 0 && (lda < (transA ? M : K) || ldb < (transB ? K : N))))
         return set_error(DH_ERR_INVALID, "dh_gemm_f32: leading dimension too small");
+    if (batch > 1 && (strideA < 0 || strideB < 0 || strideC < (long long)(M - 1) * ldc + N))
+        return set_error(DH_ERR_INVALID, "dh_gemm_f32: batch strides overlap C or are negative");
+    const Batch bt{batch > 1 ? strideA : 0, batch > 1 ? strideB : 0, batch > 1 ? strideC : 0,
+                   batch, bias, relu};
     if (transA)
-        return transB ? launch<true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc)
-                      : launch<true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
-    return transB ? launch<false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc)
-                  : launch<false, false>(M, N, K, A, lda, B, ldb, beta, C, ldc);
+        return transB ? launch<true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt)
+                      : launch<true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    return transB ? launch<false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt)
+                  : launch<false, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+}
+
+extern "C" int dh_gemm_f32(int transA, int transB, int M, int N, int K, const float* A, int lda,
+                           const float* B, int ldb, float beta, float* C, int ldc) {
+    return dh_gemm_f32_ex(transA, transB, M, N, K, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1,
+                          nullptr, 0);
 }

@@ -19,6 +19,7 @@ _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
+_ll = ctypes.c_longlong
 
 # name: (restype, argtypes) -- mirrors include/dream_hip.h
 _SIGS = {
@@ -45,6 +46,10 @@ _SIGS = {
     "dh_convert": (_i, [_vp, _i, _vp, _i, _sz]),
     "dh_gemm_f32": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i]),
     "dh_gemm_bf16": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i]),
+    "dh_gemm_f32_ex": (_i, [_i, _i, _i, _i, _i, _vp, _i, _ll, _vp, _i, _ll, _f, _vp, _i, _ll,
+                            _i, _vp, _i]),
+    "dh_gemm_bf16_ex": (_i, [_i, _i, _i, _i, _i, _vp, _i, _ll, _vp, _i, _ll, _f, _vp, _i, _ll,
+                             _i, _vp, _i]),
     "dh_flash_fwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp]),
     "dh_flash_bwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp, _vp, _vp, _i]),
@@ -167,6 +172,15 @@ def gemm_f32(transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc):
 def gemm_bf16(transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc):
     check(load().dh_gemm_bf16(int(transA), int(transB), M, N, K, _p(A), lda, _p(B), ldb,
                               float(beta), _p(C), ldc), "dh_gemm_bf16")
+
+
+def gemm_ex(dtype, transA, transB, M, N, K, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch=1,
+            bias=None, relu=False):
+    """dh_gemm_{f32,bf16}_ex: batched GEMM with the bias (+ ReLU) epilogue."""
+    fn = load().dh_gemm_bf16_ex if dtype == "bf16" else load().dh_gemm_f32_ex
+    check(fn(int(transA), int(transB), M, N, K, _p(A), lda, int(sA), _p(B), ldb, int(sB),
+             float(beta), _p(C), ldc, int(sC), int(batch), _p(bias) if bias is not None else None,
+             int(relu)), f"dh_gemm_{dtype}_ex")
 
 
 def flash_fwd(dtype, BH, S, D, scale, causal, Q, K, V, O, LSE):

@@ -105,6 +105,27 @@ int dh_gemm_f32(int transA, int transB, int M, int N, int K,
 int dh_gemm_bf16(int transA, int transB, int M, int N, int K,
                  const uint16_t* d_A, int lda, const uint16_t* d_B, int ldb,
                  float beta, float* d_C, int ldc);
+/* Batched GEMM with a fused epilogue, for every member b < batch:
+ *   C_b = op(A_b) @ op(B_b) + beta * C_b + bias,  then C_b = max(C_b, 0) when relu != 0
+ * with X_b = d_X + b * strideX (strides in elements; a zero stride for A or B shares one
+ * operand across the batch; C members must not overlap: strideC >= (M-1)*ldc + N when
+ * batch > 1).  bias (N fp32 values, added to every row) may be NULL; NaN passes the ReLU as
+ * in the reference's `y < 0 ? 0 : y`.
+ * NT with bias (+ relu) is dream_linear / linear_relu's Y = X W^T + b with W stored
+ * out x in (runtime/ops/elementwise.inc:1432-1516); batched NN is dream_bmm
+ * (elementwise.inc:1218-1252), and its backward's G B^T and A^T G are batched NT and TN
+ * with beta = 1 (runtime/ops/autograd.inc:549-574).  dh_gemm_f32 / dh_gemm_bf16 are the
+ * batch = 1, bias = NULL, relu = 0 case. */
+int dh_gemm_f32_ex(int transA, int transB, int M, int N, int K,
+                   const float* d_A, int lda, long long strideA,
+                   const float* d_B, int ldb, long long strideB,
+                   float beta, float* d_C, int ldc, long long strideC,
+                   int batch, const float* d_bias, int relu);
+int dh_gemm_bf16_ex(int transA, int transB, int M, int N, int K,
+                    const uint16_t* d_A, int lda, long long strideA,
+                    const uint16_t* d_B, int ldb, long long strideB,
+                    float beta, float* d_C, int ldc, long long strideC,
+                    int batch, const float* d_bias, int relu);
 
 /* ---- FlashAttention -----------------------------------------------------------
  * Q, K, V, O in the reference layout (B, S*dk): slice b (a batch x head pair)

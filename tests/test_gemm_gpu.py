@@ -14,6 +14,7 @@ import pytest
 
 import _oracle as O
 from _gpu import bf16_bits, bits_to_f32, elementwise_ratio, gemm, maxrel
+from dreamcompiler_amd import hip
 
 pytestmark = pytest.mark.gpu
 
@@ -255,3 +256,91 @@ def test_bf16_fast_path_two_wave_variant():
                        capture_output=True, text=True, timeout=110)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.count("two-wave variant") == 4, r.stdout
+
+
+# --------------------------------------------------------------------------- batched + epilogue
+def _ex(dtype, ta, tb, Bt, M, N, K, beta=0.0, bias=True, relu=False, share=None, seed=0):
+    """Run dh_gemm_*_ex on random inputs; returns (got, ref) as (Bt, M, N) arrays."""
+    rng = np.random.default_rng(seed)
+    shA = (K, M) if ta else (M, K)
+    shB = (N, K) if tb else (K, N)
+    A = rng.standard_normal((1 if share == "A" else Bt,) + shA).astype(np.float32)
+    B = rng.standard_normal((1 if share == "B" else Bt,) + shB).astype(np.float32)
+    C0 = rng.standard_normal((Bt, M, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    if dtype == "bf16":
+        A, B = bf16_bits(A), bf16_bits(B)
+        A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    else:
+        A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    opA = np.swapaxes(A64, 1, 2) if ta else A64
+    opB = np.swapaxes(B64, 1, 2) if tb else B64
+    ref = np.matmul(opA, opB) + beta * C0.astype(np.float64)
+    if bias:
+        ref = ref + b.astype(np.float64)
+    if relu:
+        ref = np.maximum(ref, 0.0)
+    DB = hip.DeviceBuffer
+    dA, dB, dC = DB.from_numpy(A), DB.from_numpy(B), DB.from_numpy(C0)
+    dbias = DB.from_numpy(b) if bias else None
+    sA = 0 if share == "A" else shA[0] * shA[1]
+    sB = 0 if share == "B" else shB[0] * shB[1]
+    hip.gemm_ex(dtype, ta, tb, M, N, K, dA, shA[1], sA, dB, shB[1], sB, beta, dC, N, M * N, Bt,
+                dbias, relu)
+    got = dC.numpy()
+    for x in (dA, dB, dC, dbias):
+        if x is not None:
+            x.free()
+    return got, ref
+
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("relu", [False, True])
+def test_gemm_ex_batched_bias_relu(dtype, ta, tb, relu):
+    Bt, M, N, K = 3, 70, 50, 33
+    got, ref = _ex(dtype, ta, tb, Bt, M, N, K, beta=0.5, relu=relu, seed=ta + 2 * tb + 4 * relu)
+    tol = (1e-5 * np.sqrt(K)) if dtype == "f32" else 2e-2
+    assert maxrel(got, ref) <= tol
+
+
+@pytest.mark.parametrize("share", ["A", "B"])
+def test_gemm_ex_shared_operand(share):
+    got, ref = _ex("f32", 0, 0, 4, 40, 36, 20, share=share, seed=7)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(20)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1)])
+@pytest.mark.parametrize("relu", [False, True])
+def test_gemm_ex_bf16_fast_path_batched(ta, tb, relu):
+    # 16 members of 1024 x 1024 = 256 tiles of 256 x 256: the direct-to-LDS fast path with
+    # gridDim.y batches, the bias / ReLU epilogue form.
+    Bt, M, N, K = 16, 1024, 1024, 64
+    got, ref = _ex("bf16", ta, tb, Bt, M, N, K, relu=relu, seed=40 + ta + 2 * relu)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)      # exact bf16 products, fp32 sums
+
+
+def test_gemm_ex_rejects_overlapping_batches():
+    DB = hip.DeviceBuffer
+    a, b, c = DB(4 * 64), DB(4 * 64), DB(4 * 64)
+    with pytest.raises(hip.DreamHipError):
+        hip.gemm_ex("f32", 0, 0, 4, 4, 4, a, 4, 16, b, 4, 16, 0.0, c, 4, 8, 2)
+    with pytest.raises(hip.DreamHipError):
+        hip.gemm_ex("bf16", 0, 0, 4, 4, 4, a, 4, -16, b, 4, 16, 0.0, c, 4, 16, 2)
+
+
+def test_linear_reference_golden_vectors():
+    # Y = X W^T + b (NT with the bias epilogue), and with ReLU, against the reference build's
+    # own dream_linear / dream_linear_relu outputs.
+    import os
+    G = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
+    X, W, b = (G["linear_" + c].astype(np.float32) for c in "XWb")
+    N_, K_ = X.shape
+    O_ = W.shape[0]
+    DB = hip.DeviceBuffer
+    for relu, key in ((False, "linear_Y"), (True, "linear_relu_Y")):
+        dX, dW, db, dY = DB.from_numpy(X), DB.from_numpy(W), DB.from_numpy(b.ravel()), \
+            DB.empty((N_, O_), np.float32)
+        hip.gemm_ex("f32", 0, 1, N_, O_, K_, dX, K_, 0, dW, K_, 0, 0.0, dY, O_, 0, 1, db, relu)
+        assert maxrel(dY.numpy(), G[key]) <= 1e-5 * np.sqrt(K_)
