@@ -133,6 +133,13 @@ int launch_convert(void* dst, const void* src, size_t n) {
     return check_launch("dh_convert");
 }
 
+// y += alpha x over n fp32 values (grid-stride).
+__global__ void __launch_bounds__(256) axpy_kernel(float* __restrict__ y, const float* __restrict__ x,
+                                                   float alpha, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        y[i] += alpha * x[i];
+}
+
 }  // namespace dh
 
 using namespace dh;
@@ -316,5 +323,16 @@ int dh_convert(void* dst, int dt, const void* src, int stype, size_t n) {
     return set_error(DH_ERR_UNSUPPORTED, "dh_convert: unsupported pair %d -> %d", stype, dt);
 }
 
+
+int dh_axpy(float* y, const float* x, float alpha, size_t n) {
+    DH_TRY(ensure_init());
+    if (n == 0) return DH_OK;
+    if (!y || !x) return set_error(DH_ERR_INVALID, "dh_axpy: null pointer");
+    size_t blocks = (n + 255) / 256;
+    const size_t cap = (size_t)num_cus() * 16;
+    if (blocks > cap) blocks = cap;
+    axpy_kernel<<<(unsigned)blocks, 256, 0, stream()>>>(y, x, alpha, n);
+    return check_launch("dh_axpy");
+}
 
 }  // extern "C"

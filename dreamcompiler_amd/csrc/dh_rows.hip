@@ -292,6 +292,47 @@ __global__ void __launch_bounds__(256) layer_norm_bwd_blk(const float* __restric
     }
 }
 
+// ---- linear backward: ReLU mask and bias gradient ------------------------------------------
+// Work-group (bx, by): 64 columns (one per lane, so each row's piece is one coalesced load) and
+// the rows by, by + P, by + 2P, ... split over its 4 waves.  Partial column sums go to
+// part[by][col] and a second pass adds the P partials in a fixed order: no atomics, so reruns
+// are bit-identical.
+__global__ void __launch_bounds__(256) bias_grad_partial(const float* __restrict__ Y,
+                                                         float* __restrict__ dY,
+                                                         float* __restrict__ part, int N,
+                                                         int out, int relu) {
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int col = blockIdx.x * 64 + lane;
+    const int P = gridDim.y;
+    float s = 0.f;
+    if (col < out) {
+        for (int i = blockIdx.y + P * w; i < N; i += 4 * P) {
+            const size_t e = (size_t)i * out + col;
+            float g = dY[e];
+            if (relu && !(Y[e] > 0.f)) {   // the reference zeroes dY where Y <= 0, in place
+                g = 0.f;
+                dY[e] = 0.f;
+            }
+            s += g;
+        }
+    }
+    red[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && col < out)
+        part[(size_t)blockIdx.y * out + col] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+}
+
+__global__ void __launch_bounds__(256) bias_grad_final(const float* __restrict__ part,
+                                                       float* __restrict__ db, int P, int out,
+                                                       int acc) {
+    const int col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= out) return;
+    float s = 0.f;
+    for (int p = 0; p < P; ++p) s += part[(size_t)p * out + col];
+    db[col] = acc ? db[col] + s : s;
+}
+
 // ---- dispatch --------------------------------------------------------------------------------
 constexpr int SEG_MAX_C = 1024;
 
@@ -395,6 +436,30 @@ int dh_layer_norm_bwd(const float* X, const float* Y, const float* DY, float* GX
     return SEG_DISPATCH(C, C % 4 == 0 && aligned16(X) && aligned16(Y) && aligned16(DY) &&
                                aligned16(GX),
                         launch_layer_norm_bwd, X, Y, DY, GX, R, C, accumulate);
+}
+
+int dh_linear_bias_grad(const float* Y, float* dY, float* db, int N, int out, int relu,
+                        int accumulate) {
+    DH_TRY(ensure_init());
+    if (N < 0 || out < 0) return set_error(DH_ERR_INVALID, "dh_linear_bias_grad: negative shape");
+    if (out == 0) return DH_OK;
+    if (!dY || !db || (relu && !Y))
+        return set_error(DH_ERR_INVALID, "dh_linear_bias_grad: null pointer");
+    const int cgroups = (out + 63) / 64;
+    int P = 1024 / cgroups;                       // enough work-groups to cover the chip
+    P = P < 1 ? 1 : P;
+    P = P > (N + 63) / 64 ? (N + 63) / 64 : P;    // at least 64 rows per partial
+    if (P < 1) P = 1;
+    float* part = static_cast<float*>(dh_malloc((size_t)P * out * sizeof(float)));
+    if (!part) return set_error(DH_ERR_OOM, "dh_linear_bias_grad: scratch of %d x %d", P, out);
+    bias_grad_partial<<<dim3(cgroups, P), 256, 0, stream()>>>(Y, dY, part, N, out, relu);
+    int st = check_launch("dh_linear_bias_grad");
+    if (st == DH_OK) {
+        bias_grad_final<<<(out + 255) / 256, 256, 0, stream()>>>(part, db, P, out, accumulate);
+        st = check_launch("dh_linear_bias_grad");
+    }
+    dh_free(part);   // pooled: the buffer returns to its bucket, stream order keeps it safe
+    return st;
 }
 
 }  // extern "C"

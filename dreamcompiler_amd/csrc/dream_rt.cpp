@@ -2,10 +2,18 @@
 //
 // Mirrors the reference runtime's builtin interface (names, argument meaning, +1
 // ownership, "RUNTIME ERROR in <op>" error behaviour); see include/dream_rt.h.  Every
-// GEMM and attention computation goes through include/dream_hip.h.  Tensors are host
-// fp64 (optionally with an fp32 mirror); each hot-path op stages its operands to the
-// device, runs the kernels and copies the result back, the same contract as the
-// reference's GPU branch (HostBuf + cuBLAS/OpenCL, runtime/ops/elementwise.inc:1042-1212).
+// GEMM, attention and row-wise computation goes through include/dream_hip.h.
+//
+// Data model.  Tensors are host fp64 (`data`, `grad`; optionally an fp32 mirror), and
+// generated code reads `data` directly, so every GPU result is copied home before the builtin
+// returns -- the contract of the reference's GPU branch (HostBuf + cuBLAS/OpenCL,
+// runtime/ops/elementwise.inc:1042-1212).  What stays on the device:
+//   - `dev`, an fp32 copy of `data` (the result of the op that produced the tensor, or the
+//     first upload), reused by every later GPU op while the tensor's `version` is unchanged,
+//     so chained ops and the backward pass do not upload their operands again;
+//   - `dgrad`, the gradient between GPU ops during backward(): a GPU backward op accumulates
+//     into its inputs' device gradients, the next GPU op consumes them in place, and
+//     backward() adds every device gradient into the host `grad` before it returns.
 #include "../../include/dream_rt.h"
 
 #include <algorithm>
@@ -40,7 +48,7 @@ void rt_error(const char* op, const char* fmt, ...) {
     std::fflush(stderr);
 }
 
-// Device buffer from the backend pool, returned on scope exit.
+// Device buffer from the backend pool, returned on scope exit unless released.
 struct Dev {
     void* p = nullptr;
     explicit Dev(size_t bytes) : p(dh_malloc(bytes ? bytes : 1)) {}
@@ -50,13 +58,16 @@ struct Dev {
     bool ok() const { return p != nullptr; }
     float* f() const { return static_cast<float*>(p); }
     uint16_t* h() const { return static_cast<uint16_t*>(p); }
-    double* d() const { return static_cast<double*>(p); }
+    void* release() { void* q = p; p = nullptr; return q; }
 };
 
 struct Failure {};   // thrown internally by need(), caught at the builtin boundary
 
 void need(int status) {
     if (status != DH_OK) throw Failure{};
+}
+void need_buf(const Dev& d) {
+    if (!d.ok()) throw Failure{};
 }
 
 Tensor* incref(Tensor* t) {
@@ -70,34 +81,90 @@ bool hip_ready(const char* op) {
     return false;
 }
 
-// Upload n fp64 host values as fp32 (dt = DH_F32) or bf16 (dt = DH_BF16) on the device.
-void upload(const double* h, size_t n, int dt, const Dev& out) {
-    Dev tmp(n * sizeof(double));
-    if (!tmp.ok()) throw Failure{};
-    need(dh_memcpy_h2d(tmp.p, h, n * sizeof(double)));
-    need(dh_convert(out.p, dt, tmp.p, DH_F64, n));
-}
-
-// Operand of a matmul: the live fp32 mirror when the tensor carries one.
-void upload_operand(const Tensor* t, int dt, const Dev& out) {
-    if (t->dtype == 1 && t->fdata) {
-        if (dt == DH_F32) {
-            need(dh_memcpy_h2d(out.p, t->fdata, (size_t)t->size * sizeof(float)));
-        } else {
-            Dev tmp((size_t)t->size * sizeof(float));
-            need(dh_memcpy_h2d(tmp.p, t->fdata, (size_t)t->size * sizeof(float)));
-            need(dh_convert(out.p, dt, tmp.p, DH_F32, t->size));
-        }
-    } else {
-        upload(t->data, t->size, dt, out);
+// ---- device residency ------------------------------------------------------------------
+// fp32 device copy of t->data (t->size values), uploaded (fp64 -> fp32 on the device) only
+// when there is none or `data` changed since (version).
+const float* dev_data(Tensor* t) {
+    if (t->dev && t->dev_version == t->version) return t->dev;
+    const size_t n = (size_t)t->size;
+    if (!t->dev) {
+        t->dev = static_cast<float*>(dh_malloc(n * sizeof(float)));
+        if (!t->dev) throw Failure{};
     }
+    Dev tmp(n * sizeof(double));
+    need_buf(tmp);
+    need(dh_memcpy_h2d(tmp.p, t->data, n * sizeof(double)));
+    need(dh_convert(t->dev, DH_F32, tmp.p, DH_F64, n));
+    t->dev_version = t->version;
+    return t->dev;
 }
 
-void download_f64(const Dev& src_f32, double* h, size_t n) {
+// A device fp32 result holding t's values becomes t's device copy, and is copied home.
+void adopt_result(Tensor* t, Dev& d) {
+    const size_t n = (size_t)t->size;
     Dev tmp(n * sizeof(double));
-    if (!tmp.ok()) throw Failure{};
-    need(dh_convert(tmp.p, DH_F64, src_f32.p, DH_F32, n));
-    need(dh_memcpy_d2h(h, tmp.p, n * sizeof(double)));
+    need_buf(tmp);
+    need(dh_convert(tmp.p, DH_F64, d.p, DH_F32, n));
+    need(dh_memcpy_d2h(t->data, tmp.p, n * sizeof(double)));
+    if (t->dev) dh_free(t->dev);
+    t->dev = static_cast<float*>(d.release());
+    t->dev_version = t->version;
+}
+
+// bf16 operand built on the device from the fp32 copy (round to nearest even, the rule of
+// dream_to_bf16, runtime/nn/training.inc:1969-1976).
+void dev_bf16(Tensor* t, size_t n, Dev& out) {
+    need(dh_convert(out.p, DH_BF16, dev_data(t), DH_F32, n));
+}
+
+// Device gradient accumulator of t (zero on first use).
+float* dgrad(Tensor* t) {
+    if (!t->dgrad) {
+        const size_t bytes = (size_t)t->size * sizeof(float);
+        t->dgrad = static_cast<float*>(dh_malloc(bytes));
+        if (!t->dgrad) throw Failure{};
+        need(dh_memset(t->dgrad, 0, bytes));
+    }
+    return t->dgrad;
+}
+
+// The complete incoming gradient of node t for a GPU backward op (every consumer of t has
+// run): host contributions move into t->dgrad, which holds the whole gradient until
+// backward() adds it into the host grad.
+float* grad_in(Tensor* t) {
+    float* g = dgrad(t);
+    if (!t->grad_zero) {
+        const size_t n = (size_t)t->size;
+        Dev h(n * sizeof(double)), f(n * sizeof(float));
+        need_buf(h);
+        need_buf(f);
+        need(dh_memcpy_h2d(h.p, t->grad, n * sizeof(double)));
+        need(dh_convert(f.p, DH_F32, h.p, DH_F64, n));
+        need(dh_axpy(g, f.f(), 1.f, n));
+        std::fill(t->grad, t->grad + n, 0.0);
+        t->grad_zero = 1;
+    }
+    return g;
+}
+
+// Host grad += device grad, and the device grad is released (also makes t->grad complete for
+// a host backward op).
+void flush_dgrad(Tensor* t) {
+    if (!t->dgrad) return;
+    const size_t n = (size_t)t->size;
+    std::vector<float> h(n);
+    need(dh_memcpy_d2h(h.data(), t->dgrad, n * sizeof(float)));
+    for (size_t i = 0; i < n; ++i) t->grad[i] += (double)h[i];
+    dh_free(t->dgrad);
+    t->dgrad = nullptr;
+    t->grad_zero = 0;
+}
+
+void drop_device(Tensor* t) {
+    if (t->dev) dh_free(t->dev);
+    if (t->dgrad) dh_free(t->dgrad);
+    if (t->dlse) dh_free(t->dlse);
+    t->dev = t->dgrad = t->dlse = nullptr;
 }
 
 void set_graph(Tensor* c, Tensor* l, Tensor* r, int op) {
@@ -107,9 +174,16 @@ void set_graph(Tensor* c, Tensor* l, Tensor* r, int op) {
     c->rhs = incref(r);
 }
 
+void set_parents(Tensor* c, Tensor* a, Tensor* b, Tensor* d) {
+    c->parents[0] = incref(a);
+    c->parents[1] = incref(b);
+    c->parents[2] = incref(d);
+    c->num_parents = 3;
+}
+
 int padded_dim(int dk) { return dk <= 32 ? 32 : dk <= 64 ? 64 : dk <= 128 ? 128 : -1; }
 
-// (B*S, dk) fp64 rows -> (B*S, Dp) fp32 rows with zero padding, uploaded as dt.
+// (B*S, dk) fp64 rows -> (B*S, Dp) rows with zero padding, on the device as dt.
 void upload_rows(const double* h, size_t rows, int dk, int Dp, int dt, const Dev& out) {
     std::vector<float> buf(rows * Dp, 0.f);
     for (size_t r = 0; r < rows; ++r)
@@ -118,23 +192,29 @@ void upload_rows(const double* h, size_t rows, int dk, int Dp, int dt, const Dev
         need(dh_memcpy_h2d(out.p, buf.data(), buf.size() * sizeof(float)));
     } else {
         Dev tmp(buf.size() * sizeof(float));
+        need_buf(tmp);
         need(dh_memcpy_h2d(tmp.p, buf.data(), buf.size() * sizeof(float)));
         need(dh_convert(out.p, dt, tmp.p, DH_F32, buf.size()));
     }
 }
 
-std::vector<float> download_rows_f32(const Dev& d, size_t rows, int Dp, int dt) {
+std::vector<float> download_rows_f32(const void* d, size_t rows, int Dp, int dt) {
     std::vector<float> buf(rows * Dp);
     if (dt == DH_F32) {
-        need(dh_memcpy_d2h(buf.data(), d.p, buf.size() * sizeof(float)));
+        need(dh_memcpy_d2h(buf.data(), d, buf.size() * sizeof(float)));
     } else {
         Dev tmp(buf.size() * sizeof(float));
-        need(dh_convert(tmp.p, DH_F32, d.p, dt, buf.size()));
+        need_buf(tmp);
+        need(dh_convert(tmp.p, DH_F32, d, dt, buf.size()));
         need(dh_memcpy_d2h(buf.data(), tmp.p, buf.size() * sizeof(float)));
     }
     return buf;
 }
 
+// ---- attention ---------------------------------------------------------------------------
+// Head dims 32 / 64 / 128 run on the tensors' device copies directly; other dk <= 128 are
+// zero-padded to the next kernel size on the host (zero columns of Q, K leave Q K^T
+// unchanged; zero columns of V give zero columns of O; the scale stays 1/sqrt(dk)).
 Tensor* attention_impl(const char* name, int op, bool causal, Tensor* Q, Tensor* K, Tensor* V,
                        Tensor* bt, Tensor* st, Tensor* dt_) {
     if (!Q || !K || !V || !bt || !st || !dt_) return create_scalar(0.0);
@@ -154,30 +234,46 @@ Tensor* attention_impl(const char* name, int op, bool causal, Tensor* Q, Tensor*
     Tensor* out = alloc_tensor(B, S * dk, 1, 1);
     out->is_leaf = 0;
     out->op = op;
-    out->parents[0] = incref(Q);
-    out->parents[1] = incref(K);
-    out->parents[2] = incref(V);
-    out->num_parents = 3;
+    set_parents(out, Q, K, V);
     out->attn_B = B;
     out->attn_S = S;
     out->attn_dk = dk;
-    const size_t rows = (size_t)B * S;
+    const size_t rows = (size_t)B * S, n = rows * dk;
     const int dt = g_bf16 ? DH_BF16 : DH_F32;
     const size_t esz = dt == DH_BF16 ? 2 : 4;
+    const float scale = (float)(1.0 / std::sqrt((double)dk));
     try {
-        Dev q(rows * Dp * esz), k(rows * Dp * esz), v(rows * Dp * esz), o(rows * Dp * esz);
         Dev lse(rows * sizeof(float));
-        if (!q.ok() || !k.ok() || !v.ok() || !o.ok() || !lse.ok()) throw Failure{};
-        upload_rows(Q->data, rows, dk, Dp, dt, q);
-        upload_rows(K->data, rows, dk, Dp, dt, k);
-        upload_rows(V->data, rows, dk, Dp, dt, v);
-        need(dh_flash_fwd(dt, B, S, Dp, (float)(1.0 / std::sqrt((double)dk)), causal ? 1 : 0,
-                          q.p, k.p, v.p, o.p, lse.f()));
-        std::vector<float> ob = download_rows_f32(o, rows, Dp, dt);
-        for (size_t r = 0; r < rows; ++r)
-            for (int c = 0; c < dk; ++c) out->data[r * dk + c] = (double)ob[r * Dp + c];
-        out->lse = (float*)std::malloc(rows * sizeof(float));
-        need(dh_memcpy_d2h(out->lse, lse.p, rows * sizeof(float)));
+        need_buf(lse);
+        if (Dp == dk) {
+            Dev o(n * sizeof(float));
+            need_buf(o);
+            if (dt == DH_F32) {
+                need(dh_flash_fwd(dt, B, S, dk, scale, causal ? 1 : 0, dev_data(Q), dev_data(K),
+                                  dev_data(V), o.p, lse.f()));
+            } else {
+                Dev q(n * 2), k(n * 2), v(n * 2), ob(n * 2);
+                need_buf(q), need_buf(k), need_buf(v), need_buf(ob);
+                dev_bf16(Q, n, q);
+                dev_bf16(K, n, k);
+                dev_bf16(V, n, v);
+                need(dh_flash_fwd(dt, B, S, dk, scale, causal ? 1 : 0, q.p, k.p, v.p, ob.p,
+                                  lse.f()));
+                need(dh_convert(o.p, DH_F32, ob.p, DH_BF16, n));
+            }
+            adopt_result(out, o);
+        } else {
+            Dev q(rows * Dp * esz), k(rows * Dp * esz), v(rows * Dp * esz), o(rows * Dp * esz);
+            need_buf(q), need_buf(k), need_buf(v), need_buf(o);
+            upload_rows(Q->data, rows, dk, Dp, dt, q);
+            upload_rows(K->data, rows, dk, Dp, dt, k);
+            upload_rows(V->data, rows, dk, Dp, dt, v);
+            need(dh_flash_fwd(dt, B, S, Dp, scale, causal ? 1 : 0, q.p, k.p, v.p, o.p, lse.f()));
+            std::vector<float> ob = download_rows_f32(o.p, rows, Dp, dt);
+            for (size_t r = 0; r < rows; ++r)
+                for (int c = 0; c < dk; ++c) out->data[r * dk + c] = (double)ob[r * Dp + c];
+        }
+        out->dlse = static_cast<float*>(lse.release());
     } catch (const Failure&) {
         rt_error(name, "%s", dh_last_error());
         tensor_decref(out);
@@ -189,50 +285,133 @@ Tensor* attention_impl(const char* name, int op, bool causal, Tensor* Q, Tensor*
 void attention_backward(Tensor* t, bool causal) {
     Tensor *Q = t->parents[0], *K = t->parents[1], *V = t->parents[2];
     const int B = t->attn_B, S = t->attn_S, dk = t->attn_dk, Dp = padded_dim(dk);
-    const size_t rows = (size_t)B * S;
+    const size_t rows = (size_t)B * S, n = rows * dk;
     const int dt = g_bf16 ? DH_BF16 : DH_F32;
+    const float scale = (float)(1.0 / std::sqrt((double)dk));
+    if (Dp == dk) {
+        // dO, O, Q, K, V as device copies; dQ, dK, dV accumulate into the device gradients.
+        float* g = grad_in(t);
+        if (dt == DH_F32) {
+            need(dh_flash_bwd(dt, B, S, dk, scale, causal ? 1 : 0, dev_data(Q), dev_data(K),
+                              dev_data(V), dev_data(t), g, t->dlse, dgrad(Q), dgrad(K), dgrad(V),
+                              1));
+        } else {
+            Dev q(n * 2), k(n * 2), v(n * 2), o(n * 2), gb(n * 2);
+            need_buf(q), need_buf(k), need_buf(v), need_buf(o), need_buf(gb);
+            dev_bf16(Q, n, q);
+            dev_bf16(K, n, k);
+            dev_bf16(V, n, v);
+            dev_bf16(t, n, o);
+            need(dh_convert(gb.p, DH_BF16, g, DH_F32, n));
+            need(dh_flash_bwd(dt, B, S, dk, scale, causal ? 1 : 0, q.p, k.p, v.p, o.p, gb.p,
+                              t->dlse, dgrad(Q), dgrad(K), dgrad(V), 1));
+        }
+        return;
+    }
+    flush_dgrad(t);
     const size_t esz = dt == DH_BF16 ? 2 : 4;
     Dev q(rows * Dp * esz), k(rows * Dp * esz), v(rows * Dp * esz), o(rows * Dp * esz),
-        g(rows * Dp * esz), lse(rows * sizeof(float)), dq(rows * Dp * 4), dkk(rows * Dp * 4),
-        dv(rows * Dp * 4);
-    if (!q.ok() || !k.ok() || !v.ok() || !o.ok() || !g.ok() || !lse.ok() || !dq.ok() ||
-        !dkk.ok() || !dv.ok())
-        throw Failure{};
+        g(rows * Dp * esz), dq(rows * Dp * 4), dkk(rows * Dp * 4), dv(rows * Dp * 4);
+    need_buf(q), need_buf(k), need_buf(v), need_buf(o), need_buf(g), need_buf(dq), need_buf(dkk),
+        need_buf(dv);
     upload_rows(Q->data, rows, dk, Dp, dt, q);
     upload_rows(K->data, rows, dk, Dp, dt, k);
     upload_rows(V->data, rows, dk, Dp, dt, v);
     upload_rows(t->data, rows, dk, Dp, dt, o);
     upload_rows(t->grad, rows, dk, Dp, dt, g);
-    need(dh_memcpy_h2d(lse.p, t->lse, rows * sizeof(float)));
-    need(dh_flash_bwd(dt, B, S, Dp, (float)(1.0 / std::sqrt((double)dk)), causal ? 1 : 0, q.p,
-                      k.p, v.p, o.p, g.p, lse.f(), dq.f(), dkk.f(), dv.f(), 0));
+    need(dh_flash_bwd(dt, B, S, Dp, scale, causal ? 1 : 0, q.p, k.p, v.p, o.p, g.p, t->dlse,
+                      dq.f(), dkk.f(), dv.f(), 0));
     Tensor* dst[3] = {Q, K, V};
     const Dev* src[3] = {&dq, &dkk, &dv};
     for (int x = 0; x < 3; ++x) {
-        std::vector<float> h = download_rows_f32(*src[x], rows, Dp, DH_F32);
+        flush_dgrad(dst[x]);
+        std::vector<float> h = download_rows_f32(src[x]->p, rows, Dp, DH_F32);
         for (size_t r = 0; r < rows; ++r)
             for (int c = 0; c < dk; ++c) dst[x]->grad[r * dk + c] += (double)h[r * Dp + c];
+        dst[x]->grad_zero = 0;
     }
 }
 
+// ---- GEMM-family backward ------------------------------------------------------------------
 void matmul_backward(Tensor* t) {
-    // dA += dY B^T (NT), dB += A^T dY (TN), in fp32 on the GPU, accumulated into the fp64
-    // gradients on the host (runtime/ops/autograd.inc:91-125).
+    // dA += dY B^T (NT), dB += A^T dY (TN) in fp32 on the device copies
+    // (runtime/ops/autograd.inc:91-125).
     Tensor *A = t->lhs, *B = t->rhs;
     const int M = A->d0, K = A->d1, N = B->d1;
-    Dev a((size_t)M * K * 4), b((size_t)K * N * 4), dy((size_t)M * N * 4), da((size_t)M * K * 4),
-        db((size_t)K * N * 4);
-    if (!a.ok() || !b.ok() || !dy.ok() || !da.ok() || !db.ok()) throw Failure{};
-    upload(A->data, (size_t)M * K, DH_F32, a);
-    upload(B->data, (size_t)K * N, DH_F32, b);
-    upload(t->grad, (size_t)M * N, DH_F32, dy);
-    need(dh_gemm_f32(0, 1, M, K, N, dy.f(), N, b.f(), N, 0.f, da.f(), K));
-    need(dh_gemm_f32(1, 0, K, N, M, a.f(), K, dy.f(), N, 0.f, db.f(), N));
-    std::vector<float> ha((size_t)M * K), hb((size_t)K * N);
-    need(dh_memcpy_d2h(ha.data(), da.p, ha.size() * 4));
-    need(dh_memcpy_d2h(hb.data(), db.p, hb.size() * 4));
-    for (size_t x = 0; x < ha.size(); ++x) A->grad[x] += (double)ha[x];
-    for (size_t x = 0; x < hb.size(); ++x) B->grad[x] += (double)hb[x];
+    const float* dy = grad_in(t);
+    need(dh_gemm_f32(0, 1, M, K, N, dy, N, dev_data(B), N, 1.f, dgrad(A), K));
+    need(dh_gemm_f32(1, 0, K, N, M, dev_data(A), K, dy, N, 1.f, dgrad(B), N));
+}
+
+void linear_backward(Tensor* t, bool relu) {
+    // autograd.inc:156-205: (linear_relu) dY <- 0 where Y <= 0, in place; db += colsum(dY);
+    // dX += dY W (NN); dW += dY^T X (TN).
+    Tensor *x = t->parents[0], *W = t->parents[1], *b = t->parents[2];
+    const int N = x->d0, in = x->d1, out = W->d0;
+    float* dy = grad_in(t);
+    need(dh_linear_bias_grad(relu ? dev_data(t) : nullptr, dy, dgrad(b), N, out, relu ? 1 : 0, 1));
+    need(dh_gemm_f32(0, 0, N, in, out, dy, out, dev_data(W), in, 1.f, dgrad(x), in));
+    need(dh_gemm_f32(1, 0, out, in, N, dy, out, dev_data(x), in, 1.f, dgrad(W), in));
+}
+
+void bmm_backward(Tensor* t) {
+    // autograd.inc:549-574: gA += G B^T, gB += A^T G per batch member.
+    Tensor *a = t->lhs, *b = t->rhs;
+    const int Bt = t->bmm_B, M = t->bmm_M, K = t->bmm_K, N = t->bmm_N;
+    const float* g = grad_in(t);
+    need(dh_gemm_f32_ex(0, 1, M, K, N, g, N, (long long)M * N, dev_data(b), N, (long long)K * N,
+                        1.f, dgrad(a), K, (long long)M * K, Bt, nullptr, 0));
+    need(dh_gemm_f32_ex(1, 0, K, N, M, dev_data(a), K, (long long)M * K, g, N, (long long)M * N,
+                        1.f, dgrad(b), N, (long long)K * N, Bt, nullptr, 0));
+}
+
+// Rows of the row-wise ops: softmax / layer norm take d0 rows of size/d0 (elementwise.inc:
+// 346-347, builtins.inc:174-175), log_softmax d0 rows of d1 (elementwise.inc:1556).
+void row_shape(const Tensor* t, int op, int& R, int& C) {
+    if (op == DREAM_OP_LOG_SOFTMAX) {
+        R = t->d0;
+        C = t->d1;
+    } else {
+        R = t->d0 > 0 ? t->d0 : 1;
+        C = t->size / R;
+    }
+}
+
+void row_backward(Tensor* t) {
+    Tensor* x = t->lhs;
+    int R, C;
+    row_shape(x, t->op, R, C);
+    const float* g = grad_in(t);
+    if (t->op == DREAM_OP_LAYER_NORM)
+        need(dh_layer_norm_bwd(dev_data(x), dev_data(t), g, dgrad(x), R, C, 1));
+    else
+        need(dh_row_softmax_bwd(dev_data(t), g, dgrad(x), R, C,
+                                t->op == DREAM_OP_LOG_SOFTMAX ? 1 : 0, 1));
+}
+
+Tensor* row_op(const char* name, int op, Tensor* x) {
+    if (!x) return create_scalar(0.0);
+    int R, C;
+    row_shape(x, op, R, C);
+    if (!hip_ready(name)) return alloc_tensor(1, 1, 1, 1);
+    Tensor* y = op == DREAM_OP_LOG_SOFTMAX ? alloc_tensor(x->d0, x->d1, 1, 1)
+                                           : alloc_tensor(x->d0, x->d1, x->d2, x->d3);
+    set_graph(y, x, nullptr, op);
+    try {
+        Dev d((size_t)y->size * sizeof(float));
+        need_buf(d);
+        if ((size_t)R * C < (size_t)y->size) need(dh_memset(d.p, 0, (size_t)y->size * sizeof(float)));
+        if (op == DREAM_OP_LAYER_NORM)
+            need(dh_layer_norm(dev_data(x), d.f(), R, C));
+        else
+            need(dh_row_softmax(dev_data(x), d.f(), R, C, op == DREAM_OP_LOG_SOFTMAX ? 1 : 0));
+        adopt_result(y, d);
+    } catch (const Failure&) {
+        rt_error(name, "%s", dh_last_error());
+        tensor_decref(y);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    return y;
 }
 
 void topo_sort(Tensor* root, std::vector<Tensor*>& order) {
@@ -315,6 +494,7 @@ Tensor* alloc_tensor(int d0, int d1, int d2, int d3) {
     t->d3 = d3;
     t->refcount = 1;
     t->is_leaf = 1;
+    t->grad_zero = 1;
     return t;
 }
 
@@ -331,11 +511,11 @@ Tensor* tensor_decref(Tensor* t) {
     tensor_decref(t->lhs);
     tensor_decref(t->rhs);
     for (int i = 0; i < t->num_parents; ++i) tensor_decref(t->parents[i]);
+    drop_device(t);
     std::free(t->data);
     std::free(t->grad);
     std::free(t->fdata);
     std::free(t->fgrad);
-    std::free(t->lse);
     std::free(t);
     return nullptr;
 }
@@ -398,6 +578,9 @@ Tensor* zero_grad(Tensor* t) {
         return nullptr;
     }
     std::fill(t->grad, t->grad + t->size, 0.0);
+    if (t->dgrad) dh_free(t->dgrad);
+    t->dgrad = nullptr;
+    t->grad_zero = 1;
     Tensor *l = t->lhs, *r = t->rhs;
     t->lhs = t->rhs = nullptr;
     tensor_decref(l);
@@ -405,6 +588,48 @@ Tensor* zero_grad(Tensor* t) {
     for (int i = 0; i < t->num_parents; ++i) tensor_decref(t->parents[i]);
     t->num_parents = 0;
     return incref(t);
+}
+
+Tensor* tensor_set_element(Tensor* t, Tensor* idx_t, Tensor* val) {
+    // runtime/core/indexing.inc:50-94: a flat write for vectors and 1 x N tensors, else the
+    // row idx along d0 (copying min(val.size, row) values); negative indices wrap.
+    if (!t || !idx_t || !val) return t;
+    int idx = (int)idx_t->data[0];
+    const bool inner = t->d1 > 1 || t->d2 > 1 || t->d3 > 1;
+    const int slice = t->d1 * t->d2 * t->d3;
+    const int extent = !inner ? t->d0 : (t->d0 == 1 && idx != 0) ? slice : t->d0;
+    if (idx < 0) idx += extent;
+    if (idx < 0 || idx >= extent) {
+        std::fprintf(stderr, "runtime error: set index %d out of bounds (size %d)\n",
+                     (int)idx_t->data[0], extent);
+        return t;
+    }
+    if (!inner || (t->d0 == 1 && (int)idx_t->data[0] != 0)) {
+        t->data[idx] = val->data[0];
+    } else {
+        const int n = std::min(val->size, slice);
+        std::copy(val->data, val->data + n, t->data + (size_t)idx * slice);
+    }
+    ++t->version;   // the device copy of `data` is stale from here on
+    return t;
+}
+
+Tensor* tensor_set_element_2d(Tensor* t, Tensor* row_t, Tensor* col_t, Tensor* val) {
+    // runtime/core/indexing.inc:97-113
+    if (!t || !row_t || !col_t || !val) return t;
+    int row = (int)row_t->data[0], col = (int)col_t->data[0];
+    const int cols = t->d1;
+    if (row < 0) row += t->d0;
+    if (col < 0) col += cols;
+    const long long flat = (long long)row * cols + col;
+    if (flat < 0 || flat >= t->size) {
+        std::fprintf(stderr, "runtime error: index [%d, %d] out of bounds\n", (int)row_t->data[0],
+                     (int)col_t->data[0]);
+        return t;
+    }
+    t->data[flat] = val->data[0];
+    ++t->version;
+    return t;
 }
 
 // ----------------------------------------------------------------------------- precision
@@ -418,8 +643,10 @@ Tensor* dream_set_precision(Tensor* t, int code) {
             t->dtype = 1;
         }
     } else {
-        if (t->dtype == 1 && t->fdata)
+        if (t->dtype == 1 && t->fdata) {
             for (int i = 0; i < t->size; ++i) t->data[i] = (double)t->fdata[i];
+            ++t->version;
+        }
         t->dtype = 0;
     }
     return incref(t);
@@ -435,6 +662,7 @@ Tensor* dream_to_float32(Tensor* t) {
         t->fgrad[i] = (float)t->grad[i];
     }
     t->dtype = 1;
+    ++t->version;
     return incref(t);
 }
 
@@ -472,19 +700,15 @@ Tensor* tensor_matmul(Tensor* a, Tensor* b) {
     try {
         const size_t mk = (size_t)M * K, kn = (size_t)K * N, mn = (size_t)M * N;
         Dev dc(mn * 4);
-        if (!dc.ok()) throw Failure{};
+        need_buf(dc);
         if (g_bf16 && !f32) {
             Dev da(mk * 2), db(kn * 2);
-            if (!da.ok() || !db.ok()) throw Failure{};
-            upload_operand(a, DH_BF16, da);
-            upload_operand(b, DH_BF16, db);
+            need_buf(da), need_buf(db);
+            dev_bf16(a, mk, da);
+            dev_bf16(b, kn, db);
             need(dh_gemm_bf16(0, 0, M, N, K, da.h(), K, db.h(), N, 0.f, dc.f(), N));
         } else {
-            Dev da(mk * 4), db(kn * 4);
-            if (!da.ok() || !db.ok()) throw Failure{};
-            upload_operand(a, DH_F32, da);
-            upload_operand(b, DH_F32, db);
-            need(dh_gemm_f32(0, 0, M, N, K, da.f(), K, db.f(), N, 0.f, dc.f(), N));
+            need(dh_gemm_f32(0, 0, M, N, K, dev_data(a), K, dev_data(b), N, 0.f, dc.f(), N));
         }
         if (f32) {
             // fp32 result: fdata is the live copy, data its fp64 mirror (elementwise.inc:1000-1017)
@@ -492,10 +716,8 @@ Tensor* tensor_matmul(Tensor* a, Tensor* b) {
             c->fgrad = (float*)std::calloc(c->size, sizeof(float));
             c->dtype = 1;
             need(dh_memcpy_d2h(c->fdata, dc.p, mn * 4));
-            for (size_t i = 0; i < mn; ++i) c->data[i] = (double)c->fdata[i];
-        } else {
-            download_f64(dc, c->data, mn);
         }
+        adopt_result(c, dc);
     } catch (const Failure&) {
         rt_error("matmul (@)", "%s", dh_last_error());
         tensor_decref(c);
@@ -519,32 +741,129 @@ Tensor* dream_attention_causal(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, T
     return attention_impl("attention_causal", DREAM_OP_ATTN_CAUSAL, true, Q, K, V, batch, seq, dk);
 }
 
+static Tensor* linear_impl(Tensor* x, Tensor* W, Tensor* b, bool relu) {
+    // elementwise.inc:1432-1516.  Both forms report errors as "linear", like the reference
+    // (linear_relu calls linear and then relabels the node).
+    if (!x || !W || !b) {
+        std::fprintf(stderr, "RUNTIME ERROR in linear: null arg%s%s%s\n", x ? "" : " x=null",
+                     W ? "" : " W=null", b ? "" : " b=null");
+        std::fflush(stderr);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    const int N = x->d0, in = x->d1, out = W->d0;
+    if (in != W->d1) {
+        rt_error("linear", "x.d1(%d) != W.d1(%d)", in, W->d1);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    if (b->size < out) {
+        rt_error("linear", "bias holds %d values for %d outputs", b->size, out);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    if (!hip_ready("linear")) return alloc_tensor(1, 1, 1, 1);
+    Tensor* y = alloc_tensor(N, out, 1, 1);
+    set_graph(y, x, W, relu ? DREAM_OP_LINEAR_RELU : DREAM_OP_LINEAR);
+    set_parents(y, x, W, b);
+    try {
+        Dev d((size_t)N * out * sizeof(float));
+        need_buf(d);
+        need(dh_gemm_f32_ex(0, 1, N, out, in, dev_data(x), in, 0, dev_data(W), in, 0, 0.f, d.f(),
+                            out, 0, 1, dev_data(b), relu ? 1 : 0));
+        adopt_result(y, d);
+    } catch (const Failure&) {
+        rt_error("linear", "%s", dh_last_error());
+        tensor_decref(y);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    return y;
+}
+
+Tensor* dream_linear(Tensor* x, Tensor* W, Tensor* b) { return linear_impl(x, W, b, false); }
+Tensor* dream_linear_relu(Tensor* x, Tensor* W, Tensor* b) { return linear_impl(x, W, b, true); }
+Tensor* linear(Tensor* x, Tensor* W, Tensor* b) { return dream_linear(x, W, b); }
+Tensor* linear_relu(Tensor* x, Tensor* W, Tensor* b) { return dream_linear_relu(x, W, b); }
+
+Tensor* dream_bmm(Tensor* a, Tensor* b, Tensor* batch_t, Tensor* m_t, Tensor* k_t, Tensor* n_t) {
+    // elementwise.inc:1218-1252: a (B, M*K) @ b (B, K*N) -> (B, M*N) per batch member.
+    const int Bt = (int)batch_t->data[0], M = (int)m_t->data[0], K = (int)k_t->data[0],
+              N = (int)n_t->data[0];
+    if (a->size < Bt * M * K || b->size < Bt * K * N) {
+        std::fprintf(stderr, "error: bmm size mismatch (a=%d need %d, b=%d need %d)\n", a->size,
+                     Bt * M * K, b->size, Bt * K * N);
+        std::fflush(stderr);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    if (!hip_ready("bmm")) return alloc_tensor(1, 1, 1, 1);
+    Tensor* c = alloc_tensor(Bt, M * N, 1, 1);
+    set_graph(c, a, b, DREAM_OP_BMM);
+    c->bmm_B = Bt;
+    c->bmm_M = M;
+    c->bmm_K = K;
+    c->bmm_N = N;
+    try {
+        Dev d((size_t)c->size * sizeof(float));
+        need_buf(d);
+        need(dh_gemm_f32_ex(0, 0, M, N, K, dev_data(a), K, (long long)M * K, dev_data(b), N,
+                            (long long)K * N, 0.f, d.f(), N, (long long)M * N, Bt, nullptr, 0));
+        adopt_result(c, d);
+    } catch (const Failure&) {
+        rt_error("bmm", "%s", dh_last_error());
+        tensor_decref(c);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    return c;
+}
+
+Tensor* dream_softmax(Tensor* a) { return row_op("softmax", DREAM_OP_SOFTMAX, a); }
+Tensor* dream_log_softmax(Tensor* x) { return row_op("log_softmax", DREAM_OP_LOG_SOFTMAX, x); }
+Tensor* dream_layer_norm(Tensor* t) { return row_op("layer_norm", DREAM_OP_LAYER_NORM, t); }
+
 Tensor* backward(Tensor* root) {
     if (!root) {
         std::fprintf(stderr, "error: backward(null)\n");
         return create_scalar(0);
     }
     std::fill(root->grad, root->grad + root->size, 1.0);
+    root->grad_zero = 0;
     std::vector<Tensor*> order;
     topo_sort(root, order);
+    // A host backward op first takes its node's device gradient (flush_dgrad); a GPU backward
+    // op first moves the host part onto the device (grad_in).
+    auto host_grad = [](Tensor* t) {
+        flush_dgrad(t);
+        if (t->lhs) t->lhs->grad_zero = 0;
+        if (t->rhs) t->rhs->grad_zero = 0;
+    };
     for (int x = (int)order.size() - 1; x >= 0; --x) {
         Tensor* t = order[x];
         try {
             switch (t->op) {
                 case DREAM_OP_MATMUL:
-                    if (!hip_ready("backward(matmul)")) break;
-                    matmul_backward(t);
+                    if (hip_ready("backward(matmul)")) matmul_backward(t);
+                    break;
+                case DREAM_OP_LINEAR:
+                case DREAM_OP_LINEAR_RELU:
+                    if (hip_ready("backward(linear)")) linear_backward(t, t->op == DREAM_OP_LINEAR_RELU);
+                    break;
+                case DREAM_OP_BMM:
+                    if (hip_ready("backward(bmm)")) bmm_backward(t);
+                    break;
+                case DREAM_OP_SOFTMAX:
+                case DREAM_OP_LOG_SOFTMAX:
+                case DREAM_OP_LAYER_NORM:
+                    if (hip_ready("backward(row op)")) row_backward(t);
                     break;
                 case DREAM_OP_FLASH:
                 case DREAM_OP_ATTN_CAUSAL:
                 case DREAM_OP_ATTN:
-                    if (!t->lse || !hip_ready("backward(attention)")) break;
-                    attention_backward(t, t->op != DREAM_OP_ATTN);
+                    if (t->dlse && hip_ready("backward(attention)"))
+                        attention_backward(t, t->op != DREAM_OP_ATTN);
                     break;
                 case DREAM_OP_SUM:
+                    host_grad(t);
                     for (int j = 0; j < t->lhs->size; ++j) t->lhs->grad[j] += t->grad[0];
                     break;
                 case DREAM_OP_MUL:
+                    host_grad(t);
                     for (int j = 0; j < t->size; ++j) {
                         const double g = t->grad[j];
                         t->lhs->grad[j % t->lhs->size] += g * t->rhs->data[j % t->rhs->size];
@@ -552,6 +871,7 @@ Tensor* backward(Tensor* root) {
                     }
                     break;
                 case DREAM_OP_ADD:
+                    host_grad(t);
                     for (int j = 0; j < t->size; ++j) {
                         t->lhs->grad[j % t->lhs->size] += t->grad[j];
                         t->rhs->grad[j % t->rhs->size] += t->grad[j];
@@ -560,6 +880,14 @@ Tensor* backward(Tensor* root) {
                 default:
                     break;
             }
+        } catch (const Failure&) {
+            rt_error("backward", "%s", dh_last_error());
+        }
+    }
+    // Every gradient back on the host (the reference's grad buffers are host memory).
+    for (Tensor* t : order) {
+        try {
+            flush_dgrad(t);
         } catch (const Failure&) {
             rt_error("backward", "%s", dh_last_error());
         }

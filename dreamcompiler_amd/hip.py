@@ -44,6 +44,7 @@ _SIGS = {
     "dh_timer_start": (_i, []),
     "dh_timer_stop": (_i, [ctypes.POINTER(_f)]),
     "dh_convert": (_i, [_vp, _i, _vp, _i, _sz]),
+    "dh_axpy": (_i, [_vp, _vp, _f, _sz]),
     "dh_gemm_f32": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i]),
     "dh_gemm_bf16": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _f, _vp, _i]),
     "dh_gemm_f32_ex": (_i, [_i, _i, _i, _i, _i, _vp, _i, _ll, _vp, _i, _ll, _f, _vp, _i, _ll,
@@ -57,6 +58,7 @@ _SIGS = {
     "dh_row_softmax_bwd": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "dh_layer_norm": (_i, [_vp, _vp, _i, _i]),
     "dh_layer_norm_bwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+    "dh_linear_bias_grad": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -164,6 +166,10 @@ def convert(dst, dst_type, src, src_type, n):
     check(load().dh_convert(_p(dst), dst_type, _p(src), src_type, int(n)), "dh_convert")
 
 
+def axpy(y, x, alpha, n):
+    check(load().dh_axpy(_p(y), _p(x), float(alpha), int(n)), "dh_axpy")
+
+
 def gemm_f32(transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc):
     check(load().dh_gemm_f32(int(transA), int(transB), M, N, K, _p(A), lda, _p(B), ldb,
                              float(beta), _p(C), ldc), "dh_gemm_f32")
@@ -205,6 +211,11 @@ def row_softmax_bwd(Y, G, GX, R, C, log=False, accumulate=False):
 
 def layer_norm(X, Y, R, C):
     check(load().dh_layer_norm(_p(X), _p(Y), R, C), "dh_layer_norm")
+
+
+def linear_bias_grad(Y, dY, db, N, out, relu=False, accumulate=False):
+    check(load().dh_linear_bias_grad(_p(Y) if Y is not None else None, _p(dY), _p(db), N, out,
+                                     int(relu), int(accumulate)), "dh_linear_bias_grad")
 
 
 def layer_norm_bwd(X, Y, DY, GX, R, C, accumulate=False):

@@ -86,6 +86,9 @@ int dh_timer_stop(float* ms);              /* synchronous */
  * dream_to_bf16, runtime/nn/training.inc:1969-1976), F32->BF16, BF16->F32, and F32->F32
  * (a plain device copy). */
 int dh_convert(void* d_dst, int dst_type, const void* d_src, int src_type, size_t n);
+/* y[i] += alpha * x[i] for n fp32 values: merges gradient contributions on the device (the
+ * reference's host "+=" accumulation of a node's gradient, runtime/ops/autograd.inc:26-887). */
+int dh_axpy(float* d_y, const float* d_x, float alpha, size_t n);
 
 /* ---- GEMM -------------------------------------------------------------------
  * C[M x N] = op(A) @ op(B) + beta * C, fp32 accumulate, fp32 C.
@@ -165,6 +168,12 @@ int dh_layer_norm(const float* d_X, float* d_Y, int R, int C);
  * GX (+)= inv_std / C (C DY - rowsum(DY) - Y rowsum(DY Y)). */
 int dh_layer_norm_bwd(const float* d_X, const float* d_Y, const float* d_DY, float* d_GX,
                       int R, int C, int accumulate);
+/* Bias gradient of a linear layer Y (N x out): db (+)= column sums of dY.  With relu != 0
+ * dY is first zeroed where Y <= 0, in place -- the linear_relu backward, which masks the
+ * node's own gradient the same way (runtime/ops/autograd.inc:156-183).  Deterministic (no
+ * floating-point atomics).  Y may be NULL when relu == 0. */
+int dh_linear_bias_grad(const float* d_Y, float* d_dY, float* d_db, int N, int out, int relu,
+                        int accumulate);
 
 #ifdef __cplusplus
 }

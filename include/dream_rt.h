@@ -38,15 +38,28 @@ typedef struct Tensor {
     struct Tensor* parents[3];
     int num_parents;
     int attn_B, attn_S, attn_dk;   /* "B,S,dk" of an attention node (bwd_name)    */
+    int bmm_B, bmm_M, bmm_K, bmm_N;   /* "B,M,K,N" of a bmm node (bwd_name)       */
     int dtype;                 /* 0 = fp64 storage, 1 = live fp32 mirror (as f32)  */
     float* fdata;              /* fp32 mirror when dtype == 1                      */
     float* fgrad;
-    float* lse;                /* attention nodes: per-row log-sum-exp (B*S)       */
+    /* Device residency.  `data` is always current (generated code reads it directly,
+     * src/AST.cpp:160-172, 862-870), so results are copied home before a builtin returns;
+     * `dev` is a device fp32 copy of `data` that later GPU ops reuse instead of uploading
+     * again.  It is valid while dev_version == version: every in-place mutation of `data`
+     * increments `version` (the reference's own mutation counter, runtime/runtime.h:76,
+     * bumped by its mutating builtins, runtime/io/builtins.inc:295-445). */
+    int version;
+    float* dev;                /* device fp32 copy of data, or NULL                */
+    int dev_version;
+    float* dgrad;              /* device fp32 gradient during backward(), or NULL  */
+    int grad_zero;             /* 1 while every host grad value is known to be 0   */
+    float* dlse;               /* attention nodes: device per-row log-sum-exp (B*S) */
 } Tensor;
 
 enum {
     DREAM_OP_LEAF = 0, DREAM_OP_MATMUL, DREAM_OP_FLASH, DREAM_OP_ATTN, DREAM_OP_ATTN_CAUSAL,
-    DREAM_OP_SUM, DREAM_OP_MUL, DREAM_OP_ADD
+    DREAM_OP_SUM, DREAM_OP_MUL, DREAM_OP_ADD, DREAM_OP_LINEAR, DREAM_OP_LINEAR_RELU,
+    DREAM_OP_BMM, DREAM_OP_SOFTMAX, DREAM_OP_LOG_SOFTMAX, DREAM_OP_LAYER_NORM
 };
 
 /* ---- tensors (runtime/core/tensor.inc:143-303) ---- */
@@ -62,6 +75,10 @@ Tensor* tensor_add(Tensor* a, Tensor* b);
 Tensor* tensor_mul(Tensor* a, Tensor* b);
 Tensor* tensor_get_grad(Tensor* t);                        /* autograd.inc:1-14     */
 Tensor* zero_grad(Tensor* t);                              /* autograd.inc:15-24    */
+/* t[i] = v and t[i][j] = v (runtime/io/builtins.inc:286-317): the in-place writes of
+ * generated code (src/AST.cpp:1702-1740); they bump `version`. */
+Tensor* tensor_set_element(Tensor* t, Tensor* idx, Tensor* v);
+Tensor* tensor_set_element_2d(Tensor* t, Tensor* i, Tensor* j, Tensor* v);
 
 /* ---- precision (runtime/io/builtins.inc:1168-1184, 380-394, 465-475) ---- */
 Tensor* dream_set_precision(Tensor* t, int code);          /* `as f32` (1) / `as f64` (0) */
@@ -80,8 +97,25 @@ Tensor* dream_flash_attention(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Te
 Tensor* dream_attention(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq, Tensor* dk);
 Tensor* dream_attention_causal(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq,
                                Tensor* dk);
+/* The other GEMM callers and the row-wise ops, on the GPU with their backward:
+ *   Y = x W^T + b, W stored out x in; linear_relu clamps Y < 0 to 0 (one GEMM with a fused
+ *   bias / ReLU epilogue; runtime/ops/elementwise.inc:1432-1516, autograd.inc:156-205);
+ *   batched C[b] = A[b] B[b] with A (B, M*K), B (B, K*N), scalars as 1x1 tensors
+ *   (elementwise.inc:1218-1252, autograd.inc:549-574);
+ *   row softmax over d0 rows (elementwise.inc:338-358, autograd.inc:396-409), log_softmax over
+ *   d0 x d1 (elementwise.inc:1550-1570, autograd.inc:212-233), row layer norm without affine
+ *   terms, eps 1e-5 (runtime/io/builtins.inc:167-188, autograd.inc:453-471). */
+Tensor* dream_linear(Tensor* x, Tensor* W, Tensor* b);
+Tensor* dream_linear_relu(Tensor* x, Tensor* W, Tensor* b);
+Tensor* linear(Tensor* x, Tensor* W, Tensor* b);          /* aliases, elementwise.inc:1520 */
+Tensor* linear_relu(Tensor* x, Tensor* W, Tensor* b);
+Tensor* dream_bmm(Tensor* a, Tensor* b, Tensor* batch, Tensor* m, Tensor* k, Tensor* n);
+Tensor* dream_softmax(Tensor* a);
+Tensor* dream_log_softmax(Tensor* x);
+Tensor* dream_layer_norm(Tensor* t);
 /* Reverse sweep from root (runtime/ops/autograd.inc:26-887) for the node kinds above;
- * gradients accumulate ("+=") into grad buffers like the reference. */
+ * gradients accumulate ("+=") into grad buffers like the reference.  Between two GPU ops a
+ * gradient stays on the device; every grad buffer is current on the host when it returns. */
 Tensor* backward(Tensor* root);
 
 /* ---- backend queries, selftests (runtime/backend/gpu.inc:271-273,

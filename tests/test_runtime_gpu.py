@@ -4,6 +4,8 @@ Each test restates one of the reference's own tests (tests/*.dream) or selftests
 and adds parity against the fp64 oracle.  fp32 tolerance: normwise max relative error
 <= 1e-5 * sqrt(K) (K = contraction length); bf16: <= 2e-2 on bf16-rounded inputs.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -142,3 +144,130 @@ def test_determinism_16(L):
         return rt.read(C), rt.read(o), rt.read(Q, grad=True), rt.read(K, grad=True)
     for a, b in zip(run(), run()):
         assert np.array_equal(a, b)
+
+
+# --------------------------------------------------------------------------- other GEMM callers
+
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
+
+
+def _grads_through(L, out, G, *ins):
+    """backward(sum(out * G)) through the runtime; returns the .grad of each input and of out."""
+    L.backward(L.sum(L.tensor_mul(out, rt.tensor(G))))
+    return tuple(rt.read(t, grad=True) for t in ins) + (rt.read(out, grad=True),)
+
+
+@pytest.mark.parametrize("relu", [False, True])
+def test_linear_against_reference_golden(L, relu):
+    # The reference build's own dream_linear / dream_linear_relu and their backward
+    # (tests/golden: X 9x13, W 11x13, b 1x11, upstream G 9x11), fp32 bound 1e-5 sqrt(K).
+    X, W, b, G = (GOLD["linear_" + c] for c in "XWbG")
+    key = "linear_relu" if relu else "linear"
+    x, w, bb = rt.tensor(X), rt.tensor(W), rt.tensor(b)
+    y = (L.dream_linear_relu if relu else L.dream_linear)(x, w, bb)
+    assert maxrel(rt.read(y), GOLD[key + "_Y"]) <= 1e-5 * np.sqrt(13)
+    dX, dW, db, dY = _grads_through(L, y, G, x, w, bb)
+    assert maxrel(dX, GOLD[key + "_dX"]) <= 1e-5 * np.sqrt(11)
+    assert maxrel(dW, GOLD[key + "_dW"]) <= 1e-5 * np.sqrt(9)
+    assert maxrel(db, GOLD[key + "_db"]) <= 1e-5 * np.sqrt(9)
+    assert maxrel(dY, GOLD[key + "_dY"]) <= 1e-6        # the node's own (masked) gradient
+
+
+def test_linear_mlp_c2_against_oracle(L):
+    # Config 2 through the fused builtins: h = linear_relu(X, W1^T, b1), y = linear(h, W2^T, b2),
+    # loss = sum(y * G); every gradient against the fp64 oracle.
+    rng = np.random.default_rng(2)
+    X = rng.uniform(0, 1, (4096, 784))
+    W1, W2 = rng.standard_normal((257, 784)) * np.sqrt(2 / 784), rng.standard_normal((10, 257)) * np.sqrt(2 / 257)
+    b1, b2 = rng.standard_normal(257) * 0.1, rng.standard_normal(10) * 0.1
+    G = rng.standard_normal((4096, 10))
+    H = O.linear(X, W1, b1, relu=True)
+    Y = O.linear(H, W2, b2)
+    dY2, dH, dW2, db2 = O.linear_bwd(H, W2, Y, G)
+    _, dX, dW1, db1 = O.linear_bwd(X, W1, H, dH, relu=True)
+    x, w1, bb1, w2, bb2 = (rt.tensor(a) for a in (X, W1, b1, W2, b2))
+    h = L.dream_linear_relu(x, w1, bb1)
+    y = L.dream_linear(h, w2, bb2)
+    assert maxrel(rt.read(h), H) <= 1e-5 * np.sqrt(784)
+    assert maxrel(rt.read(y), Y) <= 1e-5 * np.sqrt(784)
+    gx, gw1, gb1, gw2, gb2, _ = _grads_through(L, y, G, x, w1, bb1, w2, bb2)
+    for got, ref, K in ((gx, dX, 257), (gw1, dW1, 4096), (gb1, db1, 4096), (gw2, dW2, 4096),
+                        (gb2, db2, 4096)):
+        assert maxrel(got.reshape(ref.shape), ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_bmm_against_reference_golden(L):
+    A, B, G = GOLD["bmm_A"], GOLD["bmm_B"], GOLD["bmm_G"]
+    a, b = rt.tensor(A), rt.tensor(B)
+    c = L.dream_bmm(a, b, *(rt.scalar(v) for v in (3, 5, 7, 6)))
+    assert maxrel(rt.read(c), GOLD["bmm_C"]) <= 1e-5 * np.sqrt(7)
+    dA, dB, _ = _grads_through(L, c, G, a, b)
+    assert maxrel(dA, GOLD["bmm_dA"]) <= 1e-5 * np.sqrt(6)
+    assert maxrel(dB, GOLD["bmm_dB"]) <= 1e-5 * np.sqrt(5)
+
+
+def test_bmm_size_mismatch_message(L, capfd):
+    c = L.dream_bmm(rt.tensor(np.ones((2, 5))), rt.tensor(np.ones((2, 6))),
+                    *(rt.scalar(v) for v in (2, 2, 3, 2)))
+    assert rt.read(c).shape == (1, 1)
+    assert "error: bmm size mismatch (a=10 need 12, b=12 need 12)" in capfd.readouterr().err
+
+
+@pytest.mark.parametrize("op", ["softmax", "log_softmax", "layer_norm"])
+def test_row_builtins_against_reference_golden(L, op):
+    if op == "layer_norm":
+        X, G, Yk, dk = GOLD["layer_norm_X"], GOLD["layer_norm_G"], "layer_norm_Y", "layer_norm_dX"
+        fn = L.dream_layer_norm
+    else:
+        X, G = GOLD["softmax_X"], GOLD["softmax_G"]
+        Yk, dk = (op + "_Y"), ("softmax_dX" if op == "softmax" else "log_softmax_dX")
+        fn = L.dream_softmax if op == "softmax" else L.dream_log_softmax
+    x = rt.tensor(X)
+    y = fn(x)
+    C = X.shape[1]
+    assert np.abs(rt.read(y) - GOLD[Yk]).max() <= 1e-5 * np.sqrt(C) * max(1, np.abs(GOLD[Yk]).max())
+    dX, _ = _grads_through(L, y, G, x)
+    assert np.abs(dX - GOLD[dk]).max() <= 1e-5 * np.sqrt(C) * max(1, np.abs(GOLD[dk]).max())
+
+
+def test_device_copy_follows_in_place_writes(L):
+    # A's device copy is reused by the second product only while A is unchanged: an index
+    # assignment (tensor_set_element_2d bumps the version) must be seen by the next `@`.
+    rng = np.random.default_rng(3)
+    A0, B0 = rng.standard_normal((64, 32)), rng.standard_normal((32, 48))
+    a, b = rt.tensor(A0), rt.tensor(B0)
+    c1 = rt.read(L.tensor_matmul(a, b))
+    assert maxrel(c1, A0 @ B0) <= 1e-5 * np.sqrt(32)
+    L.tensor_set_element_2d(a, rt.scalar(3), rt.scalar(5), rt.scalar(7.0))
+    A1 = A0.copy()
+    A1[3, 5] = 7.0
+    c2 = rt.read(L.tensor_matmul(a, b))
+    assert maxrel(c2, A1 @ B0) <= 1e-5 * np.sqrt(32)
+    L.tensor_set_element(a, rt.scalar(-1), rt.tensor(np.arange(32.0)))   # last row
+    A1[-1] = np.arange(32.0)
+    c3 = rt.read(L.tensor_matmul(a, b))
+    assert maxrel(c3, A1 @ B0) <= 1e-5 * np.sqrt(32)
+
+
+def test_chained_gpu_graph_with_host_ops_gradients(L):
+    # Gradients between GPU ops stay on the device; host ops in the middle (mul, add) must
+    # see them.  loss = sum(layer_norm(softmax(((a*s) @ W) + c)) * G) against oracle/numpy.
+    rng = np.random.default_rng(4)
+    A, S, W, Cb, G = (rng.standard_normal(sh) for sh in ((16, 24), (16, 24), (24, 40), (16, 40), (16, 40)))
+    a, s, w, cb = (rt.tensor(x) for x in (A, S, W, Cb))
+    h = L.tensor_mul(a, s)
+    p = L.tensor_matmul(h, w)
+    q = L.tensor_add(p, cb)
+    r = L.dream_softmax(q)
+    y = L.dream_layer_norm(r)
+    ga, gs, gw, gc, _ = _grads_through(L, y, G, a, s, w, cb)
+    H = A * S
+    Q = H @ W + Cb
+    R = O.softmax_rows(Q)
+    Y = O.layer_norm(R)
+    gR = O.layer_norm_bwd(R, Y, G)
+    gQ = O.softmax_bwd(R, gR)
+    gW = H.T @ gQ
+    gH = gQ @ W.T
+    for got, ref in ((gw, gW), (gc, gQ), (ga, gH * S), (gs, gH * A)):
+        assert maxrel(got, ref) <= 1e-4
