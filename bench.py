@@ -105,6 +105,53 @@ def flash_workload(dtype, BH, S, D, causal, backward=False, seed=1):
     return step, 2.5 * fwd_flops, 5 * BH * S * D * elt + 3 * BH * S * D * 4 + 8 * BH * S, bufs
 
 
+def rows_workload(op, R, C, seed=4):
+    """Row-wise ops (HBM-bound): algorithmic bytes = every input read once + the output written
+    once (fp32)."""
+    rng = np.random.default_rng(seed)
+    X = DB.from_numpy(rng.standard_normal((R, C), dtype=np.float32))
+    Y, G, GX = (DB.empty((R, C), np.float32) for _ in range(3))
+    hip.row_softmax(X, Y, R, C)
+    G2 = DB.from_numpy(rng.standard_normal((R, C), dtype=np.float32))
+    n = 4.0 * R * C
+    if op == "softmax_fwd":
+        step, byts = (lambda: hip.row_softmax(X, Y, R, C)), 2 * n
+    elif op == "softmax_bwd":
+        step, byts = (lambda: hip.row_softmax_bwd(Y, G2, GX, R, C)), 3 * n
+    elif op == "layer_norm_fwd":
+        step, byts = (lambda: hip.layer_norm(X, Y, R, C)), 2 * n
+    else:   # layer_norm_bwd: X, Y, dY read, dX written
+        hip.layer_norm(X, Y, R, C)
+        step, byts = (lambda: hip.layer_norm_bwd(X, Y, G2, GX, R, C)), 4 * n
+    return step, 0.0, byts, [X, Y, G, GX, G2]
+
+
+def linear_workload(N, IN, OUT, relu=True, seed=6):
+    """Fused linear layer Y = relu(X W^T + b) (dream_linear_relu) as one GEMM with the bias /
+    ReLU epilogue, fp32."""
+    rng = np.random.default_rng(seed)
+    X = DB.from_numpy(rng.uniform(0, 1, (N, IN)).astype(np.float32))
+    W = DB.from_numpy((rng.standard_normal((OUT, IN)) * np.sqrt(2 / IN)).astype(np.float32))
+    b = DB.from_numpy(rng.standard_normal(OUT).astype(np.float32))
+    Y = DB.empty((N, OUT), np.float32)
+
+    def step():
+        hip.gemm_ex("f32", 0, 1, N, OUT, IN, X, IN, 0, W, IN, 0, 0.0, Y, OUT, 0, 1, b, relu)
+    return step, 2.0 * N * IN * OUT, 4.0 * (N * IN + OUT * IN + OUT + N * OUT), [X, W, b, Y]
+
+
+def bmm_workload(Bt, M, N, K, seed=7):
+    """dream_bmm as one batched fp32 GEMM launch (gridDim.y = batch member)."""
+    rng = np.random.default_rng(seed)
+    A = DB.from_numpy(rng.standard_normal((Bt, M * K), dtype=np.float32))
+    B = DB.from_numpy(rng.standard_normal((Bt, K * N), dtype=np.float32))
+    C = DB.empty((Bt, M * N), np.float32)
+
+    def step():
+        hip.gemm_ex("f32", 0, 0, M, N, K, A, K, M * K, B, N, K * N, 0.0, C, N, M * N, Bt)
+    return step, 2.0 * Bt * M * N * K, 4.0 * Bt * (M * K + K * N + M * N), [A, B, C]
+
+
 WORKLOADS = {
     # name: (builder, kwargs, precision for the peak, description)
     "gemm_bf16_8192": (gemm_workload, dict(dtype="bf16", M=8192, N=8192, K=8192), "bf16",
@@ -120,6 +167,18 @@ WORKLOADS = {
                      "causal FlashAttention bwd B8 H16 S4096 D128 bf16 (config 4)"),
     "flash_fwd_c3": (flash_workload, dict(dtype="fp32", BH=24, S=256, D=64, causal=True),
                      "fp32", "causal FlashAttention fwd B4 H6 S256 D64 fp32 (config 3)"),
+    "linear_relu_c2": (linear_workload, dict(N=4096, IN=784, OUT=257), "fp32",
+                       "fused linear_relu X[4096x784] W[257x784]^T + b (config 2 layer 1), fp32"),
+    "bmm_64x512": (bmm_workload, dict(Bt=64, M=512, N=512, K=512), "fp32",
+                   "dream_bmm 64 x (512x512 @ 512x512) fp32, one batched launch"),
+    "softmax_fwd_16384x1024": (rows_workload, dict(op="softmax_fwd", R=16384, C=1024), "hbm",
+                               "row softmax 16384 x 1024 fp32 (HBM-bound)"),
+    "softmax_bwd_16384x1024": (rows_workload, dict(op="softmax_bwd", R=16384, C=1024), "hbm",
+                               "row softmax backward 16384 x 1024 fp32 (HBM-bound)"),
+    "layer_norm_fwd_16384x1024": (rows_workload, dict(op="layer_norm_fwd", R=16384, C=1024),
+                                  "hbm", "row layer norm 16384 x 1024 fp32 (HBM-bound)"),
+    "layer_norm_bwd_16384x1024": (rows_workload, dict(op="layer_norm_bwd", R=16384, C=1024),
+                                  "hbm", "row layer norm backward 16384 x 1024 fp32 (HBM-bound)"),
 }
 
 MLP_SHAPES = [  # config 2: (name, transA, transB, M, N, K)
@@ -151,8 +210,55 @@ def mlp_metrics(steps, warmup):
     return out
 
 
+def _mlp_c2_inputs(seed=8):
+    rng = np.random.default_rng(seed)
+    return (rng.uniform(0, 1, (4096, 784)), rng.standard_normal((257, 784)) * np.sqrt(2 / 784),
+            rng.standard_normal((1, 257)) * 0.1, rng.standard_normal((10, 257)) * np.sqrt(2 / 257),
+            rng.standard_normal((1, 10)) * 0.1, rng.standard_normal((4096, 10)))
+
+
+def _mlp_c2_program(L, tensor, X, W1, b1, W2, b2, G):
+    """One config-2 training step as a .dream program would issue it: h = linear_relu(X, W1, b1),
+    y = linear(h, W2, b2), loss = sum(log_softmax(y) * G), backward(loss).  Returns a step
+    function (the graph of each step is released after its backward)."""
+    x, w1, bb1, w2, bb2, g = (tensor(a) for a in (X, W1, b1, W2, b2, G))
+
+    def step():
+        h = L.dream_linear_relu(x, w1, bb1)
+        y = L.dream_linear(h, w2, bb2)
+        lp = L.dream_log_softmax(y)
+        m = L.tensor_mul(lp, g)
+        loss = L.sum(m)
+        r = L.backward(loss)
+        for t in (r, loss, m, lp, y, h):
+            L.tensor_decref(t)
+        for t in (x, w1, bb1, w2, bb2):
+            L.tensor_decref(L.zero_grad(t))
+    return step
+
+
+def runtime_mlp_metrics(steps=10, warmup=3):
+    """Config 2 end to end through the Dream builtins (libdream_rt): host fp64 tensors in and
+    out, so PCIe staging is inside the time; the weights' and inputs' device copies persist
+    across steps (their versions do not change), the activations and gradients stay on the
+    device between the GPU ops of one step."""
+    from dreamcompiler_amd import runtime as rt
+    step = _mlp_c2_program(rt.load(), rt.tensor, *_mlp_c2_inputs())
+    for _ in range(warmup):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    flops = 3 * 2.0 * 4096 * (784 * 257 + 257 * 10)
+    return {"ms_per_step": round(ms, 3), "gflops": round(flops / ms / 1e6, 1),
+            "desc": "config 2 fwd+bwd step through dream_linear_relu / dream_linear / "
+                    "dream_log_softmax / backward on fp64 host tensors (PCIe-inclusive), "
+                    "no optimizer update"}
+
+
 # --------------------------------------------------------------------------- CPU baseline
-def cpu_baseline_gemm(n=8192, rows=4096, reps=2):
+def cpu_baseline_gemm(n=8192, rows=8192, reps=3):
     """The reference's CPU `@` on fp32 operands (`as f32` -> dream_gemm_f32, blocked 8x16
     AVX2 kernel, OpenMP over 128-row blocks, runtime/ops/elementwise.inc:689-738) on a
     bounded sample of the workload: `rows` rows of A times the full 8192 x 8192 B.
@@ -183,7 +289,7 @@ def cpu_baseline_gemm(n=8192, rows=4096, reps=2):
                       f"workload), best of {reps}, {best:.2f} s, OMP threads {threads}"}
 
 
-def cpu_baseline_flash(S=4096, D=128, slices=8):
+def cpu_baseline_flash(S=4096, D=128, slices=32):
     """The reference's CPU flash_attention forward (fp64, single-threaded,
     runtime/nn/training.inc:366-399) on `slices` of the 128 (batch x head) slices of
     config 4; slices are independent and equal in work, so the rate scales exactly."""
@@ -207,6 +313,26 @@ def cpu_baseline_flash(S=4096, D=128, slices=8):
             "sample": f"{slices} of 128 slices, S={S} D={D}, fp64, {dt:.1f} s"}
 
 
+def cpu_baseline_mlp(steps=2):
+    """The same config-2 step on the reference's own CPU runtime (oracle/_ref): its fused
+    linear (elementwise.inc:1432-1516), log_softmax and backward (autograd.inc:156-233), OpenMP
+    over the host's OMP_NUM_THREADS."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _ref_runtime  # noqa: E402  (test infrastructure: the CPU comparison only)
+    if not _ref_runtime.available():
+        return {"error": "oracle/_ref not built"}
+    R = _ref_runtime.RefRuntime()
+    step = _mlp_c2_program(R.L, R.tensor, *_mlp_c2_inputs())
+    step()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"ms_per_step": round(ms, 2), "cores": threads, "kind": "reference",
+            "sample": f"{steps} steps after 1 warm-up"}
+
+
 # --------------------------------------------------------------------------- main
 def load_traffic():
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), scaled
@@ -222,10 +348,16 @@ def measure(name, steps, warmup):
     builder, kw, prec, desc = WORKLOADS[name]
     step, flops, alg_bytes, bufs = builder(**kw)
     ms, wall = _time(step, steps, warmup)
-    tflops = flops / ms / 1e9
-    res = {"workload": name, "desc": desc, "ms": round(ms, 5), "tflops": round(tflops, 2),
-           "frac_peak": round(tflops / PEAK[prec], 4), "peak_tflops": PEAK[prec],
-           "alg_bytes": alg_bytes, "wall_s": round(wall, 4)}
+    gbs = alg_bytes / ms / 1e6
+    if prec == "hbm":
+        res = {"workload": name, "desc": desc, "ms": round(ms, 5), "gbs": round(gbs, 1),
+               "frac_peak": round(gbs / HBM_PEAK_GBS, 4), "peak_gbs": HBM_PEAK_GBS,
+               "alg_bytes": alg_bytes, "wall_s": round(wall, 4)}
+    else:
+        tflops = flops / ms / 1e9
+        res = {"workload": name, "desc": desc, "ms": round(ms, 5), "tflops": round(tflops, 2),
+               "frac_peak": round(tflops / PEAK[prec], 4), "peak_tflops": PEAK[prec],
+               "gbs": round(gbs, 1), "alg_bytes": alg_bytes, "wall_s": round(wall, 4)}
     traffic = load_traffic().get(name)
     if traffic:
         res["hbm_bytes_measured"] = traffic["bytes_per_launch"]
@@ -275,16 +407,22 @@ def main():
             if name != args.workload:
                 metrics[name] = measure(name, args.steps, args.warmup)
         metrics["mlp_c2"] = mlp_metrics(max(5, args.steps), 3)
+        metrics["runtime_mlp_c2_step"] = runtime_mlp_metrics()
 
     traffic = load_traffic().get(args.workload)
     prec = WORKLOADS[args.workload][2]
-    roofline = {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK[prec],
-                "unit": "TFLOP/s", "frac": head["frac_peak"],
-                "traffic": traffic["bytes_per_launch"] if traffic else None}
+    if prec == "hbm":   # a memory-bound workload chosen with --workload (profiling runs)
+        roofline = {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": head["frac_peak"],
+                    "traffic": traffic["bytes_per_launch"] if traffic else None}
+    else:
+        roofline = {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK[prec],
+                    "unit": "TFLOP/s", "frac": head["frac_peak"],
+                    "traffic": traffic["bytes_per_launch"] if traffic else None}
     line = {
         "metric": "GEMM GFLOP/s fp32 4096^3 / bf16 8192^3; FlashAttn fwd TFLOP/s; % MFMA peak",
-        "value": round(head["tflops"] * 1000.0, 1),
-        "unit": "GFLOP/s",
+        "value": round(head["gbs"] if prec == "hbm" else head["tflops"] * 1000.0, 1),
+        "unit": "GB/s" if prec == "hbm" else "GFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -292,7 +430,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if prec == "bf16" else "fp32",
+        "dtype": "bf16" if prec == "bf16" else "f32",
         "data": "synthetic N(0,1) inputs (numpy PCG64, seeded), resident in HBM",
         "config": {"workload": head["desc"], "name": args.workload},
         "roofline": roofline,
@@ -306,6 +444,7 @@ def main():
             else:
                 line["cpu_baseline"] = cpu_baseline_gemm()
             line["cpu_baseline_flash_fwd_c4"] = cpu_baseline_flash()
+            line["cpu_baseline_runtime_mlp_c2_step"] = cpu_baseline_mlp()
         except Exception as e:  # the CPU comparison must not hide the GPU result
             line["cpu_baseline"] = {"error": repr(e)}
     print(json.dumps(line), flush=True)

@@ -183,19 +183,87 @@ struct Batch {
     int relu;
 };
 
+// Split-K reduction: C = beta C + sum_s part[s] (fixed order, so reruns are bit-identical)
+// + bias, then ReLU.
+__global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ part, int S, int M,
+                                                     int N, float beta, float* __restrict__ C,
+                                                     int ldc, const float* __restrict__ bias,
+                                                     int relu) {
+    const size_t MN = (size_t)M * N;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < MN; e += (size_t)gridDim.x * 256) {
+        float v = 0.f;
+        for (int s = 0; s < S; ++s) v += part[s * MN + e];
+        const int r = (int)(e / N), c = (int)(e % N);
+        float* o = C + (size_t)r * ldc + c;
+        v = (beta == 0.f ? v : v + beta * *o) + (bias ? bias[c] : 0.f);
+        if (relu) v = v < 0.f ? 0.f : v;
+        *o = v;
+    }
+}
+
+template <bool TA, bool TB>
+auto pick_kernel(const float* A, int lda, long long sA, const float* B, int ldb, long long sB) {
+    // 128-bit loads need 16-byte aligned bases and leading dimensions and batch strides
+    // divisible by 4.
+    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0) && (sA % 4 == 0);
+    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0) && (sB % 4 == 0);
+    return va && vb ? gemm_f32_kernel<TA, TB, true, true>
+         : va       ? gemm_f32_kernel<TA, TB, true, false>
+         : vb       ? gemm_f32_kernel<TA, TB, false, true>
+                    : gemm_f32_kernel<TA, TB, false, false>;
+}
+
 template <bool TA, bool TB>
 int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
            float* C, int ldc, const Batch& bt) {
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    // 128-bit loads need 16-byte aligned bases and leading dimensions and batch strides
-    // divisible by 4.
-    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0) && (bt.sA % 4 == 0);
-    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0) && (bt.sB % 4 == 0);
     hipStream_t s = stream();
-    auto kern = va && vb ? gemm_f32_kernel<TA, TB, true, true>
-              : va       ? gemm_f32_kernel<TA, TB, true, false>
-              : vb       ? gemm_f32_kernel<TA, TB, false, true>
-                         : gemm_f32_kernel<TA, TB, false, false>;
+    // Skinny products with a long contraction (the weight gradients dW = dY^T X of a layer:
+    // few output tiles, K = the batch) would leave most CUs idle: split K into S chunks run
+    // as gridDim.y members writing fp32 partials, then reduce them in order.
+    // Only where the one-pass grid fills at most a quarter of the CUs: a 2-way split of a
+    // half-full grid loses more to the partial-sum traffic than it gains.
+    const int cus = num_cus();
+    if (bt.count == 1 && 4 * tiles <= cus && K >= 512) {
+        int S = cus / tiles;
+        S = S > 32 ? 32 : S;
+        S = S > K / 128 ? K / 128 : S;
+        const int Kc = ((K + S - 1) / S + BK - 1) / BK * BK;   // chunk of K, multiple of BK
+        S = (K + Kc - 1) / Kc;
+        const int full = K / Kc, tail = K - full * Kc;         // full chunks, last partial one
+        float* part = static_cast<float*>(dh_malloc((size_t)S * M * N * sizeof(float)));
+        if (part) {
+            // chunk j: A columns (or rows, TA) and B rows (or columns, TB) j Kc .. + Kc
+            const long long sA = TA ? (long long)Kc * lda : Kc, sB = TB ? Kc : (long long)Kc * ldb;
+            int st = DH_OK;
+            if (full > 0) {
+                auto kern = pick_kernel<TA, TB>(A, lda, sA, B, ldb, sB);
+                kern<<<dim3(tiles, full), NTHREADS, 0, s>>>(M, N, Kc, A, lda, B, ldb, 0.f, part, N,
+                                                            sA, sB, (long long)M * N, nullptr, 0);
+                st = check_launch("dh_gemm_f32(split-K)");
+            }
+            if (st == DH_OK && tail > 0) {
+                const float* At = A + full * sA;
+                const float* Bt = B + full * sB;
+                auto kern = pick_kernel<TA, TB>(At, lda, 0, Bt, ldb, 0);
+                kern<<<dim3(tiles, 1), NTHREADS, 0, s>>>(M, N, tail, At, lda, Bt, ldb, 0.f,
+                                                         part + (size_t)full * M * N, N, 0, 0, 0,
+                                                         nullptr, 0);
+                st = check_launch("dh_gemm_f32(split-K)");
+            }
+            if (st == DH_OK) {
+                size_t blocks = ((size_t)M * N + 255) / 256;
+                if (blocks > (size_t)cus * 8) blocks = (size_t)cus * 8;
+                splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(part, S, M, N, beta, C, ldc,
+                                                               bt.bias, bt.relu);
+                st = check_launch("dh_gemm_f32(split-K reduce)");
+            }
+            dh_free(part);   // pooled; later users of the buffer are ordered on the stream
+            return st;
+        }
+        // no workspace: fall through to the one-pass kernel
+    }
+    auto kern = pick_kernel<TA, TB>(A, lda, bt.sA, B, ldb, bt.sB);
     // gridDim.y carries the batch member; chunks of 65535 keep it within the y limit.
     for (int b0 = 0; b0 < bt.count; b0 += 65535) {
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;

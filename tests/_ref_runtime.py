@@ -47,7 +47,8 @@ class RefRuntime:
                             ("dream_linear_relu", 3), ("dream_bmm", 6),
                             ("dream_set_seed", 1), ("dream_randn", 2),
                             ("dream_kaiming_init", 2), ("gemm_selftest", 0),
-                            ("flash_attention_selftest", 0), ("tensor_decref", 1)]:
+                            ("flash_attention_selftest", 0), ("tensor_decref", 1),
+                            ("zero_grad", 1)]:
             fn = getattr(L, name)
             fn.restype = _TP
             if nargs is not None:

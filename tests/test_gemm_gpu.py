@@ -344,3 +344,18 @@ def test_linear_reference_golden_vectors():
             DB.empty((N_, O_), np.float32)
         hip.gemm_ex("f32", 0, 1, N_, O_, K_, dX, K_, 0, dW, K_, 0, 0.0, dY, O_, 0, 1, db, relu)
         assert maxrel(dY.numpy(), G[key]) <= 1e-5 * np.sqrt(K_)
+
+
+@pytest.mark.parametrize("M,N,K", [(40, 33, 5000), (300, 200, 2048), (784, 257, 4096), (257, 10, 4096)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_fp32_split_k_skinny_long_k(M, N, K, ta, tb):
+    # Few output tiles and a long contraction take the split-K path (K chunks as gridDim.y
+    # members, a ragged last chunk of its own, an ordered reduction with beta / bias / ReLU).
+    got, ref = _ex("f32", ta, tb, 1, M, N, K, beta=0.5, relu=bool(ta), seed=M + K + ta)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_fp32_split_k_bit_identical_reruns():
+    a, _ = _ex("f32", 1, 0, 1, 784, 257, 4096, seed=3)
+    b, _ = _ex("f32", 1, 0, 1, 784, 257, 4096, seed=3)
+    assert np.array_equal(a, b)
