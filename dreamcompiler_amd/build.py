@@ -28,6 +28,7 @@ HIP_SOURCES = [
     "dh_flash_fwd.hip",
     "dh_flash_bwd.hip",
     "dh_rows.hip",
+    "dh_conv.hip",
 ]
 RT_SOURCES = ["dream_rt.cpp"]
 

@@ -98,7 +98,7 @@ __global__ void __launch_bounds__(NTHREADS)
 gemm_bf16_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
                  const uint16_t* __restrict__ B, int ldb, float beta, float* __restrict__ C,
                  int ldc, long long sA, long long sB, long long sC,
-                 const float* __restrict__ bias, int relu) {
+                 const float* __restrict__ bias, int epi) {
     A += blockIdx.y * sA;   // batch member blockIdx.y
     B += blockIdx.y * sB;
     C += blockIdx.y * sC;
@@ -181,14 +181,16 @@ gemm_bf16_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
         for (int b = 0; b < FN; ++b) {
             const int col = n0 + wn + 32 * b + l32;
             if (col >= N) continue;
-            const float bv = bias ? bias[col] : 0.f;
+            const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS);
+            const float bv = bias && !row_bias ? bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (row < M) {
                     float* c = C + (size_t)row * ldc + col;
-                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) + bv;
-                    if (relu) v = v < 0.f ? 0.f : v;
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
+                              (row_bias ? bias[row] : bv);
+                    if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
                     *c = v;
                 }
             }
@@ -199,7 +201,7 @@ struct Batch {
     long long sA, sB, sC;   // element strides between batch members (0 for one product)
     int count;
     const float* bias;      // per-column bias of the epilogue, or null
-    int relu;
+    int epi;                // DH_EPI_* flags
 };
 
 template <int BM, int BN, int BK, int WAVES_M, bool TA, bool TB, bool VA, bool VB>
@@ -220,7 +222,7 @@ int launch_cfg(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* 
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
         kern<<<dim3(tiles, nb), NTHREADS, lds, stream()>>>(
             M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB, ldb, beta, C + b0 * bt.sC, ldc, bt.sA,
-            bt.sB, bt.sC, bt.bias, bt.relu);
+            bt.sB, bt.sC, bt.bias, bt.epi);
         DH_TRY(check_launch("dh_gemm_bf16"));
     }
     return DH_OK;
@@ -426,7 +428,7 @@ __global__ void __launch_bounds__(64 * WAVES)
 gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
                       const uint16_t* __restrict__ B, int ldb, float beta, float* __restrict__ C,
                       int ldc, long long sA, long long sB, long long sC,
-                      const float* __restrict__ bias, int relu) {
+                      const float* __restrict__ bias, int epi) {
     A += blockIdx.y * sA;   // batch member blockIdx.y
     B += blockIdx.y * sB;
     C += blockIdx.y * sC;
@@ -491,7 +493,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
         static_assert(2 * (OA::PER + OB::PER) == 16, "vmcnt below assumes 8 DMAs per stage");
         asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         __syncthreads();
-        asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(relu));
+        asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(epi));
         s16x4 f0a[FM][2], f0b[FN][2], f1a[FM][2], f1b[FN][2];
 #pragma unroll
         for (int x = 0; x < FM; ++x)
@@ -550,7 +552,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     // reads too, so they would no longer overlap the f1 MFMAs.
     // The epilogue's kernel arguments are fetched here: a scalar load still in flight at
     // the loop entry would make every LDS wait in the loop a full lgkmcnt(0).
-    asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(relu));
+    asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(epi));
     bf16x8 f0a[FM], f0b[FN], f1a[FM], f1b[FN];
     load_frags<OA, OB, FM, FN>(stage_ptr(0), 0, wm, wn, lane, f0a, f0b);
     for (int kt = 0; kt < nk - 1; ++kt) {
@@ -581,7 +583,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     auto at = [&](int a, int b, int r) {
         return cw + (size_t)(32 * a + 8 * (r >> 2) + (r & 3)) * ldc + 32 * b;
     };
-    if (beta == 0.f && !bias && !relu) {
+    if (beta == 0.f && !bias && !(epi & DH_EPI_RELU)) {
 #pragma unroll
         for (int a = 0; a < FM; ++a)
 #pragma unroll
@@ -589,10 +591,14 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 #pragma unroll
                 for (int r = 0; r < 16; ++r) *at(a, b, r) = acc[a][b][r];
     } else {
-        // C = acc + beta C + bias[col], then max(., 0) when relu (NaN passes).
+        // C = acc + beta C + bias (by column, or by row with DH_EPI_ROW_BIAS), then max(., 0)
+        // with DH_EPI_RELU (NaN passes).
+        const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS);
         float bv[FN];
 #pragma unroll
-        for (int b = 0; b < FN; ++b) bv[b] = bias ? bias[n0 + wn + 32 * b + l32] : 0.f;
+        for (int b = 0; b < FN; ++b)
+            bv[b] = bias && !row_bias ? bias[n0 + wn + 32 * b + l32] : 0.f;
+        const float* brow = row_bias ? bias + m0 + wm + 4 * h : nullptr;
 #pragma unroll
         for (int a = 0; a < FM; ++a)
 #pragma unroll
@@ -600,8 +606,9 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     float* c = at(a, b, r);
-                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) + bv[b];
-                    if (relu) v = v < 0.f ? 0.f : v;
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
+                              (row_bias ? brow[32 * a + 8 * (r >> 2) + (r & 3)] : bv[b]);
+                    if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
                     *c = v;
                 }
     }
@@ -619,7 +626,7 @@ int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t*
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
         kern<<<dim3((M / 256) * (N / 256), nb), 64 * waves, 0, stream()>>>(
             M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB, ldb, beta, C + b0 * bt.sC, ldc, bt.sA,
-            bt.sB, bt.sC, bt.bias, bt.relu);
+            bt.sB, bt.sC, bt.bias, bt.epi);
         DH_TRY(check_launch("dh_gemm_bf16(fast)"));
     }
     return DH_OK;
@@ -651,7 +658,7 @@ using namespace dh;
 extern "C" int dh_gemm_bf16_ex(int transA, int transB, int M, int N, int K, const uint16_t* A,
                                int lda, long long strideA, const uint16_t* B, int ldb,
                                long long strideB, float beta, float* C, int ldc,
-                               long long strideC, int batch, const float* bias, int relu) {
+                               long long strideC, int batch, const float* bias, int epilogue) {
     DH_TRY(ensure_init());
     if (M < 0 || N < 0 || K < 0 || batch < 0)
         return set_error(DH_ERR_INVALID, "dh_gemm_bf16: negative shape");
@@ -664,7 +671,7 @@ extern "C" int dh_gemm_bf16_ex(int transA, int transB, int M, int N, int K, cons
     if (batch > 1 && (strideA < 0 || strideB < 0 || strideC < (long long)(M - 1) * ldc + N))
         return set_error(DH_ERR_INVALID, "dh_gemm_bf16: batch strides overlap C or are negative");
     const Batch bt{batch > 1 ? strideA : 0, batch > 1 ? strideB : 0, batch > 1 ? strideC : 0,
-                   batch, bias, relu};
+                   batch, bias, epilogue};
     if (transA)
         return transB ? launch<true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt)
                       : launch<true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);

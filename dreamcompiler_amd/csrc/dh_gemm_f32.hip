@@ -89,7 +89,7 @@ __global__ void __launch_bounds__(NTHREADS)
 gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
                 const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
                 long long sA, long long sB, long long sC, const float* __restrict__ bias,
-                int relu) {
+                int epi) {
     // Batch member blockIdx.y (strides in elements; 0 for a single product).
     A += blockIdx.y * sA;
     B += blockIdx.y * sB;
@@ -155,20 +155,23 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     }
 
     // Epilogue: lanes 0..31 of a register cover 32 consecutive columns of one row.
-    // C = acc + beta C + bias[col], then max(., 0) when relu (NaN passes, like `y < 0 ? 0 : y`).
+    // C = acc + beta C + bias (bias[col], or bias[row] with DH_EPI_ROW_BIAS), then max(., 0)
+    // with DH_EPI_RELU (NaN passes, like `y < 0 ? 0 : y`).
+    const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS), relu = epi & DH_EPI_RELU;
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int col = n0 + wn + 32 * b + l32;
             if (col >= N) continue;
-            const float bv = bias ? bias[col] : 0.f;
+            const float bv = bias && !row_bias ? bias[col] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (row < M) {
                     float* c = C + (size_t)row * ldc + col;
-                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) + bv;
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
+                              (row_bias ? bias[row] : bv);
                     if (relu) v = v < 0.f ? 0.f : v;
                     *c = v;
                 }
@@ -180,23 +183,23 @@ struct Batch {
     long long sA, sB, sC;
     int count;
     const float* bias;
-    int relu;
+    int epi;                // DH_EPI_* flags
 };
 
 // Split-K reduction: C = beta C + sum_s part[s] (fixed order, so reruns are bit-identical)
-// + bias, then ReLU.
+// + bias, then ReLU (the DH_EPI_* epilogue).
 __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ part, int S, int M,
                                                      int N, float beta, float* __restrict__ C,
                                                      int ldc, const float* __restrict__ bias,
-                                                     int relu) {
+                                                     int epi) {
     const size_t MN = (size_t)M * N;
     for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < MN; e += (size_t)gridDim.x * 256) {
         float v = 0.f;
         for (int s = 0; s < S; ++s) v += part[s * MN + e];
         const int r = (int)(e / N), c = (int)(e % N);
         float* o = C + (size_t)r * ldc + c;
-        v = (beta == 0.f ? v : v + beta * *o) + (bias ? bias[c] : 0.f);
-        if (relu) v = v < 0.f ? 0.f : v;
+        v = (beta == 0.f ? v : v + beta * *o) + (bias ? bias[(epi & DH_EPI_ROW_BIAS) ? r : c] : 0.f);
+        if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
         *o = v;
     }
 }
@@ -255,7 +258,7 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
                 size_t blocks = ((size_t)M * N + 255) / 256;
                 if (blocks > (size_t)cus * 8) blocks = (size_t)cus * 8;
                 splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(part, S, M, N, beta, C, ldc,
-                                                               bt.bias, bt.relu);
+                                                               bt.bias, bt.epi);
                 st = check_launch("dh_gemm_f32(split-K reduce)");
             }
             dh_free(part);   // pooled; later users of the buffer are ordered on the stream
@@ -269,7 +272,7 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
         kern<<<dim3(tiles, nb), NTHREADS, 0, s>>>(M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB,
                                                   ldb, beta, C + b0 * bt.sC, ldc, bt.sA, bt.sB,
-                                                  bt.sC, bt.bias, bt.relu);
+                                                  bt.sC, bt.bias, bt.epi);
         DH_TRY(check_launch("dh_gemm_f32"));
     }
     return DH_OK;
@@ -283,7 +286,7 @@ using namespace dh;
 extern "C" int dh_gemm_f32_ex(int transA, int transB, int M, int N, int K, const float* A,
                               int lda, long long strideA, const float* B, int ldb,
                               long long strideB, float beta, float* C, int ldc,
-                              long long strideC, int batch, const float* bias, int relu) {
+                              long long strideC, int batch, const float* bias, int epilogue) {
     DH_TRY(ensure_init());
     if (M < 0 || N < 0 || K < 0 || batch < 0)
         return set_error(DH_ERR_INVALID, "dh_gemm_f32: negative shape");
@@ -296,7 +299,7 @@ extern "C" int dh_gemm_f32_ex(int transA, int transB, int M, int N, int K, const
     if (batch > 1 && (strideA < 0 || strideB < 0 || strideC < (long long)(M - 1) * ldc + N))
         return set_error(DH_ERR_INVALID, "dh_gemm_f32: batch strides overlap C or are negative");
     const Batch bt{batch > 1 ? strideA : 0, batch > 1 ? strideB : 0, batch > 1 ? strideC : 0,
-                   batch, bias, relu};
+                   batch, bias, epilogue};
     if (transA)
         return transB ? launch<true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt)
                       : launch<true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);

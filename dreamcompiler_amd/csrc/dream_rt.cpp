@@ -414,6 +414,39 @@ Tensor* row_op(const char* name, int op, Tensor* x) {
     return y;
 }
 
+// ---- conv2d -------------------------------------------------------------------------------
+struct ConvDims {
+    int N, Cin, H, W, Cout, KH, KW, pad, stride, OH, OW;
+    size_t K() const { return (size_t)Cin * KH * KW; }
+    size_t P() const { return (size_t)OH * OW; }
+};
+
+ConvDims conv_dims(const Tensor* t) {
+    const int* c = t->conv;
+    ConvDims d{t->lhs->d0, c[4], c[0], c[1], c[5], c[2], c[3], c[6], c[7], 0, 0};
+    d.OH = (d.H + 2 * d.pad - d.KH) / d.stride + 1;
+    d.OW = (d.W + 2 * d.pad - d.KW) / d.stride + 1;
+    return d;
+}
+
+void conv_backward(Tensor* t) {
+    // autograd.inc:507-535 over all images at once: gK += go' col^T (one NT GEMM, contraction
+    // N*OH*OW), dcol = K^T go' (TN), gX += col2im(dcol); go' = the gradient channel-first.
+    const ConvDims d = conv_dims(t);
+    Tensor *x = t->lhs, *k = t->rhs;
+    const size_t K = d.K(), NP = (size_t)d.N * d.P();
+    const float* go = grad_in(t);
+    Dev gop((size_t)d.Cout * NP * 4), col(K * NP * 4), dcol(K * NP * 4);
+    need_buf(gop), need_buf(col), need_buf(dcol);
+    need(dh_nct_to_cnt(go, gop.f(), d.N, d.Cout, d.P()));
+    need(dh_im2col(dev_data(x), col.f(), d.N, d.Cin, d.H, d.W, d.KH, d.KW, d.pad, d.stride));
+    need(dh_gemm_f32(0, 1, d.Cout, (int)K, (int)NP, gop.f(), (int)NP, col.f(), (int)NP, 1.f,
+                     dgrad(k), (int)K));
+    need(dh_gemm_f32(1, 0, (int)K, (int)NP, d.Cout, dev_data(k), (int)K, gop.f(), (int)NP, 0.f,
+                     dcol.f(), (int)NP));
+    need(dh_col2im(dcol.f(), dgrad(x), d.N, d.Cin, d.H, d.W, d.KH, d.KW, d.pad, d.stride, 1));
+}
+
 void topo_sort(Tensor* root, std::vector<Tensor*>& order) {
     // Iterative post-order DFS over lhs, rhs and parents (runtime/backend/gpu.inc:742-779).
     std::unordered_set<Tensor*> seen;
@@ -767,7 +800,7 @@ static Tensor* linear_impl(Tensor* x, Tensor* W, Tensor* b, bool relu) {
         Dev d((size_t)N * out * sizeof(float));
         need_buf(d);
         need(dh_gemm_f32_ex(0, 1, N, out, in, dev_data(x), in, 0, dev_data(W), in, 0, 0.f, d.f(),
-                            out, 0, 1, dev_data(b), relu ? 1 : 0));
+                            out, 0, 1, dev_data(b), relu ? DH_EPI_RELU : 0));
         adopt_result(y, d);
     } catch (const Failure&) {
         rt_error("linear", "%s", dh_last_error());
@@ -817,6 +850,79 @@ Tensor* dream_softmax(Tensor* a) { return row_op("softmax", DREAM_OP_SOFTMAX, a)
 Tensor* dream_log_softmax(Tensor* x) { return row_op("log_softmax", DREAM_OP_LOG_SOFTMAX, x); }
 Tensor* dream_layer_norm(Tensor* t) { return row_op("layer_norm", DREAM_OP_LAYER_NORM, t); }
 
+static Tensor* conv_impl(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h_t, Tensor* w_t,
+                         Tensor* kh_t, Tensor* kw_t, int pad, int stride, bool padded) {
+    // conv.inc:12-55 / 119-178: N = input.d0, Cin = input.d1 / (H W) (at least 1),
+    // Cout = kernel.d0; image n of the input starts at n*Cin*H*W.
+    const int H = (int)h_t->data[0], W = (int)w_t->data[0], KH = (int)kh_t->data[0],
+              KW = (int)kw_t->data[0];
+    if (stride < 1) stride = 1;
+    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    if (H + 2 * pad < KH || W + 2 * pad < KW || OH <= 0 || OW <= 0 || KH < 1 || KW < 1) {
+        std::fprintf(stderr, padded ? "error: conv2d output size <= 0\n"
+                                    : "error: conv2d kernel larger than input\n");
+        std::fflush(stderr);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    const int N = input->d0;
+    int Cin = H * W > 0 ? input->d1 / (H * W) : 1;
+    if (Cin < 1) Cin = 1;
+    const int Cout = kernel->d0;
+    const long long K = (long long)Cin * KH * KW, P = (long long)OH * OW;
+    if ((long long)N * Cin * H * W > input->size || (long long)Cout * K > kernel->size) {
+        rt_error("conv2d", "input holds %d values for %d x %d x %d x %d, kernel %d for %d x %lld",
+                 input->size, N, Cin, H, W, kernel->size, Cout, K);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    if (!hip_ready("conv2d")) return alloc_tensor(1, 1, 1, 1);
+    Tensor* out = alloc_tensor(N, (int)(Cout * P), 1, 1);
+    set_graph(out, input, kernel, DREAM_OP_CONV2D);
+    const int geom[8] = {H, W, KH, KW, Cin, Cout, pad, stride};
+    std::copy(geom, geom + 8, out->conv);
+    try {
+        const size_t NP = (size_t)N * P;
+        Dev col((size_t)K * NP * 4), y((size_t)out->size * 4);
+        need_buf(col), need_buf(y);
+        need(dh_im2col(dev_data(input), col.f(), N, Cin, H, W, KH, KW, pad, stride));
+        // The reference adds bias[co] for co < min(Cout, bias.size) (conv.inc:5-10).
+        const float* db = nullptr;
+        Dev bpad(bias ? (size_t)Cout * 4 : 4);
+        if (bias) {
+            if (bias->size >= Cout) {
+                db = dev_data(bias);
+            } else {
+                need_buf(bpad);
+                need(dh_memset(bpad.p, 0, (size_t)Cout * 4));
+                need(dh_memcpy_d2d(bpad.p, dev_data(bias), (size_t)bias->size * 4));
+                db = bpad.f();
+            }
+        }
+        need(dh_gemm_f32_ex(0, 0, Cout, (int)P, (int)K, dev_data(kernel), (int)K, 0, col.f(),
+                            (int)NP, P, 0.f, y.f(), (int)P, (long long)Cout * P, N, db,
+                            db ? DH_EPI_ROW_BIAS : 0));
+        adopt_result(out, y);
+    } catch (const Failure&) {
+        rt_error("conv2d", "%s", dh_last_error());
+        tensor_decref(out);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    return out;
+}
+
+Tensor* dream_conv2d(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h_t, Tensor* w_t,
+                     Tensor* kh_t, Tensor* kw_t) {
+    return conv_impl(input, kernel, bias, h_t, w_t, kh_t, kw_t, 0, 1, false);
+}
+
+Tensor* dream_conv2d_padded(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h_t, Tensor* w_t,
+                            Tensor* kh_t, Tensor* kw_t, Tensor* pad_t, Tensor* stride_t) {
+    // Backward: the exact gradient of the padded, strided convolution.  (The reference's node
+    // reuses the unpadded shapes in its backward, autograd.inc:507-535, which is only correct
+    // for pad 0 and stride 1.)
+    return conv_impl(input, kernel, bias, h_t, w_t, kh_t, kw_t, pad_t ? (int)pad_t->data[0] : 0,
+                     stride_t ? (int)stride_t->data[0] : 1, true);
+}
+
 Tensor* backward(Tensor* root) {
     if (!root) {
         std::fprintf(stderr, "error: backward(null)\n");
@@ -846,6 +952,9 @@ Tensor* backward(Tensor* root) {
                     break;
                 case DREAM_OP_BMM:
                     if (hip_ready("backward(bmm)")) bmm_backward(t);
+                    break;
+                case DREAM_OP_CONV2D:
+                    if (hip_ready("backward(conv2d)")) conv_backward(t);
                     break;
                 case DREAM_OP_SOFTMAX:
                 case DREAM_OP_LOG_SOFTMAX:

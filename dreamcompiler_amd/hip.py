@@ -59,6 +59,9 @@ _SIGS = {
     "dh_layer_norm": (_i, [_vp, _vp, _i, _i]),
     "dh_layer_norm_bwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "dh_linear_bias_grad": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "dh_im2col": (_i, [_vp, _vp] + [_i] * 8),
+    "dh_col2im": (_i, [_vp, _vp] + [_i] * 9),
+    "dh_nct_to_cnt": (_i, [_vp, _vp, _i, _i, _sz]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -180,13 +183,18 @@ def gemm_bf16(transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc):
                               float(beta), _p(C), ldc), "dh_gemm_bf16")
 
 
+EPI_RELU, EPI_ROW_BIAS = 1, 2
+
+
 def gemm_ex(dtype, transA, transB, M, N, K, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch=1,
-            bias=None, relu=False):
-    """dh_gemm_{f32,bf16}_ex: batched GEMM with the bias (+ ReLU) epilogue."""
+            bias=None, relu=False, row_bias=False):
+    """dh_gemm_{f32,bf16}_ex: batched GEMM with the bias (by column, or by row) + ReLU
+    epilogue."""
     fn = load().dh_gemm_bf16_ex if dtype == "bf16" else load().dh_gemm_f32_ex
+    epi = (EPI_RELU if relu else 0) | (EPI_ROW_BIAS if row_bias else 0)
     check(fn(int(transA), int(transB), M, N, K, _p(A), lda, int(sA), _p(B), ldb, int(sB),
              float(beta), _p(C), ldc, int(sC), int(batch), _p(bias) if bias is not None else None,
-             int(relu)), f"dh_gemm_{dtype}_ex")
+             epi), f"dh_gemm_{dtype}_ex")
 
 
 def flash_fwd(dtype, BH, S, D, scale, causal, Q, K, V, O, LSE):
@@ -216,6 +224,19 @@ def layer_norm(X, Y, R, C):
 def linear_bias_grad(Y, dY, db, N, out, relu=False, accumulate=False):
     check(load().dh_linear_bias_grad(_p(Y) if Y is not None else None, _p(dY), _p(db), N, out,
                                      int(relu), int(accumulate)), "dh_linear_bias_grad")
+
+
+def im2col(X, col, N, Cin, H, W, KH, KW, pad=0, stride=1):
+    check(load().dh_im2col(_p(X), _p(col), N, Cin, H, W, KH, KW, pad, stride), "dh_im2col")
+
+
+def col2im(dcol, dX, N, Cin, H, W, KH, KW, pad=0, stride=1, accumulate=False):
+    check(load().dh_col2im(_p(dcol), _p(dX), N, Cin, H, W, KH, KW, pad, stride, int(accumulate)),
+          "dh_col2im")
+
+
+def nct_to_cnt(src, dst, N, C, T):
+    check(load().dh_nct_to_cnt(_p(src), _p(dst), N, C, int(T)), "dh_nct_to_cnt")
 
 
 def layer_norm_bwd(X, Y, DY, GX, R, C, accumulate=False):

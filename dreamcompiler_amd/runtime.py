@@ -35,7 +35,7 @@ _SIGS = {
     "dream_linear": [TP] * 3, "dream_linear_relu": [TP] * 3, "linear": [TP] * 3,
     "linear_relu": [TP] * 3, "dream_bmm": [TP] * 6, "dream_softmax": [TP],
     "dream_log_softmax": [TP], "dream_layer_norm": [TP], "tensor_set_element": [TP] * 3,
-    "tensor_set_element_2d": [TP] * 4,
+    "tensor_set_element_2d": [TP] * 4, "dream_conv2d": [TP] * 7, "dream_conv2d_padded": [TP] * 9,
 }
 
 _lib = None

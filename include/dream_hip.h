@@ -109,26 +109,30 @@ int dh_gemm_bf16(int transA, int transB, int M, int N, int K,
                  const uint16_t* d_A, int lda, const uint16_t* d_B, int ldb,
                  float beta, float* d_C, int ldc);
 /* Batched GEMM with a fused epilogue, for every member b < batch:
- *   C_b = op(A_b) @ op(B_b) + beta * C_b + bias,  then C_b = max(C_b, 0) when relu != 0
+ *   C_b = op(A_b) @ op(B_b) + beta * C_b + bias,  then C_b = max(C_b, 0) with DH_EPI_RELU
  * with X_b = d_X + b * strideX (strides in elements; a zero stride for A or B shares one
  * operand across the batch; C members must not overlap: strideC >= (M-1)*ldc + N when
- * batch > 1).  bias (N fp32 values, added to every row) may be NULL; NaN passes the ReLU as
- * in the reference's `y < 0 ? 0 : y`.
- * NT with bias (+ relu) is dream_linear / linear_relu's Y = X W^T + b with W stored
+ * batch > 1).  bias (fp32, may be NULL) holds N values added to every row, or with
+ * DH_EPI_ROW_BIAS M values added to every column; NaN passes the ReLU as in the reference's
+ * `y < 0 ? 0 : y`.
+ * NT with a column bias (+ relu) is dream_linear / linear_relu's Y = X W^T + b with W stored
  * out x in (runtime/ops/elementwise.inc:1432-1516); batched NN is dream_bmm
  * (elementwise.inc:1218-1252), and its backward's G B^T and A^T G are batched NT and TN
- * with beta = 1 (runtime/ops/autograd.inc:549-574).  dh_gemm_f32 / dh_gemm_bf16 are the
- * batch = 1, bias = NULL, relu = 0 case. */
+ * with beta = 1 (runtime/ops/autograd.inc:549-574); NN with a row bias per image is
+ * dream_conv2d's kernel @ im2col + bias (runtime/nn/conv.inc:12-55).  dh_gemm_f32 /
+ * dh_gemm_bf16 are the batch = 1, bias = NULL, epilogue = 0 case.  The fp32 form splits a
+ * skinny product's long K over idle CUs by itself (deterministic ordered reduction). */
+enum { DH_EPI_RELU = 1, DH_EPI_ROW_BIAS = 2 };
 int dh_gemm_f32_ex(int transA, int transB, int M, int N, int K,
                    const float* d_A, int lda, long long strideA,
                    const float* d_B, int ldb, long long strideB,
                    float beta, float* d_C, int ldc, long long strideC,
-                   int batch, const float* d_bias, int relu);
+                   int batch, const float* d_bias, int epilogue);
 int dh_gemm_bf16_ex(int transA, int transB, int M, int N, int K,
                     const uint16_t* d_A, int lda, long long strideA,
                     const uint16_t* d_B, int ldb, long long strideB,
                     float beta, float* d_C, int ldc, long long strideC,
-                    int batch, const float* d_bias, int relu);
+                    int batch, const float* d_bias, int epilogue);
 
 /* ---- FlashAttention -----------------------------------------------------------
  * Q, K, V, O in the reference layout (B, S*dk): slice b (a batch x head pair)
@@ -174,6 +178,22 @@ int dh_layer_norm_bwd(const float* d_X, const float* d_Y, const float* d_DY, flo
  * floating-point atomics).  Y may be NULL when relu == 0. */
 int dh_linear_bias_grad(const float* d_Y, float* d_dY, float* d_db, int N, int out, int relu,
                         int accumulate);
+
+/* ---- conv2d data movement (runtime/nn/conv.inc:12-55, 119-178; im2col.inc:2-25;
+ *      autograd.inc:507-535) ------------------------------------------------------------
+ * Input X is (N, Cin, H, W) fp32; OH = (H + 2 pad - KH) / stride + 1, likewise OW.
+ * dh_im2col writes col, (Cin*KH*KW) x (N*OH*OW): row (ci*KH + kh)*KW + kw, column
+ * n*OH*OW + oh*OW + ow, zero where the window covers padding.  With it the forward is one
+ * dh_gemm_f32_ex (kernel @ col per image, the kernel shared by a zero stride, the per-channel
+ * bias as DH_EPI_ROW_BIAS).  dh_col2im is its adjoint: dX (+)= the sum, for every input
+ * element, of the dcol entries that read it (a gather in a fixed order: deterministic).
+ * dh_nct_to_cnt permutes (N, C, T) to (C, N*T), the channel-first output gradient both
+ * backward products take. */
+int dh_im2col(const float* d_X, float* d_col, int N, int Cin, int H, int W, int KH, int KW,
+              int pad, int stride);
+int dh_col2im(const float* d_dcol, float* d_dX, int N, int Cin, int H, int W, int KH, int KW,
+              int pad, int stride, int accumulate);
+int dh_nct_to_cnt(const float* d_src, float* d_dst, int N, int C, size_t T);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,7 @@ typedef struct Tensor {
     int num_parents;
     int attn_B, attn_S, attn_dk;   /* "B,S,dk" of an attention node (bwd_name)    */
     int bmm_B, bmm_M, bmm_K, bmm_N;   /* "B,M,K,N" of a bmm node (bwd_name)       */
+    int conv[8];               /* H, W, KH, KW, Cin, Cout, pad, stride of a conv2d node */
     int dtype;                 /* 0 = fp64 storage, 1 = live fp32 mirror (as f32)  */
     float* fdata;              /* fp32 mirror when dtype == 1                      */
     float* fgrad;
@@ -59,7 +60,7 @@ typedef struct Tensor {
 enum {
     DREAM_OP_LEAF = 0, DREAM_OP_MATMUL, DREAM_OP_FLASH, DREAM_OP_ATTN, DREAM_OP_ATTN_CAUSAL,
     DREAM_OP_SUM, DREAM_OP_MUL, DREAM_OP_ADD, DREAM_OP_LINEAR, DREAM_OP_LINEAR_RELU,
-    DREAM_OP_BMM, DREAM_OP_SOFTMAX, DREAM_OP_LOG_SOFTMAX, DREAM_OP_LAYER_NORM
+    DREAM_OP_BMM, DREAM_OP_SOFTMAX, DREAM_OP_LOG_SOFTMAX, DREAM_OP_LAYER_NORM, DREAM_OP_CONV2D
 };
 
 /* ---- tensors (runtime/core/tensor.inc:143-303) ---- */
@@ -113,6 +114,14 @@ Tensor* dream_bmm(Tensor* a, Tensor* b, Tensor* batch, Tensor* m, Tensor* k, Ten
 Tensor* dream_softmax(Tensor* a);
 Tensor* dream_log_softmax(Tensor* x);
 Tensor* dream_layer_norm(Tensor* t);
+/* 2-D convolution of input (N, Cin*H*W) with kernel (Cout, Cin*KH*KW) plus a per-channel bias
+ * (may be NULL) -> (N, Cout*OH*OW), scalars as 1x1 tensors: valid (runtime/nn/conv.inc:12-55)
+ * and zero-padded / strided (conv.inc:119-178).  im2col + one batched GEMM; backward dX, dK
+ * (autograd.inc:507-535; the reference computes no bias gradient, and neither does this). */
+Tensor* dream_conv2d(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h, Tensor* w,
+                     Tensor* kh, Tensor* kw);
+Tensor* dream_conv2d_padded(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h, Tensor* w,
+                            Tensor* kh, Tensor* kw, Tensor* pad, Tensor* stride);
 /* Reverse sweep from root (runtime/ops/autograd.inc:26-887) for the node kinds above;
  * gradients accumulate ("+=") into grad buffers like the reference.  Between two GPU ops a
  * gradient stays on the device; every grad buffer is current on the host when it returns. */

@@ -613,6 +613,83 @@ void orc_bmm_bwd(const double* A, const double* B, const double* G, double* gA, 
 }
 
 // ---------------------------------------------------------------------------
+// Convolution (im2col + GEMM)
+// ---------------------------------------------------------------------------
+namespace {
+// im2col with zero padding and stride (im2col.inc:2-13 for pad 0 / stride 1; conv.inc:149-171
+// for the padded, strided form): col[r][oh*OW + ow], r = (ci*KH + kh)*KW + kw.
+void im2col_ps(const double* inp, double* col, int Cin, int H, int W, int KH, int KW, int OH,
+               int OW, int pad, int stride) {
+    int r = 0;
+    for (int ci = 0; ci < Cin; ++ci)
+        for (int kh = 0; kh < KH; ++kh)
+            for (int kw = 0; kw < KW; ++kw, ++r)
+                for (int oh = 0; oh < OH; ++oh)
+                    for (int ow = 0; ow < OW; ++ow) {
+                        const int h = oh * stride + kh - pad, w = ow * stride + kw - pad;
+                        col[(size_t)r * OH * OW + oh * OW + ow] =
+                            (h >= 0 && h < H && w >= 0 && w < W) ? inp[(size_t)ci * H * W + h * W + w] : 0.0;
+                    }
+}
+}  // namespace
+
+void orc_conv2d(const double* X, const double* Kn, const double* bias, double* Y, int N, int Cin,
+                int H, int W, int Cout, int KH, int KW, int pad, int stride) {
+    // conv.inc:12-55 (pad 0, stride 1) and 119-178: per image im2col, then kernel (Cout x
+    // Cin*KH*KW) @ col with the blocked dgemm (cpu_gemm = dream_gemm_d), then + bias[co].
+    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    const int K = Cin * KH * KW, P = OH * OW;
+    std::vector<double> col((size_t)K * P);
+    for (int n = 0; n < N; ++n) {
+        im2col_ps(X + (size_t)n * Cin * H * W, col.data(), Cin, H, W, KH, KW, OH, OW, pad, stride);
+        double* y = Y + (size_t)n * Cout * P;
+        orc_gemm_d(Kn, col.data(), y, Cout, K, P);
+        if (bias)
+            for (int co = 0; co < Cout; ++co)
+                for (int j = 0; j < P; ++j) y[(size_t)co * P + j] += bias[co];
+    }
+}
+
+void orc_conv2d_bwd(const double* X, const double* Kn, const double* G, double* gX, double* gK,
+                    int N, int Cin, int H, int W, int Cout, int KH, int KW, int pad, int stride) {
+    // autograd.inc:507-535 (pad 0, stride 1): per image gK += G col^T (dot products over the
+    // output positions), dcol = K^T G, gX += col2im(dcol).  No bias gradient (the reference's
+    // conv node has none).  With pad > 0 or stride > 1 the same algebra over the padded,
+    // strided im2col -- the exact gradient, which the reference's node (reusing the unpadded
+    // shapes) does not compute.
+    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    const int K = Cin * KH * KW, P = OH * OW;
+    std::vector<double> col((size_t)K * P), dcol((size_t)K * P);
+    for (int n = 0; n < N; ++n) {
+        im2col_ps(X + (size_t)n * Cin * H * W, col.data(), Cin, H, W, KH, KW, OH, OW, pad, stride);
+        const double* go = G + (size_t)n * Cout * P;
+        for (int co = 0; co < Cout; ++co)
+            for (int cr = 0; cr < K; ++cr) {
+                double s = 0.0;
+                for (int j = 0; j < P; ++j) s += go[(size_t)co * P + j] * col[(size_t)cr * P + j];
+                gK[(size_t)co * K + cr] += s;
+            }
+        for (int cr = 0; cr < K; ++cr)
+            for (int j = 0; j < P; ++j) {
+                double s = 0.0;
+                for (int co = 0; co < Cout; ++co) s += Kn[(size_t)co * K + cr] * go[(size_t)co * P + j];
+                dcol[(size_t)cr * P + j] = s;
+            }
+        double* gx = gX + (size_t)n * Cin * H * W;
+        int r = 0;   // col2im (im2col.inc:14-25), scattering into the unpadded input
+        for (int ci = 0; ci < Cin; ++ci)
+            for (int kh = 0; kh < KH; ++kh)
+                for (int kw = 0; kw < KW; ++kw, ++r)
+                    for (int oh = 0; oh < OH; ++oh)
+                        for (int ow = 0; ow < OW; ++ow) {
+                            const int h = oh * stride + kh - pad, w = ow * stride + kw - pad;
+                            if (h >= 0 && h < H && w >= 0 && w < W)
+                                gx[(size_t)ci * H * W + h * W + w] += dcol[(size_t)r * P + oh * OW + ow];
+                        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // bf16 (training.inc:1969-1976)
 // ---------------------------------------------------------------------------
 float orc_to_bf16(float x) {

@@ -21,7 +21,12 @@
  *   orc_attention*, orc_flash_fwd, orc_flash_bwd      golden vectors + special cases
  *                       (S=1 -> O=V, constant K -> causal running mean) + finite differences
  *   orc_flash_lse       closed form log-sum-exp (scipy.special.logsumexp)
- *   orc_softmax_rows, orc_log_softmax_rows   scipy.special.softmax / log_softmax, rows sum to 1
+ *   orc_softmax_rows, orc_log_softmax_rows   golden vectors, scipy softmax / log_softmax, rows sum to 1
+ *   orc_softmax_bwd, orc_log_softmax_bwd, orc_layer_norm(_bwd)   golden vectors + finite
+ *                       differences + invariants (zero row sums, mean 0 / variance of layer norm)
+ *   orc_linear(_bwd), orc_bmm(_bwd)   golden vectors + independent numpy + finite differences
+ *   orc_conv2d(_bwd)    golden vectors (pad 0 / stride 1 forward and backward, padded strided
+ *                       forward) + finite differences (all, incl. the padded backward)
  *   orc_to_bf16         IEEE round-to-nearest-even (torch.bfloat16 cast) + hand-picked ties
  */
 #ifndef DREAM_ORACLE_H
@@ -110,6 +115,17 @@ void orc_linear_bwd(const double* X, const double* W, const double* Y, double* d
 void orc_bmm(const double* A, const double* B, double* C, int Bt, int M, int K, int N);
 void orc_bmm_bwd(const double* A, const double* B, const double* G, double* gA, double* gB,
                  int Bt, int M, int K, int N);
+
+/* Conv2d, input (N, Cin*H*W), kernel (Cout, Cin*KH*KW), output (N, Cout*OH*OW),
+ * OH = (H + 2 pad - KH) / stride + 1: im2col + blocked dgemm + per-channel bias
+ * (runtime/nn/conv.inc:12-55 for pad 0 / stride 1, 119-178 padded and strided), and the
+ * backward "+=" into gX, gK (autograd.inc:507-535; no bias gradient).  For pad > 0 or
+ * stride > 1 the backward is the exact gradient, not the reference's node (which reuses the
+ * unpadded shapes); it is pinned by finite differences only. */
+void orc_conv2d(const double* X, const double* Kn, const double* bias, double* Y, int N, int Cin,
+                int H, int W, int Cout, int KH, int KW, int pad, int stride);
+void orc_conv2d_bwd(const double* X, const double* Kn, const double* G, double* gX, double* gK,
+                    int N, int Cin, int H, int W, int Cout, int KH, int KW, int pad, int stride);
 
 /* bf16 rounding (training.inc:1969-1976): fp32 -> bf16 -> fp32, round to nearest even
  * by the bias-and-truncate rule.  orc_bf16_bits returns the upper 16 bits. */

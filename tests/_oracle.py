@@ -53,6 +53,8 @@ def lib():
             "orc_linear_bwd": [_dp] * 7 + [_i, _i, _i, _i],
             "orc_bmm": [_dp, _dp, _dp, _i, _i, _i, _i],
             "orc_bmm_bwd": [_dp] * 5 + [_i, _i, _i, _i],
+            "orc_conv2d": [_dp] * 4 + [_i] * 9,
+            "orc_conv2d_bwd": [_dp] * 5 + [_i] * 9,
             "orc_to_bf16": [ctypes.c_float],
             "orc_bf16_bits": [_fp, _u16p, _ll],
         }
@@ -279,6 +281,29 @@ def bmm_bwd(A, B, G, Bt, M, K, N):
     gA, gB = np.zeros((Bt, M * K), np.float64), np.zeros((Bt, K * N), np.float64)
     lib().orc_bmm_bwd(_ptr(A), _ptr(B), _ptr(G), _ptr(gA), _ptr(gB), Bt, M, K, N)
     return gA, gB
+
+
+def conv_out(H, W, KH, KW, pad=0, stride=1):
+    return (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+
+
+def conv2d(X, Kn, bias, N, Cin, H, W, Cout, KH, KW, pad=0, stride=1):
+    """X (N, Cin*H*W), Kn (Cout, Cin*KH*KW), bias (Cout) or None -> (N, Cout*OH*OW)."""
+    OH, OW = conv_out(H, W, KH, KW, pad, stride)
+    X, Kn = _d(X), _d(Kn)
+    b = None if bias is None else _d(bias).ravel()
+    Y = np.empty((N, Cout * OH * OW), np.float64)
+    lib().orc_conv2d(_ptr(X), _ptr(Kn), None if b is None else _ptr(b), _ptr(Y), N, Cin, H, W,
+                     Cout, KH, KW, pad, stride)
+    return Y
+
+
+def conv2d_bwd(X, Kn, G, N, Cin, H, W, Cout, KH, KW, pad=0, stride=1):
+    X, Kn, G = _d(X), _d(Kn), _d(G)
+    gX, gK = np.zeros_like(X), np.zeros_like(Kn)
+    lib().orc_conv2d_bwd(_ptr(X), _ptr(Kn), _ptr(G), _ptr(gX), _ptr(gK), N, Cin, H, W, Cout, KH,
+                         KW, pad, stride)
+    return gX, gK
 
 
 def to_bf16(x):

@@ -48,7 +48,8 @@ class RefRuntime:
                             ("dream_set_seed", 1), ("dream_randn", 2),
                             ("dream_kaiming_init", 2), ("gemm_selftest", 0),
                             ("flash_attention_selftest", 0), ("tensor_decref", 1),
-                            ("zero_grad", 1)]:
+                            ("zero_grad", 1), ("dream_conv2d", 7),
+                            ("dream_conv2d_padded", 9)]:
             fn = getattr(L, name)
             fn.restype = _TP
             if nargs is not None:
@@ -162,3 +163,17 @@ class RefRuntime:
         if grads_W is None:
             return self.read(c)
         return self._grads(c, grads_W, a, b)[:2]
+
+    def conv2d(self, X, Kn, bias, H, W, KH, KW, G=None, pad=None, stride=None):
+        """dream_conv2d (or dream_conv2d_padded when pad/stride are given); with G also the
+        gradients (dX, dK) of backward(sum(Y * G))."""
+        x, k = self.tensor(X), self.tensor(Kn)
+        b = self.tensor(bias) if bias is not None else None
+        sc = [self.scalar(v) for v in (H, W, KH, KW)]
+        if pad is None:
+            y = self.L.dream_conv2d(x, k, b, *sc)
+        else:
+            y = self.L.dream_conv2d_padded(x, k, b, *sc, self.scalar(pad), self.scalar(stride))
+        if G is None:
+            return self.read(y)
+        return self._grads(y, G, x, k)[:2]

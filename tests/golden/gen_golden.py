@@ -8,8 +8,9 @@ Every input is drawn by the reference's own RNG (set_seed + randn, elementwise.i
 and every output comes from the reference builtins through their C ABI:
 tensor_matmul (CPU dgemm / f32 fgemm), backward through "matmul", dream_attention,
 dream_attention_causal, dream_flash_attention and their backward branches,
-dream_softmax, dream_log_softmax, dream_kaiming_init.  The file holds data only
-(inputs and expected outputs, fp64).
+dream_softmax, dream_log_softmax, dream_layer_norm, dream_linear(_relu), dream_bmm,
+dream_conv2d(_padded) and their backward branches, dream_kaiming_init.  The file holds data
+only (inputs and expected outputs, fp64).
 """
 import json
 import os
@@ -108,6 +109,18 @@ def main():
     v["bmm_C"] = R.bmm(BA, BB, 3, 5, 7, 6)
     v["bmm_dA"], v["bmm_dB"] = R.bmm(BA, BB, 3, 5, 7, 6, grads_W=BG)
     manifest["bmm"] = "A=randn(3,35), B=randn(3,42), G=randn(3,30); bmm(B=3,M=5,K=7,N=6), grads"
+
+    # conv2d: N=2, Cin=3, H=7, W=6, Cout=4, KH=3, KW=2 (valid: OH=5, OW=5) with bias, and the
+    # padded / strided forward (pad 1, stride 2: OH=4, OW=4).
+    CX, CK, Cb = R.randn(2, 3 * 7 * 6), R.randn(4, 3 * 3 * 2), R.randn(1, 4)
+    CG = R.randn(2, 4 * 5 * 5)
+    v["conv_X"], v["conv_K"], v["conv_b"], v["conv_G"] = CX, CK, Cb, CG
+    v["conv_Y"] = R.conv2d(CX, CK, Cb, 7, 6, 3, 2)
+    v["conv_dX"], v["conv_dK"] = R.conv2d(CX, CK, Cb, 7, 6, 3, 2, G=CG)
+    v["conv_padded_Y"] = R.conv2d(CX, CK, Cb, 7, 6, 3, 2, pad=1, stride=2)
+    manifest["conv2d"] = ("X=randn(2,126) (N=2, Cin=3, 7x6), K=randn(4,18) (Cout=4, 3x2), "
+                          "b=randn(1,4), G=randn(2,100); conv2d Y, dX, dK of backward(sum(Y*G)); "
+                          "conv2d_padded(pad=1, stride=2) Y")
 
     np.savez_compressed(OUT, **v)
     manifest["file"] = os.path.basename(OUT)

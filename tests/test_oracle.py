@@ -407,3 +407,31 @@ def test_new_rows_against_reference_build(ref):
         dX, dW, db, dY = ref.linear_grads(Xl, Wl, bl, Gl, relu)
         for a, b in zip(got, (dY, dX, dW, db.ravel())):
             assert rel(a, b) <= 1e-12
+
+
+def test_conv2d_golden_and_finite_differences():
+    X, Kn, b, G = (GOLD["conv_" + c] for c in "XKbG")
+    dims = (2, 3, 7, 6, 4, 3, 2)
+    assert rel(O.conv2d(X, Kn, b, *dims), GOLD["conv_Y"]) <= 1e-12
+    gX, gK = O.conv2d_bwd(X, Kn, G, *dims)
+    assert rel(gX, GOLD["conv_dX"]) <= 1e-12 and rel(gK, GOLD["conv_dK"]) <= 1e-12
+    assert rel(O.conv2d(X, Kn, b, *dims, 1, 2), GOLD["conv_padded_Y"]) <= 1e-12
+    # finite differences of the forward, valid and padded / strided (the padded backward has
+    # no reference counterpart that computes it correctly)
+    rng = np.random.default_rng(34)
+    for pad, stride in ((0, 1), (1, 2), (2, 1)):
+        N, Cin, H, W, Cout, KH, KW = 2, 2, 5, 4, 3, 3, 2
+        X = rng.standard_normal((N, Cin * H * W))
+        Kn = rng.standard_normal((Cout, Cin * KH * KW))
+        OH, OW = O.conv_out(H, W, KH, KW, pad, stride)
+        G = rng.standard_normal((N, Cout * OH * OW))
+        dims = (N, Cin, H, W, Cout, KH, KW, pad, stride)
+        gX, gK = O.conv2d_bwd(X, Kn, G, *dims)
+        assert rel(gX, _fd_sumgrad(lambda x: O.conv2d(x, Kn, None, *dims), X, G)) <= 1e-6
+        assert rel(gK, _fd_sumgrad(lambda k: O.conv2d(X, k, None, *dims), Kn, G)) <= 1e-6
+    # a 1x1 kernel is a per-pixel matmul over channels
+    X = rng.standard_normal((3, 4 * 9))
+    Kn = rng.standard_normal((5, 4))
+    Y = O.conv2d(X, Kn, None, 3, 4, 3, 3, 5, 1, 1)
+    ref = np.einsum("oc,ncp->nop", Kn, X.reshape(3, 4, 9)).reshape(3, 45)
+    assert rel(Y, ref) <= 1e-14
