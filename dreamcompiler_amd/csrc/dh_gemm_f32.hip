@@ -9,9 +9,9 @@
 // (elementwise.inc:1218-1252).
 //
 // Work decomposition
-//   work-group (256 threads = 4 wave64s) owns a 128 x 128 tile of C;
-//   wave w owns the 64 x 64 sub-tile (w / 2, w % 2): 2 x 2 MFMA blocks of 32 x 32,
-//   64 fp32 accumulators per lane.
+//   work-group (256 threads = 4 wave64s) owns a 128 x 128 tile of C (64 x 256 or 256 x 64
+//   when M or N is at most 64); each wave owns a 64 x 64 sub-tile: 2 x 2 MFMA blocks of
+//   32 x 32, 64 fp32 accumulators per lane.
 //   K advances in slices of 16: both operand slices are staged in LDS k-major
 //   (As[k][i], Bs[k][j]) and double-buffered; the next slice is fetched from global
 //   memory into registers while the matrix cores work on the current one.
@@ -26,9 +26,7 @@
 namespace dh {
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 16, NTHREADS = 256;
-constexpr int LDS_A = BM + 4;   // padded k-major row strides (floats)
-constexpr int LDS_B = BN + 4;
+constexpr int BK = 16, NTHREADS = 256;
 
 // Four consecutive elements of one row of a row-major matrix:
 // row r, columns c..c+3 of a rows x cols matrix with leading dimension ld.
@@ -47,17 +45,20 @@ __device__ inline f32x4 load4(const float* __restrict__ p, int ld, int rows, int
 
 // Operand slice loader.  "Contiguous-k" operands (A in NN/NT, B in NT/TT) are read
 // along k and transposed into the k-major LDS tile; the others are copied row by row.
-// TILE = tile extent along the non-k dimension (BM or BN).
+// TILE = tile extent along the non-k dimension (64, 128 or 256).  The k-major LDS rows are
+// padded by 4 floats, which puts the 4 k-rows a transposing store touches 16 banks apart:
+// conflict-free for every TILE.
 template <bool KCONTIG, bool VEC, int TILE>
 struct Slice {
-    f32x4 v[2];   // 2 x float4 per thread per slice (TILE * BK / 4 / NTHREADS)
+    static constexpr int CH = TILE * BK / 4 / NTHREADS;   // float4 per thread per slice
+    f32x4 v[CH];
 
     // base/ld describe the stored matrix; t0 = first index along the tile dimension,
     // k0 = first k; extent_t / extent_k bound the valid region.
     __device__ void fetch(const float* __restrict__ base, int ld, int t0, int k0, int extent_t,
                           int extent_k, int tid) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < CH; ++r) {
             const int f = tid + r * NTHREADS;
             if (KCONTIG) {   // stored [t][k]: 4 k per float4
                 const int t = f / (BK / 4), kq = f % (BK / 4);
@@ -70,7 +71,7 @@ struct Slice {
     }
     __device__ void store(float* lds, int stride, int tid) const {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < CH; ++r) {
             const int f = tid + r * NTHREADS;
             if (KCONTIG) {
                 const int t = f / (BK / 4), kq = f % (BK / 4);
@@ -84,7 +85,9 @@ struct Slice {
     }
 };
 
-template <bool TA, bool TB, bool VA, bool VB>
+// Work-group tile TBM x TBN (128 x 128, or 64 x 256 / 256 x 64 for products with M or N at
+// most 64); the 4 waves tile it in 64 x 64 sub-tiles.
+template <bool TA, bool TB, bool VA, bool VB, int TBM, int TBN>
 __global__ void __launch_bounds__(NTHREADS)
 gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
                 const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
@@ -94,22 +97,25 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     A += blockIdx.y * sA;
     B += blockIdx.y * sB;
     C += blockIdx.y * sC;
+    constexpr int LDS_A = TBM + 4, LDS_B = TBN + 4;   // padded k-major row strides (floats)
+    constexpr int WN = TBN / 64;                        // waves along N
+    static_assert((TBM / 64) * WN == 4, "4 waves of 64 x 64");
     __shared__ __attribute__((aligned(16))) float As[2][BK * LDS_A];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDS_B];
 
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     int tm, tn;
     xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * TBM, n0 = tn * TBN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int wm = (wave / WN) * 64, wn = (wave % WN) * 64;
 
     // A: op(A)[i][k]; stored [i][k] when !TA (k contiguous), [k][i] when TA.
-    Slice<!TA, VA, BM> sa;
+    Slice<!TA, VA, TBM> sa;
     // B: op(B)[k][j]; stored [k][j] when !TB (j contiguous), [j][k] when TB.
-    Slice<TB, VB, BN> sb;
+    Slice<TB, VB, TBN> sb;
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -204,22 +210,22 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ p
     }
 }
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, int TBM, int TBN>
 auto pick_kernel(const float* A, int lda, long long sA, const float* B, int ldb, long long sB) {
     // 128-bit loads need 16-byte aligned bases and leading dimensions and batch strides
     // divisible by 4.
     const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0) && (sA % 4 == 0);
     const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0) && (sB % 4 == 0);
-    return va && vb ? gemm_f32_kernel<TA, TB, true, true>
-         : va       ? gemm_f32_kernel<TA, TB, true, false>
-         : vb       ? gemm_f32_kernel<TA, TB, false, true>
-                    : gemm_f32_kernel<TA, TB, false, false>;
+    return va && vb ? gemm_f32_kernel<TA, TB, true, true, TBM, TBN>
+         : va       ? gemm_f32_kernel<TA, TB, true, false, TBM, TBN>
+         : vb       ? gemm_f32_kernel<TA, TB, false, true, TBM, TBN>
+                    : gemm_f32_kernel<TA, TB, false, false, TBM, TBN>;
 }
 
-template <bool TA, bool TB>
-int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
-           float* C, int ldc, const Batch& bt) {
-    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+template <bool TA, bool TB, int TBM, int TBN>
+int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, int ldb,
+                 float beta, float* C, int ldc, const Batch& bt) {
+    const int tiles = ((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN);
     hipStream_t s = stream();
     // Skinny products with a long contraction (the weight gradients dW = dY^T X of a layer:
     // few output tiles, K = the batch) would leave most CUs idle: split K into S chunks run
@@ -240,7 +246,7 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
             const long long sA = TA ? (long long)Kc * lda : Kc, sB = TB ? Kc : (long long)Kc * ldb;
             int st = DH_OK;
             if (full > 0) {
-                auto kern = pick_kernel<TA, TB>(A, lda, sA, B, ldb, sB);
+                auto kern = pick_kernel<TA, TB, TBM, TBN>(A, lda, sA, B, ldb, sB);
                 kern<<<dim3(tiles, full), NTHREADS, 0, s>>>(M, N, Kc, A, lda, B, ldb, 0.f, part, N,
                                                             sA, sB, (long long)M * N, nullptr, 0);
                 st = check_launch("dh_gemm_f32(split-K)");
@@ -248,7 +254,7 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
             if (st == DH_OK && tail > 0) {
                 const float* At = A + full * sA;
                 const float* Bt = B + full * sB;
-                auto kern = pick_kernel<TA, TB>(At, lda, 0, Bt, ldb, 0);
+                auto kern = pick_kernel<TA, TB, TBM, TBN>(At, lda, 0, Bt, ldb, 0);
                 kern<<<dim3(tiles, 1), NTHREADS, 0, s>>>(M, N, tail, At, lda, Bt, ldb, 0.f,
                                                          part + (size_t)full * M * N, N, 0, 0, 0,
                                                          nullptr, 0);
@@ -266,7 +272,7 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
         }
         // no workspace: fall through to the one-pass kernel
     }
-    auto kern = pick_kernel<TA, TB>(A, lda, bt.sA, B, ldb, bt.sB);
+    auto kern = pick_kernel<TA, TB, TBM, TBN>(A, lda, bt.sA, B, ldb, bt.sB);
     // gridDim.y carries the batch member; chunks of 65535 keep it within the y limit.
     for (int b0 = 0; b0 < bt.count; b0 += 65535) {
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
@@ -276,6 +282,19 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
         DH_TRY(check_launch("dh_gemm_f32"));
     }
     return DH_OK;
+}
+
+// Tile shape: 64 x 256 when M <= 64 (a 128-row tile would be at least half empty -- conv's
+// kernel @ im2col with few output channels, the bias gradient shapes), 256 x 64 when N <= 64,
+// else 128 x 128.
+template <bool TA, bool TB>
+int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
+           float* C, int ldc, const Batch& bt) {
+    if (M <= 64 && N > 64)
+        return launch_tiles<TA, TB, 64, 256>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    if (N <= 64 && M > 64)
+        return launch_tiles<TA, TB, 256, 64>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    return launch_tiles<TA, TB, 128, 128>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 
 }  // namespace

@@ -259,7 +259,8 @@ def test_bf16_fast_path_two_wave_variant():
 
 
 # --------------------------------------------------------------------------- batched + epilogue
-def _ex(dtype, ta, tb, Bt, M, N, K, beta=0.0, bias=True, relu=False, share=None, seed=0):
+def _ex(dtype, ta, tb, Bt, M, N, K, beta=0.0, bias=True, relu=False, share=None, seed=0,
+        row_bias=False):
     """Run dh_gemm_*_ex on random inputs; returns (got, ref) as (Bt, M, N) arrays."""
     rng = np.random.default_rng(seed)
     shA = (K, M) if ta else (M, K)
@@ -267,7 +268,7 @@ def _ex(dtype, ta, tb, Bt, M, N, K, beta=0.0, bias=True, relu=False, share=None,
     A = rng.standard_normal((1 if share == "A" else Bt,) + shA).astype(np.float32)
     B = rng.standard_normal((1 if share == "B" else Bt,) + shB).astype(np.float32)
     C0 = rng.standard_normal((Bt, M, N)).astype(np.float32)
-    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    b = rng.standard_normal(M if row_bias else N).astype(np.float32) if bias else None
     if dtype == "bf16":
         A, B = bf16_bits(A), bf16_bits(B)
         A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
@@ -277,7 +278,7 @@ def _ex(dtype, ta, tb, Bt, M, N, K, beta=0.0, bias=True, relu=False, share=None,
     opB = np.swapaxes(B64, 1, 2) if tb else B64
     ref = np.matmul(opA, opB) + beta * C0.astype(np.float64)
     if bias:
-        ref = ref + b.astype(np.float64)
+        ref = ref + (b.astype(np.float64)[:, None] if row_bias else b.astype(np.float64))
     if relu:
         ref = np.maximum(ref, 0.0)
     DB = hip.DeviceBuffer
@@ -286,7 +287,7 @@ def _ex(dtype, ta, tb, Bt, M, N, K, beta=0.0, bias=True, relu=False, share=None,
     sA = 0 if share == "A" else shA[0] * shA[1]
     sB = 0 if share == "B" else shB[0] * shB[1]
     hip.gemm_ex(dtype, ta, tb, M, N, K, dA, shA[1], sA, dB, shB[1], sB, beta, dC, N, M * N, Bt,
-                dbias, relu)
+                dbias, relu, row_bias)
     got = dC.numpy()
     for x in (dA, dB, dC, dbias):
         if x is not None:
@@ -359,3 +360,15 @@ def test_fp32_split_k_bit_identical_reruns():
     a, _ = _ex("f32", 1, 0, 1, 784, 257, 4096, seed=3)
     b, _ = _ex("f32", 1, 0, 1, 784, 257, 4096, seed=3)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("Bt,M,N,K", [(3, 40, 300, 70), (2, 300, 50, 129), (1, 64, 4096, 576),
+                                      (1, 4096, 10, 784), (4, 1, 513, 33)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("row_bias", [False, True])
+def test_fp32_narrow_tiles(Bt, M, N, K, ta, tb, row_bias):
+    # M <= 64 takes 64 x 256 work-group tiles, N <= 64 256 x 64 (batched, split-K and the
+    # epilogue with either bias orientation go through the same shapes).
+    got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.25, relu=row_bias, row_bias=row_bias,
+                   seed=M + N + K + ta + 2 * tb)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
