@@ -18,6 +18,7 @@
 // as 4 (k) x 8 (i or j) blocks and transposed in registers with v_perm_b32 before
 // the LDS write.
 #include <cstdlib>
+#include <type_traits>
 
 #include "dh_common.hpp"
 
@@ -338,6 +339,44 @@ struct FastOperand {
     }
 };
 
+// A k-contiguous operand in double stages of 64 k for the one-wave-per-SIMD schedule: the
+// 32-k stages above fetch 64 bytes per row, half an L2 line (the next stage fetches the other
+// half again), while a 64-k stage fetches each row's full 128-byte line once.  LDS tile
+// [256 rows][64 k] = 32 KB; 16-byte chunk c of row r at position c ^ ((r >> 1) & 7): the 16
+// rows of one b128 pass fall on 8 even and 8 odd rows, so the 16-byte units they read are
+// all different (conflict free).  DMA block b = rows 8b .. 8b+7, 8 lanes x 16 B per row;
+// 4 waves x 8 blocks per double stage.
+struct DeepKOperand {
+    static constexpr int PER = 8;
+    static constexpr int PARTS = 1;
+    static constexpr int ELEMS = 256 * 64;   // elements of one double stage
+    uint32_t off[PER];                        // byte offsets from the operand base, pair 0
+    uint32_t bytes;
+
+    __device__ void init(int ld, int rows, int t0, int wave, int lane) {
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int row = 8 * (PER * wave + t) + (lane >> 3);
+            const int c = (lane & 7) ^ ((row >> 1) & 7);
+            off[t] = 2u * ((uint32_t)(t0 + row) * ld + 8 * c);
+        }
+        bytes = 2u * (uint32_t)rows * (uint32_t)ld;
+    }
+    static constexpr uint32_t STEP = 128u;    // bytes per double stage along a row
+    __device__ void issue_one(u32x4 rs, uint32_t soff, uint32_t base, int t) const {
+        lds_dma16_buf_so(off[t], rs, soff, base + 1024u * t);
+    }
+    // k-step kk (0..3, 16 k each) of the double stage for tile rows o .. o+31.
+    __device__ static void part(const uint16_t* lds, int o, int kk, int lane, int,
+                                s16x4 (&f)[2]) {
+        const int row = o + (lane & 31);
+        const int p = (2 * kk + (lane >> 5)) ^ ((row >> 1) & 7);
+        const s16x8 v = *reinterpret_cast<const s16x8*>(lds + row * 64 + 8 * p);
+        f[0] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+        f[1] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+    }
+};
+
 constexpr int FAST_TILE = 256 * 32;   // elements of one operand stage (32 k)
 constexpr int FAST_NSTAGE = 4;        // LDS ring: 4 x (A + B) x 16 KB = 128 KB
 
@@ -403,6 +442,38 @@ __device__ inline void step_interleaved(const s16x4 (&ca)[FM][2], const s16x4 (&
     }
 }
 
+// As step_interleaved, with the two operands' next fragments in separate LDS stages (A of
+// the deep ring, B of the 32-k ring) and NDB B blocks then NDA A blocks of DMA.
+template <typename OA, typename OB, int FM, int FN, int NDA, int NDB>
+__device__ inline void step_deep(const s16x4 (&ca)[FM][2], const s16x4 (&cb)[FN][2],
+                                 f32x16 (&acc)[FM][FN], const uint16_t* la, int kka,
+                                 const uint16_t* lb, int kkb, int wm, int wn, int lane,
+                                 s16x4 (&na)[FM][2], s16x4 (&nb)[FN][2], const OA& oa,
+                                 const OB& ob, u32x4 rsa, u32x4 rsb, uint32_t soa, uint32_t sob,
+                                 uint32_t basea, uint32_t baseb) {
+    constexpr int NRA = FM * OA::PARTS, NR = NRA + FN * OB::PARTS;
+    constexpr int ND = NDA + NDB;
+    static_assert(NR <= FM * FN && ND <= FM * FN, "schedule slots");
+#pragma unroll
+    for (int i = 0; i < FM * FN; ++i) {
+        const int a = i / FN, b = i % FN;
+        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat8(ca[a]), cat8(cb[b]), acc[a][b],
+                                                            0, 0, 0);
+        if (i < NRA) {
+            OA::part(la, wm + 32 * (i / OA::PARTS), kka, lane, i % OA::PARTS, na[i / OA::PARTS]);
+        } else if (i < NR) {
+            const int j = i - NRA;
+            OB::part(lb, wn + 32 * (j / OB::PARTS), kkb, lane, j % OB::PARTS, nb[j / OB::PARTS]);
+        }
+        const int d = i - (FM * FN - ND);
+        if (d >= 0) {
+            if (d < NDB) ob.issue_one(rsb, sob, baseb, d);
+            else oa.issue_one(rsa, soa, basea, d - NDB);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // Wait until at most n of this wave's DMA stages (2 * PER loads each) are in flight.
 template <int PER2>
 __device__ inline void wait_dma_stages(int n) {
@@ -437,8 +508,13 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     constexpr int WN_CNT = WAVES / 2;                 // waves along N
     constexpr int FM = 4, FN = 4 / (WAVES / 4);       // 128 x (128 or 64) per wave
     // Ring of FAST_NSTAGE stages, each an A tile then a B tile.  Stage kt + 3 is fetched
-    // while stage kt is consumed, so every DMA has three stages of MFMA work to land.
-    __shared__ __attribute__((aligned(16))) uint16_t ring[FAST_NSTAGE * 2 * FAST_TILE];
+    // while stage kt is consumed, so every DMA has three stages of MFMA work to land.  The
+    // one-wave-per-SIMD form with a k-contiguous A (NN, NT) instead holds A in 3 double stages
+    // of 64 k and B in 4 stages of 32 k: 96 + 64 = 160 KB.
+    constexpr bool DEEP_A = WAVES == 4 && !TA;
+    constexpr int RING = DEEP_A ? 3 * DeepKOperand::ELEMS + FAST_NSTAGE * FAST_TILE
+                                : FAST_NSTAGE * 2 * FAST_TILE;
+    __shared__ __attribute__((aligned(16))) uint16_t ring[RING];
 
     const int tiles_m = M / 256, tiles_n = N / 256;
     int tm, tn;
@@ -463,7 +539,97 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
     const int nk = K / 32;
-    if constexpr (WAVES == 4) {
+    if constexpr (DEEP_A) {
+        // A in double stages (pair p = stages 2p, 2p+1, slot p % 3), B in 32-k stages (slot
+        // kt % 4).  Issue order: pair p at stage 2p - 4, B stage s at stage s - 3, pairs after
+        // B within a stage; past the end both are clamped to the last pair / stage (refetched
+        // into a slot nobody reads any more), so the counts are constant: at the barrier of
+        // stage kt, stage kt+1 must have landed while the 24 (kt even) or 16 (kt odd) younger
+        // loads may still be in flight.
+        DeepKOperand da;
+        da.init(lda, M, m0, wave, lane);
+        const u32x4 rsa = make_rsrc(A, da.bytes), rsb = make_rsrc(B, ob.bytes);
+        uint16_t* const ring_a = ring;
+        uint16_t* const ring_b = ring + 3 * DeepKOperand::ELEMS;
+        const int npair = (nk + 1) / 2;
+        auto a_slot = [&](int p) { return ring_a + (p % 3) * DeepKOperand::ELEMS; };
+        auto b_slot = [&](int st) { return ring_b + (st % FAST_NSTAGE) * FAST_TILE; };
+        auto a_dma = [&](int p, uint32_t& base, uint32_t& soff) {
+            base = __builtin_amdgcn_readfirstlane(lds_addr(a_slot(p)) + 1024u * DeepKOperand::PER * wave);
+            soff = __builtin_amdgcn_readfirstlane((uint32_t)min(p, npair - 1) * DeepKOperand::STEP);
+        };
+        auto b_dma = [&](int st, uint32_t& base, uint32_t& soff) {
+            base = __builtin_amdgcn_readfirstlane(lds_addr(b_slot(st)) + 1024u * OB::PER * wave);
+            soff = __builtin_amdgcn_readfirstlane((uint32_t)min(st, nk - 1) * ob.step);
+        };
+        auto issue_a = [&](int p) {
+            uint32_t base, soff;
+            a_dma(p, base, soff);
+#pragma unroll
+            for (int t = 0; t < DeepKOperand::PER; ++t) da.issue_one(rsa, soff, base, t);
+        };
+        auto issue_b = [&](int st) {
+            uint32_t base, soff;
+            b_dma(st, base, soff);
+#pragma unroll
+            for (int t = 0; t < OB::PER; ++t) ob.issue_one(rsb, soff, base, t);
+        };
+        static_assert(OB::PER == 4 && DeepKOperand::PER == 8, "vmcnt constants below");
+        issue_a(0);
+        issue_b(0);
+        issue_b(1);
+        issue_a(1);
+        issue_b(2);
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        __syncthreads();
+        asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(epi));
+        s16x4 f0a[FM][2], f0b[FN][2], f1a[FM][2], f1b[FN][2];
+#pragma unroll
+        for (int x = 0; x < FM; ++x) DeepKOperand::part(a_slot(0), wm + 32 * x, 0, lane, 0, f0a[x]);
+#pragma unroll
+        for (int x = 0; x < FN; ++x)
+#pragma unroll
+            for (int q = 0; q < OB::PARTS; ++q) OB::part(b_slot(0), wn + 32 * x, 0, lane, q, f0b[x]);
+        // Stage kt: X = MFMA f0 | reads of k-step 1 -> f1 | DMA B kt+3 (+ A pair kt/2 + 2 when kt
+        // is even); barrier; Y = MFMA f1 | reads of stage kt+1 k-step 0 -> f0.
+        auto body = [&](int kt, auto even_tag) {
+            constexpr bool EVEN = decltype(even_tag)::value;
+            uint32_t ba = 0, sa = 0, bb, sb;
+            if (EVEN) a_dma(kt / 2 + 2, ba, sa);
+            b_dma(kt + 3, bb, sb);
+            step_deep<DeepKOperand, OB, FM, FN, EVEN ? DeepKOperand::PER : 0, OB::PER>(
+                f0a, f0b, acc, a_slot(kt / 2), 2 * (kt & 1) + 1, b_slot(kt), 1, wm, wn, lane, f1a,
+                f1b, da, ob, rsa, rsb, sa, sb, ba, bb);
+            if (EVEN) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(24)" ::: "memory");
+            else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(16)" ::: "memory");
+            __syncthreads();
+            step_deep<DeepKOperand, OB, FM, FN, 0, 0>(
+                f1a, f1b, acc, a_slot((kt + 1) / 2), 2 * ((kt + 1) & 1), b_slot(kt + 1), 0, wm, wn,
+                lane, f0a, f0b, da, ob, rsa, rsb, 0u, 0u, 0u, 0u);
+        };
+        using Even = std::integral_constant<bool, true>;
+        using Odd = std::integral_constant<bool, false>;
+        int kt = 0;
+        for (; kt + 2 < nk; kt += 2) {
+            body(kt, Even{});
+            body(kt + 1, Odd{});
+        }
+        if (kt + 1 < nk) {
+            body(kt, Even{});
+            ++kt;
+        }
+        // last stage kt = nk - 1: k-step 1 from its slots, then its MFMAs
+        step_deep<DeepKOperand, OB, FM, FN, 0, 0>(f0a, f0b, acc, a_slot(kt / 2), 2 * (kt & 1) + 1,
+                                                  b_slot(kt), 1, wm, wn, lane, f1a, f1b, da, ob,
+                                                  rsa, rsb, 0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat8(f1a[a]), cat8(f1b[b]),
+                                                                    acc[a][b], 0, 0, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // refetches land before exit
+    } else if constexpr (WAVES == 4) {
         // One wave per SIMD, 128 x 128 each: half the LDS fragment traffic per matrix-core op
         // of the two-wave form, with the reads and DMA issues interleaved op by op.  Stage
         // indices past the last stage are clamped (the last stage is fetched again into a

@@ -187,7 +187,9 @@ def test_c5_bf16_8192_full_size():
     _rowcol_sums_check(got, A64, B64, 1e-5)
 
 
-@pytest.mark.parametrize("K", [64, 256, 320])          # 1, 4 (even) and 5 (odd) LDS stages
+# 1..10 stages of 32 k: with a k-contiguous A the one-wave-per-SIMD kernel holds A in double
+# stages of 64 k, so odd stage counts (1, 3, 5) end on half a pair.
+@pytest.mark.parametrize("K", [32, 64, 96, 160, 256, 320])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_bf16_tile_aligned_fast_path(K, ta, tb):
     # M = N = 4096 gives 256 tiles of 256 x 256, the direct-to-LDS path.
