@@ -30,6 +30,8 @@ struct State {
     std::mutex pool_mu;
     std::map<size_t, std::vector<void*>> free_lists;     // exact-size buckets
     std::unordered_map<void*, size_t> live;              // pointer -> bytes
+    std::map<size_t, std::vector<void*>> host_free;      // pinned host buffers, by size
+    std::unordered_map<void*, size_t> host_live;
 };
 
 State& st() {
@@ -246,6 +248,9 @@ int dh_pool_release(void) {
     for (auto& kv : s.free_lists)
         for (void* p : kv.second) hipFree(p);
     s.free_lists.clear();
+    for (auto& kv : s.host_free)
+        for (void* p : kv.second) hipHostFree(p);
+    s.host_free.clear();
     return DH_OK;
 }
 
@@ -333,6 +338,50 @@ int dh_axpy(float* y, const float* x, float alpha, size_t n) {
     if (blocks > cap) blocks = cap;
     axpy_kernel<<<(unsigned)blocks, 256, 0, stream()>>>(y, x, alpha, n);
     return check_launch("dh_axpy");
+}
+
+// Pinned host memory for staging tensors: hipHostMalloc'd, kept in exact-size buckets (at most
+// 16 per size) so repeated tensors of one shape never re-pin.  A returned buffer may still be
+// the source or target of queued copies, so the stream is drained before it can be handed out
+// again.
+void* dh_host_alloc(size_t bytes) {
+    if (ensure_init() != DH_OK) return nullptr;
+    if (bytes == 0) bytes = 1;
+    State& s = st();
+    {
+        std::lock_guard<std::mutex> g(s.pool_mu);
+        auto it = s.host_free.find(bytes);
+        if (it != s.host_free.end() && !it->second.empty()) {
+            void* p = it->second.back();
+            it->second.pop_back();
+            s.host_live[p] = bytes;
+            return p;
+        }
+    }
+    void* p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+        set_error(DH_ERR_OOM, "hipHostMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(s.pool_mu);
+    s.host_live[p] = bytes;
+    return p;
+}
+
+int dh_host_free(void* p) {
+    if (!p) return DH_OK;
+    State& s = st();
+    hipStreamSynchronize(stream());
+    std::lock_guard<std::mutex> g(s.pool_mu);
+    auto it = s.host_live.find(p);
+    if (it == s.host_live.end())
+        return set_error(DH_ERR_INVALID, "dh_host_free: %p was not allocated by dh_host_alloc", p);
+    const size_t bytes = it->second;
+    s.host_live.erase(it);
+    auto& v = s.host_free[bytes];
+    if (v.size() < 16) v.push_back(p);
+    else hipHostFree(p);
+    return DH_OK;
 }
 
 }  // extern "C"

@@ -81,6 +81,33 @@ bool hip_ready(const char* op) {
     return false;
 }
 
+// ---- host buffers ----------------------------------------------------------------------
+// Tensor buffers of 1 MB and more live in pinned host memory from the backend's pool, so the
+// copies to and from the device run at full PCIe rate; smaller ones are plain calloc.  zero =
+// false is only for outputs the device result overwrites entirely.
+constexpr size_t PIN_MIN_BYTES = 1u << 20;
+
+double* host_buffer(size_t n, bool zero, bool& pinned) {
+    const size_t bytes = n * sizeof(double);
+    pinned = false;
+    if (bytes >= PIN_MIN_BYTES && dh_available()) {
+        if (void* p = dh_host_alloc(bytes)) {
+            if (zero) std::memset(p, 0, bytes);
+            pinned = true;
+            return static_cast<double*>(p);
+        }
+    }
+    return static_cast<double*>(std::calloc(n, sizeof(double)));
+}
+
+void release_host(double* p, bool pinned) {
+    if (pinned) dh_host_free(p);
+    else std::free(p);
+}
+
+Tensor* new_tensor(int d0, int d1, int d2, int d3, bool zero_data);
+Tensor* alloc_result(int d0, int d1, int d2, int d3);
+
 // ---- device residency ------------------------------------------------------------------
 // fp32 device copy of t->data (t->size values), uploaded (fp64 -> fp32 on the device) only
 // when there is none or `data` changed since (version).
@@ -141,6 +168,7 @@ float* grad_in(Tensor* t) {
         need(dh_memcpy_h2d(h.p, t->grad, n * sizeof(double)));
         need(dh_convert(f.p, DH_F32, h.p, DH_F64, n));
         need(dh_axpy(g, f.f(), 1.f, n));
+        need(dh_sync());   // a pinned source is read asynchronously: finish before clearing it
         std::fill(t->grad, t->grad + n, 0.0);
         t->grad_zero = 1;
     }
@@ -152,9 +180,17 @@ float* grad_in(Tensor* t) {
 void flush_dgrad(Tensor* t) {
     if (!t->dgrad) return;
     const size_t n = (size_t)t->size;
-    std::vector<float> h(n);
-    need(dh_memcpy_d2h(h.data(), t->dgrad, n * sizeof(float)));
-    for (size_t i = 0; i < n; ++i) t->grad[i] += (double)h[i];
+    if (t->grad_zero) {
+        // host grad all zero: the device gradient, widened to fp64 on the device, is the result
+        Dev d(n * sizeof(double));
+        need_buf(d);
+        need(dh_convert(d.p, DH_F64, t->dgrad, DH_F32, n));
+        need(dh_memcpy_d2h(t->grad, d.p, n * sizeof(double)));
+    } else {
+        std::vector<float> h(n);
+        need(dh_memcpy_d2h(h.data(), t->dgrad, n * sizeof(float)));
+        for (size_t i = 0; i < n; ++i) t->grad[i] += (double)h[i];
+    }
     dh_free(t->dgrad);
     t->dgrad = nullptr;
     t->grad_zero = 0;
@@ -231,7 +267,7 @@ Tensor* attention_impl(const char* name, int op, bool causal, Tensor* Q, Tensor*
         return alloc_tensor(1, 1, 1, 1);
     }
     if (!hip_ready(name)) return alloc_tensor(1, 1, 1, 1);
-    Tensor* out = alloc_tensor(B, S * dk, 1, 1);
+    Tensor* out = alloc_result(B, S * dk, 1, 1);
     out->is_leaf = 0;
     out->op = op;
     set_parents(out, Q, K, V);
@@ -394,8 +430,8 @@ Tensor* row_op(const char* name, int op, Tensor* x) {
     int R, C;
     row_shape(x, op, R, C);
     if (!hip_ready(name)) return alloc_tensor(1, 1, 1, 1);
-    Tensor* y = op == DREAM_OP_LOG_SOFTMAX ? alloc_tensor(x->d0, x->d1, 1, 1)
-                                           : alloc_tensor(x->d0, x->d1, x->d2, x->d3);
+    Tensor* y = op == DREAM_OP_LOG_SOFTMAX ? alloc_result(x->d0, x->d1, 1, 1)
+                                           : alloc_result(x->d0, x->d1, x->d2, x->d3);
     set_graph(y, x, nullptr, op);
     try {
         Dev d((size_t)y->size * sizeof(float));
@@ -504,7 +540,10 @@ void ref_causal_attention(const double* Q, const double* K, const double* V, dou
 extern "C" {
 
 // ----------------------------------------------------------------------------- tensors
-Tensor* alloc_tensor(int d0, int d1, int d2, int d3) {
+}  // extern "C"
+
+namespace {
+Tensor* new_tensor(int d0, int d1, int d2, int d3, bool zero_data) {
     if (d0 < 0 || d1 < 0 || d2 < 0 || d3 < 0) {
         std::fprintf(stderr, "RUNTIME ERROR: negative tensor dimension (%d,%d,%d,%d)\n", d0, d1,
                      d2, d3);
@@ -518,8 +557,10 @@ Tensor* alloc_tensor(int d0, int d1, int d2, int d3) {
     }
     const int size = n <= 0 ? 1 : (int)n;
     Tensor* t = (Tensor*)std::calloc(1, sizeof(Tensor));
-    t->data = (double*)std::calloc(size, sizeof(double));
-    t->grad = (double*)std::calloc(size, sizeof(double));
+    bool pd, pg;
+    t->data = host_buffer(size, zero_data, pd);
+    t->grad = host_buffer(size, true, pg);
+    t->host_pinned = (pd ? 1 : 0) | (pg ? 2 : 0);
     t->size = size;
     t->d0 = d0;
     t->d1 = d1;
@@ -530,6 +571,14 @@ Tensor* alloc_tensor(int d0, int d1, int d2, int d3) {
     t->grad_zero = 1;
     return t;
 }
+
+// Output tensor of a GPU op: its data is overwritten by the device result, so it is not zeroed.
+Tensor* alloc_result(int d0, int d1, int d2, int d3) { return new_tensor(d0, d1, d2, d3, false); }
+}  // namespace
+
+extern "C" {
+
+Tensor* alloc_tensor(int d0, int d1, int d2, int d3) { return new_tensor(d0, d1, d2, d3, true); }
 
 Tensor* create_scalar(double v) {
     Tensor* t = alloc_tensor(1, 1, 1, 1);
@@ -545,8 +594,8 @@ Tensor* tensor_decref(Tensor* t) {
     tensor_decref(t->rhs);
     for (int i = 0; i < t->num_parents; ++i) tensor_decref(t->parents[i]);
     drop_device(t);
-    std::free(t->data);
-    std::free(t->grad);
+    release_host(t->data, t->host_pinned & 1);
+    release_host(t->grad, t->host_pinned & 2);
     std::free(t->fdata);
     std::free(t->fgrad);
     std::free(t);
@@ -610,7 +659,7 @@ Tensor* zero_grad(Tensor* t) {
         rt_error("zero_grad", "tensor is null");
         return nullptr;
     }
-    std::fill(t->grad, t->grad + t->size, 0.0);
+    if (!t->grad_zero) std::fill(t->grad, t->grad + t->size, 0.0);   // else already all zero
     if (t->dgrad) dh_free(t->dgrad);
     t->dgrad = nullptr;
     t->grad_zero = 1;
@@ -727,7 +776,7 @@ Tensor* tensor_matmul(Tensor* a, Tensor* b) {
     }
     if (!hip_ready("matmul (@)")) return alloc_tensor(1, 1, 1, 1);
     const int M = a->d0, K = a->d1, N = b->d1;
-    Tensor* c = alloc_tensor(M, N, 1, 1);
+    Tensor* c = alloc_result(M, N, 1, 1);
     set_graph(c, a, b, DREAM_OP_MATMUL);
     const bool f32 = a->dtype == 1 && b->dtype == 1 && a->fdata && b->fdata;
     try {
@@ -793,7 +842,7 @@ static Tensor* linear_impl(Tensor* x, Tensor* W, Tensor* b, bool relu) {
         return alloc_tensor(1, 1, 1, 1);
     }
     if (!hip_ready("linear")) return alloc_tensor(1, 1, 1, 1);
-    Tensor* y = alloc_tensor(N, out, 1, 1);
+    Tensor* y = alloc_result(N, out, 1, 1);
     set_graph(y, x, W, relu ? DREAM_OP_LINEAR_RELU : DREAM_OP_LINEAR);
     set_parents(y, x, W, b);
     try {
@@ -826,7 +875,7 @@ Tensor* dream_bmm(Tensor* a, Tensor* b, Tensor* batch_t, Tensor* m_t, Tensor* k_
         return alloc_tensor(1, 1, 1, 1);
     }
     if (!hip_ready("bmm")) return alloc_tensor(1, 1, 1, 1);
-    Tensor* c = alloc_tensor(Bt, M * N, 1, 1);
+    Tensor* c = alloc_result(Bt, M * N, 1, 1);
     set_graph(c, a, b, DREAM_OP_BMM);
     c->bmm_B = Bt;
     c->bmm_M = M;
@@ -875,7 +924,7 @@ static Tensor* conv_impl(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h_
         return alloc_tensor(1, 1, 1, 1);
     }
     if (!hip_ready("conv2d")) return alloc_tensor(1, 1, 1, 1);
-    Tensor* out = alloc_tensor(N, (int)(Cout * P), 1, 1);
+    Tensor* out = alloc_result(N, (int)(Cout * P), 1, 1);
     set_graph(out, input, kernel, DREAM_OP_CONV2D);
     const int geom[8] = {H, W, KH, KW, Cin, Cout, pad, stride};
     std::copy(geom, geom + 8, out->conv);

@@ -34,6 +34,8 @@ _SIGS = {
     "dh_malloc": (_vp, [_sz]),
     "dh_free": (_i, [_vp]),
     "dh_pool_release": (_i, []),
+    "dh_host_alloc": (_vp, [_sz]),
+    "dh_host_free": (_i, [_vp]),
     "dh_memcpy_h2d": (_i, [_vp, _vp, _sz]),
     "dh_memcpy_d2h": (_i, [_vp, _vp, _sz]),
     "dh_memcpy_d2d": (_i, [_vp, _vp, _sz]),

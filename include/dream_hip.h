@@ -68,6 +68,13 @@ int dh_flash_eligible(int B, int S, int dk);
 void* dh_malloc(size_t bytes);
 int dh_free(void* d_ptr);
 int dh_pool_release(void);
+/* Pinned (page-locked) host buffers for staging tensors, pooled by exact size (at most 16 per
+ * size); copies to and from them run at full PCIe rate and are truly asynchronous -- a caller
+ * must not modify a buffer that a queued H2D copy still reads (dh_sync first).  dh_host_free
+ * drains the stream before the buffer can be reused; dh_pool_release frees the cached ones.
+ * dh_host_alloc returns NULL (with dh_last_error) when pinning fails. */
+void* dh_host_alloc(size_t bytes);
+int dh_host_free(void* h_ptr);
 int dh_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes);
 int dh_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes);
 int dh_memcpy_d2d(void* d_dst, const void* d_src, size_t bytes);

@@ -55,6 +55,7 @@ typedef struct Tensor {
     float* dgrad;              /* device fp32 gradient during backward(), or NULL  */
     int grad_zero;             /* 1 while every host grad value is known to be 0   */
     float* dlse;               /* attention nodes: device per-row log-sum-exp (B*S) */
+    int host_pinned;           /* bit 0: data, bit 1: grad are pinned pool buffers   */
 } Tensor;
 
 enum {
