@@ -587,6 +587,181 @@ flash_fwd_f32_kernel(int BH, int S, float scale_log2, const float* __restrict__ 
     }
 }
 
+// fp32, small grids (few slices x short sequences, e.g. config 3's 24 slices of 256): the
+// kernel above gives each work-group 128 rows and walks its key stages one after another, so a
+// short problem leaves most CUs idle while a few groups run several stages in series.  Here a
+// work-group owns 32 query rows and its 4 waves take the key stages round-robin (wave w: stages
+// w, w+4, ...), each wave with its own K/V tile in its own LDS region (no work-group barrier in
+// the loop, whose trip count differs per wave); at the end the waves' partial (m, l, O) merge
+// through LDS: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w, M = max_w m_w.
+template <int D>
+struct F32SplitCfg {
+    static constexpr int KEYS = D == 128 ? 32 : 64;        // keys per stage
+    static constexpr int KB = KEYS / 32;                   // 32-key MFMA blocks per stage
+    static constexpr int LS = D + 4;                       // LDS row stride (floats)
+    static constexpr int WAVE_FLOATS = 2 * KEYS * LS;      // K + V tile of one wave
+    static constexpr int MERGE_FLOATS = 32 * (D + 2);      // O rows + m, l of one wave
+    static constexpr int LDS_FLOATS = 4 * (WAVE_FLOATS > MERGE_FLOATS ? WAVE_FLOATS : MERGE_FLOATS);
+};
+
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(NT)
+flash_fwd_f32_split_kernel(int BH, int S, float scale_log2, const float* __restrict__ Q,
+                           const float* __restrict__ K, const float* __restrict__ V,
+                           float* __restrict__ O, float* __restrict__ LSE) {
+    using Cfg = F32SplitCfg<D>;
+    constexpr int ND = D / 32, NDQ = D / 4, KEYS = Cfg::KEYS, LS = Cfg::LS;
+    extern __shared__ __attribute__((aligned(16))) float fsm[];
+
+    const int n_qb = (S + 31) / 32;
+    const int bh = blockIdx.x % BH;
+    const int rr = blockIdx.x / BH;
+    const int qb = CAUSAL ? n_qb - 1 - rr : rr;          // longest key range first
+    const int r0 = qb * 32;
+    const size_t base = (size_t)bh * S * D;
+    const float* Qg = Q + base;
+    const float* Kg = K + base;
+    const float* Vg = V + base;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int i = r0 + l32;
+    float* const ks = fsm + wave * Cfg::WAVE_FLOATS;
+    float* const vs = ks + KEYS * LS;
+
+    float qf[NDQ][2];
+#pragma unroll
+    for (int u = 0; u < NDQ; ++u) {
+        const float* q = Qg + (size_t)i * D + 4 * u + 2 * h;
+        qf[u][0] = i < S ? q[0] : 0.f;
+        qf[u][1] = i < S ? q[1] : 0.f;
+    }
+    f32x16 oacc[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[d][r] = 0.f;
+    float m = NEG, l = 0.f;
+
+    const int kend = CAUSAL ? min(S, r0 + 32) : S;
+    const int nst = (kend + KEYS - 1) / KEYS;
+    for (int st = wave; st < nst; st += 4) {
+        const int j0 = st * KEYS;
+        // this wave's stage into its own LDS region (the previous stage's reads are done)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int c = 0; c < KEYS * D / 4 / 64; ++c) {
+            const int f = lane + 64 * c;
+            const int key = f / (D / 4), dq = f % (D / 4);
+            const int j = j0 + key;
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 kv = j < S ? *reinterpret_cast<const f32x4*>(Kg + (size_t)j * D + 4 * dq) : z;
+            const f32x4 vv = j < S ? *reinterpret_cast<const f32x4*>(Vg + (size_t)j * D + 4 * dq) : z;
+            *reinterpret_cast<f32x4*>(&ks[key * LS + 4 * dq]) = kv;
+            *reinterpret_cast<f32x4*>(&vs[key * LS + 4 * dq]) = vv;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // visible to the wave's other lanes
+
+        f32x16 sacc[Cfg::KB];
+#pragma unroll
+        for (int kb = 0; kb < Cfg::KB; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+#pragma unroll
+            for (int u = 0; u < NDQ; ++u) {
+                const float* kr = &ks[(32 * kb + l32) * LS + 4 * u + 2 * h];
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[0], qf[u][0], sacc[kb], 0, 0, 0);
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[1], qf[u][1], sacc[kb], 0, 0, 0);
+            }
+        }
+        float mx = NEG;
+#pragma unroll
+        for (int kb = 0; kb < Cfg::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = j0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+                float sc = sacc[kb][r] * scale_log2;
+                if (j >= S || (CAUSAL && j > i)) sc = NEG;
+                sacc[kb][r] = sc;
+                mx = fmaxf(mx, sc);
+            }
+        mx = fmaxf(mx, xor32(mx));
+        const float m_new = fmaxf(m, mx);
+        const float corr = fast_exp2(m - m_new);
+        m = m_new;
+        float sum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < Cfg::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(sacc[kb][r] - m_new);
+                sacc[kb][r] = p;
+                sum += p;
+            }
+        sum += xor32(sum);
+        l = l * corr + sum;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+#pragma unroll
+        for (int kb = 0; kb < Cfg::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+#pragma unroll
+                for (int d = 0; d < ND; ++d)
+                    oacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * LS + 32 * d + l32],
+                                                                  sacc[kb][r], oacc[d], 0, 0, 0);
+            }
+    }
+
+    // Merge: every wave parks (m, l, O^T) of its 32 rows; wave 0 combines them.  A wave with
+    // no stage holds m = NEG, l = 0, O = 0 and drops out (2^(NEG - M) = 0).
+    __syncthreads();   // all waves are done with their K/V tiles
+    float* const part = fsm + wave * (32 * (D + 2));   // [32 rows][D] then m[32], l[32]
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[l32 * D + 32 * d + 8 * (r >> 2) + 4 * h + (r & 3)] = oacc[d][r];
+    if (h == 0) {
+        part[32 * D + l32] = m;
+        part[32 * D + 32 + l32] = l;
+    }
+    __syncthreads();
+    if (wave != 0 || i >= S) return;
+    float mw[4], M = NEG;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        mw[w] = fsm[w * (32 * (D + 2)) + 32 * D + l32];
+        M = fmaxf(M, mw[w]);
+    }
+    float sc[4], L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        sc[w] = fast_exp2(mw[w] - M);
+        L += sc[w] * fsm[w * (32 * (D + 2)) + 32 * D + 32 + l32];
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    float* orow = O + base + (size_t)i * D;
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            f32x4 w4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int dd = 32 * d + 8 * q + 4 * h + e;
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) v += sc[w] * fsm[w * (32 * (D + 2)) + l32 * D + dd];
+                w4[e] = v * inv;
+            }
+            *reinterpret_cast<f32x4*>(orow + 32 * d + 8 * q + 4 * h) = w4;
+        }
+    if (h == 0) LSE[(size_t)bh * S + i] = (M + __log2f(L)) * 0.69314718055994531f;
+}
+
 template <typename Kern>
 int set_lds(Kern kern, size_t bytes, bool& done) {
     if (done) return DH_OK;
@@ -614,11 +789,21 @@ int launch_bf16(int BH, int S, float sl2, const void* Q, const void* K, const vo
 template <int D, bool CAUSAL>
 int launch_f32(int BH, int S, float sl2, const void* Q, const void* K, const void* V, void* O,
                float* LSE) {
+    const int grid = BH * ((S + 127) / 128);
+    if (2 * grid < num_cus()) {   // small problem: 32-row work-groups, key stages split over waves
+        auto kern = flash_fwd_f32_split_kernel<D, CAUSAL>;
+        const size_t lds = (size_t)F32SplitCfg<D>::LDS_FLOATS * sizeof(float);
+        static bool done_split = false;
+        DH_TRY(set_lds(kern, lds, done_split));
+        kern<<<BH * ((S + 31) / 32), NT, lds, stream()>>>(BH, S, sl2, (const float*)Q,
+                                                          (const float*)K, (const float*)V,
+                                                          (float*)O, LSE);
+        return check_launch("dh_flash_fwd(f32 split)");
+    }
     auto kern = flash_fwd_f32_kernel<D, CAUSAL>;
     const size_t lds = 4 * F32Stage<D>::ELEMS * sizeof(float);
     static bool done = false;
     DH_TRY(set_lds(kern, lds, done));
-    const int grid = BH * ((S + 127) / 128);
     kern<<<grid, NT, lds, stream()>>>(BH, S, sl2, (const float*)Q, (const float*)K,
                                       (const float*)V, (float*)O, LSE);
     return check_launch("dh_flash_fwd(f32)");

@@ -56,6 +56,20 @@ def test_fp32_fwd_shapes(S, D, causal):
         assert np.allclose(got.reshape(BH, S, D)[:, 0], V.reshape(BH, S, D)[:, 0], atol=1e-6)
 
 
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fp32_fwd_wide_grid(D, causal):
+    # 130 slices x 257 rows fill the chip with 128-row work-groups (the small-grid split
+    # kernel covers the 3-slice shapes above); ragged last block, fp64 oracle.
+    BH, S = 130, 257
+    Q, K, V = inputs(BH, S, D, 1000 + D + causal, n=3)
+    got, lse = flash_fwd(Q, K, V, BH, S, D, causal)
+    Q64, K64, V64 = (x.astype(np.float64) for x in (Q, K, V))
+    tol = 1e-5 * np.sqrt(S)
+    assert maxrel(got, O.attention(Q64, K64, V64, BH, S, D, causal)) <= tol
+    assert np.abs(lse - ref_lse(Q, K, BH, S, D, causal)).max() <= tol
+
+
 @pytest.mark.parametrize("S", [1, 64, 100, 257, 520])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
