@@ -126,6 +126,28 @@ def rows_workload(op, R, C, seed=4):
     return step, 0.0, byts, [X, Y, G, GX, G2]
 
 
+def elementwise_workload(op, shape_a, shape_b=None, seed=10):
+    """Elementwise op in fp64 (Dream's number type; HBM-bound): dh_binary over broadcast
+    strides or dh_unary.  Algorithmic bytes = every operand read once + C written once."""
+    rng = np.random.default_rng(seed)
+    A = DB.from_numpy(rng.standard_normal(shape_a))
+    n = int(np.prod(shape_a))
+    C = DB.empty((n,), np.float64)
+    if shape_b is None:
+        return (lambda: hip.unary(op, hip.F64, A, C, n)), 0.0, 16.0 * n, [A, C]
+    B = DB.from_numpy(rng.standard_normal(shape_b))
+    da, db = [*shape_a, 1, 1][:4], [*shape_b, 1, 1][:4]
+    sa = [da[1] * da[2] * da[3] if da[0] > 1 else 0, da[2] * da[3] if da[1] > 1 else 0,
+          da[3] if da[2] > 1 else 0, 1 if da[3] > 1 else 0]
+    sb = [db[1] * db[2] * db[3] if db[0] > 1 else 0, db[2] * db[3] if db[1] > 1 else 0,
+          db[3] if db[2] > 1 else 0, 1 if db[3] > 1 else 0]
+    nb = int(np.prod(shape_b))
+
+    def step():
+        hip.binary(op, hip.F64, A, n, sa, B, nb, sb, C, da)
+    return step, 0.0, 8.0 * (2 * n + nb), [A, B, C]
+
+
 def linear_workload(N, IN, OUT, relu=True, seed=6):
     """Fused linear layer Y = relu(X W^T + b) (dream_linear_relu) as one GEMM with the bias /
     ReLU epilogue, fp32."""
@@ -203,6 +225,16 @@ WORKLOADS = {
                                   "hbm", "row layer norm 16384 x 1024 fp32 (HBM-bound)"),
     "layer_norm_bwd_16384x1024": (rows_workload, dict(op="layer_norm_bwd", R=16384, C=1024),
                                   "hbm", "row layer norm backward 16384 x 1024 fp32 (HBM-bound)"),
+    "ew_add_f64_4096x4096": (elementwise_workload, dict(op="add", shape_a=(4096, 4096),
+                                                        shape_b=(4096, 4096)), "hbm",
+                             "elementwise A + B, 4096 x 4096 fp64 (runGPU, HBM-bound)"),
+    "ew_mul_rowbcast_f64_4096x4096": (elementwise_workload,
+                                      dict(op="mul", shape_a=(4096, 4096), shape_b=(1, 4096)),
+                                      "hbm", "elementwise A * b, 4096 x 4096 fp64 with a broadcast "
+                                             "row (runGPU strides, HBM-bound)"),
+    "ew_sigmoid_f64_4096x4096": (elementwise_workload,
+                                 dict(op="sigmoid", shape_a=(4096, 4096)), "hbm",
+                                 "elementwise sigmoid, 4096 x 4096 fp64 (runGPUUnary, HBM-bound)"),
 }
 
 MLP_SHAPES = [  # config 2: (name, transA, transB, M, N, K)
@@ -454,7 +486,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if prec == "bf16" else "f32",
+        "dtype": "bf16" if prec == "bf16" else "f64" if args.workload.startswith("ew_") else "f32",
         "data": "synthetic N(0,1) inputs (numpy PCG64, seeded), resident in HBM",
         "config": {"workload": head["desc"], "name": args.workload},
         "roofline": roofline,

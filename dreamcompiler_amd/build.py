@@ -29,6 +29,7 @@ HIP_SOURCES = [
     "dh_flash_bwd.hip",
     "dh_rows.hip",
     "dh_conv.hip",
+    "dh_elementwise.hip",
 ]
 RT_SOURCES = ["dream_rt.cpp"]
 

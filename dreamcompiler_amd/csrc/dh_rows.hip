@@ -56,15 +56,18 @@ struct Row {
             }
         }
     }
+    // Non-temporal: the output row is streamed out and not read again here, and keeping it
+    // out of the caches leaves them to the inputs.
     __device__ void store(float* __restrict__ p, int C, int s) const {
 #pragma unroll
         for (int t = 0; t < NV; ++t) {
             const int e = VEC * (t * G + s);
             if (e >= C) continue;
             if (VEC == 4) {
-                *reinterpret_cast<f4*>(p + e) = f4{v[t][0], v[t][1], v[t][2], v[t][3]};
+                __builtin_nontemporal_store(f4{v[t][0], v[t][1], v[t][2], v[t][3]},
+                                            reinterpret_cast<f4*>(p + e));
             } else {
-                p[e] = v[t][0];
+                __builtin_nontemporal_store(v[t][0], p + e);
             }
         }
     }

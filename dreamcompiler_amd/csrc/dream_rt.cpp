@@ -483,6 +483,77 @@ void conv_backward(Tensor* t) {
     need(dh_col2im(dcol.f(), dgrad(x), d.N, d.Cin, d.H, d.W, d.KH, d.KW, d.pad, d.stride, 1));
 }
 
+// Elementwise backward branches on the host, as in the reference (autograd.inc:58-90 with
+// operands indexed j % size, not by the forward's broadcast strides; pow 491-506 over the
+// base's elements).
+void binary_backward(Tensor* t) {
+    Tensor *A = t->lhs, *B = t->rhs;
+    const int na = A->size, nb = B->size, n = t->size;
+    const double *a = A->data, *b = B->data, *g = t->grad;
+    double *ga = A->grad, *gb = B->grad;
+    switch (t->op) {
+        case DREAM_OP_ADD:
+            for (int j = 0; j < n; ++j) ga[j % na] += g[j], gb[j % nb] += g[j];
+            break;
+        case DREAM_OP_SUB:
+            for (int j = 0; j < n; ++j) ga[j % na] += g[j], gb[j % nb] -= g[j];
+            break;
+        case DREAM_OP_DIV:
+            for (int j = 0; j < n; ++j) {
+                const double r = b[j % nb];
+                ga[j % na] += g[j] / r;
+                gb[j % nb] -= g[j] * a[j % na] / (r * r);
+            }
+            break;
+        case DREAM_OP_MINIMUM:
+        case DREAM_OP_MAXIMUM: {
+            const bool is_max = t->op == DREAM_OP_MAXIMUM;
+            for (int j = 0; j < n; ++j) {   // ties go to the left operand
+                const double av = a[j % na], bv = b[j % nb];
+                if (is_max ? av >= bv : av <= bv) ga[j % na] += g[j];
+                else gb[j % nb] += g[j];
+            }
+            break;
+        }
+        default: {   // DREAM_OP_POW
+            const double* y = t->data;
+            for (int j = 0; j < na; ++j) {
+                const double x = a[j], e = b[j % nb], yy = y[j % n], gg = g[j % n];
+                if (x != 0.0) ga[j] += gg * e * yy / x;
+                if (x > 0.0) gb[j % nb] += gg * yy * std::log(x);
+            }
+            break;
+        }
+    }
+}
+
+void unary_backward(Tensor* t) {
+    const int n = t->lhs->size;
+    const double *x = t->lhs->data, *y = t->data, *g = t->grad;
+    double* gx = t->lhs->grad;
+    for (int j = 0; j < n; ++j) {
+        double d;
+        switch (t->op) {
+            case DREAM_OP_RELU: d = x[j] > 0 ? 1.0 : 0.0; break;
+            case DREAM_OP_EXP: d = y[j]; break;
+            case DREAM_OP_LOG: gx[j] += g[j] / x[j]; continue;
+            case DREAM_OP_SQRT: gx[j] += g[j] / (2.0 * y[j]); continue;
+            case DREAM_OP_ABS: d = x[j] >= 0 ? 1.0 : -1.0; break;
+            case DREAM_OP_SIGMOID: d = y[j] * (1 - y[j]); break;
+            case DREAM_OP_TANH: d = 1 - y[j] * y[j]; break;
+            case DREAM_OP_SIN: d = std::cos(x[j]); break;
+            case DREAM_OP_COS: d = -std::sin(x[j]); break;
+            case DREAM_OP_TAN: {
+                const double c = std::cos(x[j]);
+                gx[j] += g[j] / (c * c);
+                continue;
+            }
+            default: gx[j] += g[j] / (1.0 + x[j] * x[j]); continue;   // DREAM_OP_ATAN
+        }
+        gx[j] += d * g[j];
+    }
+}
+
 void topo_sort(Tensor* root, std::vector<Tensor*>& order) {
     // Iterative post-order DFS over lhs, rhs and parents (runtime/backend/gpu.inc:742-779).
     std::unordered_set<Tensor*> seen;
@@ -631,18 +702,266 @@ Tensor* sum(Tensor* a) {
     return c;
 }
 
-static Tensor* binary(Tensor* a, Tensor* b, int op) {
-    Tensor* c = alloc_tensor(std::max(a->d0, b->d0), std::max(a->d1, b->d1), a->d2, a->d3);
-    for (int i = 0; i < c->size; ++i) {
-        const double x = a->data[i % a->size], y = b->data[i % b->size];
-        c->data[i] = op == DREAM_OP_MUL ? x * y : x + y;
+// ---- elementwise builtins (elementwise.inc:276-336, 1254-1270; math_extra.inc:1-10;
+// builtins.inc:85-87) over runGPU / runGPUUnary (backend/gpu.inc:637-716): outputs of at most
+// 4194304 elements run on the host (the reference's CPU-first rule, gpu.inc:640, 691), larger
+// ones on the GPU in fp64 (DREAM_ELEMWISE_CPU_MAX moves the bound; 0 sends every op to the
+// GPU).  fp64 is Dream's number type: the GPU gives the host loop's values exactly for the
+// IEEE-exact ops, and within an ulp or two for the transcendental ones.
+static long long elemwise_cpu_max() {
+    const char* e = std::getenv("DREAM_ELEMWISE_CPU_MAX");
+    return e && *e ? std::atoll(e) : 4194304;
+}
+
+static double host_bin(int op, double a, double b) {
+    switch (op) {
+        case DH_BOP_ADD: return a + b;
+        case DH_BOP_SUB: return a - b;
+        case DH_BOP_MUL: return a * b;
+        case DH_BOP_DIV: return a / b;
+        case DH_BOP_MOD: return std::fmod(a, b);
+        case DH_BOP_GT: return a > b ? 1.0 : 0.0;
+        case DH_BOP_LT: return a < b ? 1.0 : 0.0;
+        case DH_BOP_GE: return a >= b ? 1.0 : 0.0;
+        case DH_BOP_LE: return a <= b ? 1.0 : 0.0;
+        case DH_BOP_EQ: return std::fabs(a - b) < 1e-6 ? 1.0 : 0.0;
+        case DH_BOP_NE: return std::fabs(a - b) >= 1e-6 ? 1.0 : 0.0;
+        case DH_BOP_AND: return (a > 0 && b > 0) ? 1.0 : 0.0;
+        case DH_BOP_OR: return (a > 0 || b > 0) ? 1.0 : 0.0;
+        case DH_BOP_ATAN2: return std::atan2(a, b);
+        case DH_BOP_POW: return std::pow(a, b);
+        case DH_BOP_MIN: return a < b ? a : b;
+        default: return a > b ? a : b;
     }
-    set_graph(c, a, b, op);
+}
+
+static double host_un(int op, double a, double lo, double hi) {
+    switch (op) {
+        case DH_UOP_RELU: return a > 0.0 ? a : 0.0;
+        case DH_UOP_EXP: return std::exp(a);
+        case DH_UOP_LOG: return std::log(a);
+        case DH_UOP_SQRT: return std::sqrt(a);
+        case DH_UOP_ABS: return std::fabs(a);
+        case DH_UOP_SIGMOID: return 1.0 / (1.0 + std::exp(-a));
+        case DH_UOP_TANH: return std::tanh(a);
+        case DH_UOP_LNOT: return a == 0.0 ? 1.0 : 0.0;
+        case DH_UOP_SIN: return std::sin(a);
+        case DH_UOP_COS: return std::cos(a);
+        case DH_UOP_TAN: return std::tan(a);
+        case DH_UOP_ATAN: return std::atan(a);
+        case DH_UOP_FLOOR: return std::floor(a);
+        case DH_UOP_CEIL: return std::ceil(a);
+        case DH_UOP_ROUND: return std::round(a);
+        default: return std::fmax(lo, std::fmin(hi, a));
+    }
+}
+
+// bcastStrides (gpu.inc:443-449): the operand's own contiguous strides, 0 on a dim of 1.
+static void bcast_strides(const Tensor* t, int s[4]) {
+    s[0] = t->d0 > 1 ? t->d1 * t->d2 * t->d3 : 0;
+    s[1] = t->d1 > 1 ? t->d2 * t->d3 : 0;
+    s[2] = t->d2 > 1 ? t->d3 : 0;
+    s[3] = t->d3 > 1 ? 1 : 0;
+}
+
+// Largest element index the strides reach over C's dims.  The reference reads past an
+// operand whose dims do not broadcast against C's (after its shape-mismatch warning); here
+// such a pair is an error instead.
+static long long reach(const int s[4], const int cd[4]) {
+    long long r = 0;
+    for (int k = 0; k < 4; ++k) r += (long long)(cd[k] - 1) * s[k];
+    return r;
+}
+
+static int binop_node(int op) {
+    switch (op) {
+        case DH_BOP_ADD: return DREAM_OP_ADD;
+        case DH_BOP_SUB: return DREAM_OP_SUB;
+        case DH_BOP_MUL: return DREAM_OP_MUL;
+        case DH_BOP_DIV: return DREAM_OP_DIV;
+        case DH_BOP_MIN: return DREAM_OP_MINIMUM;
+        case DH_BOP_MAX: return DREAM_OP_MAXIMUM;
+        case DH_BOP_POW: return DREAM_OP_POW;
+        default: return DREAM_OP_NO_GRAD;   // no backward branch in the reference
+    }
+}
+
+static int unop_node(int op) {
+    switch (op) {
+        case DH_UOP_RELU: return DREAM_OP_RELU;
+        case DH_UOP_EXP: return DREAM_OP_EXP;
+        case DH_UOP_LOG: return DREAM_OP_LOG;
+        case DH_UOP_SQRT: return DREAM_OP_SQRT;
+        case DH_UOP_ABS: return DREAM_OP_ABS;
+        case DH_UOP_SIGMOID: return DREAM_OP_SIGMOID;
+        case DH_UOP_TANH: return DREAM_OP_TANH;
+        case DH_UOP_SIN: return DREAM_OP_SIN;
+        case DH_UOP_COS: return DREAM_OP_COS;
+        case DH_UOP_TAN: return DREAM_OP_TAN;
+        case DH_UOP_ATAN: return DREAM_OP_ATAN;
+        default: return DREAM_OP_NO_GRAD;
+    }
+}
+
+// The GPU result's fp32 rounding becomes c's device copy, like a GEMM result's.
+static void keep_dev32(Tensor* c, Dev& d32) {
+    if (c->dev) dh_free(c->dev);
+    c->dev = static_cast<float*>(d32.release());
+    c->dev_version = c->version;
+}
+
+// c = op(a, b) over c's dims; false (error printed) when the shapes do not broadcast or the
+// GPU path fails.
+static bool elementwise_binary(const char* name, int op, Tensor* a, Tensor* b, Tensor* c) {
+    int as[4], bs[4];
+    const int cd[4] = {c->d0, c->d1, c->d2, c->d3};
+    bcast_strides(a, as);
+    bcast_strides(b, bs);
+    if (reach(as, cd) >= a->size || reach(bs, cd) >= b->size) {
+        rt_error(name, "operands %dx%dx%dx%d and %dx%dx%dx%d do not broadcast", a->d0, a->d1,
+                 a->d2, a->d3, b->d0, b->d1, b->d2, b->d3);
+        return false;
+    }
+    const long long n = c->size;
+    if (n <= elemwise_cpu_max()) {
+        for (long long i = 0; i < n; ++i) {
+            long long r = i, ia = 0, ib = 0;
+            for (int k = 3; k >= 0; --k) {
+                const long long x = r % cd[k];
+                r /= cd[k];
+                ia += x * as[k];
+                ib += x * bs[k];
+            }
+            c->data[i] = host_bin(op, a->data[ia], b->data[ib]);
+        }
+        return true;
+    }
+    if (!hip_ready(name)) return false;
+    try {
+        Dev da((size_t)a->size * 8), db((size_t)b->size * 8), dc((size_t)n * 8), d32((size_t)n * 4);
+        need_buf(da), need_buf(db), need_buf(dc), need_buf(d32);
+        need(dh_memcpy_h2d(da.p, a->data, (size_t)a->size * 8));
+        need(dh_memcpy_h2d(db.p, b->data, (size_t)b->size * 8));
+        need(dh_binary(op, DH_F64, da.p, (size_t)a->size, as, db.p, (size_t)b->size, bs, dc.p, cd,
+                       d32.f()));
+        need(dh_memcpy_d2h(c->data, dc.p, (size_t)n * 8));
+        keep_dev32(c, d32);
+    } catch (const Failure&) {
+        rt_error(name, "%s", dh_last_error());
+        return false;
+    }
+    return true;
+}
+
+static bool elementwise_unary(const char* name, int op, Tensor* a, Tensor* c, double lo, double hi) {
+    const long long n = a->size;
+    if (n <= elemwise_cpu_max()) {
+        for (long long i = 0; i < n; ++i) c->data[i] = host_un(op, a->data[i], lo, hi);
+        return true;
+    }
+    if (!hip_ready(name)) return false;
+    try {
+        Dev da((size_t)n * 8), dc((size_t)n * 8), d32((size_t)n * 4);
+        need_buf(da), need_buf(dc), need_buf(d32);
+        need(dh_memcpy_h2d(da.p, a->data, (size_t)n * 8));
+        need(dh_unary(op, DH_F64, da.p, dc.p, (size_t)n, lo, hi, d32.f()));
+        need(dh_memcpy_d2h(c->data, dc.p, (size_t)n * 8));
+        keep_dev32(c, d32);
+    } catch (const Failure&) {
+        rt_error(name, "%s", dh_last_error());
+        return false;
+    }
+    return true;
+}
+
+// BINOP (elementwise.inc:284-288): null operand -> error and a 1x1 tensor; C's dims are the
+// per-dim maxima (makeBinop, elementwise.inc:269-283).
+static Tensor* binop(const char* name, int op, Tensor* a, Tensor* b) {
+    if (!a || !b) {
+        std::fprintf(stderr, "RUNTIME ERROR in '%s': null operand\n", name);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    Tensor* c = alloc_result(std::max(a->d0, b->d0), std::max(a->d1, b->d1),
+                             std::max(a->d2, b->d2), std::max(a->d3, b->d3));
+    if (!elementwise_binary(name, op, a, b, c)) {
+        tensor_decref(c);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    set_graph(c, a, b, binop_node(op));
     return c;
 }
 
-Tensor* tensor_add(Tensor* a, Tensor* b) { return binary(a, b, DREAM_OP_ADD); }
-Tensor* tensor_mul(Tensor* a, Tensor* b) { return binary(a, b, DREAM_OP_MUL); }
+// UNARY (elementwise.inc:313-318): null input -> error naming the op and a 1x1 tensor.
+static Tensor* unop(const char* name, int op, Tensor* a, double lo = 0.0, double hi = 0.0) {
+    if (!a) {
+        std::fprintf(stderr, "RUNTIME ERROR in '%s': null input\n", name);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    Tensor* c = alloc_result(a->d0, a->d1, a->d2, a->d3);
+    if (!elementwise_unary(name, op, a, c, lo, hi)) {
+        tensor_decref(c);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    set_graph(c, a, nullptr, unop_node(op));
+    return c;
+}
+
+Tensor* tensor_add(Tensor* a, Tensor* b) { return binop("+", DH_BOP_ADD, a, b); }
+Tensor* tensor_sub(Tensor* a, Tensor* b) { return binop("-", DH_BOP_SUB, a, b); }
+Tensor* tensor_mul(Tensor* a, Tensor* b) { return binop("*", DH_BOP_MUL, a, b); }
+Tensor* tensor_div(Tensor* a, Tensor* b) { return binop("/", DH_BOP_DIV, a, b); }
+Tensor* tensor_mod(Tensor* a, Tensor* b) { return binop("%", DH_BOP_MOD, a, b); }
+Tensor* tensor_gt(Tensor* a, Tensor* b) { return binop(">", DH_BOP_GT, a, b); }
+Tensor* tensor_lt(Tensor* a, Tensor* b) { return binop("<", DH_BOP_LT, a, b); }
+Tensor* tensor_ge(Tensor* a, Tensor* b) { return binop(">=", DH_BOP_GE, a, b); }
+Tensor* tensor_le(Tensor* a, Tensor* b) { return binop("<=", DH_BOP_LE, a, b); }
+Tensor* tensor_eq(Tensor* a, Tensor* b) { return binop("==", DH_BOP_EQ, a, b); }
+Tensor* tensor_ne(Tensor* a, Tensor* b) { return binop("!=", DH_BOP_NE, a, b); }
+Tensor* tensor_and(Tensor* a, Tensor* b) { return binop("&&", DH_BOP_AND, a, b); }
+Tensor* tensor_or(Tensor* a, Tensor* b) { return binop("||", DH_BOP_OR, a, b); }
+Tensor* dream_minimum(Tensor* a, Tensor* b) { return binop("min", DH_BOP_MIN, a, b); }
+Tensor* dream_maximum(Tensor* a, Tensor* b) { return binop("max", DH_BOP_MAX, a, b); }
+Tensor* dream_atan2(Tensor* y, Tensor* x) { return binop("atan2", DH_BOP_ATAN2, y, x); }
+
+// dream_pow (elementwise.inc:1254-1270): C is 2-D, (max d0, max d1).
+Tensor* dream_pow(Tensor* base, Tensor* exp_t) {
+    if (!base || !exp_t) {
+        std::fprintf(stderr, "RUNTIME ERROR in '**': null operand\n");
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    Tensor* c = alloc_result(std::max(base->d0, exp_t->d0), std::max(base->d1, exp_t->d1), 1, 1);
+    if (!elementwise_binary("**", DH_BOP_POW, base, exp_t, c)) {
+        tensor_decref(c);
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    set_graph(c, base, exp_t, DREAM_OP_POW);
+    return c;
+}
+
+Tensor* relu(Tensor* a) { return unop("relu", DH_UOP_RELU, a); }
+Tensor* dream_exp(Tensor* a) { return unop("exp", DH_UOP_EXP, a); }
+Tensor* dream_log(Tensor* a) { return unop("log", DH_UOP_LOG, a); }
+Tensor* dream_sqrt(Tensor* a) { return unop("sqrt", DH_UOP_SQRT, a); }
+Tensor* dream_abs(Tensor* a) { return unop("abs", DH_UOP_ABS, a); }
+Tensor* dream_sigmoid(Tensor* a) { return unop("sigmoid", DH_UOP_SIGMOID, a); }
+Tensor* dream_tanh(Tensor* a) { return unop("tanh", DH_UOP_TANH, a); }
+Tensor* dream_logical_not(Tensor* a) { return unop("lnot", DH_UOP_LNOT, a); }
+Tensor* dream_sin(Tensor* a) { return unop("sin", DH_UOP_SIN, a); }
+Tensor* dream_cos(Tensor* a) { return unop("cos", DH_UOP_COS, a); }
+Tensor* dream_tan(Tensor* a) { return unop("tan", DH_UOP_TAN, a); }
+Tensor* dream_atan(Tensor* a) { return unop("atan", DH_UOP_ATAN, a); }
+Tensor* dream_floor(Tensor* a) { return unop("floor", DH_UOP_FLOOR, a); }
+Tensor* dream_ceil(Tensor* a) { return unop("ceil", DH_UOP_CEIL, a); }
+Tensor* dream_round(Tensor* a) { return unop("round", DH_UOP_ROUND, a); }
+
+// dream_clip (elementwise.inc:329-336): fmax(lo, fmin(hi, x)) with the bounds' first values.
+Tensor* dream_clip(Tensor* a, Tensor* lo, Tensor* hi) {
+    if (!lo || !hi || !lo->data || !hi->data) {
+        std::fprintf(stderr, "RUNTIME ERROR in 'clip': null bound\n");
+        return alloc_tensor(1, 1, 1, 1);
+    }
+    return unop("clip", DH_UOP_CLIP, a, lo->data[0], hi->data[0]);
+}
 
 Tensor* tensor_get_grad(Tensor* t) {
     if (!t) {
@@ -1029,11 +1348,27 @@ Tensor* backward(Tensor* root) {
                     }
                     break;
                 case DREAM_OP_ADD:
+                case DREAM_OP_SUB:
+                case DREAM_OP_DIV:
+                case DREAM_OP_MINIMUM:
+                case DREAM_OP_MAXIMUM:
+                case DREAM_OP_POW:
                     host_grad(t);
-                    for (int j = 0; j < t->size; ++j) {
-                        t->lhs->grad[j % t->lhs->size] += t->grad[j];
-                        t->rhs->grad[j % t->rhs->size] += t->grad[j];
-                    }
+                    binary_backward(t);
+                    break;
+                case DREAM_OP_RELU:
+                case DREAM_OP_EXP:
+                case DREAM_OP_LOG:
+                case DREAM_OP_SQRT:
+                case DREAM_OP_ABS:
+                case DREAM_OP_SIGMOID:
+                case DREAM_OP_TANH:
+                case DREAM_OP_SIN:
+                case DREAM_OP_COS:
+                case DREAM_OP_TAN:
+                case DREAM_OP_ATAN:
+                    host_grad(t);
+                    unary_backward(t);
                     break;
                 default:
                     break;

@@ -64,6 +64,9 @@ _SIGS = {
     "dh_im2col": (_i, [_vp, _vp] + [_i] * 8),
     "dh_col2im": (_i, [_vp, _vp] + [_i] * 9),
     "dh_nct_to_cnt": (_i, [_vp, _vp, _i, _i, _sz]),
+    "dh_binary": (_i, [_i, _i, _vp, _sz, ctypes.POINTER(_i), _vp, _sz, ctypes.POINTER(_i), _vp,
+                       ctypes.POINTER(_i), _vp]),
+    "dh_unary": (_i, [_i, _i, _vp, _vp, _sz, ctypes.c_double, ctypes.c_double, _vp]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -239,6 +242,31 @@ def col2im(dcol, dX, N, Cin, H, W, KH, KW, pad=0, stride=1, accumulate=False):
 
 def nct_to_cnt(src, dst, N, C, T):
     check(load().dh_nct_to_cnt(_p(src), _p(dst), N, C, int(T)), "dh_nct_to_cnt")
+
+
+# Elementwise op codes (include/dream_hip.h, the reference's BinopCode / UnopCode order).
+BINOPS = ["add", "sub", "mul", "div", "mod", "gt", "lt", "ge", "le", "eq", "ne", "and", "or",
+          "atan2", "pow", "min", "max"]
+UNOPS = ["relu", "exp", "log", "sqrt", "abs", "sigmoid", "tanh", "lnot", "sin", "cos", "tan",
+         "atan", "floor", "ceil", "round", "clip"]
+
+
+def _i4(v):
+    return (_i * 4)(*[int(x) for x in v])
+
+
+def binary(op, dtype, A, a_len, a_strides, B, b_len, b_strides, C, c_dims, C32=None):
+    """dh_binary: op is a name of BINOPS or its code; strides / dims are 4 ints each."""
+    code = BINOPS.index(op) if isinstance(op, str) else int(op)
+    check(load().dh_binary(code, int(dtype), _p(A), int(a_len), _i4(a_strides), _p(B),
+                           int(b_len), _i4(b_strides), _p(C), _i4(c_dims), _p(C32)),
+          "dh_binary")
+
+
+def unary(op, dtype, A, C, n, lo=0.0, hi=0.0, C32=None):
+    code = UNOPS.index(op) if isinstance(op, str) else int(op)
+    check(load().dh_unary(code, int(dtype), _p(A), _p(C), int(n), float(lo), float(hi), _p(C32)),
+          "dh_unary")
 
 
 def layer_norm_bwd(X, Y, DY, GX, R, C, accumulate=False):

@@ -36,7 +36,21 @@ _SIGS = {
     "linear_relu": [TP] * 3, "dream_bmm": [TP] * 6, "dream_softmax": [TP],
     "dream_log_softmax": [TP], "dream_layer_norm": [TP], "tensor_set_element": [TP] * 3,
     "tensor_set_element_2d": [TP] * 4, "dream_conv2d": [TP] * 7, "dream_conv2d_padded": [TP] * 9,
+    "dream_clip": [TP] * 3,
 }
+# Elementwise builtins by op name (include/dream_rt.h).
+BINARY = {"add": "tensor_add", "sub": "tensor_sub", "mul": "tensor_mul", "div": "tensor_div",
+          "mod": "tensor_mod", "gt": "tensor_gt", "lt": "tensor_lt", "ge": "tensor_ge",
+          "le": "tensor_le", "eq": "tensor_eq", "ne": "tensor_ne", "and": "tensor_and",
+          "or": "tensor_or", "atan2": "dream_atan2", "pow": "dream_pow", "min": "dream_minimum",
+          "max": "dream_maximum"}
+UNARY = {"relu": "relu", "exp": "dream_exp", "log": "dream_log", "sqrt": "dream_sqrt",
+         "abs": "dream_abs", "sigmoid": "dream_sigmoid", "tanh": "dream_tanh",
+         "lnot": "dream_logical_not", "sin": "dream_sin", "cos": "dream_cos", "tan": "dream_tan",
+         "atan": "dream_atan", "floor": "dream_floor", "ceil": "dream_ceil",
+         "round": "dream_round"}
+_SIGS.update({n: [TP, TP] for n in BINARY.values()})
+_SIGS.update({n: [TP] for n in UNARY.values()})
 
 _lib = None
 

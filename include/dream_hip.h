@@ -202,6 +202,38 @@ int dh_col2im(const float* d_dcol, float* d_dX, int N, int Cin, int H, int W, in
               int pad, int stride, int accumulate);
 int dh_nct_to_cnt(const float* d_src, float* d_dst, int N, int C, size_t T);
 
+/* ---- elementwise ops (runGPU / runGPUUnary, runtime/backend/gpu.inc:637-716) ---------------
+ * Op codes follow the reference's BinopCode / UnopCode (gpu.inc:455-460, 571-577); each
+ * computes, in the operand type, what the reference's CPU loop (runCPUBinary / runCPUUnary,
+ * gpu.inc:484-598) computes in fp64: eq / ne compare |a - b| against 1e-6, and / or test
+ * a > 0, b > 0, min / max pick a on ties of the other test, clip is fmax(lo, fmin(hi, a))
+ * (the OpenCL expression of dream_clip, elementwise.inc:329-336). */
+enum {
+    DH_BOP_ADD = 0, DH_BOP_SUB, DH_BOP_MUL, DH_BOP_DIV, DH_BOP_MOD,
+    DH_BOP_GT, DH_BOP_LT, DH_BOP_GE, DH_BOP_LE, DH_BOP_EQ, DH_BOP_NE,
+    DH_BOP_AND, DH_BOP_OR, DH_BOP_ATAN2, DH_BOP_POW, DH_BOP_MIN, DH_BOP_MAX, DH_BOP_COUNT
+};
+enum {
+    DH_UOP_RELU = 0, DH_UOP_EXP, DH_UOP_LOG, DH_UOP_SQRT, DH_UOP_ABS,
+    DH_UOP_SIGMOID, DH_UOP_TANH, DH_UOP_LNOT,
+    DH_UOP_SIN, DH_UOP_COS, DH_UOP_TAN, DH_UOP_ATAN,
+    DH_UOP_FLOOR, DH_UOP_CEIL, DH_UOP_ROUND, DH_UOP_CLIP, DH_UOP_COUNT
+};
+/* C[i] = op(A[ia], B[ib]) over C's dims c_dims[0..3] (d0 outermost, row-major), where i's
+ * indices (i0, i1, i2, i3) give ia = sum ik * a_strides[k] (element strides, 0 on a broadcast
+ * dim: the bcastStrides rule, gpu.inc:443-449) and likewise ib.  dtype DH_F32 or DH_F64 for
+ * A, B, C.  a_len / b_len are the operands' element counts: a stride pattern that would read
+ * past them is DH_ERR_INVALID.  C holds at most 2^31 - 1 elements.  d_C32, DH_F64 only and
+ * may be NULL: also receives C rounded to fp32 (the device copy of the result for fp32
+ * consumers). */
+int dh_binary(int op, int dtype, const void* d_A, size_t a_len, const int* a_strides,
+              const void* d_B, size_t b_len, const int* b_strides, void* d_C, const int* c_dims,
+              float* d_C32);
+/* C[i] = op(A[i]) for n contiguous values; lo / hi are clip's bounds (ignored otherwise).
+ * Pointers 16-byte aligned (every dh_malloc block is).  d_C32 as for dh_binary. */
+int dh_unary(int op, int dtype, const void* d_A, void* d_C, size_t n, double lo, double hi,
+             float* d_C32);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,7 +61,13 @@ typedef struct Tensor {
 enum {
     DREAM_OP_LEAF = 0, DREAM_OP_MATMUL, DREAM_OP_FLASH, DREAM_OP_ATTN, DREAM_OP_ATTN_CAUSAL,
     DREAM_OP_SUM, DREAM_OP_MUL, DREAM_OP_ADD, DREAM_OP_LINEAR, DREAM_OP_LINEAR_RELU,
-    DREAM_OP_BMM, DREAM_OP_SOFTMAX, DREAM_OP_LOG_SOFTMAX, DREAM_OP_LAYER_NORM, DREAM_OP_CONV2D
+    DREAM_OP_BMM, DREAM_OP_SOFTMAX, DREAM_OP_LOG_SOFTMAX, DREAM_OP_LAYER_NORM, DREAM_OP_CONV2D,
+    /* elementwise nodes with a backward branch (autograd.inc:58-90, 284-288, 342-378,
+     * 491-506), and the elementwise nodes without one (comparisons, mod, and/or, atan2,
+     * logical not, floor/ceil/round, clip) */
+    DREAM_OP_SUB, DREAM_OP_DIV, DREAM_OP_MINIMUM, DREAM_OP_MAXIMUM, DREAM_OP_POW,
+    DREAM_OP_RELU, DREAM_OP_EXP, DREAM_OP_LOG, DREAM_OP_SQRT, DREAM_OP_ABS, DREAM_OP_SIGMOID,
+    DREAM_OP_TANH, DREAM_OP_SIN, DREAM_OP_COS, DREAM_OP_TAN, DREAM_OP_ATAN, DREAM_OP_NO_GRAD
 };
 
 /* ---- tensors (runtime/core/tensor.inc:143-303) ---- */
@@ -73,8 +79,49 @@ Tensor* ones(Tensor* d0, Tensor* d1);                      /* elementwise.inc:2 
 Tensor* dream_set_seed(Tensor* seed);                      /* elementwise.inc:35-40 */
 Tensor* dream_randn(Tensor* d0, Tensor* d1);               /* elementwise.inc:48-54 */
 Tensor* sum(Tensor* a);                                    /* elementwise.inc:56    */
+/* ---- elementwise ops (elementwise.inc:276-336, 1254-1270; math_extra.inc:1-10;
+ * builtins.inc:85-87), the reference's runGPU / runGPUUnary path (backend/gpu.inc:637-716).
+ * Binary: C's dims are the per-dim maxima of the operands', each operand read through
+ * bcastStrides (its own contiguous strides, 0 on a dim of 1); operands that do not broadcast
+ * (which the reference reads out of bounds after a warning) are an error.  Outputs of at
+ * most 4194304 elements are computed on the host, larger ones on the GPU in fp64
+ * (DREAM_ELEMWISE_CPU_MAX overrides the bound).  The error text names the operator symbol
+ * ('+', '-', '*', '/', '%', '>', ..., 'min', 'max', 'atan2', '**') or the unary op. */
 Tensor* tensor_add(Tensor* a, Tensor* b);
+Tensor* tensor_sub(Tensor* a, Tensor* b);
 Tensor* tensor_mul(Tensor* a, Tensor* b);
+Tensor* tensor_div(Tensor* a, Tensor* b);
+Tensor* tensor_mod(Tensor* a, Tensor* b);
+Tensor* tensor_gt(Tensor* a, Tensor* b);
+Tensor* tensor_lt(Tensor* a, Tensor* b);
+Tensor* tensor_ge(Tensor* a, Tensor* b);
+Tensor* tensor_le(Tensor* a, Tensor* b);
+Tensor* tensor_eq(Tensor* a, Tensor* b);
+Tensor* tensor_ne(Tensor* a, Tensor* b);
+Tensor* tensor_and(Tensor* a, Tensor* b);
+Tensor* tensor_or(Tensor* a, Tensor* b);
+Tensor* dream_minimum(Tensor* a, Tensor* b);
+Tensor* dream_maximum(Tensor* a, Tensor* b);
+Tensor* dream_atan2(Tensor* y, Tensor* x);
+Tensor* dream_pow(Tensor* base, Tensor* exp_t);            /* C is (max d0, max d1) */
+Tensor* relu(Tensor* a);
+Tensor* dream_exp(Tensor* a);
+Tensor* dream_log(Tensor* a);
+Tensor* dream_sqrt(Tensor* a);
+Tensor* dream_abs(Tensor* a);
+Tensor* dream_sigmoid(Tensor* a);
+Tensor* dream_tanh(Tensor* a);
+Tensor* dream_logical_not(Tensor* a);
+Tensor* dream_sin(Tensor* a);
+Tensor* dream_cos(Tensor* a);
+Tensor* dream_tan(Tensor* a);
+Tensor* dream_atan(Tensor* a);
+Tensor* dream_floor(Tensor* a);
+Tensor* dream_ceil(Tensor* a);
+Tensor* dream_round(Tensor* a);
+/* fmax(lo, fmin(hi, a)) with lo, hi the bounds' first values: the OpenCL expression of the
+ * reference (elementwise.inc:329-336), whose CPU interpreter has no form of it. */
+Tensor* dream_clip(Tensor* a, Tensor* lo, Tensor* hi);
 Tensor* tensor_get_grad(Tensor* t);                        /* autograd.inc:1-14     */
 Tensor* zero_grad(Tensor* t);                              /* autograd.inc:15-24    */
 /* t[i] = v and t[i][j] = v (runtime/io/builtins.inc:286-317): the in-place writes of

@@ -690,6 +690,168 @@ void orc_conv2d_bwd(const double* X, const double* Kn, const double* G, double* 
 }
 
 // ---------------------------------------------------------------------------
+// Elementwise ops (runCPUBinary / runCPUUnary, runtime/backend/gpu.inc:443-598) and their
+// backward branches (autograd.inc:58-90, 284-288, 342-378, 491-506)
+// ---------------------------------------------------------------------------
+namespace {
+
+double bin_op(int op, double a, double b) {
+    switch (op) {   // BinopCode order, gpu.inc:455-460; expressions of gpu.inc:511-527
+        case 0: return a + b;
+        case 1: return a - b;
+        case 2: return a * b;
+        case 3: return a / b;
+        case 4: return std::fmod(a, b);
+        case 5: return a > b ? 1.0 : 0.0;
+        case 6: return a < b ? 1.0 : 0.0;
+        case 7: return a >= b ? 1.0 : 0.0;
+        case 8: return a <= b ? 1.0 : 0.0;
+        case 9: return std::fabs(a - b) < 1e-6 ? 1.0 : 0.0;
+        case 10: return std::fabs(a - b) >= 1e-6 ? 1.0 : 0.0;
+        case 11: return (a > 0 && b > 0) ? 1.0 : 0.0;
+        case 12: return (a > 0 || b > 0) ? 1.0 : 0.0;
+        case 13: return std::atan2(a, b);
+        case 14: return std::pow(a, b);
+        case 15: return a < b ? a : b;
+        default: return a > b ? a : b;
+    }
+}
+
+// bcastStrides (gpu.inc:443-449): contiguous strides of the operand's own dims, 0 where the
+// dim is 1.
+void bcast_strides(const int* d, long long* s) {
+    s[0] = d[0] > 1 ? (long long)d[1] * d[2] * d[3] : 0;
+    s[1] = d[1] > 1 ? (long long)d[2] * d[3] : 0;
+    s[2] = d[2] > 1 ? d[3] : 0;
+    s[3] = d[3] > 1 ? 1 : 0;
+}
+
+}  // namespace
+
+void orc_binary(int op, const double* A, const int* a_dims, const double* B, const int* b_dims,
+                double* C, const int* c_dims) {
+    const long long sz = (long long)c_dims[0] * c_dims[1] * c_dims[2] * c_dims[3];
+    const long long asz = (long long)a_dims[0] * a_dims[1] * a_dims[2] * a_dims[3];
+    const long long bsz = (long long)b_dims[0] * b_dims[1] * b_dims[2] * b_dims[3];
+    if (asz == sz && bsz == sz) {   // same-shape path, gpu.inc:504-528
+        for (long long i = 0; i < sz; ++i) C[i] = bin_op(op, A[i], B[i]);
+        return;
+    }
+    long long as[4], bs[4];   // broadcasting path, gpu.inc:530-564
+    bcast_strides(a_dims, as);
+    bcast_strides(b_dims, bs);
+    const long long cd3 = c_dims[3], cd2 = c_dims[2], cd1 = c_dims[1];
+    for (long long i = 0; i < sz; ++i) {
+        const long long i3 = i % cd3, i2 = (i / cd3) % cd2, i1 = (i / (cd3 * cd2)) % cd1,
+                        i0 = i / (cd3 * cd2 * cd1);
+        const long long ai = i0 * as[0] + i1 * as[1] + i2 * as[2] + i3 * as[3];
+        const long long bi = i0 * bs[0] + i1 * bs[1] + i2 * bs[2] + i3 * bs[3];
+        C[i] = bin_op(op, A[ai], B[bi]);
+    }
+}
+
+void orc_unary(int op, const double* A, double* C, long long n, double lo, double hi) {
+    for (long long i = 0; i < n; ++i) {
+        const double a = A[i];
+        double c;
+        switch (op) {   // UnopCode order, gpu.inc:571-577; expressions of gpu.inc:614-629
+            case 0: c = a > 0.0 ? a : 0.0; break;
+            case 1: c = std::exp(a); break;
+            case 2: c = std::log(a); break;
+            case 3: c = std::sqrt(a); break;
+            case 4: c = std::fabs(a); break;
+            case 5: c = 1.0 / (1.0 + std::exp(-a)); break;
+            case 6: c = std::tanh(a); break;
+            case 7: c = a == 0.0 ? 1.0 : 0.0; break;
+            case 8: c = std::sin(a); break;
+            case 9: c = std::cos(a); break;
+            case 10: c = std::tan(a); break;
+            case 11: c = std::atan(a); break;
+            case 12: c = std::floor(a); break;
+            case 13: c = std::ceil(a); break;
+            case 14: c = std::round(a); break;
+            default: c = std::fmax(lo, std::fmin(hi, a)); break;   // clip's expression
+        }
+        C[i] = c;
+    }
+}
+
+void orc_binary_bwd(int op, const double* A, long long a_size, const double* B, long long b_size,
+                    const double* Y, const double* G, long long n, double* gA, double* gB) {
+    // Operands are indexed j % size (autograd.inc:58-90), not by the forward's strides.
+    switch (op) {
+        case 0:   // add
+            for (long long j = 0; j < n; ++j) {
+                gA[j % a_size] += G[j];
+                gB[j % b_size] += G[j];
+            }
+            break;
+        case 1:   // sub
+            for (long long j = 0; j < n; ++j) {
+                gA[j % a_size] += G[j];
+                gB[j % b_size] -= G[j];
+            }
+            break;
+        case 2:   // mul
+            for (long long j = 0; j < n; ++j) {
+                gA[j % a_size] += G[j] * B[j % b_size];
+                gB[j % b_size] += G[j] * A[j % a_size];
+            }
+            break;
+        case 3:   // div
+            for (long long j = 0; j < n; ++j) {
+                const double r = B[j % b_size], g = G[j];
+                gA[j % a_size] += g / r;
+                gB[j % b_size] -= g * A[j % a_size] / (r * r);
+            }
+            break;
+        case 14:   // pow: over the base's elements, autograd.inc:491-506
+            for (long long j = 0; j < a_size; ++j) {
+                const double x = A[j], e = B[j % b_size], y = Y[j % n], g = G[j % n];
+                if (x != 0.0) gA[j] += g * e * y / x;
+                if (x > 0.0) gB[j % b_size] += g * y * std::log(x);
+            }
+            break;
+        case 15:   // minimum / maximum: all to the chosen side, ties to lhs (autograd.inc:68-79)
+        case 16:
+            for (long long j = 0; j < n; ++j) {
+                const double av = A[j % a_size], bv = B[j % b_size];
+                const bool lhs = op == 16 ? av >= bv : av <= bv;
+                if (lhs) gA[j % a_size] += G[j];
+                else gB[j % b_size] += G[j];
+            }
+            break;
+        default:   // the comparisons, mod, and / or, atan2: no backward branch
+            break;
+    }
+}
+
+void orc_unary_bwd(int op, const double* X, const double* Y, const double* G, double* GX,
+                   long long n) {
+    for (long long j = 0; j < n; ++j) {
+        const double x = X[j], y = Y[j], g = G[j];
+        switch (op) {
+            case 0: GX[j] += (x > 0 ? 1.0 : 0.0) * g; break;   // relu, autograd.inc:284-288
+            case 1: GX[j] += y * g; break;                      // exp, 342-344
+            case 2: GX[j] += g / x; break;                      // log
+            case 3: GX[j] += g / (2.0 * y); break;              // sqrt
+            case 4: GX[j] += (x >= 0 ? 1.0 : -1.0) * g; break;  // abs
+            case 5: GX[j] += y * (1 - y) * g; break;            // sigmoid
+            case 6: GX[j] += (1 - y * y) * g; break;            // tanh
+            case 8: GX[j] += std::cos(x) * g; break;            // sin, 363-365
+            case 9: GX[j] += -std::sin(x) * g; break;           // cos
+            case 10: {                                          // tan
+                const double c = std::cos(x);
+                GX[j] += g / (c * c);
+                break;
+            }
+            case 11: GX[j] += g / (1.0 + x * x); break;         // atan, 375-378
+            default: break;   // lnot, floor, ceil, round, clip: no backward branch
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // bf16 (training.inc:1969-1976)
 // ---------------------------------------------------------------------------
 float orc_to_bf16(float x) {

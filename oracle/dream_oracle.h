@@ -27,6 +27,10 @@
  *   orc_linear(_bwd), orc_bmm(_bwd)   golden vectors + independent numpy + finite differences
  *   orc_conv2d(_bwd)    golden vectors (pad 0 / stride 1 forward and backward, padded strided
  *                       forward) + finite differences (all, incl. the padded backward)
+ *   orc_binary, orc_unary   golden vectors (every op, same shape and 2-D broadcasts) + numpy
+ *                       broadcasting on 4-D shapes (independent code)
+ *   orc_binary_bwd, orc_unary_bwd   golden vectors (reference backward, incl. its j % size
+ *                       broadcast rule) + finite differences on same-shape operands
  *   orc_to_bf16         IEEE round-to-nearest-even (torch.bfloat16 cast) + hand-picked ties
  */
 #ifndef DREAM_ORACLE_H
@@ -126,6 +130,24 @@ void orc_conv2d(const double* X, const double* Kn, const double* bias, double* Y
                 int H, int W, int Cout, int KH, int KW, int pad, int stride);
 void orc_conv2d_bwd(const double* X, const double* Kn, const double* G, double* gX, double* gK,
                     int N, int Cin, int H, int W, int Cout, int KH, int KW, int pad, int stride);
+
+/* Elementwise ops in fp64.  orc_binary: runCPUBinary (runtime/backend/gpu.inc:484-565) --
+ * same-shape operands element by element, otherwise C's flat index i split over c_dims and
+ * each operand read through bcastStrides (gpu.inc:443-449: its own contiguous strides, 0 on
+ * a dim of 1).  op in BinopCode order (gpu.inc:455-460): add sub mul div mod gt lt ge le eq
+ * ne and or atan2 pow min max = 0..16.  orc_unary: runCPUUnary (gpu.inc:599-634) in UnopCode
+ * order (relu exp log sqrt abs sigmoid tanh lnot sin cos tan atan floor ceil round = 0..14),
+ * 15 = clip, fmax(lo, fmin(hi, a)) (the expression of dream_clip, elementwise.inc:329-336).
+ * Their backward "+=": orc_binary_bwd (autograd.inc:58-90 add, sub, minimum/maximum, mul,
+ * div with operands indexed j % size; 491-506 pow over the base's elements; Y = the forward
+ * output, n = its size) and orc_unary_bwd (autograd.inc:284-288, 342-378). */
+void orc_binary(int op, const double* A, const int* a_dims, const double* B, const int* b_dims,
+                double* C, const int* c_dims);
+void orc_unary(int op, const double* A, double* C, long long n, double lo, double hi);
+void orc_binary_bwd(int op, const double* A, long long a_size, const double* B, long long b_size,
+                    const double* Y, const double* G, long long n, double* gA, double* gB);
+void orc_unary_bwd(int op, const double* X, const double* Y, const double* G, double* GX,
+                   long long n);
 
 /* bf16 rounding (training.inc:1969-1976): fp32 -> bf16 -> fp32, round to nearest even
  * by the bias-and-truncate rule.  orc_bf16_bits returns the upper 16 bits. */

@@ -16,6 +16,7 @@ _fp = ctypes.POINTER(ctypes.c_float)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _i = ctypes.c_int
 _ll = ctypes.c_longlong
+_ip = ctypes.POINTER(ctypes.c_int)
 
 _lib = None
 
@@ -55,6 +56,10 @@ def lib():
             "orc_bmm_bwd": [_dp] * 5 + [_i, _i, _i, _i],
             "orc_conv2d": [_dp] * 4 + [_i] * 9,
             "orc_conv2d_bwd": [_dp] * 5 + [_i] * 9,
+            "orc_binary": [_i, _dp, _ip, _dp, _ip, _dp, _ip],
+            "orc_unary": [_i, _dp, _dp, _ll, ctypes.c_double, ctypes.c_double],
+            "orc_binary_bwd": [_i, _dp, _ll, _dp, _ll, _dp, _dp, _ll, _dp, _dp],
+            "orc_unary_bwd": [_i, _dp, _dp, _dp, _dp, _ll],
             "orc_to_bf16": [ctypes.c_float],
             "orc_bf16_bits": [_fp, _u16p, _ll],
         }
@@ -304,6 +309,57 @@ def conv2d_bwd(X, Kn, G, N, Cin, H, W, Cout, KH, KW, pad=0, stride=1):
     lib().orc_conv2d_bwd(_ptr(X), _ptr(Kn), _ptr(G), _ptr(gX), _ptr(gK), N, Cin, H, W, Cout, KH,
                          KW, pad, stride)
     return gX, gK
+
+
+# Elementwise op codes: the reference's BinopCode / UnopCode order (gpu.inc:455-460, 571-577).
+BINOPS = ["add", "sub", "mul", "div", "mod", "gt", "lt", "ge", "le", "eq", "ne", "and", "or",
+          "atan2", "pow", "min", "max"]
+UNOPS = ["relu", "exp", "log", "sqrt", "abs", "sigmoid", "tanh", "lnot", "sin", "cos", "tan",
+         "atan", "floor", "ceil", "round", "clip"]
+
+
+def dims4(shape):
+    """A Dream tensor's (d0, d1, d2, d3) for a numpy shape of up to 4 dims."""
+    d = list(shape) + [1] * (4 - len(shape))
+    return np.array(d, np.int32)
+
+
+def _code(op, table):
+    return op if isinstance(op, (int, np.integer)) else table.index(op)
+
+
+def binary(op, A, B, c_shape=None):
+    """runCPUBinary on Dream shapes: C's dims are the per-dim max of A's and B's."""
+    A, B = _d(A), _d(B)
+    ad, bd = dims4(A.shape), dims4(B.shape)
+    cd = np.maximum(ad, bd).astype(np.int32) if c_shape is None else dims4(c_shape)
+    C = np.empty(int(np.prod(cd)), np.float64)
+    lib().orc_binary(_code(op, BINOPS), _ptr(A), _ptr(ad, _ip), _ptr(B), _ptr(bd, _ip), _ptr(C),
+                     _ptr(cd, _ip))
+    return C.reshape([int(x) for x in cd])
+
+
+def unary(op, A, lo=0.0, hi=0.0):
+    A = _d(A)
+    C = np.empty_like(A)
+    lib().orc_unary(_code(op, UNOPS), _ptr(A), _ptr(C), A.size, lo, hi)
+    return C
+
+
+def binary_bwd(op, A, B, Y, G):
+    """(gA, gB) of the reference's backward branch for one node (fresh zero accumulators)."""
+    A, B, Y, G = _d(A), _d(B), _d(Y), _d(G)
+    gA, gB = np.zeros_like(A), np.zeros_like(B)
+    lib().orc_binary_bwd(_code(op, BINOPS), _ptr(A), A.size, _ptr(B), B.size, _ptr(Y), _ptr(G),
+                         G.size, _ptr(gA), _ptr(gB))
+    return gA, gB
+
+
+def unary_bwd(op, X, Y, G):
+    X, Y, G = _d(X), _d(Y), _d(G)
+    GX = np.zeros_like(X)
+    lib().orc_unary_bwd(_code(op, UNOPS), _ptr(X), _ptr(Y), _ptr(G), _ptr(GX), X.size)
+    return GX
 
 
 def to_bf16(x):

@@ -31,6 +31,20 @@ class _TensorHead(ctypes.Structure):
 _TP = ctypes.POINTER(_TensorHead)
 
 
+# Elementwise builtins by op name (elementwise.inc:290-311, 320-327; math_extra.inc:1-10;
+# builtins.inc:85-87; dream_pow, elementwise.inc:1254).
+BINARY = {"add": "tensor_add", "sub": "tensor_sub", "mul": "tensor_mul", "div": "tensor_div",
+          "mod": "tensor_mod", "gt": "tensor_gt", "lt": "tensor_lt", "ge": "tensor_ge",
+          "le": "tensor_le", "eq": "tensor_eq", "ne": "tensor_ne", "and": "tensor_and",
+          "or": "tensor_or", "atan2": "dream_atan2", "pow": "dream_pow", "min": "dream_minimum",
+          "max": "dream_maximum"}
+UNARY = {"relu": "relu", "exp": "dream_exp", "log": "dream_log", "sqrt": "dream_sqrt",
+         "abs": "dream_abs", "sigmoid": "dream_sigmoid", "tanh": "dream_tanh",
+         "lnot": "dream_logical_not", "sin": "dream_sin", "cos": "dream_cos", "tan": "dream_tan",
+         "atan": "dream_atan", "floor": "dream_floor", "ceil": "dream_ceil",
+         "round": "dream_round"}
+
+
 def available():
     return os.path.exists(LIB_PATH)
 
@@ -49,7 +63,9 @@ class RefRuntime:
                             ("dream_kaiming_init", 2), ("gemm_selftest", 0),
                             ("flash_attention_selftest", 0), ("tensor_decref", 1),
                             ("zero_grad", 1), ("dream_conv2d", 7),
-                            ("dream_conv2d_padded", 9)]:
+                            ("dream_conv2d_padded", 9), ("dream_clip", 3),
+                            *[(n, 2) for n in BINARY.values()],
+                            *[(n, 1) for n in UNARY.values()]]:
             fn = getattr(L, name)
             fn.restype = _TP
             if nargs is not None:
@@ -177,3 +193,22 @@ class RefRuntime:
         if G is None:
             return self.read(y)
         return self._grads(y, G, x, k)[:2]
+
+    def binary(self, op, A, B, W=None):
+        """The builtin's output for 2-D A, B; with W also (A.grad, B.grad) of
+        backward(sum(C * W))."""
+        a, b = self.tensor(A), self.tensor(B)
+        c = getattr(self.L, BINARY[op])(a, b)
+        if W is None:
+            return self.read(c)
+        return self.read(c), *self._grads(c, W, a, b)[:2]
+
+    def unary(self, op, A, W=None):
+        a = self.tensor(A)
+        c = getattr(self.L, UNARY[op])(a)
+        if W is None:
+            return self.read(c)
+        return self.read(c), self._grads(c, W, a)[0]
+
+    def clip(self, A, lo, hi):
+        return self.read(self.L.dream_clip(self.tensor(A), self.scalar(lo), self.scalar(hi)))

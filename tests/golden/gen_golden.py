@@ -9,7 +9,9 @@ and every output comes from the reference builtins through their C ABI:
 tensor_matmul (CPU dgemm / f32 fgemm), backward through "matmul", dream_attention,
 dream_attention_causal, dream_flash_attention and their backward branches,
 dream_softmax, dream_log_softmax, dream_layer_norm, dream_linear(_relu), dream_bmm,
-dream_conv2d(_padded) and their backward branches, dream_kaiming_init.  The file holds data
+dream_conv2d(_padded) and their backward branches, the elementwise builtins (tensor_add ...
+dream_maximum, dream_pow, relu ... dream_round) and their backward branches,
+dream_kaiming_init.  The file holds data
 only (inputs and expected outputs, fp64).
 """
 import json
@@ -20,7 +22,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from _ref_runtime import RefRuntime  # noqa: E402
+from _ref_runtime import BINARY as R_BINARY, UNARY as R_UNARY, RefRuntime  # noqa: E402
 
 OUT = os.path.join(HERE, "ref_vectors.npz")
 
@@ -121,6 +123,39 @@ def main():
     manifest["conv2d"] = ("X=randn(2,126) (N=2, Cin=3, 7x6), K=randn(4,18) (Cout=4, 3x2), "
                           "b=randn(1,4), G=randn(2,100); conv2d Y, dX, dK of backward(sum(Y*G)); "
                           "conv2d_padded(pad=1, stride=2) Y")
+
+    # Elementwise builtins: every binary op on a same-shape, a row (1 x C), a column (R x 1)
+    # and a scalar (1 x 1) right operand, with the backward of the ops that have one; every
+    # unary op with its backward.  Half of E's entries copy X's so eq / ne see both answers.
+    R.set_seed(17)
+    EX, EY, EG = R.randn(6, 9), R.randn(6, 9), R.randn(6, 9)
+    EY[:, ::2] = EX[:, ::2]
+    rights = {"same": EY, "row": R.randn(1, 9), "col": R.randn(6, 1), "scalar": R.randn(1, 1)}
+    v["ew_X"], v["ew_G"] = EX, EG
+    for name, Bx in rights.items():
+        v["ew_B_" + name] = Bx
+    grad_ops = ("add", "sub", "mul", "div", "min", "max", "pow")
+    for op in R_BINARY:
+        for name, Bx in rights.items():
+            A = np.abs(EX) + 0.25 if op == "pow" else EX
+            key = f"ew_{op}_{name}"
+            if op in grad_ops:
+                v[key + "_C"], v[key + "_dA"], v[key + "_dB"] = R.binary(op, A, Bx, EG)
+            else:
+                v[key + "_C"] = R.binary(op, A, Bx)
+    no_grad = ("lnot", "floor", "ceil", "round")
+    for op in R_UNARY:
+        A = np.abs(EX) + 0.1 if op in ("log", "sqrt") else EX * 3.0 if op in no_grad else EX
+        key = f"ew_u_{op}"
+        if op in no_grad:
+            v[key + "_C"] = R.unary(op, A)
+        else:
+            v[key + "_C"], v[key + "_dA"] = R.unary(op, A, EG)
+    manifest["elementwise"] = ("set_seed(17); X, Y, G = randn(6,9), Y[:, ::2] = X[:, ::2]; right "
+                               "operands same=Y, row=randn(1,9), col=randn(6,1), "
+                               "scalar=randn(1,1); C = op(X, B) (pow: |X|+0.25 as base), "
+                               "dA/dB of backward(sum(C*G)); unary on X (log, sqrt: |X|+0.1; "
+                               "lnot/floor/ceil/round: 3X) with dA")
 
     np.savez_compressed(OUT, **v)
     manifest["file"] = os.path.basename(OUT)

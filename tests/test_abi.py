@@ -12,7 +12,7 @@ from dreamcompiler_amd import hip
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DECL = re.compile(r"^[A-Za-z_][\w\s\*]*?\b((?:dh|dream|tensor)_\w+|backward|gpu_selftest|"
-                  r"flash_attention_selftest|alloc_tensor|create_scalar|sum|ones)\s*\(", re.M)
+                  r"flash_attention_selftest|alloc_tensor|create_scalar|sum|ones|relu)\s*\(", re.M)
 
 
 def declared(header):

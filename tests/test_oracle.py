@@ -435,3 +435,140 @@ def test_conv2d_golden_and_finite_differences():
     Y = O.conv2d(X, Kn, None, 3, 4, 3, 3, 5, 1, 1)
     ref = np.einsum("oc,ncp->nop", Kn, X.reshape(3, 4, 9)).reshape(3, 45)
     assert rel(Y, ref) <= 1e-14
+
+
+# --------------------------------------------------------------------------- elementwise
+EW_RIGHTS = ("same", "row", "col", "scalar")
+EW_GRAD_OPS = ("add", "sub", "mul", "div", "min", "max", "pow")
+EW_NO_GRAD_UNARY = ("lnot", "floor", "ceil", "round")
+
+
+def _ew_base(op):
+    X = GOLD["ew_X"]
+    return np.abs(X) + 0.25 if op == "pow" else X
+
+
+def _ew_unary_input(op):
+    X = GOLD["ew_X"]
+    return np.abs(X) + 0.1 if op in ("log", "sqrt") else X * 3.0 if op in EW_NO_GRAD_UNARY else X
+
+
+def _np_binary(op, A, B):
+    """Independent numpy statement of each op under numpy's own broadcasting."""
+    one = lambda m: m.astype(np.float64)   # noqa: E731
+    return {
+        "add": lambda: A + B, "sub": lambda: A - B, "mul": lambda: A * B, "div": lambda: A / B,
+        "mod": lambda: np.fmod(A, B), "gt": lambda: one(A > B), "lt": lambda: one(A < B),
+        "ge": lambda: one(A >= B), "le": lambda: one(A <= B),
+        "eq": lambda: one(np.abs(A - B) < 1e-6), "ne": lambda: one(np.abs(A - B) >= 1e-6),
+        "and": lambda: one((A > 0) & (B > 0)), "or": lambda: one((A > 0) | (B > 0)),
+        "atan2": lambda: np.arctan2(A, B), "pow": lambda: np.power(A, B),
+        "min": lambda: np.where(A < B, A, B), "max": lambda: np.where(A > B, A, B),
+    }[op]()
+
+
+def _np_unary(op, A, lo=-0.5, hi=0.5):
+    return {
+        "relu": lambda: np.where(A > 0, A, 0.0), "exp": lambda: np.exp(A),
+        "log": lambda: np.log(A), "sqrt": lambda: np.sqrt(A), "abs": lambda: np.abs(A),
+        "sigmoid": lambda: 1 / (1 + np.exp(-A)), "tanh": lambda: np.tanh(A),
+        "lnot": lambda: (A == 0).astype(np.float64), "sin": lambda: np.sin(A),
+        "cos": lambda: np.cos(A), "tan": lambda: np.tan(A), "atan": lambda: np.arctan(A),
+        "floor": lambda: np.floor(A), "ceil": lambda: np.ceil(A),
+        "round": lambda: np.where(A >= 0, np.floor(A + 0.5), -np.floor(-A + 0.5)),
+        "clip": lambda: np.maximum(lo, np.minimum(hi, A)),
+    }[op]()
+
+
+@pytest.mark.parametrize("op", O.BINOPS)
+def test_binary_golden(op):
+    A, G = _ew_base(op), GOLD["ew_G"]
+    for r in EW_RIGHTS:
+        key, B = f"ew_{op}_{r}", GOLD["ew_B_" + r]
+        C = O.binary(op, A, B)[:, :, 0, 0]
+        assert rel(C, GOLD[key + "_C"]) <= 1e-15, (op, r)
+        if op in EW_GRAD_OPS:
+            gA, gB = O.binary_bwd(op, A, B, C, G)
+            assert rel(gA, GOLD[key + "_dA"]) <= 1e-14, (op, r)
+            assert rel(gB, GOLD[key + "_dB"]) <= 1e-14, (op, r)
+
+
+@pytest.mark.parametrize("op", O.UNOPS[:-1])
+def test_unary_golden(op):
+    A = _ew_unary_input(op)
+    C = O.unary(op, A)
+    assert rel(C, GOLD[f"ew_u_{op}_C"]) <= 1e-15
+    if op not in EW_NO_GRAD_UNARY:
+        assert rel(O.unary_bwd(op, A, C, GOLD["ew_G"]), GOLD[f"ew_u_{op}_dA"]) <= 1e-15
+
+
+@pytest.mark.parametrize("shapes", [((2, 3, 4, 5), (1, 3, 1, 5)), ((2, 1, 4, 1), (1, 3, 1, 5)),
+                                    ((3, 4, 5, 6), (3, 4, 5, 6)), ((1, 1, 1, 7), (4, 3, 2, 1)),
+                                    ((5, 2, 1, 3), (1, 1, 1, 1))])
+def test_binary_broadcast_against_numpy(shapes):
+    # 4-D broadcasts (the golden vectors only reach 2-D): numpy's broadcasting is an
+    # independent statement of the bcastStrides rule on compatible shapes.
+    rng = np.random.default_rng(sum(map(sum, shapes)))
+    # one decimal: many equal pairs for eq / ne / min / max, no zero divisors
+    A, B = (np.round(rng.standard_normal(s), 1) for s in shapes)
+    B[B == 0] = 0.5
+    for op in O.BINOPS:
+        a = np.abs(A) + 0.25 if op == "pow" else A
+        want = _np_binary(op, a, B)
+        got = O.binary(op, a, B)
+        assert got.shape == want.shape
+        assert rel(got, want) <= 4e-16 or np.array_equal(got, want), op
+
+
+def test_unary_against_numpy():
+    rng = np.random.default_rng(5)
+    X = rng.standard_normal(1000) * 3
+    X[:8] = [0.0, -0.0, 0.5, -0.5, 1.5, -2.5, 2.0, -1e-300]
+    for op in O.UNOPS:
+        A = np.abs(X) + 0.1 if op in ("log", "sqrt") else X
+        assert rel(O.unary(op, A, -0.5, 0.5), _np_unary(op, A)) <= 4e-16, op
+
+
+def test_elementwise_backward_finite_differences():
+    rng = np.random.default_rng(6)
+    A, B, G = rng.standard_normal((4, 5)), rng.standard_normal((4, 5)), rng.standard_normal((4, 5))
+    B += np.sign(B) * 0.5   # away from 0 for div, away from A for min / max
+    for op in ("add", "sub", "mul", "div", "pow", "min", "max"):
+        a = np.abs(A) + 0.5 if op == "pow" else A
+        f = lambda x, y: O.binary(op, x, y).reshape(4, 5)   # noqa: E731
+        gA, gB = O.binary_bwd(op, a, B, f(a, B), G)
+        assert rel(gA, _fd_sumgrad(lambda x: f(x, B), a, G)) <= 1e-6, op
+        assert rel(gB, _fd_sumgrad(lambda y: f(a, y), B, G)) <= 1e-6, op
+    for op in ("relu", "exp", "log", "sqrt", "abs", "sigmoid", "tanh", "sin", "cos", "tan", "atan"):
+        X = np.abs(A) + 0.2 if op in ("log", "sqrt") else A * 0.7
+        gX = O.unary_bwd(op, X, O.unary(op, X), G)
+        assert rel(gX, _fd_sumgrad(lambda x: O.unary(op, x), X, G)) <= 1e-6, op
+
+
+def test_elementwise_planted_mistakes_are_caught():
+    A, B, G = GOLD["ew_X"], GOLD["ew_B_col"], GOLD["ew_G"]
+    # sub's backward with the rhs sign flipped
+    gA, gB = O.binary_bwd("add", A, B, O.binary("sub", A, B), G)
+    assert rel(gB, GOLD["ew_sub_col_dB"]) > 1e-3
+    # a column operand read by the flat index modulo its size (the backward's rule) in the forward
+    modular = A + B.ravel()[np.arange(A.size) % B.size].reshape(A.shape)
+    assert rel(modular, GOLD["ew_add_col_C"]) > 1e-3
+    # the forward's broadcast strides used in the backward (the reference uses j % size)
+    assert rel(G.sum(axis=1, keepdims=True), GOLD["ew_add_col_dB"]) > 1e-3
+
+
+@needs_ref
+def test_elementwise_against_reference_build(ref):
+    rng = np.random.default_rng(35)
+    A, G = rng.standard_normal((13, 21)), rng.standard_normal((13, 21))
+    for B in (rng.standard_normal((13, 21)), rng.standard_normal((1, 21)),
+              rng.standard_normal((13, 1))):
+        for op in O.BINOPS:
+            a = np.abs(A) + 0.25 if op == "pow" else A
+            if op in EW_GRAD_OPS:
+                C, dA, dB = ref.binary(op, a, B, G)
+                gA, gB = O.binary_bwd(op, a, B, C, G)
+                assert rel(gA, dA) <= 1e-14 and rel(gB, dB) <= 1e-14, op
+            else:
+                C = ref.binary(op, a, B)
+            assert rel(O.binary(op, a, B)[:, :, 0, 0], C) <= 1e-15, op
