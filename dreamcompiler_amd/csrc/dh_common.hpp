@@ -21,6 +21,26 @@ int num_cus();
         if (_s != DH_OK) return _s;       \
     } while (0)
 
+// ---- division by a launch-invariant divisor -------------------------------------
+// Multiply-high, add and shift (the round-up method of Granlund & Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994): for 1 <= d < 2^31,
+// s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 (< 2^32), and for every
+// 0 <= n < 2^31, n / d = (umulhi(n, m) + n) >> s (the sum stays below 2^32).
+struct FastDiv {
+    uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+    return {d, (uint32_t)m, s};
+}
+
+__device__ inline uint32_t fdiv(uint32_t n, const FastDiv& f) {
+    return (__umulhi(n, f.m) + n) >> f.s;
+}
+
 // ---- vector types -------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));

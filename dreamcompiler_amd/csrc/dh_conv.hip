@@ -10,9 +10,10 @@
 //        with contraction length N*OH*OW;
 //   go'  Cout x (N*OH*OW): the output gradient with its channel axis first (dh_nct_to_cnt),
 //        the other operand of both backward products.
-// All three kernels are HBM-bound gathers/scatters with one thread per output element;
-// col2im gathers (each input element sums its KH*KW contributions in a fixed order), so it
+// All three kernels are HBM-bound gathers / permutes; col2im gathers (each input element sums its KH*KW contributions in a fixed order), so it
 // needs no atomics and reruns are bit-identical.
+#include <algorithm>
+
 #include "dh_common.hpp"
 
 namespace dh {
@@ -22,67 +23,109 @@ struct ConvShape {
     int N, Cin, H, W, KH, KW, pad, stride, OH, OW;
 };
 
+// Grids are 3-D: x = a chunk of one row's columns (or of one image plane), y = the col row
+// (or channel), z = the image, so every per-row / per-plane index is decomposed once per
+// work-group and a thread's own index with one multiply-shift division (32-bit: planes and
+// rows of fewer than 2^31 elements, checked on the host).  y and z are launched in chunks of
+// at most 65535 (y0, z0 the chunk's first row / image).  Outputs are streamed with
+// non-temporal stores.
+
+// col[r][n*P + p] for p = oh*OW + ow.  A work-group covers up to IM_SPAN columns of one
+// (row, image); thread t takes columns t, t + 256, ... so every load and store instruction of
+// a wave touches 64 consecutive columns (consecutive input elements where stride is 1).
+constexpr uint32_t IM_SPAN = 4096, IM_UNROLL = 4;
+
 __global__ void __launch_bounds__(256) im2col_kernel(const float* __restrict__ X,
-                                                     float* __restrict__ col, ConvShape s) {
-    const size_t P = (size_t)s.OH * s.OW, cols = (size_t)s.N * P;
-    const size_t total = (size_t)s.Cin * s.KH * s.KW * cols;
-    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total;
-         e += (size_t)gridDim.x * 256) {
-        const size_t r = e / cols, c = e % cols;
-        const int kw = (int)(r % s.KW), kh = (int)((r / s.KW) % s.KH), ci = (int)(r / s.KW / s.KH);
-        const int n = (int)(c / P), p = (int)(c % P), oh = p / s.OW, ow = p % s.OW;
-        const int h = oh * s.stride + kh - s.pad, w = ow * s.stride + kw - s.pad;
-        col[e] = (h >= 0 && h < s.H && w >= 0 && w < s.W)
-                     ? X[(((size_t)n * s.Cin + ci) * s.H + h) * s.W + w]
-                     : 0.f;
-    }
-}
-
-// dX[n][ci][h][w] (+)= sum over (kh, kw) with h = oh*stride + kh - pad, w = ow*stride + kw - pad.
-__global__ void __launch_bounds__(256) col2im_kernel(const float* __restrict__ dcol,
-                                                     float* __restrict__ dX, ConvShape s, int acc) {
-    const size_t P = (size_t)s.OH * s.OW, cols = (size_t)s.N * P;
-    const size_t total = (size_t)s.N * s.Cin * s.H * s.W;
-    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total;
-         e += (size_t)gridDim.x * 256) {
-        const int w = (int)(e % s.W), h = (int)((e / s.W) % s.H);
-        const int ci = (int)((e / ((size_t)s.W * s.H)) % s.Cin), n = (int)(e / ((size_t)s.W * s.H * s.Cin));
-        float v = 0.f;
-        for (int kh = 0; kh < s.KH; ++kh) {
-            const int th = h + s.pad - kh;
-            if (th < 0 || th % s.stride) continue;
-            const int oh = th / s.stride;
-            if (oh >= s.OH) continue;
-            for (int kw = 0; kw < s.KW; ++kw) {
-                const int tw = w + s.pad - kw;
-                if (tw < 0 || tw % s.stride) continue;
-                const int ow = tw / s.stride;
-                if (ow >= s.OW) continue;
-                const size_t r = ((size_t)ci * s.KH + kh) * s.KW + kw;
-                v += dcol[r * cols + (size_t)n * P + (size_t)oh * s.OW + ow];
+                                                     float* __restrict__ col, ConvShape s,
+                                                     FastDiv f_ow, int y0, int z0) {
+    const int r = y0 + blockIdx.y, n = z0 + blockIdx.z;
+    const int kw = r % s.KW, kh = (r / s.KW) % s.KH, ci = r / (s.KW * s.KH);
+    const uint32_t P = (uint32_t)s.OH * (uint32_t)s.OW;
+    const uint32_t end = min(P, (blockIdx.x + 1u) * IM_SPAN);
+    const float* Xc = X + ((size_t)n * s.Cin + ci) * s.H * s.W;
+    float* dst = col + (size_t)r * ((size_t)s.N * P) + (size_t)n * P;
+    for (uint32_t p0 = blockIdx.x * IM_SPAN + threadIdx.x; p0 < end; p0 += 256u * IM_UNROLL) {
+        float v[IM_UNROLL];
+#pragma unroll
+        for (uint32_t u = 0; u < IM_UNROLL; ++u) {
+            const uint32_t p = p0 + 256u * u;
+            float x = 0.f;
+            if (p < end) {
+                const uint32_t oh = fdiv(p, f_ow), ow = p - oh * (uint32_t)s.OW;
+                const int h = (int)oh * s.stride + kh - s.pad, w = (int)ow * s.stride + kw - s.pad;
+                if (h >= 0 && h < s.H && w >= 0 && w < s.W) x = Xc[h * s.W + w];
             }
+            v[u] = x;
         }
-        dX[e] = acc ? dX[e] + v : v;
+#pragma unroll
+        for (uint32_t u = 0; u < IM_UNROLL; ++u) {
+            const uint32_t p = p0 + 256u * u;
+            if (p < end) __builtin_nontemporal_store(v[u], dst + p);
+        }
     }
 }
 
-// (N, C, T) -> (C, N*T)
+// dX[n][ci][h][w] (+)= sum over (kh, kw) with h = oh*stride + kh - pad, w = ow*stride + kw - pad,
+// in the order kh, then kw.
+__global__ void __launch_bounds__(256) col2im_kernel(const float* __restrict__ dcol,
+                                                     float* __restrict__ dX, ConvShape s,
+                                                     FastDiv f_w, int acc, int y0, int z0) {
+    const int ci = y0 + blockIdx.y, n = z0 + blockIdx.z;
+    const uint32_t HW = (uint32_t)s.H * (uint32_t)s.W;
+    const uint32_t hw = blockIdx.x * 256u + threadIdx.x;
+    if (hw >= HW) return;
+    const int h = (int)fdiv(hw, f_w), w = (int)(hw - (uint32_t)h * (uint32_t)s.W);
+    const size_t P = (size_t)s.OH * s.OW, cols = (size_t)s.N * P;
+    const float* src = dcol + (size_t)n * P;
+    float v = 0.f;
+    for (int kh = 0; kh < s.KH; ++kh) {
+        const int th = h + s.pad - kh;
+        if (th < 0 || th % s.stride) continue;
+        const int oh = th / s.stride;
+        if (oh >= s.OH) continue;
+        for (int kw = 0; kw < s.KW; ++kw) {
+            const int tw = w + s.pad - kw;
+            if (tw < 0 || tw % s.stride) continue;
+            const int ow = tw / s.stride;
+            if (ow >= s.OW) continue;
+            const size_t r = ((size_t)ci * s.KH + kh) * s.KW + kw;
+            v += src[r * cols + (size_t)oh * s.OW + ow];
+        }
+    }
+    float* o = dX + ((size_t)n * s.Cin + ci) * HW + hw;
+    if (acc) *o += v;
+    else __builtin_nontemporal_store(v, o);
+}
+
+// (N, C, T) -> (C, N*T): dst[(c*N + n)*T + t] = src[(n*C + c)*T + t], 4 values per thread.
+template <bool VEC>
 __global__ void __launch_bounds__(256) nct_to_cnt_kernel(const float* __restrict__ src,
                                                          float* __restrict__ dst, int N, int C,
-                                                         size_t T) {
-    const size_t total = (size_t)N * C * T;
-    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total;
-         e += (size_t)gridDim.x * 256) {
-        const size_t t = e % T, c = (e / T) % C, n = e / (T * C);
-        dst[(c * N + n) * T + t] = src[e];
+                                                         uint32_t T, int y0, int z0) {
+    const int c = y0 + blockIdx.y, n = z0 + blockIdx.z;
+    const uint32_t t0 = (blockIdx.x * 256u + threadIdx.x) * 4u;
+    if (t0 >= T) return;
+    const float* a = src + ((size_t)n * C + c) * T + t0;
+    float* b = dst + ((size_t)c * N + n) * T + t0;
+    if (VEC) {
+        __builtin_nontemporal_store(*reinterpret_cast<const f32x4*>(a), reinterpret_cast<f32x4*>(b));
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (t0 + e < T) __builtin_nontemporal_store(a[e], b + e);
     }
 }
 
-unsigned grid_for(size_t total) {
-    size_t b = (total + 255) / 256;
-    const size_t cap = (size_t)num_cus() * 32;
-    return (unsigned)(b < cap ? (b ? b : 1) : cap);
+// Launch kern over a (gx, Y, Z) grid in y / z chunks of at most 65535.
+template <typename Launch>
+void launch_yz(unsigned gx, int Y, int Z, Launch launch) {
+    for (int z0 = 0; z0 < Z; z0 += 65535)
+        for (int y0 = 0; y0 < Y; y0 += 65535)
+            launch(dim3(gx, (unsigned)std::min(65535, Y - y0), (unsigned)std::min(65535, Z - z0)),
+                   y0, z0);
 }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int make_shape(const char* op, int N, int Cin, int H, int W, int KH, int KW, int pad, int stride,
                ConvShape& s) {
@@ -107,10 +150,15 @@ int dh_im2col(const float* X, float* col, int N, int Cin, int H, int W, int KH, 
     DH_TRY(ensure_init());
     ConvShape s;
     DH_TRY(make_shape("dh_im2col", N, Cin, H, W, KH, KW, pad, stride, s));
-    const size_t total = (size_t)Cin * KH * KW * N * s.OH * s.OW;
-    if (total == 0) return DH_OK;
+    const size_t P = (size_t)s.OH * s.OW, R = (size_t)Cin * KH * KW;
+    if (R * N * P == 0) return DH_OK;
     if (!X || !col) return set_error(DH_ERR_INVALID, "dh_im2col: null pointer");
-    im2col_kernel<<<grid_for(total), 256, 0, stream()>>>(X, col, s);
+    if (P >= (1u << 31) || R >= (1u << 31))
+        return set_error(DH_ERR_UNSUPPORTED, "dh_im2col: %zu output positions x %zu rows", P, R);
+    const FastDiv f_ow = make_fastdiv((uint32_t)s.OW);
+    launch_yz((unsigned)((P + IM_SPAN - 1) / IM_SPAN), (int)R, N, [&](dim3 g, int y0, int z0) {
+        im2col_kernel<<<g, 256, 0, stream()>>>(X, col, s, f_ow, y0, z0);
+    });
     return check_launch("dh_im2col");
 }
 
@@ -119,20 +167,28 @@ int dh_col2im(const float* dcol, float* dX, int N, int Cin, int H, int W, int KH
     DH_TRY(ensure_init());
     ConvShape s;
     DH_TRY(make_shape("dh_col2im", N, Cin, H, W, KH, KW, pad, stride, s));
-    const size_t total = (size_t)N * Cin * H * W;
-    if (total == 0) return DH_OK;
+    const size_t HW = (size_t)H * W;
+    if ((size_t)N * Cin * HW == 0) return DH_OK;
     if (!dcol || !dX) return set_error(DH_ERR_INVALID, "dh_col2im: null pointer");
-    col2im_kernel<<<grid_for(total), 256, 0, stream()>>>(dcol, dX, s, accumulate);
+    if (HW >= (1u << 31)) return set_error(DH_ERR_UNSUPPORTED, "dh_col2im: %zu-element planes", HW);
+    const FastDiv f_w = make_fastdiv((uint32_t)W);
+    launch_yz((unsigned)((HW + 255) / 256), Cin, N, [&](dim3 g, int y0, int z0) {
+        col2im_kernel<<<g, 256, 0, stream()>>>(dcol, dX, s, f_w, accumulate, y0, z0);
+    });
     return check_launch("dh_col2im");
 }
 
 int dh_nct_to_cnt(const float* src, float* dst, int N, int C, size_t T) {
     DH_TRY(ensure_init());
     if (N < 0 || C < 0) return set_error(DH_ERR_INVALID, "dh_nct_to_cnt: negative shape");
-    const size_t total = (size_t)N * C * T;
-    if (total == 0) return DH_OK;
+    if ((size_t)N * C * T == 0) return DH_OK;
     if (!src || !dst) return set_error(DH_ERR_INVALID, "dh_nct_to_cnt: null pointer");
-    nct_to_cnt_kernel<<<grid_for(total), 256, 0, stream()>>>(src, dst, N, C, T);
+    if (T >= (1u << 31)) return set_error(DH_ERR_UNSUPPORTED, "dh_nct_to_cnt: T = %zu", T);
+    const bool vec = T % 4 == 0 && aligned16(src) && aligned16(dst);
+    launch_yz((unsigned)((T + 1023) / 1024), C, N, [&](dim3 g, int y0, int z0) {
+        if (vec) nct_to_cnt_kernel<true><<<g, 256, 0, stream()>>>(src, dst, N, C, (uint32_t)T, y0, z0);
+        else nct_to_cnt_kernel<false><<<g, 256, 0, stream()>>>(src, dst, N, C, (uint32_t)T, y0, z0);
+    });
     return check_launch("dh_nct_to_cnt");
 }
 

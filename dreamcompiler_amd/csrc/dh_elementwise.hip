@@ -19,25 +19,6 @@ namespace {
 constexpr int EW_THREADS = 256;
 constexpr int EW_UNROLL = 4;
 
-// Division by an invariant divisor as multiply-high, add and shift (the round-up method of
-// Granlund & Montgomery, "Division by invariant integers using multiplication", PLDI 1994):
-// for 1 <= d < 2^31, s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 (< 2^32), and for
-// every 0 <= n < 2^31, n / d = (umulhi(n, m) + n) >> s (the sum stays below 2^32).
-struct FastDiv {
-    uint32_t d, m, s;
-};
-
-FastDiv make_fastdiv(uint32_t d) {
-    uint32_t s = 0;
-    while ((1ull << s) < d) ++s;
-    const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
-    return {d, (uint32_t)m, s};
-}
-
-__device__ inline uint32_t fdiv(uint32_t n, const FastDiv& f) {
-    return (__umulhi(n, f.m) + n) >> f.s;
-}
-
 // Binary op codes in the order of the reference's BinopCode (gpu.inc:455-460).
 template <int OP, typename T>
 __device__ inline T bin(T a, T b) {
