@@ -389,6 +389,96 @@ def cpu_baseline_mlp(steps=2):
             "sample": f"{steps} steps after 1 warm-up"}
 
 
+def cpu_baseline_workloads(gpu_ms):
+    """The reference's own CPU path (oracle/_ref) timed on each secondary workload's shape, or
+    on a stated sample of it: ms per full workload (sampled runs scaled by the exact work
+    ratio), beside the GPU's ms.  fp64 (Dream's type) on the host's OMP_NUM_THREADS where the
+    reference uses OpenMP, single-threaded where it does not."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _ref_runtime  # noqa: E402  (test infrastructure: the CPU comparison only)
+    if not _ref_runtime.available():
+        return {"error": "oracle/_ref not built"}
+    R = _ref_runtime.RefRuntime()
+    L = R.L
+    rng = np.random.default_rng(12)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    out = {}
+
+    def timed(fn, reps=1):
+        fn()   # warm-up (page-in, OpenMP pool)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) * 1000.0 / reps
+
+    def record(name, ms_sample, scale, sample, cores=threads):
+        ms = ms_sample * scale
+        g = gpu_ms.get(name)
+        out[name] = {"value": round(ms, 3), "unit": "ms", "cores": cores, "kind": "reference",
+                     "sample": sample, "gpu_ms": g,
+                     "gpu_speedup": round(ms / g, 1) if g else None}
+
+    # row ops at 16384 x 1024: forward builtins, and the backward of backward(sum(Y * G))
+    X, G = rng.standard_normal((16384, 1024)), rng.standard_normal((16384, 1024))
+    x, g = R.tensor(X), R.tensor(G)
+    for name, fn in (("softmax_fwd_16384x1024", L.dream_softmax),
+                     ("layer_norm_fwd_16384x1024", L.dream_layer_norm)):
+        record(name, timed(lambda: L.tensor_decref(fn(x))), 1, "full shape, fp64", 1)
+    # backward(Y) on the op's own output runs exactly that op's backward branch (upstream
+    # gradient of ones: the same work as any other upstream)
+    for name, fn in (("softmax_bwd_16384x1024", L.dream_softmax),
+                     ("layer_norm_bwd_16384x1024", L.dream_layer_norm)):
+        y = fn(x)
+        record(name, timed(lambda: L.backward(y)), 1, "full shape, fp64; backward(Y) of the op", 1)
+    # elementwise at 4096 x 4096 (runCPUBinary / runCPUUnary, OpenMP on the same-shape path)
+    A, B, b = rng.standard_normal((4096, 4096)), rng.standard_normal((4096, 4096)), \
+        rng.standard_normal((1, 4096))
+    a, bb, brow = R.tensor(A), R.tensor(B), R.tensor(b)
+    record("ew_add_f64_4096x4096", timed(lambda: L.tensor_decref(L.tensor_add(a, bb)), 3), 1,
+           "full shape, fp64")
+    record("ew_mul_rowbcast_f64_4096x4096",
+           timed(lambda: L.tensor_decref(L.tensor_mul(a, brow)), 3), 1,
+           "full shape, fp64 (the broadcast loop is single-threaded)", 1)
+    record("ew_sigmoid_f64_4096x4096", timed(lambda: L.tensor_decref(L.dream_sigmoid(a)), 3), 1,
+           "full shape, fp64")
+    # fused linear_relu of config 2's first layer
+    Xl = rng.uniform(0, 1, (4096, 784))
+    Wl, bl = rng.standard_normal((257, 784)) * np.sqrt(2 / 784), rng.standard_normal((1, 257))
+    xl, wl, bl_ = R.tensor(Xl), R.tensor(Wl), R.tensor(bl)
+    record("linear_relu_c2", timed(lambda: L.tensor_decref(L.dream_linear_relu(xl, wl, bl_)), 3),
+           1, "full shape, fp64")
+    # bmm 64 x 512^3: 4 of the 64 batch members (the reference's loop is the same per member)
+    nb = 2
+    Ab, Bb = rng.standard_normal((nb, 512 * 512)), rng.standard_normal((nb, 512 * 512))
+    ab, bbm = R.tensor(Ab), R.tensor(Bb)
+    sc = [R.scalar(v) for v in (nb, 512, 512, 512)]
+    record("bmm_64x512", timed(lambda: L.tensor_decref(L.dream_bmm(ab, bbm, *sc))), 64 / nb,
+           f"{nb} of 64 batch members, fp64, scaled by 64/{nb}", 1)
+    # conv2d 64 x 64ch 56x56 -> 64ch 3x3 pad 1: 8 of the 64 images (per-image host loop)
+    ni = 4
+    Xc = rng.standard_normal((ni, 64 * 56 * 56))
+    Kc, bc = rng.standard_normal((64, 64 * 9)) * 0.05, rng.standard_normal((1, 64))
+    xc, kc, bcc = R.tensor(Xc), R.tensor(Kc), R.tensor(bc)
+    scc = [R.scalar(v) for v in (56, 56, 3, 3, 1, 1)]
+    record("conv2d_resnet_64x56x56",
+           timed(lambda: L.tensor_decref(L.dream_conv2d_padded(xc, kc, bcc, *scc))), 64 / ni,
+           f"{ni} of 64 images, fp64, scaled by 64/{ni}")
+    # config 3 flash forward (fp64, single-threaded) on the whole config
+    Q3, K3, V3 = (rng.standard_normal((24, 256 * 64)) * 0.5 for _ in range(3))
+    record("flash_fwd_c3", timed(lambda: R.attention("flash", Q3, K3, V3, 24, 256, 64, 64)), 1,
+           "full config, fp64", 1)
+    # config 4 flash backward: 1 of the 128 slices (fp64, single-threaded), backward(O) only
+    ns = 1
+    q4, k4, v4 = (R.tensor(rng.standard_normal((ns, 4096 * 128))) for _ in range(3))
+    o4 = L.dream_flash_attention(q4, k4, v4, *(R.scalar(v) for v in (ns, 4096, 128, 64)))
+    t0 = time.perf_counter()
+    L.backward(o4)
+    bwd_ms = (time.perf_counter() - t0) * 1000.0
+    record("flash_bwd_c4", bwd_ms, 128 / ns,
+           f"{ns} of 128 slices, S=4096 D=128, fp64, backward(O) only, scaled by 128/{ns}", 1)
+    return out
+
+
 # --------------------------------------------------------------------------- main
 def load_traffic():
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), scaled
@@ -501,6 +591,8 @@ def main():
                 line["cpu_baseline"] = cpu_baseline_gemm()
             line["cpu_baseline_flash_fwd_c4"] = cpu_baseline_flash()
             line["cpu_baseline_runtime_mlp_c2_step"] = cpu_baseline_mlp()
+            line["cpu_baseline_workloads"] = cpu_baseline_workloads(
+                {k: v["ms"] for k, v in metrics.items() if isinstance(v, dict) and "ms" in v})
         except Exception as e:  # the CPU comparison must not hide the GPU result
             line["cpu_baseline"] = {"error": repr(e)}
     print(json.dumps(line), flush=True)
