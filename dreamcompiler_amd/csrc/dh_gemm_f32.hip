@@ -21,6 +21,8 @@
 // Edges: rows/cols beyond M, N and K are loaded as zeros and never stored, so any
 //   shape is exact.  When a matrix's leading dimension and base address allow it the
 //   contiguous dimension is fetched with 128-bit loads.
+#include <type_traits>
+
 #include "dh_common.hpp"
 
 namespace dh {
@@ -30,13 +32,22 @@ constexpr int BK = 16, NTHREADS = 256;
 
 // Four consecutive elements of one row of a row-major matrix:
 // row r, columns c..c+3 of a rows x cols matrix with leading dimension ld.
+// VEC: 16-byte aligned rows and cols % 4 == 0, so a chunk (c % 4 == 0) is wholly inside or
+// outside; an outside chunk then reads 16 zero bytes (g_zero4) instead.  The load is
+// branch-free and nothing touches its result before the LDS store, so the wait for it can
+// sit there (a select or branch on the value would force the wait right after the load).
+__device__ __attribute__((aligned(16))) float g_zero4[4];   // zero-initialised, never written
+
 template <bool VEC>
 __device__ inline f32x4 load4(const float* __restrict__ p, int ld, int rows, int cols, int r,
                               int c) {
     f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (VEC) {
+        const bool in = r < rows && c < cols;
+        return *reinterpret_cast<const f32x4*>(in ? p + (size_t)r * ld + c : g_zero4);
+    }
     if (r >= rows) return v;
     const float* q = p + (size_t)r * ld + c;
-    if (VEC && c + 3 < cols) return *reinterpret_cast<const f32x4*>(q);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
         if (c + e < cols) v[e] = q[e];
@@ -113,9 +124,12 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     const int wm = (wave / WN) * 64, wn = (wave % WN) * 64;
 
     // A: op(A)[i][k]; stored [i][k] when !TA (k contiguous), [k][i] when TA.
-    Slice<!TA, VA, TBM> sa;
     // B: op(B)[k][j]; stored [k][j] when !TB (j contiguous), [j][k] when TB.
-    Slice<TB, VB, TBN> sb;
+    // Two register sets: slice kt + 2 is fetched while slice kt is computed and slice kt + 1
+    // waits in the other set, so a load has two slices' compute to land -- with one or two
+    // work-groups per CU (small products, split-K chunks) nothing else hides it.
+    Slice<!TA, VA, TBM> sa[2];
+    Slice<TB, VB, TBN> sb[2];
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -125,23 +139,21 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
+    // The loop is branch-free so the compiler's wait for a slice's loads can sit at its LDS
+    // store, two slices later (with a guarded fetch it waited for every load right away):
+    // fetches are unconditional (a slice at or past K reads zeros) and the slice count is
+    // taken up to an even number (a zero slice adds nothing).  fp32 4096^3: 1.26 -> 1.15 ms.
     const int nk = (K + BK - 1) / BK;
     if (nk > 0) {
-        sa.fetch(A, lda, m0, 0, M, K, tid);
-        sb.fetch(B, ldb, n0, 0, N, K, tid);
-        sa.store(As[0], LDS_A, tid);
-        sb.store(Bs[0], LDS_B, tid);
+        sa[0].fetch(A, lda, m0, 0, M, K, tid);
+        sb[0].fetch(B, ldb, n0, 0, N, K, tid);
+        sa[1].fetch(A, lda, m0, BK, M, K, tid);
+        sb[1].fetch(B, ldb, n0, BK, N, K, tid);
+        sa[0].store(As[0], LDS_A, tid);
+        sb[0].store(Bs[0], LDS_B, tid);
         __syncthreads();
     }
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            sa.fetch(A, lda, m0, (kt + 1) * BK, M, K, tid);
-            sb.fetch(B, ldb, n0, (kt + 1) * BK, N, K, tid);
-        }
-        const float* as = As[cur];
-        const float* bs = Bs[cur];
+    auto mma = [&](const float* as, const float* bs) {   // one k-slice from LDS
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
             float a0 = as[(kk + h) * LDS_A + wm + l32];
@@ -153,11 +165,27 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
             acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
             acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
         }
-        if (more) {
-            sa.store(As[cur ^ 1], LDS_A, tid);
-            sb.store(Bs[cur ^ 1], LDS_B, tid);
-        }
+    };
+    // One k-slice of the loop; the register set index is a template constant (a runtime
+    // index would put both sets in scratch).
+    auto step = [&](auto cur_c, int kt) {
+        constexpr int cur = decltype(cur_c)::value;
+        // set cur held slice kt, already in LDS: refill it with slice kt + 2
+        sa[cur].fetch(A, lda, m0, (kt + 2) * BK, M, K, tid);
+        sb[cur].fetch(B, ldb, n0, (kt + 2) * BK, N, K, tid);
+        mma(As[cur], Bs[cur]);
+        // slice kt + 1, fetched an iteration ago (past the last slice: unread zeros)
+        sa[cur ^ 1].store(As[cur ^ 1], LDS_A, tid);
+        sb[cur ^ 1].store(Bs[cur ^ 1], LDS_B, tid);
         __syncthreads();
+    };
+    if (nk == 1) {   // one slice (tiny K): no loop, no zero slice
+        mma(As[0], Bs[0]);
+    } else {
+        for (int kt = 0; kt < nk; kt += 2) {
+            step(std::integral_constant<int, 0>{}, kt);
+            step(std::integral_constant<int, 1>{}, kt + 1);
+        }
     }
 
     // Epilogue: lanes 0..31 of a register cover 32 consecutive columns of one row.
@@ -211,11 +239,13 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ p
 }
 
 template <bool TA, bool TB, int TBM, int TBN>
-auto pick_kernel(const float* A, int lda, long long sA, const float* B, int ldb, long long sB) {
-    // 128-bit loads need 16-byte aligned bases and leading dimensions and batch strides
-    // divisible by 4.
-    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0) && (sA % 4 == 0);
-    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0) && (sB % 4 == 0);
+auto pick_kernel(int M, int N, int K, const float* A, int lda, long long sA, const float* B,
+                 int ldb, long long sB) {
+    // 128-bit loads need 16-byte aligned bases, leading dimensions and batch strides divisible
+    // by 4, and a contiguous extent (K, or M / N for the transposed storage) divisible by 4.
+    const int ca = TA ? M : K, cb = TB ? K : N;
+    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0) && (sA % 4 == 0) && (ca % 4 == 0);
+    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0) && (sB % 4 == 0) && (cb % 4 == 0);
     return va && vb ? gemm_f32_kernel<TA, TB, true, true, TBM, TBN>
          : va       ? gemm_f32_kernel<TA, TB, true, false, TBM, TBN>
          : vb       ? gemm_f32_kernel<TA, TB, false, true, TBM, TBN>
@@ -227,14 +257,15 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
                  float beta, float* C, int ldc, const Batch& bt) {
     const int tiles = ((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN);
     hipStream_t s = stream();
-    // Skinny products with a long contraction (the weight gradients dW = dY^T X of a layer:
-    // few output tiles, K = the batch) would leave most CUs idle: split K into S chunks run
-    // as gridDim.y members writing fp32 partials, then reduce them in order.
-    // Only where the one-pass grid fills at most a quarter of the CUs: a 2-way split of a
-    // half-full grid loses more to the partial-sum traffic than it gains.
+    // Products with few output tiles and a long contraction (the weight gradients dW = dY^T X
+    // of a layer, K = the batch; a layer's forward with few output columns) would leave most
+    // CUs idle: split K into S chunks run as gridDim.y members writing fp32 partials, then
+    // reduce them in order.  Where the one-pass grid fills at most half the CUs, S aims at 4
+    // work-groups per CU (measured on config 2's layer shapes: 96 tiles with K = 784, 0.088 ->
+    // 0.067 ms; 21 tiles with K = 4096, 0.086 -> 0.061 ms; 1 or 2 per CU gain less).
     const int cus = num_cus();
-    if (bt.count == 1 && 4 * tiles <= cus && K >= 512) {
-        int S = cus / tiles;
+    if (bt.count == 1 && 2 * tiles <= cus && K >= 512) {
+        int S = 4 * cus / tiles;
         S = S > 32 ? 32 : S;
         S = S > K / 128 ? K / 128 : S;
         const int Kc = ((K + S - 1) / S + BK - 1) / BK * BK;   // chunk of K, multiple of BK
@@ -246,7 +277,7 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
             const long long sA = TA ? (long long)Kc * lda : Kc, sB = TB ? Kc : (long long)Kc * ldb;
             int st = DH_OK;
             if (full > 0) {
-                auto kern = pick_kernel<TA, TB, TBM, TBN>(A, lda, sA, B, ldb, sB);
+                auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, Kc, A, lda, sA, B, ldb, sB);
                 kern<<<dim3(tiles, full), NTHREADS, 0, s>>>(M, N, Kc, A, lda, B, ldb, 0.f, part, N,
                                                             sA, sB, (long long)M * N, nullptr, 0);
                 st = check_launch("dh_gemm_f32(split-K)");
@@ -254,7 +285,7 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
             if (st == DH_OK && tail > 0) {
                 const float* At = A + full * sA;
                 const float* Bt = B + full * sB;
-                auto kern = pick_kernel<TA, TB, TBM, TBN>(At, lda, 0, Bt, ldb, 0);
+                auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, tail, At, lda, 0, Bt, ldb, 0);
                 kern<<<dim3(tiles, 1), NTHREADS, 0, s>>>(M, N, tail, At, lda, Bt, ldb, 0.f,
                                                          part + (size_t)full * M * N, N, 0, 0, 0,
                                                          nullptr, 0);
@@ -272,7 +303,7 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
         }
         // no workspace: fall through to the one-pass kernel
     }
-    auto kern = pick_kernel<TA, TB, TBM, TBN>(A, lda, bt.sA, B, ldb, bt.sB);
+    auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, K, A, lda, bt.sA, B, ldb, bt.sB);
     // gridDim.y carries the batch member; chunks of 65535 keep it within the y limit.
     for (int b0 = 0; b0 < bt.count; b0 += 65535) {
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
