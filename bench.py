@@ -175,24 +175,21 @@ def bmm_workload(Bt, M, N, K, seed=7):
 
 
 def conv_workload(N, Cin, H, W, Cout, KH, KW, pad, stride, seed=9):
-    """dream_conv2d's device work: im2col of the whole batch + one batched GEMM with the
-    per-channel bias epilogue (fp32).  Algorithmic bytes: input, kernel, bias read and output
-    written once (the im2col matrix is traffic of this algorithm, not of the convolution)."""
+    """dream_conv2d's device work: one implicit-GEMM launch (dh_conv2d_fwd: the im2col matrix
+    gathered inside the GEMM's operand loader, never stored) with the per-channel bias, fp32.
+    Algorithmic bytes: input, kernel, bias read and output written once."""
     rng = np.random.default_rng(seed)
     OH, OW = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
     K, P = Cin * KH * KW, OH * OW
     X = DB.from_numpy(rng.standard_normal((N, Cin * H * W), dtype=np.float32))
     Kn = DB.from_numpy((rng.standard_normal((Cout, K)) * 0.05).astype(np.float32))
     b = DB.from_numpy(rng.standard_normal(Cout).astype(np.float32))
-    col = DB.empty((K, N * P), np.float32)
     Y = DB.empty((N, Cout * P), np.float32)
 
     def step():
-        hip.im2col(X, col, N, Cin, H, W, KH, KW, pad, stride)
-        hip.gemm_ex("f32", 0, 0, Cout, P, K, Kn, K, 0, col, N * P, P, 0.0, Y, P, Cout * P, N, b,
-                    row_bias=True)
+        hip.conv2d_fwd(X, Kn, b, Y, N, Cin, H, W, Cout, KH, KW, pad, stride)
     flops = 2.0 * N * Cout * P * K
-    return step, flops, 4.0 * (N * Cin * H * W + Cout * K + Cout + N * Cout * P), [X, Kn, b, col, Y]
+    return step, flops, 4.0 * (N * Cin * H * W + Cout * K + Cout + N * Cout * P), [X, Kn, b, Y]
 
 
 WORKLOADS = {
@@ -216,7 +213,7 @@ WORKLOADS = {
                    "dream_bmm 64 x (512x512 @ 512x512) fp32, one batched launch"),
     "conv2d_resnet_64x56x56": (conv_workload, dict(N=64, Cin=64, H=56, W=56, Cout=64, KH=3, KW=3,
                                                    pad=1, stride=1), "fp32",
-                               "conv2d 64 x 64ch 56x56, 64 out ch, 3x3 pad 1 (im2col + batched GEMM), fp32"),
+                               "conv2d 64 x 64ch 56x56, 64 out ch, 3x3 pad 1 (implicit GEMM), fp32"),
     "softmax_fwd_16384x1024": (rows_workload, dict(op="softmax_fwd", R=16384, C=1024), "hbm",
                                "row softmax 16384 x 1024 fp32 (HBM-bound)"),
     "softmax_bwd_16384x1024": (rows_workload, dict(op="softmax_bwd", R=16384, C=1024), "hbm",

@@ -213,6 +213,168 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
         }
 }
 
+// ---- conv2d forward as an implicit GEMM ---------------------------------------------
+// Y[n][co][p] = sum_r Kn[co][r] col_n[r][p] + bias[co] with col_n[r][p] = X[n][ci][h][w],
+// r = (ci KH + kh) KW + kw, p = oh OW + ow, h = oh stride + kh - pad, w = ow stride + kw - pad
+// (zero outside the input): the im2col matrix is gathered by the B loader and never stored.
+struct ConvGeom {
+    int Cin, H, W, KH, KW, pad, stride, OH, OW;
+    FastDiv f_ow, f_kw, f_khkw;   // division by OW, KW and KH*KW
+};
+
+// B slice of the implicit GEMM: rows k0 .. k0 + BK of col_n, columns t0 .. t0 + TILE, laid out
+// like Slice<false, ...> (row k, 4 consecutive columns per chunk).  A thread's chunks all sit
+// in the same 4 columns (tq = tid % (TILE / 4)) and in rows RSTEP apart, so the columns'
+// window origins are computed once per tile and a slice only decomposes its rows.  Every
+// element is one branch-free scalar load (a tap outside the input reads g_zero4).
+template <int TILE>
+struct ConvSlice {
+    static constexpr int CH = TILE * BK / 4 / NTHREADS;
+    static constexpr int RSTEP = NTHREADS / (TILE / 4);
+    f32x4 v[CH];
+    int hb[4], wb[4];   // oh * stride - pad, ow * stride - pad of the thread's 4 columns
+
+    __device__ void init(const ConvGeom& g, int t0, int P, int tid) {
+        const int tq = tid % (TILE / 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int p = t0 + 4 * tq + e;
+            const int oh = (int)fdiv((uint32_t)p, g.f_ow), ow = p - oh * g.OW;
+            hb[e] = p < P ? oh * g.stride - g.pad : -(1 << 30);   // a column past P: h < 0
+            wb[e] = ow * g.stride - g.pad;
+        }
+    }
+    __device__ void fetch(const float* __restrict__ Xn, const ConvGeom& g, int R, int k0,
+                          int tid) {
+#pragma unroll
+        for (int r = 0; r < CH; ++r) {
+            const int k = k0 + tid / (TILE / 4) + RSTEP * r;
+            const int q = (int)fdiv((uint32_t)k, g.f_kw), kw = k - q * g.KW;
+            const int ci = (int)fdiv((uint32_t)k, g.f_khkw), kh = q - ci * g.KH;
+            const float* xc = Xn + (size_t)ci * g.H * g.W;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int h = hb[e] + kh, w = wb[e] + kw;
+                const bool in = k < R && (unsigned)h < (unsigned)g.H && (unsigned)w < (unsigned)g.W;
+                v[r][e] = *(in ? xc + h * g.W + w : g_zero4);
+            }
+        }
+    }
+    __device__ void store(float* lds, int stride, int tid) const {
+#pragma unroll
+        for (int r = 0; r < CH; ++r) {
+            const int f = tid + r * NTHREADS;
+            *reinterpret_cast<f32x4*>(&lds[(f / (TILE / 4)) * stride + 4 * (f % (TILE / 4))]) = v[r];
+        }
+    }
+};
+
+// Work-group tile TBM (output channels) x TBN (output positions of image z0 + blockIdx.y);
+// the k-loop is the GEMM kernel's (two register sets, branch-free), A = the kernel matrix
+// Cout x R (k contiguous), epilogue: + bias[co], stored into Y's (N, Cout, OH OW) layout.
+template <int TBM, int TBN, bool VA>
+__global__ void __launch_bounds__(NTHREADS)
+conv_fwd_kernel(int Cout, int P, int R, const float* __restrict__ Kn, const float* __restrict__ X,
+                ConvGeom g, float* __restrict__ Y, const float* __restrict__ bias, int z0) {
+    const int n = z0 + blockIdx.y;
+    const float* Xn = X + (size_t)n * g.Cin * g.H * g.W;
+    float* Yn = Y + (size_t)n * Cout * P;
+    constexpr int LDS_A = TBM + 4, LDS_B = TBN + 4;
+    constexpr int WN = TBN / 64;
+    static_assert((TBM / 64) * WN == 4, "4 waves of 64 x 64");
+    __shared__ __attribute__((aligned(16))) float As[2][BK * LDS_A];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDS_B];
+
+    const int tiles_m = (Cout + TBM - 1) / TBM, tiles_n = (P + TBN - 1) / TBN;
+    int tm, tn;
+    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
+    const int m0 = tm * TBM, n0 = tn * TBN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm = (wave / WN) * 64, wn = (wave % WN) * 64;
+
+    Slice<true, VA, TBM> sa[2];
+    ConvSlice<TBN> sb[2];
+    sb[0].init(g, n0, P, tid);
+    sb[1].init(g, n0, P, tid);
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    const int nk = (R + BK - 1) / BK;   // R >= 1
+    sa[0].fetch(Kn, R, m0, 0, Cout, R, tid);
+    sb[0].fetch(Xn, g, R, 0, tid);
+    sa[1].fetch(Kn, R, m0, BK, Cout, R, tid);
+    sb[1].fetch(Xn, g, R, BK, tid);
+    sa[0].store(As[0], LDS_A, tid);
+    sb[0].store(Bs[0], LDS_B, tid);
+    __syncthreads();
+    auto mma = [&](const float* as, const float* bs) {
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            float a0 = as[(kk + h) * LDS_A + wm + l32];
+            float a1 = as[(kk + h) * LDS_A + wm + 32 + l32];
+            float b0 = bs[(kk + h) * LDS_B + wn + l32];
+            float b1 = bs[(kk + h) * LDS_B + wn + 32 + l32];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+    };
+    auto step = [&](auto cur_c, int kt) {
+        constexpr int cur = decltype(cur_c)::value;
+        sa[cur].fetch(Kn, R, m0, (kt + 2) * BK, Cout, R, tid);
+        sb[cur].fetch(Xn, g, R, (kt + 2) * BK, tid);
+        mma(As[cur], Bs[cur]);
+        sa[cur ^ 1].store(As[cur ^ 1], LDS_A, tid);
+        sb[cur ^ 1].store(Bs[cur ^ 1], LDS_B, tid);
+        __syncthreads();
+    };
+    if (nk == 1) {
+        mma(As[0], Bs[0]);
+    } else {
+        for (int kt = 0; kt < nk; kt += 2) {
+            step(std::integral_constant<int, 0>{}, kt);
+            step(std::integral_constant<int, 1>{}, kt + 1);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int col = n0 + wn + 32 * b + l32;
+            if (col >= P) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < Cout)
+                    Yn[(size_t)row * P + col] = acc[a][b][r] + (bias ? bias[row] : 0.f);
+            }
+        }
+}
+
+template <int TBM, int TBN>
+int launch_conv(int N, int Cout, int P, int R, const float* Kn, const float* X,
+                const ConvGeom& g, float* Y, const float* bias) {
+    const bool va = ((uintptr_t)Kn % 16 == 0) && (R % 4 == 0);
+    const int tiles = ((Cout + TBM - 1) / TBM) * ((P + TBN - 1) / TBN);
+    for (int z0 = 0; z0 < N; z0 += 65535) {
+        const dim3 grid(tiles, N - z0 < 65535 ? N - z0 : 65535);
+        if (va)
+            conv_fwd_kernel<TBM, TBN, true><<<grid, NTHREADS, 0, stream()>>>(Cout, P, R, Kn, X, g, Y, bias, z0);
+        else
+            conv_fwd_kernel<TBM, TBN, false><<<grid, NTHREADS, 0, stream()>>>(Cout, P, R, Kn, X, g, Y, bias, z0);
+        DH_TRY(check_launch("dh_conv2d_fwd"));
+    }
+    return DH_OK;
+}
+
 struct Batch {
     long long sA, sB, sC;
     int count;
@@ -361,4 +523,27 @@ extern "C" int dh_gemm_f32(int transA, int transB, int M, int N, int K, const fl
                            const float* B, int ldb, float beta, float* C, int ldc) {
     return dh_gemm_f32_ex(transA, transB, M, N, K, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1,
                           nullptr, 0);
+}
+
+extern "C" int dh_conv2d_fwd(const float* X, const float* Kn, const float* bias, float* Y, int N,
+                             int Cin, int H, int W, int Cout, int KH, int KW, int pad,
+                             int stride) {
+    DH_TRY(ensure_init());
+    if (N < 0 || Cin < 1 || H < 1 || W < 1 || Cout < 1 || KH < 1 || KW < 1 || pad < 0 ||
+        stride < 1)
+        return set_error(DH_ERR_INVALID, "dh_conv2d_fwd: invalid shape");
+    if (H + 2 * pad < KH || W + 2 * pad < KW)
+        return set_error(DH_ERR_INVALID, "dh_conv2d_fwd: kernel larger than the padded input");
+    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    const long long P = (long long)OH * OW, R = (long long)Cin * KH * KW;
+    if (N == 0) return DH_OK;
+    if (!X || !Kn || !Y) return set_error(DH_ERR_INVALID, "dh_conv2d_fwd: null pointer");
+    if (P >= (1ll << 30) || R >= (1ll << 30) || (long long)H * W >= (1ll << 30) ||
+        (long long)Cout * P >= (1ll << 31))
+        return set_error(DH_ERR_UNSUPPORTED, "dh_conv2d_fwd: plane or window too large");
+    ConvGeom g{Cin, H, W, KH, KW, pad, stride, OH, OW, make_fastdiv((uint32_t)OW),
+               make_fastdiv((uint32_t)KW), make_fastdiv((uint32_t)(KH * KW))};
+    if (Cout <= 64)
+        return launch_conv<64, 256>(N, Cout, (int)P, (int)R, Kn, X, g, Y, bias);
+    return launch_conv<128, 128>(N, Cout, (int)P, (int)R, Kn, X, g, Y, bias);
 }

@@ -1248,10 +1248,8 @@ static Tensor* conv_impl(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h_
     const int geom[8] = {H, W, KH, KW, Cin, Cout, pad, stride};
     std::copy(geom, geom + 8, out->conv);
     try {
-        const size_t NP = (size_t)N * P;
-        Dev col((size_t)K * NP * 4), y((size_t)out->size * 4);
-        need_buf(col), need_buf(y);
-        need(dh_im2col(dev_data(input), col.f(), N, Cin, H, W, KH, KW, pad, stride));
+        Dev y((size_t)out->size * 4);
+        need_buf(y);
         // The reference adds bias[co] for co < min(Cout, bias.size) (conv.inc:5-10).
         const float* db = nullptr;
         Dev bpad(bias ? (size_t)Cout * 4 : 4);
@@ -1265,9 +1263,9 @@ static Tensor* conv_impl(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h_
                 db = bpad.f();
             }
         }
-        need(dh_gemm_f32_ex(0, 0, Cout, (int)P, (int)K, dev_data(kernel), (int)K, 0, col.f(),
-                            (int)NP, P, 0.f, y.f(), (int)P, (long long)Cout * P, N, db,
-                            db ? DH_EPI_ROW_BIAS : 0));
+        // one implicit-GEMM launch: the im2col matrix is gathered inside the GEMM, never stored
+        need(dh_conv2d_fwd(dev_data(input), dev_data(kernel), db, y.f(), N, Cin, H, W, Cout, KH,
+                           KW, pad, stride));
         adopt_result(out, y);
     } catch (const Failure&) {
         rt_error("conv2d", "%s", dh_last_error());

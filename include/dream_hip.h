@@ -201,6 +201,12 @@ int dh_im2col(const float* d_X, float* d_col, int N, int Cin, int H, int W, int 
 int dh_col2im(const float* d_dcol, float* d_dX, int N, int Cin, int H, int W, int KH, int KW,
               int pad, int stride, int accumulate);
 int dh_nct_to_cnt(const float* d_src, float* d_dst, int N, int C, size_t T);
+/* The forward in one launch, as an implicit GEMM: Y (N, Cout, OH*OW) = kernel (Cout x
+ * Cin*KH*KW) @ col_n + bias[co] per image, the im2col matrix gathered inside the GEMM's operand
+ * loader and never stored (dream_conv2d / dream_conv2d_padded, conv.inc:12-55, 119-178).
+ * bias may be NULL; otherwise it holds Cout values. */
+int dh_conv2d_fwd(const float* d_X, const float* d_kernel, const float* d_bias, float* d_Y,
+                  int N, int Cin, int H, int W, int Cout, int KH, int KW, int pad, int stride);
 
 /* ---- elementwise ops (runGPU / runGPUUnary, runtime/backend/gpu.inc:637-716) ---------------
  * Op codes follow the reference's BinopCode / UnopCode (gpu.inc:455-460, 571-577); each

@@ -1,5 +1,6 @@
-"""GPU parity of conv2d: the data-movement kernels (dh_im2col, dh_col2im, dh_nct_to_cnt) and the
-dream_conv2d / dream_conv2d_padded builtins with their backward.
+"""GPU parity of conv2d: the data-movement kernels (dh_im2col, dh_col2im, dh_nct_to_cnt), the
+implicit-GEMM forward (dh_conv2d_fwd) and the dream_conv2d / dream_conv2d_padded builtins with
+their backward.
 
 Tolerances: im2col and the permute are copies (bit-exact); col2im sums at most KH*KW values per
 element (fp32 vs fp64 numpy: 1e-6 relative).  The builtins (fp32 on the GPU) against the fp64
@@ -69,6 +70,49 @@ def test_im2col_col2im_permute(shape):
     dY, dP = DB.from_numpy(Y), DB.empty((5, N * T), np.float32)
     hip.nct_to_cnt(dY, dP, N, 5, T)
     assert np.array_equal(dP.numpy(), Y.transpose(1, 0, 2).reshape(5, N * T))
+
+
+@pytest.mark.parametrize("shape", [
+    (2, 3, 7, 6, 4, 3, 2, 0, 1),        # golden-vector geometry, Cout <= 64 (64 x 256 tiles)
+    (3, 5, 9, 8, 70, 3, 3, 1, 2),       # Cout > 64: 128 x 128 tiles, padded and strided
+    (1, 2, 5, 5, 1, 5, 5, 2, 1),        # window as large as the padded input, one channel out
+    (2, 16, 23, 17, 33, 3, 1, 1, 1),    # ragged positions, a K = 48 contraction
+    (4, 7, 15, 15, 65, 1, 1, 0, 1),     # 1x1 kernel: R = Cin = 7 (a single k-slice)
+    (2, 64, 20, 20, 64, 3, 3, 1, 1),    # R = 576, as in the ResNet-like bench layer
+])
+def test_conv2d_fwd_implicit_gemm_against_oracle(shape):
+    # dh_conv2d_fwd against the fp64 oracle (orc_conv2d, pinned by the reference's golden
+    # vectors) and against the stored im2col + GEMM path; bias and no bias.
+    N, Cin, H, W, Cout, KH, KW, pad, stride = shape
+    OH, OW = O.conv_out(H, W, KH, KW, pad, stride)
+    rng = np.random.default_rng(sum(shape))
+    X = rng.standard_normal((N, Cin * H * W)).astype(np.float32)
+    Kn = rng.standard_normal((Cout, Cin * KH * KW)).astype(np.float32)
+    b = rng.standard_normal(Cout).astype(np.float32)
+    dX, dK, db = DB.from_numpy(X), DB.from_numpy(Kn), DB.from_numpy(b)
+    dY = DB.empty((N, Cout * OH * OW), np.float32)
+    try:
+        for bias in (db, None):
+            hip.conv2d_fwd(dX, dK, bias, dY, N, Cin, H, W, Cout, KH, KW, pad, stride)
+            got = dY.numpy()
+            ref = O.conv2d(X.astype(np.float64), Kn.astype(np.float64),
+                           None if bias is None else b.astype(np.float64), N, Cin, H, W, Cout,
+                           KH, KW, pad, stride)
+            assert maxrel(got, ref) <= 1e-5 * np.sqrt(Cin * KH * KW), (shape, bias is None)
+    finally:
+        for t in (dX, dK, db, dY):
+            t.free()
+
+
+def test_conv2d_fwd_rejects_bad_shapes():
+    d = DB.empty((64,), np.float32)
+    try:
+        with pytest.raises(hip.DreamHipError, match="kernel larger"):
+            hip.conv2d_fwd(d, d, None, d, 1, 1, 2, 2, 1, 5, 5, 0, 1)
+        with pytest.raises(hip.DreamHipError, match="invalid shape"):
+            hip.conv2d_fwd(d, d, None, d, 1, 1, 2, 2, 1, 1, 1, 0, 0)
+    finally:
+        d.free()
 
 
 @pytest.fixture(scope="module")
