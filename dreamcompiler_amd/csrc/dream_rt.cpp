@@ -1452,6 +1452,83 @@ Tensor* gpu_selftest(void) {
     return create_scalar(pass == total ? 1.0 : 0.0);
 }
 
+// gemm_selftest (elementwise.inc:888-968): the reference checks its CPU blocked kernels on 11
+// adversarial fp64 shapes and 6 short-K fp32 shapes against the naive loop.  Here `@` is the
+// GPU GEMM, so the same 17 shapes (same seed and draws) go through tensor_matmul -- the last 6
+// with `as f32` operands -- against the fp64 naive product, under the reference's own GPU gate
+// (absolute sqrt(K) 1e-4, elementwise.inc:843-845); then the 512^3 throughput line.
+Tensor* gemm_selftest(void) {
+    std::printf("=== gemm_selftest: GPU GEMM (the `@` path) vs naive fp64 reference ===\n");
+    if (!dh_available()) {
+        std::printf("  GEMM: SKIP (no HIP device: this runtime's `@` runs on the GPU)\n");
+        std::fflush(stdout);
+        return create_scalar(1.0);
+    }
+    rng().seed(20260707);
+    std::uniform_real_distribution<double> dist(-1.0, 1.0);
+    std::uniform_real_distribution<float> fdist(-1.0f, 1.0f);
+    struct Shape {
+        int M, K, N;
+        bool f32;
+    };
+    const Shape shapes[] = {{1, 1, 1, false},     {1, 7, 1, false},     {5, 1, 9, false},
+                            {3, 4, 5, false},     {7, 13, 17, false},   {31, 33, 37, false},
+                            {64, 64, 64, false},  {65, 63, 66, false},  {128, 100, 96, false},
+                            {200, 50, 300, false}, {257, 129, 255, false}, {8, 16, 16, true},
+                            {7, 15, 13, true},    {9, 8, 17, true},     {1, 4, 1, true},
+                            {16, 32, 24, true},   {32, 16, 32, true}};
+    int pass = 0, total = 0;
+    double worst = 0.0;
+    for (const Shape& sh : shapes) {
+        Tensor* A = alloc_tensor(sh.M, sh.K, 1, 1);
+        Tensor* B = alloc_tensor(sh.K, sh.N, 1, 1);
+        for (int i = 0; i < A->size; ++i) A->data[i] = sh.f32 ? (double)fdist(rng()) : dist(rng());
+        for (int i = 0; i < B->size; ++i) B->data[i] = sh.f32 ? (double)fdist(rng()) : dist(rng());
+        if (sh.f32) {
+            dream_set_precision(A, 1);
+            dream_set_precision(B, 1);
+        }
+        Tensor* C = tensor_matmul(A, B);
+        std::vector<double> R((size_t)sh.M * sh.N);
+        ref_gemm(A->data, B->data, R.data(), sh.M, sh.K, sh.N);
+        double max_abs = 0.0;
+        const bool shaped = C->size == (int)R.size();
+        for (size_t i = 0; shaped && i < R.size(); ++i)
+            max_abs = std::max(max_abs, std::fabs(C->data[i] - R[i]));
+        const double tol = std::sqrt((double)sh.K) * 1e-4;
+        const bool ok = shaped && max_abs < tol;
+        std::printf("  %s%4dx%-4dx%-4d max_abs=%.2e (tol %.1e)  %s\n", sh.f32 ? "f32 " : "",
+                    sh.M, sh.K, sh.N, max_abs, tol, ok ? "PASS" : "FAIL");
+        worst = std::max(worst, max_abs);
+        ++total;
+        pass += ok;
+        for (Tensor* t : {A, B, C}) tensor_decref(t);
+    }
+    {   // throughput: 512^3 through `@`, best of 3 (host tensors in, host result out)
+        const int n = 512;
+        Tensor* A = alloc_tensor(n, n, 1, 1);
+        Tensor* B = alloc_tensor(n, n, 1, 1);
+        for (int i = 0; i < A->size; ++i) A->data[i] = dist(rng());
+        for (int i = 0; i < B->size; ++i) B->data[i] = dist(rng());
+        double best = 1e30;
+        for (int rep = 0; rep < 3; ++rep) {
+            ++A->version;   // time the whole builtin, operand upload included
+            const auto t0 = std::chrono::steady_clock::now();
+            Tensor* C = tensor_matmul(A, B);
+            const auto t1 = std::chrono::steady_clock::now();
+            best = std::min(best, std::chrono::duration<double>(t1 - t0).count());
+            tensor_decref(C);
+        }
+        std::printf("  throughput: 512^3 in %.2f ms = %.1f GFLOPS (`@` incl. copies)\n",
+                    best * 1e3, 2.0 * n * n * (double)n / best / 1e9);
+        tensor_decref(A);
+        tensor_decref(B);
+    }
+    std::printf("  GEMM: %d/%d PASS (worst abs err %.2e)\n", pass, total, worst);
+    std::fflush(stdout);
+    return create_scalar(pass == total ? 1.0 : 0.0);
+}
+
 Tensor* dream_gpu_warmup(void) {
     const auto t0 = std::chrono::steady_clock::now();
     if (!dh_available()) {

@@ -182,6 +182,10 @@ Tensor* backward(Tensor* root);
 int dream_gpu_available(void);
 /* 1 when the HIP backend can run the GEMM and attention builtins. */
 int dream_hip_available(void);
+/* gemm_selftest (elementwise.inc:888-968): the reference's 17 shapes, seed and draws through
+ * `@` (the GPU GEMM; the 6 short-K shapes with `as f32` operands) against the naive fp64
+ * product under the GPU gate sqrt(K) 1e-4; prints "GEMM: 17/17 PASS" like the reference. */
+Tensor* gemm_selftest(void);
 Tensor* gpu_selftest(void);
 Tensor* dream_gpu_warmup(void);
 Tensor* flash_attention_selftest(void);

@@ -123,7 +123,9 @@ def test_26_flash_backward_matches_standard(L):
     assert abs(g2 - ref) <= 1e-5 * np.sqrt(32) * ref
 
 
-def test_18_25_selftests(L, capfd):
+def test_15_18_25_selftests(L, capfd):
+    assert rt.read(L.gemm_selftest())[0, 0] == 1.0
+    assert "GEMM: 17/17 PASS" in capfd.readouterr().out   # tests/15_gemm.dream
     assert rt.read(L.gpu_selftest())[0, 0] == 1.0
     assert rt.read(L.flash_attention_selftest())[0, 0] == 1.0
     assert rt.read(L.dream_gpu_warmup())[0, 0] > 0.0
