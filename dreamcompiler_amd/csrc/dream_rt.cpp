@@ -1529,6 +1529,103 @@ Tensor* gemm_selftest(void) {
     return create_scalar(pass == total ? 1.0 : 0.0);
 }
 
+// bf16_selftest (runtime/nn/training.inc:1978-2025): range and precision of the bf16 rounding
+// -- here the device conversion every bf16 operand goes through (dh_convert, round to nearest
+// even) -- and the reference's mixed-precision convergence check (a scalar host loop).
+static float host_bf16(float x) {   // the same RNE rule, for the host loop of check 3
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+    float r;
+    std::memcpy(&r, &u, 4);
+    return r;
+}
+
+Tensor* bf16_selftest(void) {
+    std::printf("=== bf16_selftest: mixed-precision training ===\n");
+    if (!dh_available()) {
+        std::printf("  BF16_MIXED: SKIP (no HIP device: bf16 rounding runs on the GPU)\n");
+        std::fflush(stdout);
+        return create_scalar(1.0);
+    }
+    int pass = 0, total = 0;
+    // the device round trip fp32 -> bf16 -> fp32 of n host values
+    auto round_dev = [](std::vector<float>& v) {
+        const size_t n = v.size();
+        Dev f(n * 4), b(n * 2);
+        need_buf(f), need_buf(b);
+        need(dh_memcpy_h2d(f.p, v.data(), n * 4));
+        need(dh_convert(b.p, DH_BF16, f.p, DH_F32, n));
+        need(dh_convert(f.p, DH_F32, b.p, DH_BF16, n));
+        need(dh_memcpy_d2h(v.data(), f.p, n * 4));
+    };
+    try {
+        {   // 1. range: bf16 keeps fp32's exponent, so 1e30 survives
+            std::vector<float> v{1e30f};
+            round_dev(v);
+            const bool ok = v[0] > 1e29f && v[0] < 1e31f;
+            std::printf("  bf16 range (1e30 survives; fp16 would overflow): %s\n", ok ? "PASS" : "FAIL");
+            ++total, pass += ok;
+        }
+        {   // 2. precision: relative error <= 2^-9 for values in [0.1, 10)
+            rng().seed(1);
+            std::uniform_real_distribution<float> d(0.1f, 10.0f);
+            std::vector<float> x(10000), r;
+            for (float& e : x) e = d(rng());
+            r = x;
+            round_dev(r);
+            double mr = 0.0;
+            for (size_t i = 0; i < x.size(); ++i) mr = std::max(mr, (double)std::fabs(r[i] - x[i]) / x[i]);
+            const bool ok = mr < 0.01;
+            std::printf("  bf16 precision (max rel err %.4f, expect <0.01): %s\n", mr, ok ? "PASS" : "FAIL");
+            ++total, pass += ok;
+        }
+    } catch (const Failure&) {
+        rt_error("bf16_selftest", "%s", dh_last_error());
+        return create_scalar(0.0);
+    }
+    {   // 3. convergence: bf16 compute with fp32 master weights trains y = 3x + 0.5
+        rng().seed(2);
+        std::uniform_real_distribution<float> d(0.1f, 10.0f);
+        const int N = 64;
+        std::vector<float> X(N), Y(N);
+        for (int i = 0; i < N; ++i) {
+            X[i] = d(rng());
+            Y[i] = 3.0f * X[i] + 0.5f;
+        }
+        auto train = [&](bool mixed) {
+            float w = 0, b = 0;
+            const float lr = 0.01f;
+            for (int ep = 0; ep < 200; ++ep) {
+                float gw = 0, gb = 0;
+                for (int i = 0; i < N; ++i) {
+                    const float xi = mixed ? host_bf16(X[i]) : X[i];
+                    const float wi = mixed ? host_bf16(w) : w, bi = mixed ? host_bf16(b) : b;
+                    const float pred = mixed ? host_bf16(wi * xi + bi) : wi * xi + bi;
+                    const float err = pred - Y[i];
+                    gw += err * xi;
+                    gb += err;
+                }
+                w -= lr * gw / N;
+                b -= lr * gb / N;
+            }
+            float loss = 0;
+            for (int i = 0; i < N; ++i) {
+                const float p = w * X[i] + b;
+                loss += (p - Y[i]) * (p - Y[i]);
+            }
+            return loss / N;
+        };
+        const float lf = train(false), lm = train(true);
+        const bool ok = lm < 0.01;
+        std::printf("  fp32 loss %.6f, mixed loss %.6f -> converges: %s\n", lf, lm, ok ? "PASS" : "FAIL");
+        ++total, pass += ok;
+    }
+    std::printf("  BF16_MIXED: %d/%d PASS\n", pass, total);
+    std::fflush(stdout);
+    return create_scalar(pass == total ? 1.0 : 0.0);
+}
+
 Tensor* dream_gpu_warmup(void) {
     const auto t0 = std::chrono::steady_clock::now();
     if (!dh_available()) {

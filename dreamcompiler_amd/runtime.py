@@ -32,6 +32,7 @@ _SIGS = {
     "dream_flash_attention": [TP] * 7, "dream_attention": [TP] * 6,
     "dream_attention_causal": [TP] * 6, "backward": [TP], "gpu_selftest": [],
     "dream_gpu_warmup": [], "flash_attention_selftest": [], "gemm_selftest": [],
+    "bf16_selftest": [],
     "dream_linear": [TP] * 3, "dream_linear_relu": [TP] * 3, "linear": [TP] * 3,
     "linear_relu": [TP] * 3, "dream_bmm": [TP] * 6, "dream_softmax": [TP],
     "dream_log_softmax": [TP], "dream_layer_norm": [TP], "tensor_set_element": [TP] * 3,

@@ -186,6 +186,10 @@ int dream_hip_available(void);
  * `@` (the GPU GEMM; the 6 short-K shapes with `as f32` operands) against the naive fp64
  * product under the GPU gate sqrt(K) 1e-4; prints "GEMM: 17/17 PASS" like the reference. */
 Tensor* gemm_selftest(void);
+/* bf16_selftest (runtime/nn/training.inc:1978-2025): bf16 range and precision through the
+ * device rounding (dh_convert), and the mixed-precision convergence check; prints
+ * "BF16_MIXED: 3/3 PASS" like the reference. */
+Tensor* bf16_selftest(void);
 Tensor* gpu_selftest(void);
 Tensor* dream_gpu_warmup(void);
 Tensor* flash_attention_selftest(void);

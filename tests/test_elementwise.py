@@ -87,3 +87,16 @@ def test_gpu_side_fails_loudly_without_a_device(capfd, monkeypatch):
     assert "RUNTIME ERROR in +: HIP backend unavailable" in capfd.readouterr().err
     assert c.contents.size == 1
     rt.release(a, c)
+
+
+def test_34_minmax_program():
+    # tests/34_minmax.dream: min(3, 5) = 3, max(3, 5) = 5 on scalars; max(ones, 2 ones) sends
+    # the whole gradient of sum(c) to the larger operand (gb = 4).
+    L = rt.load()
+    lo, hi = L.dream_minimum(rt.scalar(3.0), rt.scalar(5.0)), L.dream_maximum(rt.scalar(3.0), rt.scalar(5.0))
+    a = rt.tensor(np.ones((2, 2)))
+    b = L.tensor_add(rt.tensor(np.ones((2, 2))), rt.tensor(np.ones((2, 2))))
+    c = L.dream_maximum(a, b)
+    L.backward(L.sum(c))
+    assert rt.read(lo)[0, 0] == 3.0 and rt.read(hi)[0, 0] == 5.0
+    assert rt.read(b, grad=True).sum() == 4.0 and rt.read(a, grad=True).sum() == 0.0

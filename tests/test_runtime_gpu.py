@@ -126,6 +126,8 @@ def test_26_flash_backward_matches_standard(L):
 def test_15_18_25_selftests(L, capfd):
     assert rt.read(L.gemm_selftest())[0, 0] == 1.0
     assert "GEMM: 17/17 PASS" in capfd.readouterr().out   # tests/15_gemm.dream
+    assert rt.read(L.bf16_selftest())[0, 0] == 1.0
+    assert "BF16_MIXED: 3/3 PASS" in capfd.readouterr().out   # tests/30_bf16.dream
     assert rt.read(L.gpu_selftest())[0, 0] == 1.0
     assert rt.read(L.flash_attention_selftest())[0, 0] == 1.0
     assert rt.read(L.dream_gpu_warmup())[0, 0] > 0.0
