@@ -192,7 +192,7 @@ gemm_bf16_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
                     float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
                               (row_bias ? bias[row] : bv);
                     if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
-                    *c = v;
+                    __builtin_nontemporal_store(v, c);
                 }
             }
         }
@@ -743,7 +743,10 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     }
 
     // Register r of block (a, b) is C[32 a + 8 (r / 4) + 4 (lane / 32) + r % 4][32 b + lane % 32]
-    // (relative to the wave's tile): each store instruction writes two 128-byte row pieces.
+    // (relative to the wave's tile): each store instruction writes two 128-byte row pieces,
+    // non-temporally -- C is not read again here, and streaming it past the caches leaves them
+    // to the A / B panels (8192^3: +3.2%, measured A/B on one box; the flash kernels' narrower
+    // output pieces lost 8-9% the same way, so they store normally).
     // One uniform branch on the epilogue form keeps each form straight-line code.
     float* cw = C + (size_t)(m0 + wm + 4 * h) * ldc + n0 + wn + l32;
     auto at = [&](int a, int b, int r) {
@@ -755,7 +758,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 #pragma unroll
             for (int b = 0; b < FN; ++b)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) *at(a, b, r) = acc[a][b][r];
+                for (int r = 0; r < 16; ++r) __builtin_nontemporal_store(acc[a][b][r], at(a, b, r));
     } else {
         // C = acc + beta C + bias (by column, or by row with DH_EPI_ROW_BIAS), then max(., 0)
         // with DH_EPI_RELU (NaN passes).
@@ -775,7 +778,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
                     float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
                               (row_bias ? brow[32 * a + 8 * (r >> 2) + (r & 3)] : bv[b]);
                     if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
-                    *c = v;
+                    __builtin_nontemporal_store(v, c);
                 }
     }
 }
