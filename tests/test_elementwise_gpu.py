@@ -187,6 +187,11 @@ def test_binary_rejects_out_of_bounds_strides_and_bad_args():
         with pytest.raises(hip.DreamHipError, match="C32"):
             hip.binary("add", hip.F32, A, 12, [0, 1, 0, 0], A, 12, [0, 1, 0, 0], C, [1, 12, 1, 1],
                        C)
+        with pytest.raises(hip.DreamHipError, match="limit 2"):   # 2^31 outputs, host-side check
+            hip.binary("add", hip.F64, A, 12, [0, 0, 0, 0], A, 12, [0, 0, 0, 0], C,
+                       [1 << 16, 1 << 15, 1, 1])
+        with pytest.raises(hip.DreamHipError, match="negative"):
+            hip.binary("add", hip.F64, A, 12, [0, -1, 0, 0], A, 12, [0, 1, 0, 0], C, [1, 12, 1, 1])
         with pytest.raises(hip.DreamHipError, match="aligned"):
             hip.unary("exp", hip.F64, A.ptr + 8, C, 4)
         with pytest.raises(hip.DreamHipError, match="unknown op"):
