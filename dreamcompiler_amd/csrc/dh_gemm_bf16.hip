@@ -786,10 +786,15 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 template <bool TA, bool TB>
 int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
                 float beta, float* C, int ldc, const Batch& bt) {
-    static const int waves = [] {
+    // Default: 8 waves (two per SIMD) for NN, 4 (one per SIMD) for the other layouts -- with
+    // the non-temporal epilogue, NN at 8192^3 ran 1301-1305 TFLOP/s on 8 waves against
+    // 1283-1289 on 4 on one box and equal on another (same-box A/Bs), while NT / TN / TT stay
+    // faster on 4.
+    static const int env_waves = [] {
         const char* e = std::getenv("DH_GEMM_BF16_WAVES");   // tuning knob: 4 or 8
-        return (e && std::atoi(e) == 8) ? 8 : 4;
+        return e ? (std::atoi(e) == 8 ? 8 : 4) : 0;
     }();
+    const int waves = env_waves ? env_waves : (!TA && !TB ? 8 : 4);
     auto kern = waves == 4 ? gemm_bf16_fast_kernel<TA, TB, 4> : gemm_bf16_fast_kernel<TA, TB, 8>;
     for (int b0 = 0; b0 < bt.count; b0 += 65535) {   // gridDim.y = batch member
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
