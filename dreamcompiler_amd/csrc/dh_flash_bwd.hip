@@ -486,21 +486,28 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
                 sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[t], sc[kb], 0, 0, 0);
                 dp[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, gf[t], dp[kb], 0, 0, 0);
             }
-        // dS^T[key][i]; keys after the query (causal) or past S are dropped
-        const bool msk = j0 + DQ_BN - 1 > (CAUSAL ? r0 : S - 1);   // wave-uniform
-        const int rel = lim - j0 - 4 * h;
-        uint32_t pd[16];
+        // P in place of the scores; on the diagonal or tail stages (wave-uniform) keys after
+        // the query (causal) or past S are dropped.  The empty volatile asm keeps the mask a
+        // real branch: the compiler otherwise if-converted its 32 compares and selects into
+        // every stage (96 of ~250 VALU instructions of a stage).
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sc[kb][r] = fast_exp2(__builtin_fmaf(sc[kb][r], sl2, -lse2));
+        if (j0 + DQ_BN - 1 > (CAUSAL ? r0 : S - 1)) {
+            asm volatile("" ::: "memory");
+            const int rel = lim - j0 - 4 * h;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) sc[kb][r] = 0.f;
+        }
+        uint32_t pd[16];   // dS^T[key][i] as bf16 pairs
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
             const int kb = q >> 3, r = 2 * (q & 7);
-            float p0 = fast_exp2(__builtin_fmaf(sc[kb][r], sl2, -lse2));
-            float p1 = fast_exp2(__builtin_fmaf(sc[kb][r + 1], sl2, -lse2));
-            if (msk) {
-                const int o = 32 * kb + 8 * (r >> 2) + (r & 3);
-                if (o > rel) p0 = 0.f;
-                if (o + 1 > rel) p1 = 0.f;
-            }
-            pd[q] = cvt_pk_bf16(p0 * (dp[kb][r] - dvi), p1 * (dp[kb][r + 1] - dvi));
+            pd[q] = cvt_pk_bf16(sc[kb][r] * (dp[kb][r] - dvi), sc[kb][r + 1] * (dp[kb][r + 1] - dvi));
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
