@@ -109,8 +109,11 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     B += blockIdx.y * sB;
     C += blockIdx.y * sC;
     constexpr int LDS_A = TBM + 4, LDS_B = TBN + 4;   // padded k-major row strides (floats)
-    constexpr int WN = TBN / 64;                        // waves along N
-    static_assert((TBM / 64) * WN == 4, "4 waves of 64 x 64");
+    // Wave sub-tile WT x WT: 64 (2 x 2 MFMA blocks) for the 128 x 128 / 64 x 256 / 256 x 64
+    // tiles, 32 (one block) for 64 x 64 tiles.
+    constexpr int WT = TBM == 64 && TBN == 64 ? 32 : 64, NB = WT / 32;
+    constexpr int WN = TBN / WT;                        // waves along N
+    static_assert((TBM / WT) * WN == 4, "4 waves");
     __shared__ __attribute__((aligned(16))) float As[2][BK * LDS_A];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDS_B];
 
@@ -121,7 +124,7 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
-    const int wm = (wave / WN) * 64, wn = (wave % WN) * 64;
+    const int wm = (wave / WN) * WT, wn = (wave % WN) * WT;
 
     // A: op(A)[i][k]; stored [i][k] when !TA (k contiguous), [k][i] when TA.
     // B: op(B)[k][j]; stored [k][j] when !TB (j contiguous), [j][k] when TB.
@@ -131,11 +134,11 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     Slice<!TA, VA, TBM> sa[2];
     Slice<TB, VB, TBN> sb[2];
 
-    f32x16 acc[2][2];
+    f32x16 acc[NB][NB];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < NB; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
@@ -156,14 +159,17 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     auto mma = [&](const float* as, const float* bs) {   // one k-slice from LDS
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
-            float a0 = as[(kk + h) * LDS_A + wm + l32];
-            float a1 = as[(kk + h) * LDS_A + wm + 32 + l32];
-            float b0 = bs[(kk + h) * LDS_B + wn + l32];
-            float b1 = bs[(kk + h) * LDS_B + wn + 32 + l32];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+            float av[NB], bv[NB];
+#pragma unroll
+            for (int x = 0; x < NB; ++x) {
+                av[x] = as[(kk + h) * LDS_A + wm + 32 * x + l32];
+                bv[x] = bs[(kk + h) * LDS_B + wn + 32 * x + l32];
+            }
+#pragma unroll
+            for (int a = 0; a < NB; ++a)
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
     };
     // One k-slice of the loop; the register set index is a template constant (a runtime
@@ -193,9 +199,9 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     // with DH_EPI_RELU (NaN passes, like `y < 0 ? 0 : y`).
     const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS), relu = epi & DH_EPI_RELU;
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < NB; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < NB; ++b) {
             const int col = n0 + wn + 32 * b + l32;
             if (col >= N) continue;
             const float bv = bias && !row_bias ? bias[col] : 0.f;
@@ -477,16 +483,29 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
     return DH_OK;
 }
 
-// Tile shape: 64 x 256 when M <= 64 (a 128-row tile would be at least half empty -- conv's
+// Tile shape.  64 x 256 when M <= 64 (a 128-row tile would be at least half empty -- conv's
 // kernel @ im2col with few output channels, the bias gradient shapes), 256 x 64 when N <= 64,
-// else 128 x 128.
+// else 128 x 128; but 64 x 64 tiles (one 32 x 32 block per wave, 8 waves per SIMD fit) when
+// the larger tiles leave the chip mostly idle: a 128 x 128 grid of less than one tile per CU
+// that 64 x 64 tiles take past half the CUs, or a narrow grid of at most a quarter of the CUs
+// that 64 x 64 tiles at least double.  Measured (config 1 and config 2's layer products):
+// fp32 1024^3 43.2 -> 30.7 us; 4096 x 257 x 784 67 -> 41 us; 4096 x 784 x 257 48 -> 42 us;
+// 4096 x 10 x 257 43 -> 15 us; 257 x 10 x 4096 31 -> 18 us.
 template <bool TA, bool TB>
 int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
            float* C, int ldc, const Batch& bt) {
-    if (M <= 64 && N > 64)
-        return launch_tiles<TA, TB, 64, 256>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
-    if (N <= 64 && M > 64)
+    const int cus = num_cus();
+    const long long t64 = (long long)((M + 63) / 64) * ((N + 63) / 64) * bt.count;
+    if ((M <= 64 && N > 64) || (N <= 64 && M > 64)) {
+        const long long tn = (long long)((M <= 64 ? N : M) + 255) / 256 * bt.count;
+        if (4 * tn <= cus && 2 * tn < t64)
+            return launch_tiles<TA, TB, 64, 64>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+        if (M <= 64) return launch_tiles<TA, TB, 64, 256>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
         return launch_tiles<TA, TB, 256, 64>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    }
+    const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * bt.count;
+    if (t128 < cus && 2 * t64 > cus)
+        return launch_tiles<TA, TB, 64, 64>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
     return launch_tiles<TA, TB, 128, 128>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 

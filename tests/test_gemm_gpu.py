@@ -365,12 +365,25 @@ def test_fp32_split_k_bit_identical_reruns():
 
 
 @pytest.mark.parametrize("Bt,M,N,K", [(3, 40, 300, 70), (2, 300, 50, 129), (1, 64, 4096, 576),
-                                      (1, 4096, 10, 784), (4, 1, 513, 33)])
+                                      (1, 4096, 10, 784), (4, 1, 513, 33), (1, 64, 40000, 40),
+                                      (1, 40000, 48, 40)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("row_bias", [False, True])
 def test_fp32_narrow_tiles(Bt, M, N, K, ta, tb, row_bias):
-    # M <= 64 takes 64 x 256 work-group tiles, N <= 64 256 x 64 (batched, split-K and the
-    # epilogue with either bias orientation go through the same shapes).
+    # M <= 64 takes 64 x 256 work-group tiles, N <= 64 256 x 64 -- or 64 x 64 when those grids
+    # are small (the first five shapes); the last two keep the wide tiles.  Batched, split-K
+    # and the epilogue with either bias orientation go through the same shapes.
     got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.25, relu=row_bias, row_bias=row_bias,
                    seed=M + N + K + ta + 2 * tb)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+@pytest.mark.parametrize("Bt,M,N,K", [(1, 1024, 1024, 1024), (1, 1000, 777, 100), (2, 520, 700, 33),
+                                      (1, 4096, 257, 784), (1, 700, 900, 7)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_fp32_64x64_tiles(Bt, M, N, K, ta, tb):
+    # Products whose 128 x 128 grid is under one tile per CU run on 64 x 64 tiles (one 32 x 32
+    # MFMA block per wave): config 1, ragged edges, batched, config 2's first layer, a single
+    # k-slice (K = 7); beta and a per-column bias with ReLU through the epilogue.
+    got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.5, relu=True, seed=M + N + K + ta + 2 * tb)
     assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
