@@ -73,12 +73,13 @@ def test_im2col_col2im_permute(shape):
 
 
 @pytest.mark.parametrize("shape", [
-    (2, 3, 7, 6, 4, 3, 2, 0, 1),        # golden-vector geometry, Cout <= 64 (64 x 256 tiles)
+    (2, 3, 7, 6, 4, 3, 2, 0, 1),        # golden-vector geometry, Cout <= 64 (64 x 64 tiles)
     (3, 5, 9, 8, 70, 3, 3, 1, 2),       # Cout > 64: 128 x 128 tiles, padded and strided
     (1, 2, 5, 5, 1, 5, 5, 2, 1),        # window as large as the padded input, one channel out
     (2, 16, 23, 17, 33, 3, 1, 1, 1),    # ragged positions, a K = 48 contraction
     (4, 7, 15, 15, 65, 1, 1, 0, 1),     # 1x1 kernel: R = Cin = 7 (a single k-slice)
     (2, 64, 20, 20, 64, 3, 3, 1, 1),    # R = 576, as in the ResNet-like bench layer
+    (8, 16, 30, 30, 96, 3, 3, 1, 1),    # Cout > 64 on a small grid: 64 x 64 tiles
 ])
 def test_conv2d_fwd_implicit_gemm_against_oracle(shape):
     # dh_conv2d_fwd against the fp64 oracle (orc_conv2d, pinned by the reference's golden
