@@ -241,34 +241,77 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
         __builtin_amdgcn_s_barrier();
         if (sp + 1 < nsteps) issue_step(sp + 1);     // into the slots of step sp - 1
     };
+    // One stage, one MFMA per chunk, chunks fenced by sched_barrier(0) and operands read
+    // one chunk ahead:
+    //   S = Q K^T (NTK MFMAs);
+    //   dP = dO V^T (NTK MFMAs), each chunk also exponentiating 16 / NTK scores of S, so
+    //     the exponentials run while the matrix cores work;
+    //   the mask (a branch, taken on diagonal and tail stages only);
+    //   dS = P o (dP - Dvec) and the bf16 packing of P, dS for k-step 0;
+    //   dV^T += dO^T P, dK^T += Q^T dS for k-step 0 (2 ND MFMAs), the chunks also packing
+    //     k-step 1; then the same MFMAs for k-step 1.
+    // k-step kk pairs queries 16 kk + 4 h + (0..3) and + 8: score registers 8 kk .. + 7.
     auto compute = [&](int st) {
         const uint8_t* qt = ring + (st % KV_NSTAGE) * STAGE;
         const uint8_t* gt = qt + T::TILE;
         const float* vec = reinterpret_cast<const float*>(qt + VEC);
         const int i0 = qstart + st * KV_BQ;
+        constexpr int EPC = 16 / NTK;                // exponentials per dP chunk
+        constexpr int NP = 2 * ND;                   // dV, dK MFMAs per k-step
+        auto rowf = [&](const uint8_t* tile, int t) {
+            return *reinterpret_cast<const bf16x8*>(tile + rofs[t]);
+        };
+        auto keyf = [&](int t, int v) {
+            return *reinterpret_cast<const bf16x8*>(ring + kofs[t] + v * R::TILE);
+        };
+        // transposed operand of P2 slot s of k-step kk: dO^T (even s) or Q^T (odd s), d = s / 2
+        auto trf = [&](int kk, int s) {
+            return tr_operand((s & 1 ? qt : gt) + 16 * kk * T::ROWB, tofs0[s >> 1], tofs1[s >> 1]);
+        };
         f32x16 sc, dp;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
+        f32x4 l4[4], d4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) l4[q] = *reinterpret_cast<const f32x4*>(vec + 8 * q + 4 * h);
+        // operands of S/dP MFMA i (i < NTK: S, else dP), read two chunks ahead
+        auto opa = [&](int i) { return rowf(i < NTK ? qt : gt, i % NTK); };
+        auto opb = [&](int i) { return keyf(i % NTK, i < NTK ? 0 : 1); };
+        bf16x8 fa[2] = {opa(0), opa(1)}, fb[2] = {opb(0), opb(1)};
 #pragma unroll
         for (int t = 0; t < NTK; ++t) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(qt + rofs[t]);
-            const bf16x8 g = *reinterpret_cast<const bf16x8*>(gt + rofs[t]);
-            const bf16x8 kb = *reinterpret_cast<const bf16x8*>(ring + kofs[t]);
-            const bf16x8 vb = *reinterpret_cast<const bf16x8*>(ring + kofs[t] + R::TILE);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kb, sc, 0, 0, 0);
-            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(g, vb, dp, 0, 0, 0);
+            const bf16x8 a = fa[t & 1], b = fb[t & 1];
+            fa[t & 1] = opa(t + 2);
+            fb[t & 1] = opb(t + 2);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, sc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // Phase fences keep the scheduler from hoisting every fragment read of the stage.
-        __builtin_amdgcn_sched_barrier(0);
-        // P; queries past S and (causal) keys after the query are dropped.  Register r
-        // holds query i0 + 4 h + o(r), o(r) = 8 (r / 4) + r % 4.
         float p[16];
+        bf16x8 ta[2];                                // P2 operands, two MFMAs ahead
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 l4 = *reinterpret_cast<const f32x4*>(vec + 8 * q + 4 * h);
+        for (int t = 0; t < NTK; ++t) {
+            const bf16x8 a = fa[t & 1], b = fb[t & 1];
+            if (t + 2 < NTK) {
+                fa[t & 1] = opa(NTK + t + 2);
+                fb[t & 1] = opb(NTK + t + 2);
+            }
+            if (t + 1 == NTK) {
+                ta[0] = trf(0, 0);
+                ta[1] = trf(0, 1);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) p[4 * q + e] = fast_exp2(__builtin_fmaf(sc[4 * q + e], sl2, -l4[e]));
+                for (int q = 0; q < 4; ++q)
+                    d4[q] = *reinterpret_cast<const f32x4*>(vec + 256 + 8 * q + 4 * h);
+            }
+            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, dp, 0, 0, 0);
+#pragma unroll
+            for (int e = EPC * t; e < EPC * (t + 1); ++e) {
+                p[e] = fast_exp2(__builtin_fmaf(sc[e], sl2, -l4[e >> 2][e & 3]));
+                asm volatile("" : "+v"(p[e]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+        // Queries past S and (causal) keys after the query are dropped.  Register r holds
+        // query i0 + 4 h + o(r), o(r) = 8 (r / 4) + r % 4.
         if (i0 + KV_BQ > S || (CAUSAL && i0 < k0 + 31)) {   // wave-uniform: tail or diagonal
             const int lo = CAUSAL ? j - i0 - 4 * h : -KV_BQ;   // keep o >= lo (key <= query)
             const int hi = S - i0 - 4 * h;                      // keep o < hi (query < S)
@@ -278,31 +321,35 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
                 if (o < lo || o >= hi) p[r] = 0.f;
             }
         }
-        // dS = P o (dP - Dvec), both packed to bf16 pairs
+        // unit u: P and dS of registers 2u, 2u + 1 packed to bf16 pairs
         uint32_t pk[8], pd[8];
+        auto pack = [&](int u) {
+            const int r = 2 * u;
+            const float ds0 = p[r] * (dp[r] - d4[r >> 2][r & 3]);
+            const float ds1 = p[r + 1] * (dp[r + 1] - d4[r >> 2][(r + 1) & 3]);
+            pk[u] = cvt_pk_bf16(p[r], p[r + 1]);
+            pd[u] = cvt_pk_bf16(ds0, ds1);
+            asm volatile("" : "+v"(pk[u]), "+v"(pd[u]));
+        };
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 d4 = *reinterpret_cast<const f32x4*>(vec + 256 + 8 * q + 4 * h);
-            float ds[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ds[e] = p[4 * q + e] * (dp[4 * q + e] - d4[e]);
-            pk[2 * q] = cvt_pk_bf16(p[4 * q], p[4 * q + 1]);
-            pk[2 * q + 1] = cvt_pk_bf16(p[4 * q + 2], p[4 * q + 3]);
-            pd[2 * q] = cvt_pk_bf16(ds[0], ds[1]);
-            pd[2 * q + 1] = cvt_pk_bf16(ds[2], ds[3]);
-        }
-        // k-step kk pairs queries 16 kk + 4 h + (0..3) and + 8: score registers 8 kk .. + 7
+        for (int u = 0; u < 4; ++u) pack(u);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            __builtin_amdgcn_sched_barrier(0);
             const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]});
             const bf16x8 sf = __builtin_bit_cast(bf16x8, u32x4{pd[4 * kk], pd[4 * kk + 1], pd[4 * kk + 2], pd[4 * kk + 3]});
-            const uint8_t* gk = gt + 16 * kk * T::ROWB;
-            const uint8_t* qk = qt + 16 * kk * T::ROWB;
 #pragma unroll
-            for (int d = 0; d < ND; ++d) {
-                dvacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_operand(gk, tofs0[d], tofs1[d]), pf, dvacc[d], 0, 0, 0);
-                dkacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_operand(qk, tofs0[d], tofs1[d]), sf, dkacc[d], 0, 0, 0);
+            for (int sl = 0; sl < NP; ++sl) {
+                const int g = kk * NP + sl;
+                const bf16x8 a = ta[g & 1];
+                if (g + 2 < 2 * NP) ta[g & 1] = trf((g + 2) / NP, (g + 2) % NP);
+                if (sl & 1) dkacc[sl >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, sf, dkacc[sl >> 1], 0, 0, 0);
+                else dvacc[sl >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf, dvacc[sl >> 1], 0, 0, 0);
+                if (kk == 0) {
+#pragma unroll
+                    for (int u = 4 + 4 * sl / NP; u < 4 + 4 * (sl + 1) / NP; ++u) pack(u);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     };
