@@ -516,31 +516,52 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
         if (st + DQ_NSTAGE - 1 < nst) issue(st + DQ_NSTAGE - 1);
         if (st >= wlast) continue;
 
+        // One MFMA per chunk, chunks fenced by sched_barrier(0), operands read two chunks
+        // ahead: S^T (2 NTK MFMAs, two chains), dP^T (2 NTK MFMAs) with two exponentials of
+        // P per chunk, the mask, dS^T of group 0, then dQ^T += K^T dS^T by groups g =
+        // (key block kb, k-step kk) of ND MFMAs, each chunk also packing part of group g + 1.
         const uint8_t* kt = ring + (st % DQ_NSTAGE) * STAGE;
         const uint8_t* vt = kt + T::TILE;
         const int j0 = st * DQ_BN;
+        constexpr int NSD = 2 * NTK;                 // S^T (and dP^T) MFMAs per stage
+        constexpr int NOP = 2 * NSD + 4 * ND;        // MFMAs per stage
+        auto opnd = [&](int c) -> bf16x8 {          // A operand of MFMA c
+            if (c < 2 * NSD) {
+                const int t = (c % NSD) >> 1, kb = c & 1;
+                return *reinterpret_cast<const bf16x8*>((c < NSD ? kt + kofs[t] : vt + vofs[t]) + 32 * kb * T::ROWB);
+            }
+            const int g = (c - 2 * NSD) / ND, d = (c - 2 * NSD) % ND;
+            return tr_operand(kt + (32 * (g >> 1) + 16 * (g & 1)) * T::ROWB, tofs0[d], tofs1[d]);
+        };
         f32x16 sc[2], dp[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sc[kb][r] = dp[kb][r] = 0.f;
+        bf16x8 fa[2] = {opnd(0), opnd(1)};
 #pragma unroll
-        for (int t = 0; t < NTK; ++t)
+        for (int c = 0; c < NSD; ++c) {
+            const bf16x8 a = fa[c & 1];
+            fa[c & 1] = opnd(c + 2);
+            sc[c & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c >> 1], sc[c & 1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float p[2][16];                              // P in the score layout
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + kofs[t] + 32 * kb * T::ROWB);
-                const bf16x8 v = *reinterpret_cast<const bf16x8*>(vt + vofs[t] + 32 * kb * T::ROWB);
-                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[t], sc[kb], 0, 0, 0);
-                dp[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, gf[t], dp[kb], 0, 0, 0);
+        for (int c = 0; c < NSD; ++c) {
+            const bf16x8 a = fa[c & 1];
+            fa[c & 1] = opnd(NSD + c + 2);
+            dp[c & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, gf[c >> 1], dp[c & 1], 0, 0, 0);
+#pragma unroll
+            for (int e = 32 * c / NSD; e < 32 * (c + 1) / NSD; ++e) {
+                p[e >> 4][e & 15] = fast_exp2(__builtin_fmaf(sc[e >> 4][e & 15], sl2, -lse2));
+                asm volatile("" : "+v"(p[e >> 4][e & 15]));
             }
-        // P in place of the scores; on the diagonal or tail stages (wave-uniform) keys after
-        // the query (causal) or past S are dropped.  The empty volatile asm keeps the mask a
-        // real branch: the compiler otherwise if-converted its 32 compares and selects into
-        // every stage (96 of ~250 VALU instructions of a stage).
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) sc[kb][r] = fast_exp2(__builtin_fmaf(sc[kb][r], sl2, -lse2));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // On the diagonal or tail stages (wave-uniform) keys after the query (causal) or past
+        // S are dropped.  The empty volatile asm keeps the mask a real branch: the compiler
+        // otherwise if-converts its 32 compares and selects into every stage.
         if (j0 + DQ_BN - 1 > (CAUSAL ? r0 : S - 1)) {
             asm volatile("" ::: "memory");
             const int rel = lim - j0 - 4 * h;
@@ -548,25 +569,30 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) sc[kb][r] = 0.f;
+                    if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) p[kb][r] = 0.f;
         }
-        uint32_t pd[16];   // dS^T[key][i] as bf16 pairs
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
+        uint32_t pd[16];   // dS^T[key][i] as bf16 pairs; pd[4 g + u] belongs to group g
+        auto pack = [&](int q) {
             const int kb = q >> 3, r = 2 * (q & 7);
-            pd[q] = cvt_pk_bf16(sc[kb][r] * (dp[kb][r] - dvi), sc[kb][r + 1] * (dp[kb][r + 1] - dvi));
-        }
+            pd[q] = cvt_pk_bf16(p[kb][r] * (dp[kb][r] - dvi), p[kb][r + 1] * (dp[kb][r + 1] - dvi));
+            asm volatile("" : "+v"(pd[q]));
+        };
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int u = 0; u < 4; ++u) pack(u);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int q0p = 8 * kb + 4 * kk;
-                const bf16x8 sf = __builtin_bit_cast(bf16x8, u32x4{pd[q0p], pd[q0p + 1], pd[q0p + 2], pd[q0p + 3]});
-                const uint8_t* kk_ = kt + (32 * kb + 16 * kk) * T::ROWB;
+        for (int c = 2 * NSD; c < NOP; ++c) {
+            const int g = (c - 2 * NSD) / ND, d = (c - 2 * NSD) % ND;
+            const bf16x8 a = fa[c & 1];
+            if (c + 2 < NOP) fa[c & 1] = opnd(c + 2);
+            const bf16x8 sf = __builtin_bit_cast(bf16x8, u32x4{pd[4 * g], pd[4 * g + 1], pd[4 * g + 2], pd[4 * g + 3]});
+            dqacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, sf, dqacc[d], 0, 0, 0);
+            if (g < 3) {
 #pragma unroll
-                for (int d = 0; d < ND; ++d)
-                    dqacc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_operand(kk_, tofs0[d], tofs1[d]), sf, dqacc[d], 0, 0, 0);
+                for (int u = 4 * d / ND; u < 4 * (d + 1) / ND; ++u) pack(4 * (g + 1) + u);
             }
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     if (i >= S) return;
     float* dqr = dQ + base + (size_t)i * D;
