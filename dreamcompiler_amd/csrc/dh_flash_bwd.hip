@@ -31,33 +31,64 @@ __device__ inline uint32_t cvt_pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));   // RNE
 }
 
-template <typename T> __device__ inline float to_f(T x);
-template <> __device__ inline float to_f<float>(float x) { return x; }
-template <> __device__ inline float to_f<uint16_t>(uint16_t x) { return bf16_bits_to_f32(x); }
+// ---------------------------------------------------------------------------------
+// 1. Dvec = rowsum(dO * O).  16 lanes per row, each reading its D / 16 consecutive
+//    elements of O and of dO as one vector (4 to 32 bytes; the entry point requires
+//    16-byte aligned tensors and D is a multiple of 32); work-groups stride over the
+//    16-row groups so that a large BH * S does not launch one tiny work-group per group.
+// ---------------------------------------------------------------------------------
+template <int NDW>
+__device__ inline void load_dw(const uint32_t* __restrict__ p, uint32_t (&w)[NDW]) {
+    if constexpr (NDW % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < NDW / 4; ++q) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(p + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[4 * q + e] = v[e];
+        }
+    } else if constexpr (NDW == 2) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+        w[0] = v[0];
+        w[1] = v[1];
+    } else {
+        w[0] = *p;
+    }
+}
 
-// ---------------------------------------------------------------------------------
-// 1. Dvec = rowsum(dO * O), 16 lanes per row, 8 elements per lane per step.
-// ---------------------------------------------------------------------------------
 template <typename T, int D>
 __global__ void __launch_bounds__(NT)
 dvec_kernel(int rows, const T* __restrict__ O, const T* __restrict__ dO, float* __restrict__ Dv,
             const float* __restrict__ LSE, float* __restrict__ L2) {
-    const int row = blockIdx.x * (NT / 16) + (threadIdx.x >> 4);
+    constexpr int NDW = D * (int)sizeof(T) / 4 / 16;   // dwords per lane
+    static_assert(NDW == 1 || NDW == 2 || NDW % 4 == 0, "lane chunk of 4, 8 or 16n bytes");
     const int sub = threadIdx.x & 15;
-    float acc = 0.f;
-    if (row < rows) {
-        const T* o = O + (size_t)row * D;
-        const T* g = dO + (size_t)row * D;
-        for (int d = sub; d < D; d += 16) acc += to_f<T>(o[d]) * to_f<T>(g[d]);
-    }
-    // reduce over the 16 lanes of a DPP row
-    acc += dpp_quad_xor1(acc);
-    acc += dpp_quad_xor2(acc);
-    acc += dpp_half_mirror(acc);
-    acc += dpp_row_mirror(acc);
-    if (row < rows && sub == 0) {
-        Dv[row] = acc;
-        if (L2) L2[row] = LSE[row] * 1.4426950408889634f;   // log2-domain LSE (bf16 kernels)
+    // row0 depends on the work-group only: every lane runs every iteration (DPP below)
+    for (int row0 = blockIdx.x * (NT / 16); row0 < rows; row0 += gridDim.x * (NT / 16)) {
+        const int row = row0 + (threadIdx.x >> 4);
+        float acc = 0.f;
+        if (row < rows) {
+            uint32_t a[NDW], b[NDW];
+            load_dw<NDW>(reinterpret_cast<const uint32_t*>(O + (size_t)row * D) + NDW * sub, a);
+            load_dw<NDW>(reinterpret_cast<const uint32_t*>(dO + (size_t)row * D) + NDW * sub, b);
+#pragma unroll
+            for (int q = 0; q < NDW; ++q) {
+                if constexpr (sizeof(T) == 2) {   // two bf16 per dword
+                    acc += __uint_as_float(a[q] << 16) * __uint_as_float(b[q] << 16);
+                    acc += __uint_as_float(a[q] & 0xffff0000u) * __uint_as_float(b[q] & 0xffff0000u);
+                } else {
+                    acc += __uint_as_float(a[q]) * __uint_as_float(b[q]);
+                }
+            }
+        }
+        // reduce over the 16 lanes of a DPP row
+        acc += dpp_quad_xor1(acc);
+        acc += dpp_quad_xor2(acc);
+        acc += dpp_half_mirror(acc);
+        acc += dpp_row_mirror(acc);
+        if (row < rows && sub == 0) {
+            Dv[row] = acc;
+            if (L2) L2[row] = LSE[row] * 1.4426950408889634f;   // log2-domain LSE (bf16 kernels)
+        }
     }
 }
 
@@ -947,8 +978,10 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
 
 template <typename T, int D>
 int run_dvec(int rows, const void* O, const void* dO, float* Dv, const float* LSE, float* L2) {
-    dvec_kernel<T, D><<<(rows + 15) / 16, NT, 0, stream()>>>(rows, (const T*)O, (const T*)dO, Dv,
-                                                             LSE, L2);
+    // eight work-groups (32 waves) per CU, each striding over 16-row groups
+    const int groups = (rows + NT / 16 - 1) / (NT / 16);
+    const int grid = groups < 8 * num_cus() ? groups : 8 * num_cus();
+    dvec_kernel<T, D><<<grid, NT, 0, stream()>>>(rows, (const T*)O, (const T*)dO, Dv, LSE, L2);
     return check_launch("dh_flash_bwd(Dvec)");
 }
 
