@@ -192,6 +192,33 @@ def conv_workload(N, Cin, H, W, Cout, KH, KW, pad, stride, seed=9):
     return step, flops, 4.0 * (N * Cin * H * W + Cout * K + Cout + N * Cout * P), [X, Kn, b, Y]
 
 
+def conv_bwd_workload(N, Cin, H, W, Cout, KH, KW, pad, stride, seed=10):
+    """dream_conv2d's backward as the runtime issues it (autograd.inc:507-535 over all images
+    at once): the upstream gradient made channel-first, the im2col matrix, gK += go' col^T (one
+    NT GEMM, contraction N*OH*OW), and gX += col2im(K^T go') as one implicit-GEMM convolution of
+    go with the flipped kernel (dh_conv2d_bwd_data, stride 1).  FLOPs: the two products;
+    algorithmic bytes: go, X, K read, gK and gX read and written once (no col)."""
+    rng = np.random.default_rng(seed)
+    OH, OW = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    K, P = Cin * KH * KW, OH * OW
+    NP = N * P
+    X = DB.from_numpy(rng.standard_normal((N, Cin * H * W), dtype=np.float32))
+    Kn = DB.from_numpy((rng.standard_normal((Cout, K)) * 0.05).astype(np.float32))
+    go = DB.from_numpy(rng.standard_normal((N, Cout * P), dtype=np.float32))
+    gop, col = DB.empty((Cout, NP), np.float32), DB.empty((K, NP), np.float32)
+    gK, gX = DB.from_numpy(np.zeros((Cout, K), np.float32)), \
+        DB.from_numpy(np.zeros((N, Cin * H * W), np.float32))
+
+    def step():
+        hip.nct_to_cnt(go, gop, N, Cout, P)
+        hip.im2col(X, col, N, Cin, H, W, KH, KW, pad, stride)
+        hip.gemm_f32(0, 1, Cout, K, NP, gop, NP, col, NP, 1.0, gK, K)
+        hip.conv2d_bwd_data(go, Kn, gX, N, Cin, H, W, Cout, KH, KW, pad, stride, accumulate=True)
+    flops = 4.0 * Cout * K * NP
+    alg = 4.0 * (N * Cout * P + N * Cin * H * W + Cout * K) + 8.0 * (Cout * K + N * Cin * H * W)
+    return step, flops, alg, [X, Kn, go, gop, col, gK, gX]
+
+
 WORKLOADS = {
     # name: (builder, kwargs, precision for the peak, description)
     "gemm_bf16_8192": (gemm_workload, dict(dtype="bf16", M=8192, N=8192, K=8192), "bf16",
@@ -214,6 +241,10 @@ WORKLOADS = {
     "conv2d_resnet_64x56x56": (conv_workload, dict(N=64, Cin=64, H=56, W=56, Cout=64, KH=3, KW=3,
                                                    pad=1, stride=1), "fp32",
                                "conv2d 64 x 64ch 56x56, 64 out ch, 3x3 pad 1 (implicit GEMM), fp32"),
+    "conv2d_bwd_resnet_64x56x56": (conv_bwd_workload, dict(N=64, Cin=64, H=56, W=56, Cout=64, KH=3,
+                                                           KW=3, pad=1, stride=1), "fp32",
+                                   "conv2d backward, same layer: im2col + NT GEMM (gK) + "
+                                   "implicit-GEMM data gradient, fp32"),
     "softmax_fwd_16384x1024": (rows_workload, dict(op="softmax_fwd", R=16384, C=1024), "hbm",
                                "row softmax 16384 x 1024 fp32 (HBM-bound)"),
     "softmax_bwd_16384x1024": (rows_workload, dict(op="softmax_bwd", R=16384, C=1024), "hbm",
@@ -460,6 +491,12 @@ def cpu_baseline_workloads(gpu_ms):
     record("conv2d_resnet_64x56x56",
            timed(lambda: L.tensor_decref(L.dream_conv2d_padded(xc, kc, bcc, *scc))), 64 / ni,
            f"{ni} of 64 images, fp64, scaled by 64/{ni}")
+    # its backward: backward(Y) on the conv output runs the conv branch only (autograd.inc:507-535)
+    yc = L.dream_conv2d_padded(xc, kc, bcc, *scc)
+    t0 = time.perf_counter()
+    L.backward(yc)
+    record("conv2d_bwd_resnet_64x56x56", (time.perf_counter() - t0) * 1000.0, 64 / ni,
+           f"{ni} of 64 images, fp64, backward(Y) of the conv, scaled by 64/{ni}")
     # config 3 flash forward (fp64, single-threaded) on the whole config
     Q3, K3, V3 = (rng.standard_normal((24, 256 * 64)) * 0.5 for _ in range(3))
     record("flash_fwd_c3", timed(lambda: R.attention("flash", Q3, K3, V3, 24, 256, 64, 64)), 1,

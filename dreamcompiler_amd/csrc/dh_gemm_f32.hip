@@ -223,8 +223,10 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
 // Y[n][co][p] = sum_r Kn[co][r] col_n[r][p] + bias[co] with col_n[r][p] = X[n][ci][h][w],
 // r = (ci KH + kh) KW + kw, p = oh OW + ow, h = oh stride + kh - pad, w = ow stride + kw - pad
 // (zero outside the input): the im2col matrix is gathered by the B loader and never stored.
+// Rows and columns have their own padding (the data gradient pads by KH - 1 - pad and
+// KW - 1 - pad).
 struct ConvGeom {
-    int Cin, H, W, KH, KW, pad, stride, OH, OW;
+    int Cin, H, W, KH, KW, padh, padw, stride, OH, OW;
     FastDiv f_ow, f_kw, f_khkw;   // division by OW, KW and KH*KW
 };
 
@@ -246,8 +248,8 @@ struct ConvSlice {
         for (int e = 0; e < 4; ++e) {
             const int p = t0 + 4 * tq + e;
             const int oh = (int)fdiv((uint32_t)p, g.f_ow), ow = p - oh * g.OW;
-            hb[e] = p < P ? oh * g.stride - g.pad : -(1 << 30);   // a column past P: h < 0
-            wb[e] = ow * g.stride - g.pad;
+            hb[e] = p < P ? oh * g.stride - g.padh : -(1 << 30);   // a column past P: h < 0
+            wb[e] = ow * g.stride - g.padw;
         }
     }
     __device__ void fetch(const float* __restrict__ Xn, const ConvGeom& g, int R, int k0,
@@ -277,11 +279,13 @@ struct ConvSlice {
 
 // Work-group tile TBM (output channels) x TBN (output positions of image z0 + blockIdx.y);
 // the k-loop is the GEMM kernel's (two register sets, branch-free), A = the kernel matrix
-// Cout x R (k contiguous), epilogue: + bias[co], stored into Y's (N, Cout, OH OW) layout.
+// Cout x R (k contiguous), epilogue: + bias[co] (+ the old Y with accumulate), stored into
+// Y's (N, Cout, OH OW) layout.
 template <int TBM, int TBN, bool VA>
 __global__ void __launch_bounds__(NTHREADS)
 conv_fwd_kernel(int Cout, int P, int R, const float* __restrict__ Kn, const float* __restrict__ X,
-                ConvGeom g, float* __restrict__ Y, const float* __restrict__ bias, int z0) {
+                ConvGeom g, float* __restrict__ Y, const float* __restrict__ bias, int z0,
+                int accumulate) {
     const int n = z0 + blockIdx.y;
     const float* Xn = X + (size_t)n * g.Cin * g.H * g.W;
     float* Yn = Y + (size_t)n * Cout * P;
@@ -363,24 +367,27 @@ conv_fwd_kernel(int Cout, int P, int R, const float* __restrict__ Kn, const floa
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < Cout)
-                    Yn[(size_t)row * P + col] = acc[a][b][r] + (bias ? bias[row] : 0.f);
+                if (row < Cout) {
+                    float* y = Yn + (size_t)row * P + col;
+                    const float v = acc[a][b][r] + (bias ? bias[row] : 0.f);
+                    *y = accumulate ? *y + v : v;
+                }
             }
         }
 }
 
 template <int TBM, int TBN>
 int launch_conv(int N, int Cout, int P, int R, const float* Kn, const float* X,
-                const ConvGeom& g, float* Y, const float* bias) {
+                const ConvGeom& g, float* Y, const float* bias, int accumulate) {
     const bool va = ((uintptr_t)Kn % 16 == 0) && (R % 4 == 0);
     const int tiles = ((Cout + TBM - 1) / TBM) * ((P + TBN - 1) / TBN);
     for (int z0 = 0; z0 < N; z0 += 65535) {
         const dim3 grid(tiles, N - z0 < 65535 ? N - z0 : 65535);
         if (va)
-            conv_fwd_kernel<TBM, TBN, true><<<grid, NTHREADS, 0, stream()>>>(Cout, P, R, Kn, X, g, Y, bias, z0);
+            conv_fwd_kernel<TBM, TBN, true><<<grid, NTHREADS, 0, stream()>>>(Cout, P, R, Kn, X, g, Y, bias, z0, accumulate);
         else
-            conv_fwd_kernel<TBM, TBN, false><<<grid, NTHREADS, 0, stream()>>>(Cout, P, R, Kn, X, g, Y, bias, z0);
-        DH_TRY(check_launch("dh_conv2d_fwd"));
+            conv_fwd_kernel<TBM, TBN, false><<<grid, NTHREADS, 0, stream()>>>(Cout, P, R, Kn, X, g, Y, bias, z0, accumulate);
+        DH_TRY(check_launch("dh_conv2d"));
     }
     return DH_OK;
 }
@@ -513,6 +520,34 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
     return launch_tiles<TA, TB, 128, 128>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 
+// Tile choice and launch shared by the forward and the data gradient: 64 x 64 tiles for few
+// output channels (the bench layer: 0.271 -> 0.212 ms against 64 x 256 tiles -- 3136
+// work-groups at 8 waves per SIMD instead of 832 at 2) and for small grids; 128 x 128
+// otherwise.
+int run_conv(int N, int Cout, long long P, long long R, const float* Kn, const float* X,
+             const ConvGeom& g, float* Y, const float* bias, int accumulate) {
+    const int cus = num_cus();
+    const long long t128 = (long long)((Cout + 127) / 128) * ((P + 127) / 128) * N;
+    const long long t64 = (long long)((Cout + 63) / 64) * ((P + 63) / 64) * N;
+    if (Cout <= 64 || (t128 < cus && 2 * t64 > cus))
+        return launch_conv<64, 64>(N, Cout, (int)P, (int)R, Kn, X, g, Y, bias, accumulate);
+    return launch_conv<128, 128>(N, Cout, (int)P, (int)R, Kn, X, g, Y, bias, accumulate);
+}
+
+// Kt[ci][(co KH + kh) KW + kw] = Kn[co][(ci KH + KH-1-kh) KW + KW-1-kw]: the kernel of the
+// data gradient (channels swapped, window flipped).
+__global__ void __launch_bounds__(256) conv_flip_kernel(const float* __restrict__ Kn,
+                                                        float* __restrict__ Kt, int Cout, int Cin,
+                                                        int KH, int KW) {
+    const size_t win = (size_t)KH * KW, n = (size_t)Cout * Cin * win;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const size_t ci = i / (Cout * win), rem = i % (Cout * win);
+        const size_t co = rem / win, t = rem % win;
+        const int kh = (int)(t / KW), kw = (int)(t % KW);
+        Kt[i] = Kn[co * Cin * win + (ci * KH + KH - 1 - kh) * KW + KW - 1 - kw];
+    }
+}
+
 }  // namespace
 }  // namespace dh
 
@@ -564,15 +599,48 @@ extern "C" int dh_conv2d_fwd(const float* X, const float* Kn, const float* bias,
     if (P >= (1ll << 30) || R >= (1ll << 30) || (long long)H * W >= (1ll << 30) ||
         (long long)Cout * P >= (1ll << 31))
         return set_error(DH_ERR_UNSUPPORTED, "dh_conv2d_fwd: plane or window too large");
-    ConvGeom g{Cin, H, W, KH, KW, pad, stride, OH, OW, make_fastdiv((uint32_t)OW),
+    ConvGeom g{Cin, H, W, KH, KW, pad, pad, stride, OH, OW, make_fastdiv((uint32_t)OW),
                make_fastdiv((uint32_t)KW), make_fastdiv((uint32_t)(KH * KW))};
-    // 64 x 64 tiles for few output channels (the bench layer: 0.271 -> 0.212 ms against
-    // 64 x 256 tiles -- 3136 work-groups at 8 waves per SIMD instead of 832 at 2) and for
-    // small grids; 128 x 128 otherwise.
-    const int cus = num_cus();
-    const long long t128 = (long long)((Cout + 127) / 128) * ((P + 127) / 128) * N;
-    const long long t64 = (long long)((Cout + 63) / 64) * ((P + 63) / 64) * N;
-    if (Cout <= 64 || (t128 < cus && 2 * t64 > cus))
-        return launch_conv<64, 64>(N, Cout, (int)P, (int)R, Kn, X, g, Y, bias);
-    return launch_conv<128, 128>(N, Cout, (int)P, (int)R, Kn, X, g, Y, bias);
+    return run_conv(N, Cout, P, R, Kn, X, g, Y, bias, 0);
+}
+
+// dX (+)= the input gradient of a stride-1 convolution: for stride 1, col2im(K^T dY) is the
+// convolution of dY (Cout channels, OH x OW) with the flipped, channel-swapped kernel, padded
+// by KH - 1 - pad rows and KW - 1 - pad columns -- one implicit-GEMM launch (Cin x H W x
+// Cout KH KW per image) after a small flip kernel, no column matrices.
+extern "C" int dh_conv2d_bwd_data(const float* dY, const float* Kn, float* dX, int N, int Cin,
+                                  int H, int W, int Cout, int KH, int KW, int pad, int stride,
+                                  int accumulate) {
+    DH_TRY(ensure_init());
+    if (N < 0 || Cin < 1 || H < 1 || W < 1 || Cout < 1 || KH < 1 || KW < 1 || pad < 0 ||
+        stride < 1)
+        return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_data: invalid shape");
+    if (H + 2 * pad < KH || W + 2 * pad < KW)
+        return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_data: kernel larger than the padded input");
+    if (stride != 1 || pad > KH - 1 || pad > KW - 1)
+        return set_error(DH_ERR_UNSUPPORTED,
+                         "dh_conv2d_bwd_data: stride %d, pad %d (stride 1 and pad < kernel size "
+                         "only; use dh_gemm_f32 + dh_col2im)", stride, pad);
+    const int OH = H + 2 * pad - KH + 1, OW = W + 2 * pad - KW + 1;
+    const long long P = (long long)H * W, R = (long long)Cout * KH * KW;
+    if (N == 0) return DH_OK;
+    if (!dY || !Kn || !dX) return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_data: null pointer");
+    if (P >= (1ll << 30) || R >= (1ll << 30) || (long long)OH * OW >= (1ll << 30) ||
+        (long long)Cin * P >= (1ll << 31))
+        return set_error(DH_ERR_UNSUPPORTED, "dh_conv2d_bwd_data: plane or window too large");
+    float* Kt = static_cast<float*>(dh_malloc((size_t)Cin * R * sizeof(float)));
+    if (!Kt) return set_error(DH_ERR_OOM, "dh_conv2d_bwd_data: flipped kernel");
+    const size_t nk = (size_t)Cin * R;
+    size_t blocks = (nk + 255) / 256;
+    if (blocks > (size_t)num_cus() * 8) blocks = (size_t)num_cus() * 8;
+    conv_flip_kernel<<<(unsigned)blocks, 256, 0, stream()>>>(Kn, Kt, Cout, Cin, KH, KW);
+    int st = check_launch("dh_conv2d_bwd_data(flip)");
+    if (st == DH_OK) {
+        ConvGeom g{Cout, OH, OW, KH, KW, KH - 1 - pad, KW - 1 - pad, 1, H, W,
+                   make_fastdiv((uint32_t)W), make_fastdiv((uint32_t)KW),
+                   make_fastdiv((uint32_t)(KH * KW))};
+        st = run_conv(N, Cin, P, R, Kt, dY, g, dX, nullptr, accumulate ? 1 : 0);
+    }
+    dh_free(Kt);   // pooled; later users of the buffer are ordered on the stream
+    return st;
 }

@@ -207,6 +207,15 @@ int dh_nct_to_cnt(const float* d_src, float* d_dst, int N, int C, size_t T);
  * bias may be NULL; otherwise it holds Cout values. */
 int dh_conv2d_fwd(const float* d_X, const float* d_kernel, const float* d_bias, float* d_Y,
                   int N, int Cin, int H, int W, int Cout, int KH, int KW, int pad, int stride);
+/* The input gradient of a stride-1 convolution in one implicit-GEMM launch (after a small
+ * kernel-flip launch): dX (N, Cin*H*W) (+)= col2im(kernel^T dY) per image, the dX half of the
+ * conv node's backward (autograd.inc:507-535, the cpu_gemm of conv.inc:175), computed as the
+ * convolution of dY (N, Cout, OH*OW) with the flipped, channel-swapped kernel padded by
+ * KH-1-pad / KW-1-pad.  accumulate = 1 adds into dX.  Stride > 1 or pad > KH-1 / KW-1 is
+ * DH_ERR_UNSUPPORTED: those take dh_gemm_f32 + dh_col2im. */
+int dh_conv2d_bwd_data(const float* d_dY, const float* d_kernel, float* d_dX, int N, int Cin,
+                       int H, int W, int Cout, int KH, int KW, int pad, int stride,
+                       int accumulate);
 
 /* ---- elementwise ops (runGPU / runGPUUnary, runtime/backend/gpu.inc:637-716) ---------------
  * Op codes follow the reference's BinopCode / UnopCode (gpu.inc:455-460, 571-577); each

@@ -1,6 +1,6 @@
 """GPU parity of conv2d: the data-movement kernels (dh_im2col, dh_col2im, dh_nct_to_cnt), the
-implicit-GEMM forward (dh_conv2d_fwd) and the dream_conv2d / dream_conv2d_padded builtins with
-their backward.
+implicit-GEMM forward (dh_conv2d_fwd) and data gradient (dh_conv2d_bwd_data), and the
+dream_conv2d / dream_conv2d_padded builtins with their backward.
 
 Tolerances: im2col and the permute are copies (bit-exact); col2im sums at most KH*KW values per
 element (fp32 vs fp64 numpy: 1e-6 relative).  The builtins (fp32 on the GPU) against the fp64
@@ -112,6 +112,62 @@ def test_conv2d_fwd_rejects_bad_shapes():
             hip.conv2d_fwd(d, d, None, d, 1, 1, 2, 2, 1, 5, 5, 0, 1)
         with pytest.raises(hip.DreamHipError, match="invalid shape"):
             hip.conv2d_fwd(d, d, None, d, 1, 1, 2, 2, 1, 1, 1, 0, 0)
+    finally:
+        d.free()
+
+
+@pytest.mark.parametrize("shape", [
+    # N, Cin, H, W, Cout, KH, KW, pad
+    (2, 3, 7, 6, 4, 3, 2, 0),       # valid conv, KH != KW
+    (3, 5, 9, 8, 6, 3, 3, 1),       # 'same' padding
+    (1, 2, 5, 5, 3, 5, 5, 4),       # pad = KH - 1 (the largest handled): a full correlation
+    (2, 4, 11, 7, 2, 5, 3, 2),      # KH != KW with pad = KW - 1, the largest both allow
+    (4, 7, 15, 15, 65, 1, 1, 0),    # 1x1 kernel, Cout = 65 (a partial k-slice of Cout KH KW)
+    (2, 64, 20, 20, 64, 3, 3, 1),   # the bench layer's channels
+    (2, 96, 12, 12, 32, 3, 3, 1),   # Cin = 96 > 64 output rows of the data-gradient GEMM
+])
+def test_conv2d_bwd_data_against_oracle(shape):
+    # dh_conv2d_bwd_data (dX as the convolution of dY with the flipped, channel-swapped kernel)
+    # against the fp64 oracle's conv backward (orc_conv2d_bwd, pinned by the reference's golden
+    # vectors and finite differences) and against the stored dcol + col2im path; overwrite and
+    # accumulate.
+    N, Cin, H, W, Cout, KH, KW, pad = shape
+    OH, OW = O.conv_out(H, W, KH, KW, pad, 1)
+    rng = np.random.default_rng(sum(shape) + 7)
+    X = rng.standard_normal((N, Cin * H * W)).astype(np.float32)
+    Kn = rng.standard_normal((Cout, Cin * KH * KW)).astype(np.float32)
+    G = rng.standard_normal((N, Cout * OH * OW)).astype(np.float32)
+    X0 = rng.standard_normal((N, Cin * H * W)).astype(np.float32)
+    rX, _ = O.conv2d_bwd(X.astype(np.float64), Kn.astype(np.float64), G.astype(np.float64),
+                         N, Cin, H, W, Cout, KH, KW, pad, 1)
+    dG, dK, dX = DB.from_numpy(G), DB.from_numpy(Kn), DB.from_numpy(X0)
+    try:
+        tol = 1e-5 * np.sqrt(Cout * KH * KW)
+        hip.conv2d_bwd_data(dG, dK, dX, N, Cin, H, W, Cout, KH, KW, pad, 1)
+        got = dX.numpy()
+        assert maxrel(got, rX) <= tol, shape
+        hip.conv2d_bwd_data(dG, dK, dX, N, Cin, H, W, Cout, KH, KW, pad, 1, accumulate=True)
+        assert maxrel(dX.numpy(), 2 * rX) <= tol, shape
+    finally:
+        for t in (dG, dK, dX):
+            t.free()
+
+
+def test_conv2d_bwd_data_rejects():
+    d = DB.empty((4096,), np.float32)
+    try:
+        with pytest.raises(hip.DreamHipError, match="stride 2"):
+            hip.conv2d_bwd_data(d, d, d, 1, 1, 8, 8, 1, 3, 3, 1, 2)
+        with pytest.raises(hip.DreamHipError, match="pad 3"):
+            hip.conv2d_bwd_data(d, d, d, 1, 1, 8, 8, 1, 3, 3, 3, 1)
+        with pytest.raises(hip.DreamHipError, match="pad 2"):
+            hip.conv2d_bwd_data(d, d, d, 1, 1, 8, 8, 1, 5, 2, 2, 1)   # pad > KW - 1
+        with pytest.raises(hip.DreamHipError, match="kernel larger"):
+            hip.conv2d_bwd_data(d, d, d, 1, 1, 2, 2, 1, 5, 5, 0, 1)
+        with pytest.raises(hip.DreamHipError, match="invalid shape"):
+            hip.conv2d_bwd_data(d, d, d, 1, 0, 8, 8, 1, 3, 3, 0, 1)
+        with pytest.raises(hip.DreamHipError, match="null pointer"):
+            hip.conv2d_bwd_data(None, d, d, 1, 1, 8, 8, 1, 3, 3, 0, 1)
     finally:
         d.free()
 
