@@ -194,10 +194,11 @@ def conv_workload(N, Cin, H, W, Cout, KH, KW, pad, stride, seed=9):
 
 def conv_bwd_workload(N, Cin, H, W, Cout, KH, KW, pad, stride, seed=10):
     """dream_conv2d's backward as the runtime issues it (autograd.inc:507-535 over all images
-    at once): the upstream gradient made channel-first, the im2col matrix, gK += go' col^T (one
-    NT GEMM, contraction N*OH*OW), and gX += col2im(K^T go') as one implicit-GEMM convolution of
-    go with the flipped kernel (dh_conv2d_bwd_data, stride 1).  FLOPs: the two products;
-    algorithmic bytes: go, X, K read, gK and gX read and written once (no col)."""
+    at once): gK += sum_n go_n col_n^T as one implicit GEMM (dh_conv2d_bwd_filter: col gathered
+    in the loader, partials over the (image, position) contraction reduced in order), and
+    gX += col2im(K^T go') as one implicit-GEMM convolution of go with the flipped kernel
+    (dh_conv2d_bwd_data, stride 1).  FLOPs: the two products; algorithmic bytes: go, X, K read,
+    gK and gX read and written once."""
     rng = np.random.default_rng(seed)
     OH, OW = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
     K, P = Cin * KH * KW, OH * OW
@@ -205,18 +206,15 @@ def conv_bwd_workload(N, Cin, H, W, Cout, KH, KW, pad, stride, seed=10):
     X = DB.from_numpy(rng.standard_normal((N, Cin * H * W), dtype=np.float32))
     Kn = DB.from_numpy((rng.standard_normal((Cout, K)) * 0.05).astype(np.float32))
     go = DB.from_numpy(rng.standard_normal((N, Cout * P), dtype=np.float32))
-    gop, col = DB.empty((Cout, NP), np.float32), DB.empty((K, NP), np.float32)
     gK, gX = DB.from_numpy(np.zeros((Cout, K), np.float32)), \
         DB.from_numpy(np.zeros((N, Cin * H * W), np.float32))
 
     def step():
-        hip.nct_to_cnt(go, gop, N, Cout, P)
-        hip.im2col(X, col, N, Cin, H, W, KH, KW, pad, stride)
-        hip.gemm_f32(0, 1, Cout, K, NP, gop, NP, col, NP, 1.0, gK, K)
+        hip.conv2d_bwd_filter(go, X, gK, N, Cin, H, W, Cout, KH, KW, pad, stride, accumulate=True)
         hip.conv2d_bwd_data(go, Kn, gX, N, Cin, H, W, Cout, KH, KW, pad, stride, accumulate=True)
     flops = 4.0 * Cout * K * NP
     alg = 4.0 * (N * Cout * P + N * Cin * H * W + Cout * K) + 8.0 * (Cout * K + N * Cin * H * W)
-    return step, flops, alg, [X, Kn, go, gop, col, gK, gX]
+    return step, flops, alg, [X, Kn, go, gK, gX]
 
 
 WORKLOADS = {
@@ -243,8 +241,8 @@ WORKLOADS = {
                                "conv2d 64 x 64ch 56x56, 64 out ch, 3x3 pad 1 (implicit GEMM), fp32"),
     "conv2d_bwd_resnet_64x56x56": (conv_bwd_workload, dict(N=64, Cin=64, H=56, W=56, Cout=64, KH=3,
                                                            KW=3, pad=1, stride=1), "fp32",
-                                   "conv2d backward, same layer: im2col + NT GEMM (gK) + "
-                                   "implicit-GEMM data gradient, fp32"),
+                                   "conv2d backward, same layer: implicit-GEMM kernel and "
+                                   "data gradients, fp32"),
     "softmax_fwd_16384x1024": (rows_workload, dict(op="softmax_fwd", R=16384, C=1024), "hbm",
                                "row softmax 16384 x 1024 fp32 (HBM-bound)"),
     "softmax_bwd_16384x1024": (rows_workload, dict(op="softmax_bwd", R=16384, C=1024), "hbm",

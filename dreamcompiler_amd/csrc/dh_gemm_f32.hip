@@ -417,6 +417,229 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ p
     }
 }
 
+// ---- conv2d weight gradient as an implicit GEMM ---------------------------------------
+// gK[co][r] (+)= sum_n sum_p dY[n][co][p] col_n[r][p]: an NT product whose contraction runs
+// over (image, output position).  A = dY_n read in place ([co][p], p contiguous); B = col_n^T
+// gathered from X by the loader (the im2col matrix is never stored).  The contraction is cut
+// per image into BK-wide slices (an image's last slice padded with zeros) and the slices
+// into chunks, one per gridDim.y member, each writing an fp32 partial that splitk_reduce adds
+// in a fixed order.
+
+// The thread's rows of B (kernel taps r): chunk c covers tap t0 + f / (BK / 4), f = tid +
+// c NTHREADS, at output positions p0 + 4 (f % (BK / 4)) + (0..3) -- its tap and hence the
+// input plane and window offset stay fixed across slices.
+template <int TILE>
+struct ColTGeom {
+    static constexpr int CH = TILE * BK / 4 / NTHREADS;
+    int xoff[CH], dh[CH], dw[CH];   // ci H W, kh - padh (-2^30 past R), kw - padw
+    __device__ void init(const ConvGeom& g, int R, int t0, int tid) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int r = t0 + (tid + c * NTHREADS) / (BK / 4);
+            const int q = (int)fdiv((uint32_t)r, g.f_kw), kw = r - q * g.KW;
+            const int ci = (int)fdiv((uint32_t)r, g.f_khkw), kh = q - ci * g.KH;
+            xoff[c] = ci * g.H * g.W;
+            dh[c] = r < R ? kh - g.padh : -(1 << 30);
+            dw[c] = kw - g.padw;
+        }
+    }
+};
+
+template <int TILE>
+struct ColTSlice {
+    static constexpr int CH = TILE * BK / 4 / NTHREADS;
+    f32x4 v[CH];
+    // positions p0 .. p0 + BK of image plane Xn; np = number of valid positions (0: zeros)
+    __device__ void fetch(const float* __restrict__ Xn, const ConvGeom& g, const ColTGeom<TILE>& c,
+                          int p0, int np, int tid) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int pq = 4 * ((tid + k * NTHREADS) % (BK / 4));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int p = p0 + pq + e;
+                const int oh = (int)fdiv((uint32_t)p, g.f_ow), ow = p - oh * g.OW;
+                const int h = oh * g.stride + c.dh[k], w = ow * g.stride + c.dw[k];
+                const bool in = pq + e < np && (unsigned)h < (unsigned)g.H && (unsigned)w < (unsigned)g.W;
+                v[k][e] = *(in ? Xn + c.xoff[k] + h * g.W + w : g_zero4);
+            }
+        }
+    }
+    __device__ void store(float* lds, int stride, int tid) const {   // transposing, as Slice<true>
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int f = tid + k * NTHREADS;
+            const int t = f / (BK / 4), kq = f % (BK / 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) lds[(4 * kq + e) * stride + t] = v[k][e];
+        }
+    }
+};
+
+// Work-group: tile TBM (output channels) x TBN (taps) of chunk blockIdx.y, i.e. the slices
+// [y chunk, min((y + 1) chunk, total)) of the flattened (image, slice) contraction, nkp
+// slices per image.  Writes its partial to part + y Cout R.
+template <int TBM, int TBN, bool VA>
+__global__ void __launch_bounds__(NTHREADS)
+conv_wgrad_kernel(int Cout, int P, int R, const float* __restrict__ dY, const float* __restrict__ X,
+                  ConvGeom g, int nkp, int total, int chunk, float* __restrict__ part) {
+    const int sbeg = blockIdx.y * chunk;
+    const int ns = min(total - sbeg, chunk);          // slices of this chunk (>= 1)
+    float* C = part + (size_t)blockIdx.y * Cout * R;
+    constexpr int LDS_A = TBM + 4, LDS_B = TBN + 4;
+    constexpr int WT = TBM == 64 && TBN == 64 ? 32 : 64, NB = WT / 32;
+    constexpr int WN = TBN / WT;
+    static_assert((TBM / WT) * WN == 4, "4 waves");
+    __shared__ __attribute__((aligned(16))) float As[2][BK * LDS_A];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDS_B];
+
+    const int tiles_m = (Cout + TBM - 1) / TBM, tiles_n = (R + TBN - 1) / TBN;
+    int tm, tn;
+    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
+    const int m0 = tm * TBM, n0 = tn * TBN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm = (wave / WN) * WT, wn = (wave % WN) * WT;
+    const size_t plane = (size_t)g.Cin * g.H * g.W;
+
+    ColTGeom<TBN> cg;
+    cg.init(g, R, n0, tid);
+    Slice<true, VA, TBM> sa[2];
+    ColTSlice<TBN> sb[2];
+    // slice kt of the chunk: image n, positions p0 ..; past the chunk's end: zeros
+    auto fetch = [&](auto set_c, int kt) {
+        constexpr int set = decltype(set_c)::value;
+        const int s = sbeg + kt;
+        const bool live = kt < ns;
+        const int n = live ? s / nkp : 0;
+        const int p0 = live ? (s - n * nkp) * BK : 0;
+        const int np = live ? min(BK, P - p0) : 0;
+        sa[set].fetch(dY + (size_t)n * Cout * P, P, m0, p0, Cout, live ? P : 0, tid);
+        sb[set].fetch(X + (size_t)n * plane, g, cg, p0, np, tid);
+    };
+
+    f32x16 acc[NB][NB];
+#pragma unroll
+    for (int a = 0; a < NB; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    fetch(std::integral_constant<int, 0>{}, 0);
+    fetch(std::integral_constant<int, 1>{}, 1);
+    sa[0].store(As[0], LDS_A, tid);
+    sb[0].store(Bs[0], LDS_B, tid);
+    __syncthreads();
+    auto mma = [&](const float* as, const float* bs) {
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            float av[NB], bv[NB];
+#pragma unroll
+            for (int x = 0; x < NB; ++x) {
+                av[x] = as[(kk + h) * LDS_A + wm + 32 * x + l32];
+                bv[x] = bs[(kk + h) * LDS_B + wn + 32 * x + l32];
+            }
+#pragma unroll
+            for (int a = 0; a < NB; ++a)
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
+    };
+    auto step = [&](auto cur_c, int kt) {
+        constexpr int cur = decltype(cur_c)::value;
+        fetch(cur_c, kt + 2);
+        mma(As[cur], Bs[cur]);
+        sa[cur ^ 1].store(As[cur ^ 1], LDS_A, tid);
+        sb[cur ^ 1].store(Bs[cur ^ 1], LDS_B, tid);
+        __syncthreads();
+    };
+    if (ns == 1) {
+        mma(As[0], Bs[0]);
+    } else {
+        for (int kt = 0; kt < ns; kt += 2) {
+            step(std::integral_constant<int, 0>{}, kt);
+            step(std::integral_constant<int, 1>{}, kt + 1);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < NB; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int col = n0 + wn + 32 * b + l32;
+            if (col >= R) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + 32 * a + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < Cout) C[(size_t)row * R + col] = acc[a][b][r];
+            }
+        }
+}
+
+// out = beta out + sum_s part[s] for many partials: wave w of a work-group sums partials
+// [w S / 4, (w + 1) S / 4) of 64 consecutive elements, then wave 0 adds the four sums in
+// order (fixed order: bit-identical reruns), so four times as many waves share the loads as
+// in splitk_reduce's one thread per element.
+__global__ void __launch_bounds__(256) partial_sum4(const float* __restrict__ part, int S,
+                                                    size_t n, float beta, float* __restrict__ out) {
+    __shared__ float red[3][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sb = (int)((long long)S * w / 4), se = (int)((long long)S * (w + 1) / 4);
+    for (size_t e0 = (size_t)blockIdx.x * 64; e0 < n; e0 += (size_t)gridDim.x * 64) {
+        const size_t e = e0 + lane;
+        float v = 0.f;
+        if (e < n)
+            for (int q = sb; q < se; ++q) v += part[(size_t)q * n + e];
+        if (w > 0) red[w - 1][lane] = v;
+        __syncthreads();
+        if (w == 0 && e < n) {
+            v = ((v + red[0][lane]) + red[1][lane]) + red[2][lane];
+            out[e] = beta == 0.f ? v : v + beta * out[e];
+        }
+        __syncthreads();
+    }
+}
+
+template <int TBM, int TBN>
+int launch_wgrad(int N, int Cout, int P, int R, const float* dY, const float* X,
+                 const ConvGeom& g, float* dK, int accumulate) {
+    const int cus = num_cus();
+    const int tiles = ((Cout + TBM - 1) / TBM) * ((R + TBN - 1) / TBN);
+    const int nkp = (P + BK - 1) / BK;
+    const long long total = (long long)N * nkp;
+    // chunks: about 8 work-groups per CU in all, partials within 256 MB, at most 65535
+    long long S = 8ll * cus / tiles;
+    const long long cap = (64ll << 20) / ((long long)Cout * R);
+    S = S < 1 ? 1 : S;
+    S = S > cap ? (cap < 1 ? 1 : cap) : S;
+    S = S > total ? total : S;
+    S = S > 65535 ? 65535 : S;
+    const long long chunk = (total + S - 1) / S;
+    if (chunk > INT32_MAX || total > INT32_MAX)
+        return set_error(DH_ERR_UNSUPPORTED, "dh_conv2d_bwd_filter: contraction too long");
+    S = (total + chunk - 1) / chunk;
+    float* part = static_cast<float*>(dh_malloc((size_t)S * Cout * R * sizeof(float)));
+    if (!part) return set_error(DH_ERR_OOM, "dh_conv2d_bwd_filter: partials");
+    const bool va = ((uintptr_t)dY % 16 == 0) && (P % 4 == 0);
+    const dim3 grid(tiles, (unsigned)S);
+    hipStream_t s = stream();
+    if (va)
+        conv_wgrad_kernel<TBM, TBN, true><<<grid, NTHREADS, 0, s>>>(Cout, P, R, dY, X, g, nkp, (int)total, (int)chunk, part);
+    else
+        conv_wgrad_kernel<TBM, TBN, false><<<grid, NTHREADS, 0, s>>>(Cout, P, R, dY, X, g, nkp, (int)total, (int)chunk, part);
+    int st = check_launch("dh_conv2d_bwd_filter");
+    if (st == DH_OK) {
+        const size_t n = (size_t)Cout * R;
+        size_t blocks = (n + 63) / 64;
+        if (blocks > (size_t)cus * 16) blocks = (size_t)cus * 16;
+        partial_sum4<<<(unsigned)blocks, 256, 0, s>>>(part, (int)S, n, accumulate ? 1.f : 0.f, dK);
+        st = check_launch("dh_conv2d_bwd_filter(reduce)");
+    }
+    dh_free(part);   // pooled; later users of the buffer are ordered on the stream
+    return st;
+}
+
 template <bool TA, bool TB, int TBM, int TBN>
 auto pick_kernel(int M, int N, int K, const float* A, int lda, long long sA, const float* B,
                  int ldb, long long sB) {
@@ -643,4 +866,34 @@ extern "C" int dh_conv2d_bwd_data(const float* dY, const float* Kn, float* dX, i
     }
     dh_free(Kt);   // pooled; later users of the buffer are ordered on the stream
     return st;
+}
+
+// gK (+)= the kernel gradient of a convolution, any pad and stride: sum over images of
+// dY_n col_n^T with col_n gathered from X inside the GEMM loader (no im2col matrix, no
+// channel-first copy of dY), split over the (image, position) contraction and reduced in a
+// fixed order.
+extern "C" int dh_conv2d_bwd_filter(const float* dY, const float* X, float* dK, int N, int Cin,
+                                    int H, int W, int Cout, int KH, int KW, int pad, int stride,
+                                    int accumulate) {
+    DH_TRY(ensure_init());
+    if (N < 0 || Cin < 1 || H < 1 || W < 1 || Cout < 1 || KH < 1 || KW < 1 || pad < 0 ||
+        stride < 1)
+        return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_filter: invalid shape");
+    if (H + 2 * pad < KH || W + 2 * pad < KW)
+        return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_filter: kernel larger than the padded input");
+    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    const long long P = (long long)OH * OW, R = (long long)Cin * KH * KW;
+    if (!dK) return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_filter: null pointer");
+    if (P >= (1ll << 30) || R >= (1ll << 30) || (long long)H * W >= (1ll << 30) ||
+        (long long)Cout * P >= (1ll << 31) || (long long)Cout * R >= (1ll << 31) ||
+        (long long)Cin * H * W >= (1ll << 31))
+        return set_error(DH_ERR_UNSUPPORTED, "dh_conv2d_bwd_filter: plane or window too large");
+    if (N == 0)   // an empty sum: dK = 0, or unchanged with accumulate
+        return accumulate ? DH_OK : dh_memset(dK, 0, (size_t)Cout * R * sizeof(float));
+    if (!dY || !X) return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_filter: null pointer");
+    ConvGeom g{Cin, H, W, KH, KW, pad, pad, stride, OH, OW, make_fastdiv((uint32_t)OW),
+               make_fastdiv((uint32_t)KW), make_fastdiv((uint32_t)(KH * KW))};
+    if (Cout <= 64)
+        return launch_wgrad<64, 64>(N, Cout, (int)P, (int)R, dY, X, g, dK, accumulate);
+    return launch_wgrad<128, 128>(N, Cout, (int)P, (int)R, dY, X, g, dK, accumulate);
 }

@@ -466,33 +466,28 @@ ConvDims conv_dims(const Tensor* t) {
 }
 
 void conv_backward(Tensor* t) {
-    // autograd.inc:507-535 over all images at once: gK += go' col^T (one NT GEMM, contraction
-    // N*OH*OW; go' = the gradient channel-first); gX += col2im(K^T go'), which for stride 1
-    // (pad < kernel size) is one implicit-GEMM convolution of go with the flipped kernel
-    // (dh_conv2d_bwd_data) and otherwise a TN GEMM into dcol + col2im.
+    // autograd.inc:507-535 over all images at once: gK += sum_n go_n col_n^T as one implicit
+    // GEMM (dh_conv2d_bwd_filter, col gathered in the loader); gX += col2im(K^T go'), which for
+    // stride 1 (pad < kernel size) is one implicit-GEMM convolution of go with the flipped
+    // kernel (dh_conv2d_bwd_data) and otherwise a TN GEMM into dcol + col2im (go' = the
+    // gradient channel-first).
     const ConvDims d = conv_dims(t);
     Tensor *x = t->lhs, *k = t->rhs;
     const size_t K = d.K(), NP = (size_t)d.N * d.P();
     const float* go = grad_in(t);
-    {
-        Dev gop((size_t)d.Cout * NP * 4), col(K * NP * 4);
-        need_buf(gop), need_buf(col);
-        need(dh_nct_to_cnt(go, gop.f(), d.N, d.Cout, d.P()));
-        need(dh_im2col(dev_data(x), col.f(), d.N, d.Cin, d.H, d.W, d.KH, d.KW, d.pad, d.stride));
-        need(dh_gemm_f32(0, 1, d.Cout, (int)K, (int)NP, gop.f(), (int)NP, col.f(), (int)NP, 1.f,
-                         dgrad(k), (int)K));
-        if (d.stride != 1 || d.pad > d.KH - 1 || d.pad > d.KW - 1) {
-            Dev dcol(K * NP * 4);
-            need_buf(dcol);
-            need(dh_gemm_f32(1, 0, (int)K, (int)NP, d.Cout, dev_data(k), (int)K, gop.f(),
-                             (int)NP, 0.f, dcol.f(), (int)NP));
-            need(dh_col2im(dcol.f(), dgrad(x), d.N, d.Cin, d.H, d.W, d.KH, d.KW, d.pad,
-                           d.stride, 1));
-            return;
-        }
+    need(dh_conv2d_bwd_filter(go, dev_data(x), dgrad(k), d.N, d.Cin, d.H, d.W, d.Cout, d.KH,
+                              d.KW, d.pad, d.stride, 1));
+    if (d.stride == 1 && d.pad <= d.KH - 1 && d.pad <= d.KW - 1) {
+        need(dh_conv2d_bwd_data(go, dev_data(k), dgrad(x), d.N, d.Cin, d.H, d.W, d.Cout, d.KH,
+                                d.KW, d.pad, 1, 1));
+        return;
     }
-    need(dh_conv2d_bwd_data(go, dev_data(k), dgrad(x), d.N, d.Cin, d.H, d.W, d.Cout, d.KH, d.KW,
-                            d.pad, 1, 1));
+    Dev gop((size_t)d.Cout * NP * 4), dcol(K * NP * 4);
+    need_buf(gop), need_buf(dcol);
+    need(dh_nct_to_cnt(go, gop.f(), d.N, d.Cout, d.P()));
+    need(dh_gemm_f32(1, 0, (int)K, (int)NP, d.Cout, dev_data(k), (int)K, gop.f(), (int)NP, 0.f,
+                     dcol.f(), (int)NP));
+    need(dh_col2im(dcol.f(), dgrad(x), d.N, d.Cin, d.H, d.W, d.KH, d.KW, d.pad, d.stride, 1));
 }
 
 // Elementwise backward branches on the host, as in the reference (autograd.inc:58-90 with

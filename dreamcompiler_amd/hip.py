@@ -66,6 +66,7 @@ _SIGS = {
     "dh_nct_to_cnt": (_i, [_vp, _vp, _i, _i, _sz]),
     "dh_conv2d_fwd": (_i, [_vp, _vp, _vp, _vp] + [_i] * 9),
     "dh_conv2d_bwd_data": (_i, [_vp, _vp, _vp] + [_i] * 10),
+    "dh_conv2d_bwd_filter": (_i, [_vp, _vp, _vp] + [_i] * 10),
     "dh_binary": (_i, [_i, _i, _vp, _sz, ctypes.POINTER(_i), _vp, _sz, ctypes.POINTER(_i), _vp,
                        ctypes.POINTER(_i), _vp]),
     "dh_unary": (_i, [_i, _i, _vp, _vp, _sz, ctypes.c_double, ctypes.c_double, _vp]),
@@ -250,6 +251,11 @@ def conv2d_fwd(X, Kn, bias, Y, N, Cin, H, W, Cout, KH, KW, pad=0, stride=1):
 def conv2d_bwd_data(dY, Kn, dX, N, Cin, H, W, Cout, KH, KW, pad=0, stride=1, accumulate=False):
     check(load().dh_conv2d_bwd_data(_p(dY), _p(Kn), _p(dX), N, Cin, H, W, Cout, KH, KW, pad,
                                     stride, int(accumulate)), "dh_conv2d_bwd_data")
+
+
+def conv2d_bwd_filter(dY, X, dK, N, Cin, H, W, Cout, KH, KW, pad=0, stride=1, accumulate=False):
+    check(load().dh_conv2d_bwd_filter(_p(dY), _p(X), _p(dK), N, Cin, H, W, Cout, KH, KW, pad,
+                                      stride, int(accumulate)), "dh_conv2d_bwd_filter")
 
 
 def nct_to_cnt(src, dst, N, C, T):

@@ -216,6 +216,16 @@ int dh_conv2d_fwd(const float* d_X, const float* d_kernel, const float* d_bias, 
 int dh_conv2d_bwd_data(const float* d_dY, const float* d_kernel, float* d_dX, int N, int Cin,
                        int H, int W, int Cout, int KH, int KW, int pad, int stride,
                        int accumulate);
+/* The kernel gradient of a convolution (any pad and stride): dK (Cout x Cin*KH*KW) (+)= sum
+ * over images of dY_n (Cout x OH*OW) col_n^T, the gK half of the conv node's backward
+ * (autograd.inc:507-535), as an implicit GEMM: col_n is gathered from X inside the operand
+ * loader and dY is read in its (N, Cout, OH*OW) layout (no im2col matrix, no channel-first
+ * copy).  The (image, position) contraction is split over work-groups and the fp32 partials
+ * (at most 256 MB of pool memory) are summed in a fixed order: reruns are bit-identical.
+ * accumulate = 1 adds into dK. */
+int dh_conv2d_bwd_filter(const float* d_dY, const float* d_X, float* d_dK, int N, int Cin,
+                         int H, int W, int Cout, int KH, int KW, int pad, int stride,
+                         int accumulate);
 
 /* ---- elementwise ops (runGPU / runGPUUnary, runtime/backend/gpu.inc:637-716) ---------------
  * Op codes follow the reference's BinopCode / UnopCode (gpu.inc:455-460, 571-577); each

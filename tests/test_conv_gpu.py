@@ -1,6 +1,7 @@
 """GPU parity of conv2d: the data-movement kernels (dh_im2col, dh_col2im, dh_nct_to_cnt), the
-implicit-GEMM forward (dh_conv2d_fwd) and data gradient (dh_conv2d_bwd_data), and the
-dream_conv2d / dream_conv2d_padded builtins with their backward.
+implicit-GEMM forward (dh_conv2d_fwd), data gradient (dh_conv2d_bwd_data) and kernel gradient
+(dh_conv2d_bwd_filter), and the dream_conv2d / dream_conv2d_padded builtins with their
+backward.
 
 Tolerances: im2col and the permute are copies (bit-exact); col2im sums at most KH*KW values per
 element (fp32 vs fp64 numpy: 1e-6 relative).  The builtins (fp32 on the GPU) against the fp64
@@ -151,6 +152,65 @@ def test_conv2d_bwd_data_against_oracle(shape):
     finally:
         for t in (dG, dK, dX):
             t.free()
+
+
+@pytest.mark.parametrize("shape", [
+    # N, Cin, H, W, Cout, KH, KW, pad, stride
+    (2, 3, 7, 6, 4, 3, 2, 0, 1),       # P = 20: one partial slice per image
+    (3, 5, 9, 8, 6, 3, 3, 1, 2),       # strided, P = 20
+    (1, 2, 5, 5, 3, 5, 5, 2, 1),       # one image
+    (2, 1, 11, 7, 1, 1, 1, 0, 3),      # 1x1 taps, stride 3, P = 12
+    (5, 4, 13, 13, 130, 3, 3, 2, 3),   # Cout > 64: 128 x 128 tiles; P = 25 (not a multiple of 4)
+    (16, 64, 14, 14, 64, 3, 3, 1, 1),  # the bench layer's channels: many chunks over 16 images
+    (64, 3, 8, 8, 8, 3, 3, 1, 1),      # a long contraction over 64 small images
+])
+def test_conv2d_bwd_filter_against_oracle(shape):
+    # dh_conv2d_bwd_filter (implicit GEMM over the (image, position) contraction, col
+    # gathered in the loader) against the fp64 oracle's kernel gradient (orc_conv2d_bwd,
+    # pinned by the reference's golden vectors and finite differences); overwrite, accumulate,
+    # and bit-identical reruns.
+    N, Cin, H, W, Cout, KH, KW, pad, stride = shape
+    OH, OW = O.conv_out(H, W, KH, KW, pad, stride)
+    rng = np.random.default_rng(sum(shape) + 11)
+    X = rng.standard_normal((N, Cin * H * W)).astype(np.float32)
+    Kn = rng.standard_normal((Cout, Cin * KH * KW)).astype(np.float32)
+    G = rng.standard_normal((N, Cout * OH * OW)).astype(np.float32)
+    _, rK = O.conv2d_bwd(X.astype(np.float64), Kn.astype(np.float64), G.astype(np.float64),
+                         N, Cin, H, W, Cout, KH, KW, pad, stride)
+    K0 = rng.standard_normal((Cout, Cin * KH * KW)).astype(np.float32)
+    dG, dX, dK = DB.from_numpy(G), DB.from_numpy(X), DB.from_numpy(K0)
+    try:
+        tol = 1e-5 * np.sqrt(N * OH * OW)
+        hip.conv2d_bwd_filter(dG, dX, dK, N, Cin, H, W, Cout, KH, KW, pad, stride)
+        got = dK.numpy()
+        assert maxrel(got, rK) <= tol, shape
+        hip.conv2d_bwd_filter(dG, dX, dK, N, Cin, H, W, Cout, KH, KW, pad, stride)
+        assert np.array_equal(dK.numpy(), got), shape
+        hip.conv2d_bwd_filter(dG, dX, dK, N, Cin, H, W, Cout, KH, KW, pad, stride, accumulate=True)
+        assert maxrel(dK.numpy(), 2 * rK) <= tol, shape
+    finally:
+        for t in (dG, dX, dK):
+            t.free()
+
+
+def test_conv2d_bwd_filter_empty_batch_and_rejects():
+    K0 = np.arange(2 * 9, dtype=np.float32).reshape(2, 9)
+    d, dK = DB.empty((4096,), np.float32), DB.from_numpy(K0)
+    try:
+        # N = 0: an empty sum -- dK unchanged with accumulate, zeros without
+        hip.conv2d_bwd_filter(d, d, dK, 0, 1, 8, 8, 2, 3, 3, 1, 1, accumulate=True)
+        assert np.array_equal(dK.numpy(), K0)
+        hip.conv2d_bwd_filter(d, d, dK, 0, 1, 8, 8, 2, 3, 3, 1, 1)
+        assert not dK.numpy().any()
+        with pytest.raises(hip.DreamHipError, match="kernel larger"):
+            hip.conv2d_bwd_filter(d, d, d, 1, 1, 2, 2, 1, 5, 5, 0, 1)
+        with pytest.raises(hip.DreamHipError, match="invalid shape"):
+            hip.conv2d_bwd_filter(d, d, d, 1, 1, 8, 8, 1, 3, 3, 0, 0)
+        with pytest.raises(hip.DreamHipError, match="null pointer"):
+            hip.conv2d_bwd_filter(None, d, d, 1, 1, 8, 8, 1, 3, 3, 0, 1)
+    finally:
+        d.free()
+        dK.free()
 
 
 def test_conv2d_bwd_data_rejects():
