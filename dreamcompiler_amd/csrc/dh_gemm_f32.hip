@@ -234,13 +234,18 @@ struct ConvGeom {
 // like Slice<false, ...> (row k, 4 consecutive columns per chunk).  A thread's chunks all sit
 // in the same 4 columns (tq = tid % (TILE / 4)) and in rows RSTEP apart, so the columns'
 // window origins are computed once per tile and a slice only decomposes its rows.  Every
-// element is one branch-free scalar load (a tap outside the input reads g_zero4).
+// element is one 32-bit-offset buffer load of the image's planes: byte offset = 4 (tap term
+// of its row + pixel term of its column); a tap outside the input takes an offset past the
+// buffer's range, which reads zero.
+constexpr uint32_t CONV_OOB = 0xFFFFFFF0u;   // past every image buffer (entries check the size)
+
 template <int TILE>
 struct ConvSlice {
     static constexpr int CH = TILE * BK / 4 / NTHREADS;
     static constexpr int RSTEP = NTHREADS / (TILE / 4);
     f32x4 v[CH];
     int hb[4], wb[4];   // oh * stride - pad, ow * stride - pad of the thread's 4 columns
+    int pix[4];         // 4 (hb W + wb): the column's part of the byte offset
 
     __device__ void init(const ConvGeom& g, int t0, int P, int tid) {
         const int tq = tid % (TILE / 4);
@@ -248,23 +253,26 @@ struct ConvSlice {
         for (int e = 0; e < 4; ++e) {
             const int p = t0 + 4 * tq + e;
             const int oh = (int)fdiv((uint32_t)p, g.f_ow), ow = p - oh * g.OW;
-            hb[e] = p < P ? oh * g.stride - g.padh : -(1 << 30);   // a column past P: h < 0
+            const int h0 = oh * g.stride - g.padh;
             wb[e] = ow * g.stride - g.padw;
+            pix[e] = 4 * (h0 * g.W + wb[e]);
+            hb[e] = p < P ? h0 : -(1 << 30);   // a column past P: h < 0
         }
     }
-    __device__ void fetch(const float* __restrict__ Xn, const ConvGeom& g, int R, int k0,
-                          int tid) {
+    __device__ void fetch(__amdgpu_buffer_rsrc_t rs, const ConvGeom& g, int R, int k0, int tid) {
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
             const int k = k0 + tid / (TILE / 4) + RSTEP * r;
             const int q = (int)fdiv((uint32_t)k, g.f_kw), kw = k - q * g.KW;
             const int ci = (int)fdiv((uint32_t)k, g.f_khkw), kh = q - ci * g.KH;
-            const float* xc = Xn + (size_t)ci * g.H * g.W;
+            const int tap = 4 * ((ci * g.H + kh) * g.W + kw);
+            const bool kin = k < R;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int h = hb[e] + kh, w = wb[e] + kw;
-                const bool in = k < R && (unsigned)h < (unsigned)g.H && (unsigned)w < (unsigned)g.W;
-                v[r][e] = *(in ? xc + h * g.W + w : g_zero4);
+                const bool in = kin && (unsigned)h < (unsigned)g.H && (unsigned)w < (unsigned)g.W;
+                const uint32_t off = in ? (uint32_t)(tap + pix[e]) : CONV_OOB;
+                v[r][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
             }
         }
     }
@@ -287,7 +295,9 @@ conv_fwd_kernel(int Cout, int P, int R, const float* __restrict__ Kn, const floa
                 ConvGeom g, float* __restrict__ Y, const float* __restrict__ bias, int z0,
                 int accumulate) {
     const int n = z0 + blockIdx.y;
-    const float* Xn = X + (size_t)n * g.Cin * g.H * g.W;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X) + (size_t)n * g.Cin * g.H * g.W, 0, (int)(4u * g.Cin * g.H * g.W),
+        0x00020000);
     float* Yn = Y + (size_t)n * Cout * P;
     constexpr int LDS_A = TBM + 4, LDS_B = TBN + 4;
     constexpr int WT = TBM == 64 && TBN == 64 ? 32 : 64, NB = WT / 32;   // wave sub-tile
@@ -319,9 +329,9 @@ conv_fwd_kernel(int Cout, int P, int R, const float* __restrict__ Kn, const floa
 
     const int nk = (R + BK - 1) / BK;   // R >= 1
     sa[0].fetch(Kn, R, m0, 0, Cout, R, tid);
-    sb[0].fetch(Xn, g, R, 0, tid);
+    sb[0].fetch(xr, g, R, 0, tid);
     sa[1].fetch(Kn, R, m0, BK, Cout, R, tid);
-    sb[1].fetch(Xn, g, R, BK, tid);
+    sb[1].fetch(xr, g, R, BK, tid);
     sa[0].store(As[0], LDS_A, tid);
     sb[0].store(Bs[0], LDS_B, tid);
     __syncthreads();
@@ -344,7 +354,7 @@ conv_fwd_kernel(int Cout, int P, int R, const float* __restrict__ Kn, const floa
     auto step = [&](auto cur_c, int kt) {
         constexpr int cur = decltype(cur_c)::value;
         sa[cur].fetch(Kn, R, m0, (kt + 2) * BK, Cout, R, tid);
-        sb[cur].fetch(Xn, g, R, (kt + 2) * BK, tid);
+        sb[cur].fetch(xr, g, R, (kt + 2) * BK, tid);
         mma(As[cur], Bs[cur]);
         sa[cur ^ 1].store(As[cur ^ 1], LDS_A, tid);
         sb[cur ^ 1].store(Bs[cur ^ 1], LDS_B, tid);
@@ -431,37 +441,44 @@ __global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ p
 template <int TILE>
 struct ColTGeom {
     static constexpr int CH = TILE * BK / 4 / NTHREADS;
-    int xoff[CH], dh[CH], dw[CH];   // ci H W, kh - padh (-2^30 past R), kw - padw
+    int tap[CH], dh[CH], dw[CH];    // 4 (ci H W + dh W + dw); kh - padh (-2^30 past R); kw - padw
     __device__ void init(const ConvGeom& g, int R, int t0, int tid) {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int r = t0 + (tid + c * NTHREADS) / (BK / 4);
             const int q = (int)fdiv((uint32_t)r, g.f_kw), kw = r - q * g.KW;
             const int ci = (int)fdiv((uint32_t)r, g.f_khkw), kh = q - ci * g.KH;
-            xoff[c] = ci * g.H * g.W;
-            dh[c] = r < R ? kh - g.padh : -(1 << 30);
             dw[c] = kw - g.padw;
+            tap[c] = 4 * ((ci * g.H + kh - g.padh) * g.W + dw[c]);
+            dh[c] = r < R ? kh - g.padh : -(1 << 30);
         }
     }
 };
 
+// A thread's chunks share their 4 positions (f % (BK / 4) = tid % (BK / 4)), so a slice
+// decomposes them once; each element is then one 32-bit-offset buffer load (tap term + pixel
+// term; taps outside the input read zero through an offset past the buffer).
 template <int TILE>
 struct ColTSlice {
     static constexpr int CH = TILE * BK / 4 / NTHREADS;
     f32x4 v[CH];
-    // positions p0 .. p0 + BK of image plane Xn; np = number of valid positions (0: zeros)
-    __device__ void fetch(const float* __restrict__ Xn, const ConvGeom& g, const ColTGeom<TILE>& c,
+    // positions p0 .. p0 + BK of the image behind rs; np = number of valid positions (0: zeros)
+    __device__ void fetch(__amdgpu_buffer_rsrc_t rs, const ConvGeom& g, const ColTGeom<TILE>& c,
                           int p0, int np, int tid) {
+        const int pq = 4 * (tid % (BK / 4));
 #pragma unroll
-        for (int k = 0; k < CH; ++k) {
-            const int pq = 4 * ((tid + k * NTHREADS) % (BK / 4));
+        for (int e = 0; e < 4; ++e) {
+            const int p = p0 + pq + e;
+            const int oh = (int)fdiv((uint32_t)p, g.f_ow), ow = p - oh * g.OW;
+            const int hs = oh * g.stride, ws = ow * g.stride;
+            const int pix = 4 * (hs * g.W + ws);
+            const bool pin = pq + e < np;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int p = p0 + pq + e;
-                const int oh = (int)fdiv((uint32_t)p, g.f_ow), ow = p - oh * g.OW;
-                const int h = oh * g.stride + c.dh[k], w = ow * g.stride + c.dw[k];
-                const bool in = pq + e < np && (unsigned)h < (unsigned)g.H && (unsigned)w < (unsigned)g.W;
-                v[k][e] = *(in ? Xn + c.xoff[k] + h * g.W + w : g_zero4);
+            for (int k = 0; k < CH; ++k) {
+                const int h = hs + c.dh[k], w = ws + c.dw[k];
+                const bool in = pin && (unsigned)h < (unsigned)g.H && (unsigned)w < (unsigned)g.W;
+                const uint32_t off = in ? (uint32_t)(c.tap[k] + pix) : CONV_OOB;
+                v[k][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
             }
         }
     }
@@ -515,7 +532,9 @@ conv_wgrad_kernel(int Cout, int P, int R, const float* __restrict__ dY, const fl
         const int p0 = live ? (s - n * nkp) * BK : 0;
         const int np = live ? min(BK, P - p0) : 0;
         sa[set].fetch(dY + (size_t)n * Cout * P, P, m0, p0, Cout, live ? P : 0, tid);
-        sb[set].fetch(X + (size_t)n * plane, g, cg, p0, np, tid);
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(X) + (size_t)n * plane, 0, (int)(4 * plane), 0x00020000);
+        sb[set].fetch(xr, g, cg, p0, np, tid);
     };
 
     f32x16 acc[NB][NB];
@@ -820,7 +839,7 @@ extern "C" int dh_conv2d_fwd(const float* X, const float* Kn, const float* bias,
     if (N == 0) return DH_OK;
     if (!X || !Kn || !Y) return set_error(DH_ERR_INVALID, "dh_conv2d_fwd: null pointer");
     if (P >= (1ll << 30) || R >= (1ll << 30) || (long long)H * W >= (1ll << 30) ||
-        (long long)Cout * P >= (1ll << 31))
+        (long long)Cout * P >= (1ll << 31) || 4ll * Cin * H * W >= (long long)CONV_OOB)
         return set_error(DH_ERR_UNSUPPORTED, "dh_conv2d_fwd: plane or window too large");
     ConvGeom g{Cin, H, W, KH, KW, pad, pad, stride, OH, OW, make_fastdiv((uint32_t)OW),
                make_fastdiv((uint32_t)KW), make_fastdiv((uint32_t)(KH * KW))};
@@ -849,7 +868,7 @@ extern "C" int dh_conv2d_bwd_data(const float* dY, const float* Kn, float* dX, i
     if (N == 0) return DH_OK;
     if (!dY || !Kn || !dX) return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_data: null pointer");
     if (P >= (1ll << 30) || R >= (1ll << 30) || (long long)OH * OW >= (1ll << 30) ||
-        (long long)Cin * P >= (1ll << 31))
+        (long long)Cin * P >= (1ll << 31) || 4ll * Cout * OH * OW >= (long long)CONV_OOB)
         return set_error(DH_ERR_UNSUPPORTED, "dh_conv2d_bwd_data: plane or window too large");
     float* Kt = static_cast<float*>(dh_malloc((size_t)Cin * R * sizeof(float)));
     if (!Kt) return set_error(DH_ERR_OOM, "dh_conv2d_bwd_data: flipped kernel");
@@ -886,7 +905,7 @@ extern "C" int dh_conv2d_bwd_filter(const float* dY, const float* X, float* dK, 
     if (!dK) return set_error(DH_ERR_INVALID, "dh_conv2d_bwd_filter: null pointer");
     if (P >= (1ll << 30) || R >= (1ll << 30) || (long long)H * W >= (1ll << 30) ||
         (long long)Cout * P >= (1ll << 31) || (long long)Cout * R >= (1ll << 31) ||
-        (long long)Cin * H * W >= (1ll << 31))
+        4ll * Cin * H * W >= (long long)CONV_OOB)
         return set_error(DH_ERR_UNSUPPORTED, "dh_conv2d_bwd_filter: plane or window too large");
     if (N == 0)   // an empty sum: dK = 0, or unchanged with accumulate
         return accumulate ? DH_OK : dh_memset(dK, 0, (size_t)Cout * R * sizeof(float));
