@@ -59,9 +59,9 @@ __device__ inline f32x4 load4(const float* __restrict__ p, int ld, int rows, int
 // TILE = tile extent along the non-k dimension (64, 128 or 256).  The k-major LDS rows are
 // padded by 4 floats, which puts the 4 k-rows a transposing store touches 16 banks apart:
 // conflict-free for every TILE.
-template <bool KCONTIG, bool VEC, int TILE>
+template <bool KCONTIG, bool VEC, int TILE, int BKT = BK, int NT = NTHREADS>
 struct Slice {
-    static constexpr int CH = TILE * BK / 4 / NTHREADS;   // float4 per thread per slice
+    static constexpr int CH = TILE * BKT / 4 / NT;   // float4 per thread per slice
     f32x4 v[CH];
 
     // base/ld describe the stored matrix; t0 = first index along the tile dimension,
@@ -70,9 +70,9 @@ struct Slice {
                           int extent_k, int tid) {
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
-            const int f = tid + r * NTHREADS;
+            const int f = tid + r * NT;
             if (KCONTIG) {   // stored [t][k]: 4 k per float4
-                const int t = f / (BK / 4), kq = f % (BK / 4);
+                const int t = f / (BKT / 4), kq = f % (BKT / 4);
                 v[r] = load4<VEC>(base, ld, extent_t, extent_k, t0 + t, k0 + 4 * kq);
             } else {         // stored [k][t]: 4 t per float4
                 const int k = f / (TILE / 4), tq = f % (TILE / 4);
@@ -83,9 +83,9 @@ struct Slice {
     __device__ void store(float* lds, int stride, int tid) const {
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
-            const int f = tid + r * NTHREADS;
+            const int f = tid + r * NT;
             if (KCONTIG) {
-                const int t = f / (BK / 4), kq = f % (BK / 4);
+                const int t = f / (BKT / 4), kq = f % (BKT / 4);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) lds[(4 * kq + e) * stride + t] = v[r][e];
             } else {
@@ -217,6 +217,106 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
                 }
             }
         }
+}
+
+// 64 x 64 tiles with two waves per SIMD: for grids of about one work-group per CU (config 1's
+// 1024^3, a layer's forward) one wave per SIMD leaves the matrix core idle across each
+// slice's LDS stores, barrier and fragment reads.  Here 8 waves share a 64 x 64 tile: 32-wide
+// k-slices, waves w and w + 4 own the same 32 x 32 block and take the slice's first and second
+// 16 k; at the end waves 4..7 hand their sums to waves 0..3 through LDS (fixed order), which
+// run the epilogue.
+constexpr int KS_NT = 512, KS_BK = 32;
+
+template <bool TA, bool TB, bool VA, bool VB>
+__global__ void __launch_bounds__(KS_NT)
+gemm_f32_ks_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
+                   const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
+                   long long sA, long long sB, long long sC, const float* __restrict__ bias,
+                   int epi) {
+    A += blockIdx.y * sA;
+    B += blockIdx.y * sB;
+    C += blockIdx.y * sC;
+    constexpr int T = 64, LDS_A = T + 4, LDS_B = T + 4;
+    __shared__ __attribute__((aligned(16))) float As[2][KS_BK * LDS_A];
+    __shared__ __attribute__((aligned(16))) float Bs[2][KS_BK * LDS_B];
+
+    const int tiles_m = (M + T - 1) / T, tiles_n = (N + T - 1) / T;
+    int tm, tn;
+    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
+    const int m0 = tm * T, n0 = tn * T;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    const int blk = wave & 3, kh0 = (wave >> 2) * (KS_BK / 2);
+    const int wm = (blk >> 1) * 32, wn = (blk & 1) * 32;
+
+    Slice<!TA, VA, T, KS_BK, KS_NT> sa[2];
+    Slice<TB, VB, T, KS_BK, KS_NT> sb[2];
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+
+    const int nk = (K + KS_BK - 1) / KS_BK;
+    if (nk > 0) {
+        sa[0].fetch(A, lda, m0, 0, M, K, tid);
+        sb[0].fetch(B, ldb, n0, 0, N, K, tid);
+        sa[1].fetch(A, lda, m0, KS_BK, M, K, tid);
+        sb[1].fetch(B, ldb, n0, KS_BK, N, K, tid);
+        sa[0].store(As[0], LDS_A, tid);
+        sb[0].store(Bs[0], LDS_B, tid);
+        __syncthreads();
+    }
+    auto mma = [&](const float* as, const float* bs) {   // this wave's half of a k-slice
+#pragma unroll
+        for (int kk = 0; kk < KS_BK / 2; kk += 2) {
+            const float av = as[(kh0 + kk + h) * LDS_A + wm + l32];
+            const float bv = bs[(kh0 + kk + h) * LDS_B + wn + l32];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+        }
+    };
+    auto step = [&](auto cur_c, int kt) {
+        constexpr int cur = decltype(cur_c)::value;
+        sa[cur].fetch(A, lda, m0, (kt + 2) * KS_BK, M, K, tid);
+        sb[cur].fetch(B, ldb, n0, (kt + 2) * KS_BK, N, K, tid);
+        mma(As[cur], Bs[cur]);
+        sa[cur ^ 1].store(As[cur ^ 1], LDS_A, tid);
+        sb[cur ^ 1].store(Bs[cur ^ 1], LDS_B, tid);
+        __syncthreads();
+    };
+    if (nk == 1) {
+        mma(As[0], Bs[0]);
+        __syncthreads();
+    } else {
+        for (int kt = 0; kt < nk; kt += 2) {
+            step(std::integral_constant<int, 0>{}, kt);
+            step(std::integral_constant<int, 1>{}, kt + 1);
+        }
+    }
+    // waves 4..7 -> LDS (lane-major, conflict free; As is free after the loop's last barrier)
+    float* red = &As[0][0];
+    if (wave >= 4) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[(blk * 16 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave >= 4) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += red[(blk * 16 + r) * 64 + lane];
+
+    const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS), relu = epi & DH_EPI_RELU;
+    const int col = n0 + wn + l32;
+    if (col >= N) return;
+    const float bcol = bias && !row_bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (row < M) {
+            float* c = C + (size_t)row * ldc + col;
+            float v = (beta == 0.f ? acc[r] : acc[r] + beta * *c) + (row_bias ? bias[row] : bcol);
+            if (relu) v = v < 0.f ? 0.f : v;
+            *c = v;
+        }
+    }
 }
 
 // ---- conv2d forward as an implicit GEMM ---------------------------------------------
@@ -745,6 +845,27 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
 // fp32 1024^3 43.2 -> 30.7 us; 4096 x 257 x 784 67 -> 41 us; 4096 x 784 x 257 48 -> 42 us;
 // 4096 x 10 x 257 43 -> 15 us; 257 x 10 x 4096 31 -> 18 us.
 template <bool TA, bool TB>
+int launch_ks(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
+              float* C, int ldc, const Batch& bt) {
+    const int ca = TA ? M : K, cb = TB ? K : N;
+    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0) && (bt.sA % 4 == 0) && (ca % 4 == 0);
+    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0) && (bt.sB % 4 == 0) && (cb % 4 == 0);
+    auto kern = va && vb ? gemm_f32_ks_kernel<TA, TB, true, true>
+              : va       ? gemm_f32_ks_kernel<TA, TB, true, false>
+              : vb       ? gemm_f32_ks_kernel<TA, TB, false, true>
+                         : gemm_f32_ks_kernel<TA, TB, false, false>;
+    const int tiles = ((M + 63) / 64) * ((N + 63) / 64);
+    for (int b0 = 0; b0 < bt.count; b0 += 65535) {
+        const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
+        kern<<<dim3(tiles, nb), KS_NT, 0, stream()>>>(M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB,
+                                                       ldb, beta, C + b0 * bt.sC, ldc, bt.sA,
+                                                       bt.sB, bt.sC, bt.bias, bt.epi);
+        DH_TRY(check_launch("dh_gemm_f32(64x64, 8 waves)"));
+    }
+    return DH_OK;
+}
+
+template <bool TA, bool TB>
 int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
            float* C, int ldc, const Batch& bt) {
     const int cus = num_cus();
@@ -757,8 +878,16 @@ int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb
         return launch_tiles<TA, TB, 256, 64>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
     }
     const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * bt.count;
-    if (t128 < cus && 2 * t64 > cus)
+    if (t128 < cus && 2 * t64 > cus) {
+        // At most one work-group per CU and a contraction of several 32-wide slices: two
+        // waves per SIMD on each tile (config 1, 1024^3: 0.0316 -> 0.0296 ms).  With more
+        // work-groups than CUs the second work-group of a CU already fills the gaps (config
+        // 2's first layer, 320 tiles: 0.0382 -> 0.0406 ms with this kernel), and short
+        // contractions (K = 10: 0.0058 -> 0.0070 ms) do not amortise the wide slices.
+        if (t64 <= cus && K >= 256)
+            return launch_ks<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
         return launch_tiles<TA, TB, 64, 64>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    }
     return launch_tiles<TA, TB, 128, 128>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 

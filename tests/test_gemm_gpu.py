@@ -387,3 +387,17 @@ def test_fp32_64x64_tiles(Bt, M, N, K, ta, tb):
     # k-slice (K = 7); beta and a per-column bias with ReLU through the epilogue.
     got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.5, relu=True, seed=M + N + K + ta + 2 * tb)
     assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+@pytest.mark.parametrize("Bt,M,N,K", [(1, 1000, 1000, 300), (1, 999, 1001, 257), (2, 512, 900, 512),
+                                      (1, 1024, 960, 1000)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("row_bias", [False, True])
+def test_fp32_64x64_two_waves_per_simd(Bt, M, N, K, ta, tb, row_bias):
+    # At most one 64 x 64 tile per CU (256 on MI355X) and K >= 256: the 8-wave kernel, two
+    # waves per 32 x 32 block splitting each 32-wide k-slice and reducing through LDS.
+    # Ragged M / N, K not a multiple of 32 (300, 1000) or of 4 (257: scalar loads), batched,
+    # all layouts, beta and either bias orientation with ReLU.
+    got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.5, relu=True, row_bias=row_bias,
+                   seed=M + N + K + ta + 2 * tb + row_bias)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
