@@ -15,6 +15,8 @@
 // (Q, dO in launch 2; K, V in launch 3) arrive by direct-to-LDS DMA in 4-deep rings and
 // the transposed operands come from the same tiles through transpose reads; fp32: tiles
 // are staged through registers into row-major LDS.
+#include <mutex>
+
 #include "dh_common.hpp"
 
 namespace dh {
@@ -29,6 +31,25 @@ __device__ inline uint32_t cvt_pk_bf16(float a, float b) {
     typedef float f2 __attribute__((ext_vector_type(2)));
     typedef __bf16 b2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));   // RNE
+}
+
+// dK/dV epilogue store of one lane's 4 columns.  kv_alias: dK and dV are the same buffer
+// (K and V are one tensor, e.g. attention(q, q, q)); it then receives dK + dV (+ its old
+// contents), the sum the reference's per-input "+=" leaves there (autograd.inc:693-728).
+__device__ inline void store_dkdv(float* dk, float* dv, f32x4 a, f32x4 b, int accumulate,
+                                  int kv_alias) {
+    if (kv_alias) {
+        a += b;
+        if (accumulate) a += *reinterpret_cast<const f32x4*>(dk);
+        *reinterpret_cast<f32x4*>(dk) = a;
+        return;
+    }
+    if (accumulate) {
+        a += *reinterpret_cast<const f32x4*>(dk);
+        b += *reinterpret_cast<const f32x4*>(dv);
+    }
+    *reinterpret_cast<f32x4*>(dk) = a;
+    *reinterpret_cast<f32x4*>(dv) = b;
 }
 
 // ---------------------------------------------------------------------------------
@@ -162,7 +183,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
                      const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                      const uint16_t* __restrict__ dO, const float* __restrict__ L2,
                      const float* __restrict__ Dv, float* __restrict__ dK,
-                     float* __restrict__ dV, int accumulate) {
+                     float* __restrict__ dV, int accumulate, int kv_alias) {
     using T = BwTile<D, KV_BQ>;
     using R = BwTile<D, KV_KEYS>;                    // resident K, V of the work-group's keys
     constexpr int ND = D / 32, NTK = D / 16;
@@ -426,12 +447,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
             f32x4 a = {dkacc[d][4 * q] * scale, dkacc[d][4 * q + 1] * scale,
                        dkacc[d][4 * q + 2] * scale, dkacc[d][4 * q + 3] * scale};
             f32x4 b = {dvacc[d][4 * q], dvacc[d][4 * q + 1], dvacc[d][4 * q + 2], dvacc[d][4 * q + 3]};
-            if (accumulate) {
-                a += *reinterpret_cast<const f32x4*>(dkr + col);
-                b += *reinterpret_cast<const f32x4*>(dvr + col);
-            }
-            *reinterpret_cast<f32x4*>(dkr + col) = a;
-            *reinterpret_cast<f32x4*>(dvr + col) = b;
+            store_dkdv(dkr + col, dvr + col, a, b, accumulate, kv_alias);
         }
 }
 
@@ -675,7 +691,7 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
                     const float* __restrict__ K, const float* __restrict__ V,
                     const float* __restrict__ dO, const float* __restrict__ LSE,
                     const float* __restrict__ Dv, float* __restrict__ dK,
-                    float* __restrict__ dV, int accumulate) {
+                    float* __restrict__ dV, int accumulate, int kv_alias) {
     using Tl = Tile32<D>;
     constexpr int ND = D / 32, NDQ = D / 4;
     extern __shared__ __attribute__((aligned(16))) float fsm[];
@@ -789,12 +805,7 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
                        dkacc[d][4 * q + 2] * scale, dkacc[d][4 * q + 3] * scale};
             f32x4 b = {dvacc[d][4 * q], dvacc[d][4 * q + 1], dvacc[d][4 * q + 2],
                        dvacc[d][4 * q + 3]};
-            if (accumulate) {
-                a += *reinterpret_cast<const f32x4*>(dkr + col);
-                b += *reinterpret_cast<const f32x4*>(dvr + col);
-            }
-            *reinterpret_cast<f32x4*>(dkr + col) = a;
-            *reinterpret_cast<f32x4*>(dvr + col) = b;
+            store_dkdv(dkr + col, dvr + col, a, b, accumulate, kv_alias);
         }
 }
 
@@ -919,7 +930,7 @@ int set_lds(Kern kern, size_t bytes, bool& done) {
 template <int D, bool CAUSAL>
 int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const void* V,
              const void* dO, const float* L2, const float* Dv, float* dQ, float* dK, float* dV,
-             int acc) {
+             int acc, int kv_alias, int acc_q) {
     const float sl2 = scale * 1.4426950408889634f;
     {
         auto kern = bwd_dkdv_bf16_kernel<D, CAUSAL>;
@@ -930,7 +941,7 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
         const int grid = BH * ((S + KV_KEYS - 1) / KV_KEYS);
         kern<<<grid, KV_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
                                              (const uint16_t*)K, (const uint16_t*)V,
-                                             (const uint16_t*)dO, L2, Dv, dK, dV, acc);
+                                             (const uint16_t*)dO, L2, Dv, dK, dV, acc, kv_alias);
         DH_TRY(check_launch("dh_flash_bwd(dK,dV bf16)"));
     }
     {
@@ -941,7 +952,7 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
         const int grid = BH * ((S + DQ_ROWS - 1) / DQ_ROWS);
         kern<<<grid, DQ_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
                                              (const uint16_t*)K, (const uint16_t*)V,
-                                             (const uint16_t*)dO, L2, Dv, dQ, acc);
+                                             (const uint16_t*)dO, L2, Dv, dQ, acc_q);
         DH_TRY(check_launch("dh_flash_bwd(dQ bf16)"));
     }
     return DH_OK;
@@ -950,7 +961,7 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
 template <int D, bool CAUSAL>
 int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void* V,
             const void* dO, const float* LSE, const float* Dv, float* dQ, float* dK, float* dV,
-            int acc) {
+            int acc, int kv_alias, int acc_q) {
     using Tl = Tile32<D>;
     const float sl2 = scale * 1.4426950408889634f;
     const int tiles = (S + 127) / 128;
@@ -961,7 +972,7 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
         DH_TRY(set_lds(kern, lds, done));
         kern<<<BH * tiles, NT, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,
                                                 (const float*)K, (const float*)V,
-                                                (const float*)dO, LSE, Dv, dK, dV, acc);
+                                                (const float*)dO, LSE, Dv, dK, dV, acc, kv_alias);
         DH_TRY(check_launch("dh_flash_bwd(dK,dV f32)"));
     }
     {
@@ -970,7 +981,7 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
         DH_TRY(set_lds(kern, lds, done));
         kern<<<BH * tiles, NT, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,
                                                 (const float*)K, (const float*)V,
-                                                (const float*)dO, LSE, Dv, dQ, acc);
+                                                (const float*)dO, LSE, Dv, dQ, acc_q);
         DH_TRY(check_launch("dh_flash_bwd(dQ f32)"));
     }
     return DH_OK;
@@ -988,17 +999,17 @@ int run_dvec(int rows, const void* O, const void* dO, float* Dv, const float* LS
 template <int D>
 int dispatch(int dtype, int causal, int BH, int S, float scale, const void* Q, const void* K,
              const void* V, const void* O, const void* dO, const float* LSE, float* Dv,
-             float* dQ, float* dK, float* dV, int acc) {
+             float* dQ, float* dK, float* dV, int acc, int kv_alias, int acc_q) {
     const int rows = BH * S;
     if (dtype == DH_BF16) {
         float* L2 = Dv + rows;                       // second half of the scratch
         DH_TRY((run_dvec<uint16_t, D>(rows, O, dO, Dv, LSE, L2)));
-        return causal ? run_bf16<D, true>(BH, S, scale, Q, K, V, dO, L2, Dv, dQ, dK, dV, acc)
-                      : run_bf16<D, false>(BH, S, scale, Q, K, V, dO, L2, Dv, dQ, dK, dV, acc);
+        return causal ? run_bf16<D, true>(BH, S, scale, Q, K, V, dO, L2, Dv, dQ, dK, dV, acc, kv_alias, acc_q)
+                      : run_bf16<D, false>(BH, S, scale, Q, K, V, dO, L2, Dv, dQ, dK, dV, acc, kv_alias, acc_q);
     }
     DH_TRY((run_dvec<float, D>(rows, O, dO, Dv, LSE, nullptr)));
-    return causal ? run_f32<D, true>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc)
-                  : run_f32<D, false>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc);
+    return causal ? run_f32<D, true>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc, kv_alias, acc_q)
+                  : run_f32<D, false>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc, kv_alias, acc_q);
 }
 
 }  // namespace
@@ -1006,11 +1017,14 @@ int dispatch(int dtype, int causal, int BH, int S, float scale, const void* Q, c
 
 using namespace dh;
 
-extern "C" int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int causal,
-                            const void* Q, const void* K, const void* V, const void* O,
-                            const void* dO, const float* LSE, float* dQ, float* dK, float* dV,
-                            int accumulate) {
-    DH_TRY(ensure_init());
+namespace {
+
+// Argument checks shared by the entry points.  Any two of dQ, dK, dV may be the same buffer
+// (one tensor passed as two or three of Q, K, V); buffers that overlap without being equal are
+// rejected.
+int check_bwd_args(int dtype, int BH, int S, int D, const void* Q, const void* K,
+                   const void* V, const void* O, const void* dO, const float* LSE,
+                   const float* dQ, const float* dK, const float* dV) {
     if (BH < 0 || S < 0) return set_error(DH_ERR_INVALID, "dh_flash_bwd: negative shape");
     if (BH == 0 || S == 0) return DH_OK;
     if (!Q || !K || !V || !O || !dO || !LSE || !dQ || !dK || !dV)
@@ -1021,15 +1035,53 @@ extern "C" int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int ca
         return set_error(DH_ERR_UNSUPPORTED, "dh_flash_bwd: dtype %d", dtype);
     for (const void* p : {Q, K, V, O, dO, (const void*)dQ, (const void*)dK, (const void*)dV})
         if ((uintptr_t)p % 16) return set_error(DH_ERR_INVALID, "dh_flash_bwd: 16-byte alignment");
+    const uintptr_t bytes = (uintptr_t)BH * S * D * sizeof(float);
+    const float* g[3] = {dQ, dK, dV};
+    for (int a = 0; a < 3; ++a)
+        for (int b = a + 1; b < 3; ++b) {
+            const uintptr_t x = (uintptr_t)g[a], y = (uintptr_t)g[b];
+            if (x != y && x < y + bytes && y < x + bytes)
+                return set_error(DH_ERR_INVALID,
+                                 "dh_flash_bwd: gradient buffers overlap without being equal");
+        }
+    return DH_OK;
+}
+
+// The three or four launches over caller-supplied scratch Dv (BH*S floats, twice that for
+// bf16).  The dK/dV launch runs before the dQ launch on the same stream, so a dQ buffer shared
+// with dK or dV accumulates onto what that launch stored.
+int run_bwd(int dtype, int BH, int S, int D, float scale, int causal, const void* Q,
+            const void* K, const void* V, const void* O, const void* dO, const float* LSE,
+            float* dQ, float* dK, float* dV, int accumulate, float* Dv) {
+    const int kv_alias = dK == dV;
+    const int acc_q = accumulate || dQ == dK || dQ == dV;
+    if (D == 128)
+        return dispatch<128>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV,
+                             accumulate, kv_alias, acc_q);
+    if (D == 64)
+        return dispatch<64>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV,
+                            accumulate, kv_alias, acc_q);
+    return dispatch<32>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV,
+                        accumulate, kv_alias, acc_q);
+}
+
+}  // namespace
+
+extern "C" int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int causal,
+                            const void* Q, const void* K, const void* V, const void* O,
+                            const void* dO, const float* LSE, float* dQ, float* dK, float* dV,
+                            int accumulate) {
+    DH_TRY(ensure_init());
+    DH_TRY(check_bwd_args(dtype, BH, S, D, Q, K, V, O, dO, LSE, dQ, dK, dV));
+    if (BH == 0 || S == 0) return DH_OK;
     // Scratch from the pool: Dvec (BH*S floats) and, for bf16, LSE*log2(e) (BH*S floats);
     // returned to the pool once the work is queued (later users of the buffer are ordered
     // after these kernels on the same stream).
     float* Dv = (float*)dh_malloc((size_t)BH * S * sizeof(float) * (dtype == DH_BF16 ? 2 : 1));
     if (!Dv) return DH_ERR_OOM;
-    int st;
-    if (D == 128) st = dispatch<128>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV, accumulate);
-    else if (D == 64) st = dispatch<64>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV, accumulate);
-    else st = dispatch<32>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV, accumulate);
+    const int st = run_bwd(dtype, BH, S, D, scale, causal, Q, K, V, O, dO, LSE, dQ, dK, dV,
+                           accumulate, Dv);
     dh_free(Dv);
     return st;
 }
+

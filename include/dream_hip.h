@@ -156,7 +156,12 @@ int dh_flash_fwd(int dtype, int BH, int S, int D, float scale, int causal,
                  void* d_O, float* d_LSE);
 /* Backward of dh_flash_fwd given its O and LSE (runtime/ops/autograd.inc:779-840).
  * dQ, dK, dV are fp32 (B, S*D).  accumulate = 1 adds into them (the reference
- * backward's "+="), 0 overwrites.  Deterministic: no floating-point atomics. */
+ * backward's "+="), 0 overwrites.  Any two of dQ, dK, dV may be the same buffer (one
+ * tensor passed as several of Q, K, V): that buffer then receives the sum of the
+ * gradients aimed at it, as the reference's per-input "+=" leaves it
+ * (autograd.inc:693-728); buffers that overlap without being equal are DH_ERR_INVALID.
+ * Deterministic: no floating-point atomics.  Scratch (BH*S floats, twice that for bf16)
+ * comes from the pool. */
 int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int causal,
                  const void* d_Q, const void* d_K, const void* d_V,
                  const void* d_O, const void* d_dO, const float* d_LSE,

@@ -226,33 +226,46 @@ void sdpa_slice(const double* Q, const double* K, const double* V, double* O,
         for (int j = 0; j < jn; ++j) { p[j] = std::exp(p[j] - mx); sum += p[j]; }
         for (int j = 0; j < jn; ++j) p[j] /= sum;
     }
+    // O = P V; each O[i][k] sums over j in ascending order (the loop over k is innermost
+    // only so that rows are read contiguously).
     for (int i = 0; i < S; ++i) {
         const int jn = causal ? i + 1 : S;
-        for (int k = 0; k < dk; ++k) {
-            double s = 0.0;
-            for (int j = 0; j < jn; ++j) s += P[(size_t)i * S + j] * V[(size_t)j * dk + k];
-            O[(size_t)i * dk + k] = s;
+        double* o = O + (size_t)i * dk;
+        for (int k = 0; k < dk; ++k) o[k] = 0.0;
+        for (int j = 0; j < jn; ++j) {
+            const double p = P[(size_t)i * S + j];
+            const double* v = V + (size_t)j * dk;
+            for (int k = 0; k < dk; ++k) o[k] += p * v[k];
         }
     }
 }
 
 }  // namespace
 
+// Slices are independent; they run in parallel, each with the single-slice loop order.
 void orc_attention(const double* Q, const double* K, const double* V, double* O,
                    int B, int S, int dk) {
-    std::vector<double> P;
-    for (int b = 0; b < B; ++b) {
-        const size_t off = (size_t)b * S * dk;
-        sdpa_slice(Q + off, K + off, V + off, O + off, S, dk, false, P);
+#pragma omp parallel
+    {
+        std::vector<double> P;
+#pragma omp for schedule(dynamic, 1)
+        for (int b = 0; b < B; ++b) {
+            const size_t off = (size_t)b * S * dk;
+            sdpa_slice(Q + off, K + off, V + off, O + off, S, dk, false, P);
+        }
     }
 }
 
 void orc_attention_causal(const double* Q, const double* K, const double* V, double* O,
                           int B, int S, int dk) {
-    std::vector<double> P;
-    for (int b = 0; b < B; ++b) {
-        const size_t off = (size_t)b * S * dk;
-        sdpa_slice(Q + off, K + off, V + off, O + off, S, dk, true, P);
+#pragma omp parallel
+    {
+        std::vector<double> P;
+#pragma omp for schedule(dynamic, 1)
+        for (int b = 0; b < B; ++b) {
+            const size_t off = (size_t)b * S * dk;
+            sdpa_slice(Q + off, K + off, V + off, O + off, S, dk, true, P);
+        }
     }
 }
 
@@ -300,48 +313,114 @@ void orc_attention_bwd(const double* Q, const double* K, const double* V, const 
                        double* dQ, double* dK, double* dV, int B, int S, int dk, int causal) {
     // autograd.inc:675-778.  P recomputed; dV = P^T dO; dP = dO V^T;
     // dS = P o (dP - rowsum(dP o P)); dQ += dS K * scale; dK += dS^T Q * scale.
+    // Every output element sums its terms in ascending order of the contracted index; the
+    // innermost loop runs over the head dim so that rows are read contiguously.  Slices are
+    // independent and run in parallel.
     const double scale = 1.0 / std::sqrt((double)dk);
-    std::vector<double> P, dP((size_t)S * S), dS((size_t)S * S), O((size_t)S * dk);
-    for (int b = 0; b < B; ++b) {
-        const size_t off = (size_t)b * S * dk;
-        const double *Qb = Q + off, *Kb = K + off, *Vb = V + off, *dOb = dO + off;
-        double *dQb = dQ + off, *dKb = dK + off, *dVb = dV + off;
-        sdpa_slice(Qb, Kb, Vb, O.data(), S, dk, causal != 0, P);
-        for (int j = 0; j < S; ++j)
-            for (int k = 0; k < dk; ++k) {
-                double s = 0.0;
-                for (int i = causal ? j : 0; i < S; ++i)
-                    s += P[(size_t)i * S + j] * dOb[(size_t)i * dk + k];
-                dVb[(size_t)j * dk + k] += s;
-            }
-        std::fill(dP.begin(), dP.end(), 0.0);
-        for (int i = 0; i < S; ++i) {
-            const int jn = causal ? i + 1 : S;
-            for (int j = 0; j < jn; ++j)
-                dP[(size_t)i * S + j] = dot(dOb + (size_t)i * dk, Vb + (size_t)j * dk, dk);
-        }
-        std::fill(dS.begin(), dS.end(), 0.0);
-        for (int i = 0; i < S; ++i) {
-            const int jn = causal ? i + 1 : S;
-            double rd = 0.0;
-            for (int j = 0; j < jn; ++j) rd += dP[(size_t)i * S + j] * P[(size_t)i * S + j];
-            for (int j = 0; j < jn; ++j)
-                dS[(size_t)i * S + j] = P[(size_t)i * S + j] * (dP[(size_t)i * S + j] - rd);
-        }
-        for (int i = 0; i < S; ++i)
-            for (int k = 0; k < dk; ++k) {
-                double s = 0.0;
+#pragma omp parallel
+    {
+        std::vector<double> P, dP((size_t)S * S), dS((size_t)S * S), O((size_t)S * dk),
+            acc((size_t)S * dk);
+#pragma omp for schedule(dynamic, 1)
+        for (int b = 0; b < B; ++b) {
+            const size_t off = (size_t)b * S * dk;
+            const double *Qb = Q + off, *Kb = K + off, *Vb = V + off, *dOb = dO + off;
+            double *dQb = dQ + off, *dKb = dK + off, *dVb = dV + off;
+            sdpa_slice(Qb, Kb, Vb, O.data(), S, dk, causal != 0, P);
+            // dV[j] += sum_i P[i][j] dO[i]   (i ascending)
+            std::fill(acc.begin(), acc.end(), 0.0);
+            for (int i = 0; i < S; ++i)
+                for (int j = 0; j < (causal ? i + 1 : S); ++j) {
+                    const double p = P[(size_t)i * S + j];
+                    const double* g = dOb + (size_t)i * dk;
+                    double* a = &acc[(size_t)j * dk];
+                    for (int k = 0; k < dk; ++k) a[k] += p * g[k];
+                }
+            for (size_t x = 0; x < (size_t)S * dk; ++x) dVb[x] += acc[x];
+            std::fill(dP.begin(), dP.end(), 0.0);
+            for (int i = 0; i < S; ++i) {
                 const int jn = causal ? i + 1 : S;
-                for (int j = 0; j < jn; ++j) s += dS[(size_t)i * S + j] * Kb[(size_t)j * dk + k];
-                dQb[(size_t)i * dk + k] += s * scale;
+                for (int j = 0; j < jn; ++j)
+                    dP[(size_t)i * S + j] = dot(dOb + (size_t)i * dk, Vb + (size_t)j * dk, dk);
             }
-        for (int j = 0; j < S; ++j)
-            for (int k = 0; k < dk; ++k) {
-                double s = 0.0;
-                for (int i = causal ? j : 0; i < S; ++i)
-                    s += dS[(size_t)i * S + j] * Qb[(size_t)i * dk + k];
-                dKb[(size_t)j * dk + k] += s * scale;
+            std::fill(dS.begin(), dS.end(), 0.0);
+            for (int i = 0; i < S; ++i) {
+                const int jn = causal ? i + 1 : S;
+                double rd = 0.0;
+                for (int j = 0; j < jn; ++j) rd += dP[(size_t)i * S + j] * P[(size_t)i * S + j];
+                for (int j = 0; j < jn; ++j)
+                    dS[(size_t)i * S + j] = P[(size_t)i * S + j] * (dP[(size_t)i * S + j] - rd);
             }
+            // dQ[i] += scale * sum_j dS[i][j] K[j]   (j ascending)
+            for (int i = 0; i < S; ++i) {
+                const int jn = causal ? i + 1 : S;
+                double* a = &acc[(size_t)i * dk];
+                for (int k = 0; k < dk; ++k) a[k] = 0.0;
+                for (int j = 0; j < jn; ++j) {
+                    const double d = dS[(size_t)i * S + j];
+                    const double* kr = Kb + (size_t)j * dk;
+                    for (int k = 0; k < dk; ++k) a[k] += d * kr[k];
+                }
+                for (int k = 0; k < dk; ++k) dQb[(size_t)i * dk + k] += a[k] * scale;
+            }
+            // dK[j] += scale * sum_i dS[i][j] Q[i]   (i ascending)
+            std::fill(acc.begin(), acc.end(), 0.0);
+            for (int i = 0; i < S; ++i)
+                for (int j = 0; j < (causal ? i + 1 : S); ++j) {
+                    const double d = dS[(size_t)i * S + j];
+                    const double* q = Qb + (size_t)i * dk;
+                    double* a = &acc[(size_t)j * dk];
+                    for (int k = 0; k < dk; ++k) a[k] += d * q[k];
+                }
+            for (size_t x = 0; x < (size_t)S * dk; ++x) dKb[x] += acc[x] * scale;
+        }
+    }
+}
+
+void orc_attention_rows(const double* Q, const double* K, const double* V, const double* dO,
+                        const int* rows, int nrows, double* O_rows, double* dQ_rows, int B,
+                        int S, int dk, int causal) {
+    // One query row i at a time, the operations of sdpa_slice (training.inc:196-217,
+    // 235-260) and of orc_attention_bwd's dQ (autograd.inc:675-778) restricted to that row:
+    // scores, max-subtracted exp, divide by the sum, O_i = sum_j P_ij V_j; dP_ij = dO_i . V_j,
+    // rd = sum_j dP_ij P_ij, dS_ij = P_ij (dP_ij - rd), dQ_i = scale * sum_j dS_ij K_j.
+    const double scale = 1.0 / std::sqrt((double)dk);
+#pragma omp parallel
+    {
+        std::vector<double> p((size_t)S), ds((size_t)S), acc((size_t)dk);
+#pragma omp for schedule(dynamic, 1)
+        for (int b = 0; b < B; ++b) {
+            const size_t off = (size_t)b * S * dk;
+            const double *Qb = Q + off, *Kb = K + off, *Vb = V + off, *dOb = dO + off;
+            for (int r = 0; r < nrows; ++r) {
+                const int i = rows[(size_t)b * nrows + r];
+                const int jn = causal ? i + 1 : S;
+                double mx = -1e30;
+                for (int j = 0; j < jn; ++j) {
+                    p[j] = dot(Qb + (size_t)i * dk, Kb + (size_t)j * dk, dk) * scale;
+                    if (p[j] > mx) mx = p[j];
+                }
+                double sum = 0.0;
+                for (int j = 0; j < jn; ++j) { p[j] = std::exp(p[j] - mx); sum += p[j]; }
+                for (int j = 0; j < jn; ++j) p[j] /= sum;
+                double* o = O_rows + ((size_t)b * nrows + r) * dk;
+                for (int k = 0; k < dk; ++k) o[k] = 0.0;
+                for (int j = 0; j < jn; ++j)
+                    for (int k = 0; k < dk; ++k) o[k] += p[j] * Vb[(size_t)j * dk + k];
+                const double* g = dOb + (size_t)i * dk;
+                double rd = 0.0;
+                for (int j = 0; j < jn; ++j) {
+                    ds[j] = dot(g, Vb + (size_t)j * dk, dk);
+                    rd += ds[j] * p[j];
+                }
+                for (int j = 0; j < jn; ++j) ds[j] = p[j] * (ds[j] - rd);
+                for (int k = 0; k < dk; ++k) acc[k] = 0.0;
+                for (int j = 0; j < jn; ++j)
+                    for (int k = 0; k < dk; ++k) acc[k] += ds[j] * Kb[(size_t)j * dk + k];
+                double* q = dQ_rows + ((size_t)b * nrows + r) * dk;
+                for (int k = 0; k < dk; ++k) q[k] = acc[k] * scale;
+            }
+        }
     }
 }
 
@@ -414,11 +493,15 @@ void orc_flash_bwd(const double* Q, const double* K, const double* V, const doub
 void orc_flash_lse(const double* Q, const double* K, double* lse, int B, int S, int dk,
                    int causal) {
     const double scale = 1.0 / std::sqrt((double)dk);
-    std::vector<double> sc(64), m(S), l(S);
-    for (int b = 0; b < B; ++b) {
-        const size_t off = (size_t)b * S * dk;
-        row_stats(Q + off, K + off, S, dk, 64, causal != 0, scale, sc, m.data(), l.data());
-        for (int i = 0; i < S; ++i) lse[(size_t)b * S + i] = m[i] + std::log(l[i]);
+#pragma omp parallel
+    {
+        std::vector<double> sc(64), m(S), l(S);
+#pragma omp for schedule(dynamic, 1)
+        for (int b = 0; b < B; ++b) {
+            const size_t off = (size_t)b * S * dk;
+            row_stats(Q + off, K + off, S, dk, 64, causal != 0, scale, sc, m.data(), l.data());
+            for (int i = 0; i < S; ++i) lse[(size_t)b * S + i] = m[i] + std::log(l[i]);
+        }
     }
 }
 

@@ -12,7 +12,9 @@
  * like the reference backward branches do.
  *
  * Pinning status (what checks each function, see tests/test_oracle.py):
- *   orc_set_seed/orc_randn/orc_uniform/orc_kaiming   golden vectors from the reference build
+ *   orc_set_seed/orc_randn/orc_kaiming   golden vectors from the reference build
+ *   orc_uniform(_f32)   bit-exact vs an independent mt19937 stream through libstdc++'s
+ *                       generate_canonical; range and moments
  *   orc_gemm_ref_d      closed forms (all-ones -> K), identity, brute-force fp64 sums via numpy
  *   orc_gemm_d          golden vectors + gemm_ref_d (1e-11, the reference gate)
  *   orc_gemm_f32        golden vectors + fp64 on the same fp32 inputs (2e-4, the reference gate)
@@ -21,6 +23,7 @@
  *   orc_attention*, orc_flash_fwd, orc_flash_bwd      golden vectors + special cases
  *                       (S=1 -> O=V, constant K -> causal running mean) + finite differences
  *   orc_flash_lse       closed form log-sum-exp (scipy.special.logsumexp)
+ *   orc_attention_rows  the rows of orc_attention(_causal) / orc_attention_bwd's dQ
  *   orc_softmax_rows, orc_log_softmax_rows   golden vectors, scipy softmax / log_softmax, rows sum to 1
  *   orc_softmax_bwd, orc_log_softmax_bwd, orc_layer_norm(_bwd)   golden vectors + finite
  *                       differences + invariants (zero row sums, mean 0 / variance of layer norm)
@@ -87,6 +90,13 @@ void orc_attention_bwd(const double* Q, const double* K, const double* V, const 
                        double* dQ, double* dK, double* dV, int B, int S, int dk, int causal);
 void orc_flash_bwd(const double* Q, const double* K, const double* V, const double* dO,
                    double* dQ, double* dK, double* dV, int B, int S, int dk);
+/* orc_attention_rows : O and dQ of selected query rows, standard attention (causal or not):
+ * rows[b * nrows + r] is the r-th row taken from slice b; O_rows, dQ_rows are
+ * (B, nrows * dk).  The same operations as orc_attention(_causal) / orc_attention_bwd for
+ * those rows (training.inc:178-263, autograd.inc:675-778), O(S * dk) per row. */
+void orc_attention_rows(const double* Q, const double* K, const double* V, const double* dO,
+                        const int* rows, int nrows, double* O_rows, double* dQ_rows, int B,
+                        int S, int dk, int causal);
 
 /* Per-row natural-log log-sum-exp of the scaled scores, lse[b*S+i] = m_i + log(l_i),
  * from the (m, l) recurrence of pass 1 in autograd.inc:799-812 (causal) or the full row

@@ -43,6 +43,7 @@ def lib():
             "orc_flash_fwd": [_dp, _dp, _dp, _dp, _i, _i, _i, _i],
             "orc_attention_bwd": [_dp] * 7 + [_i, _i, _i, _i],
             "orc_flash_bwd": [_dp] * 7 + [_i, _i, _i],
+            "orc_attention_rows": [_dp, _dp, _dp, _dp, _ip, _i, _dp, _dp, _i, _i, _i, _i],
             "orc_flash_lse": [_dp, _dp, _dp, _i, _i, _i, _i],
             "orc_softmax_rows": [_dp, _dp, _i, _i],
             "orc_log_softmax_rows": [_dp, _dp, _i, _i],
@@ -187,6 +188,20 @@ def attention_bwd(Q, K, V, dO, B, S, dk, causal):
     lib().orc_attention_bwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(dO), _ptr(dQ), _ptr(dK), _ptr(dV),
                             B, S, dk, int(causal))
     return dQ, dK, dV
+
+
+def attention_rows(Q, K, V, dO, rows, B, S, dk, causal):
+    """O and dQ of the query rows rows[b] (an int array of shape (B, n)) of every slice:
+    returns two (B, n, dk) arrays."""
+    Q, K, V = _qkv(Q, K, V)
+    dO = _d(dO)
+    rows = np.ascontiguousarray(rows, np.int32)
+    n = rows.shape[1]
+    Orow, dQrow = np.zeros((B, n, dk)), np.zeros((B, n, dk))
+    lib().orc_attention_rows(_ptr(Q), _ptr(K), _ptr(V), _ptr(dO),
+                             rows.ctypes.data_as(_ip), n, _ptr(Orow), _ptr(dQrow), B, S, dk,
+                             int(causal))
+    return Orow, dQrow
 
 
 def flash_bwd(Q, K, V, dO, B, S, dk):

@@ -38,6 +38,69 @@ def test_rng_matches_reference_stream():
     assert np.array_equal(O.kaiming(16, 10), GOLD["rng_kaiming_s7_16x10"])
 
 
+def _mt19937_raw(seed, n):
+    """n raw 32-bit outputs of an independent mt19937: numpy's legacy RandomState seeds an
+    integer with init_genrand, the seeding of std::mt19937(seed)."""
+    return np.random.RandomState(seed)._bit_generator.random_raw(n).astype(np.uint64)
+
+
+def _round_f32(v):
+    """Exact rational v rounded to the nearest float32 (ties to even)."""
+    from fractions import Fraction
+    c = np.float32(float(v))
+    best = None
+    for x in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+        d = abs(Fraction(float(x)) - v)
+        key = (d, int(np.float32(x).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, x)
+    return np.float32(best[1])
+
+
+@pytest.mark.parametrize("lo,hi", [(0.0, 1.0), (-1.0, 1.0), (0.1, 10.0), (-2.5, 0.3)])
+def test_uniform_draws_follow_generate_canonical(lo, hi):
+    """orc_uniform / orc_uniform_f32 are std::uniform_real_distribution over the reference's
+    mt19937 (elementwise.inc:897, builtins.inc:158-160).  Restated independently: libstdc++'s
+    generate_canonical<T, digits> takes ceil(digits / 32) raw words, sum_i w_i 2^(32 i) / 2^(32 k)
+    (1.0 clamped to the largest value below it), then a + (b - a) r, fused into one rounding
+    by the reference's -ffast-math -mfma build.  Bit-exact on 2000 draws per seed."""
+    from fractions import Fraction
+    for seed in (1, 42, 20260707):
+        n = 2000
+        O.set_seed(seed)
+        got = O.uniform(n, lo, hi)
+        w = _mt19937_raw(seed, 2 * n)
+        r = (w[0::2].astype(np.float64) + w[1::2].astype(np.float64) * 2.0 ** 32) / 2.0 ** 64
+        r = np.where(r >= 1.0, np.nextafter(1.0, 0.0), r)
+        want = np.array([float(Fraction(x) * Fraction(hi - lo) + Fraction(lo)) for x in r])
+        assert np.array_equal(got, want), seed
+        # one word per float draw (24 digits <= 32)
+        lo32, hi32 = np.float32(lo), np.float32(hi)
+        O.set_seed(seed)
+        got32 = O.uniform_f32(n, lo32, hi32)
+        w = _mt19937_raw(seed, n)
+        r32 = w.astype(np.float32) / np.float32(2.0 ** 32)
+        r32 = np.where(r32 >= 1, np.nextafter(np.float32(1), np.float32(0)), r32)
+        span = Fraction(float(hi32 - lo32))
+        want32 = np.array([_round_f32(Fraction(float(x)) * span + Fraction(float(lo32)))
+                           for x in r32], np.float32)
+        assert np.array_equal(got32, want32), seed
+
+
+def test_uniform_draws_range_and_moments():
+    """10^6 draws: inside [lo, hi), mean and variance of U(lo, hi) within 5 sigma, and a
+    planted mistake (one word per double draw) breaks the bit-exact restatement."""
+    O.set_seed(7)
+    u = O.uniform(10 ** 6, -1.0, 3.0)
+    assert u.min() >= -1.0 and u.max() < 3.0
+    n, mu, var = u.size, 1.0, 16.0 / 12.0
+    assert abs(u.mean() - mu) < 5 * np.sqrt(var / n)
+    assert abs(u.var() - var) < 5 * np.sqrt((16.0 ** 2 / 80.0 - var ** 2) / n)
+    O.set_seed(7)
+    one_word = _mt19937_raw(7, 8).astype(np.float64)[:8] / 2.0 ** 32 * 4.0 - 1.0
+    assert not np.array_equal(O.uniform(8, -1.0, 3.0), one_word)
+
+
 @pytest.mark.parametrize("shape", [(65, 63, 66), (33, 300, 35), (1, 7, 1), (5, 1, 9)])
 def test_gemm_d_golden(shape):
     key = "gemm_d_%dx%dx%d" % shape
@@ -199,6 +262,28 @@ def test_attention_against_independent_numpy():
         assert rel(O.attention(Q, K, V, B, S, dk, causal), ref) <= 1e-13
         lse = sps.logsumexp(s, axis=-1)
         assert rel(O.flash_lse(Q, K, B, S, dk, causal), lse) <= 1e-13
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_rows_are_rows_of_the_full_oracle(causal):
+    """orc_attention_rows (the row-sampled check of full-size attention) against the rows of
+    orc_attention(_causal) and of orc_attention_bwd's dQ, both pinned above, on ragged
+    shapes with random row choices per slice (incl. row 0 and row S - 1)."""
+    rng = np.random.default_rng(11 + causal)
+    for B, S, dk in ((3, 37, 16), (2, 130, 64)):
+        Q, K, V, G = (rng.standard_normal((B, S * dk)) for _ in range(4))
+        rows = np.stack([np.r_[0, S - 1, rng.choice(np.arange(1, S - 1), 5, replace=False)]
+                         for _ in range(B)])
+        Orow, dQrow = O.attention_rows(Q, K, V, G, rows, B, S, dk, causal)
+        Of = O.attention(Q, K, V, B, S, dk, causal).reshape(B, S, dk)
+        dQf = O.attention_bwd(Q, K, V, G, B, S, dk, causal)[0].reshape(B, S, dk)
+        for b in range(B):
+            assert rel(Orow[b], Of[b, rows[b]]) <= 1e-13
+            assert rel(dQrow[b], dQf[b, rows[b]]) <= 1e-12
+    # a planted wrong mask (non-causal rows where causal ones were asked) is caught
+    if causal:
+        Orow_nc, _ = O.attention_rows(Q, K, V, G, rows, B, S, dk, False)
+        assert rel(Orow_nc[:, 2:], Of[np.arange(B)[:, None], rows][:, 2:]) > 1e-3
 
 
 def test_attention_bwd_invariants():
