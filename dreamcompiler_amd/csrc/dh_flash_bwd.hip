@@ -1085,3 +1085,60 @@ extern "C" int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int ca
     return st;
 }
 
+// ---------------------------------------------------------------------------------
+// dh_flash_bwd_noalloc: the same launches over a fixed device array instead of pool
+// memory, for callers that cannot allocate (code under graph capture, serving loops).
+// ---------------------------------------------------------------------------------
+namespace {
+
+// Dvec (BH*S floats) and, for bf16, LSE*log2(e) (BH*S more) of one call: 8 MB, held by every
+// device the library runs on until the process ends.
+constexpr size_t kNoAllocRows = size_t(1) << 20;
+static __device__ __align__(256) float scratch[2 * kNoAllocRows];
+
+// Device address of `scratch`, looked up once per device with that device current.  The
+// host-side name `scratch` is only a stand-in for the symbol and is never passed to a kernel.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_addr[kMaxDevices] = {};
+
+int scratch_address(float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return set_error(DH_ERR_HIP, "dh_flash_bwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(DH_ERR_UNSUPPORTED, "dh_flash_bwd_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(DH_ERR_HIP, "dh_flash_bwd_noalloc: hipGetSymbolAddress: %s",
+                             hipGetErrorString(e));
+        g_scratch_addr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_addr[dev];
+    return DH_OK;
+}
+
+}  // namespace
+
+extern "C" int dh_flash_bwd_noalloc(int dtype, int BH, int S, int D, float scale, int causal,
+                                    const void* Q, const void* K, const void* V, const void* O,
+                                    const void* dO, const float* LSE, float* dQ, float* dK,
+                                    float* dV, int accumulate) {
+    DH_TRY(ensure_init());
+    if (BH > 0 && S > 0 && (size_t)BH * (size_t)S > kNoAllocRows)
+        return set_error(DH_ERR_INVALID,
+                         "dh_flash_bwd_noalloc: BH*S = %zu rows exceeds the %zu-row scratch",
+                         (size_t)BH * (size_t)S, kNoAllocRows);
+    DH_TRY(check_bwd_args(dtype, BH, S, D, Q, K, V, O, dO, LSE, dQ, dK, dV));
+    if (BH == 0 || S == 0) return DH_OK;
+    float* Dv = nullptr;
+    DH_TRY(scratch_address(&Dv));
+    // Every Dvec / LSE*log2(e) entry the later launches read is written by the Dvec launch of
+    // this call first, so nothing is cleared.
+    return run_bwd(dtype, BH, S, D, scale, causal, Q, K, V, O, dO, LSE, dQ, dK, dV, accumulate,
+                   Dv);
+}

@@ -56,6 +56,8 @@ _SIGS = {
     "dh_flash_fwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp]),
     "dh_flash_bwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp, _vp, _vp, _i]),
+    "dh_flash_bwd_noalloc": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _vp, _vp, _vp, _i]),
     "dh_row_softmax": (_i, [_vp, _vp, _i, _i, _i]),
     "dh_row_softmax_bwd": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "dh_layer_norm": (_i, [_vp, _vp, _i, _i]),

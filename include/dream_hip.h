@@ -166,6 +166,17 @@ int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int causal,
                  const void* d_Q, const void* d_K, const void* d_V,
                  const void* d_O, const void* d_dO, const float* d_LSE,
                  float* d_dQ, float* d_dK, float* d_dV, int accumulate);
+/* dh_flash_bwd without any allocation.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, results and errors as dh_flash_bwd; the scratch is
+ * a fixed 8 MB device array per GPU (held until the process ends), so BH*S must be at most
+ * 1048576 rows, else DH_ERR_INVALID.  Every call on one GPU shares that array: calls that
+ * overlap in time on one GPU (other host threads, or another stream set with dh_set_stream)
+ * race; calls ordered on one stream do not. */
+int dh_flash_bwd_noalloc(int dtype, int BH, int S, int D, float scale, int causal,
+                         const void* d_Q, const void* d_K, const void* d_V,
+                         const void* d_O, const void* d_dO, const float* d_LSE,
+                         float* d_dQ, float* d_dK, float* d_dV, int accumulate);
 
 /* ---- row-wise ops: fp32, R rows of C contiguous values -------------------------
  * accumulate = 1 adds into GX (the reference backward's "+="), 0 overwrites it.
