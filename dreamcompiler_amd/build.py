@@ -30,6 +30,7 @@ HIP_SOURCES = [
     "dh_rows.hip",
     "dh_conv.hip",
     "dh_elementwise.hip",
+    "dh_f64.hip",
 ]
 RT_SOURCES = ["dream_rt.cpp"]
 

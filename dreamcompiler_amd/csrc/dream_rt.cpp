@@ -57,6 +57,7 @@ struct Dev {
     Dev& operator=(const Dev&) = delete;
     bool ok() const { return p != nullptr; }
     float* f() const { return static_cast<float*>(p); }
+    double* d() const { return static_cast<double*>(p); }
     uint16_t* h() const { return static_cast<uint16_t*>(p); }
     void* release() { void* q = p; p = nullptr; return q; }
 };
@@ -247,10 +248,30 @@ std::vector<float> download_rows_f32(const void* d, size_t rows, int Dp, int dt)
     return buf;
 }
 
+// ---- fp64 ----------------------------------------------------------------------------------
+// The shapes the reference computes in fp64 (below its GPU thresholds) run on the fp64
+// kernels from the host fp64 values, uploaded afresh on every call: these are the small
+// products, and a fresh upload also sees a direct write through `data` that did not bump
+// `version` (the reference's gradcheck perturbs leaves that way, training.inc:3886-3890).
+void upload_f64(const double* h, size_t n, Dev& d) {
+    need_buf(d);
+    need(dh_memcpy_h2d(d.p, h, n * sizeof(double)));
+}
+
+// Host grad += the device fp64 gradient g (n values).
+void add_grad_f64(Tensor* t, const Dev& g, size_t n) {
+    std::vector<double> h(n);
+    need(dh_memcpy_d2h(h.data(), g.p, n * sizeof(double)));
+    for (size_t i = 0; i < n; ++i) t->grad[i] += h[i];
+    t->grad_zero = 0;
+}
+
 // ---- attention ---------------------------------------------------------------------------
-// Head dims 32 / 64 / 128 run on the tensors' device copies directly; other dk <= 128 are
-// zero-padded to the next kernel size on the host (zero columns of Q, K leave Q K^T
-// unchanged; zero columns of V give zero columns of O; the scale stays 1/sqrt(dk)).
+// Shapes under the reference's GPU rule (B*S*S >= 262144, dk <= 128) run on the FlashAttention
+// kernels: head dims 32 / 64 / 128 on the tensors' device copies directly, other dk zero-padded
+// to the next kernel size on the host (zero columns of Q, K leave Q K^T unchanged; zero columns
+// of V give zero columns of O; the scale stays 1/sqrt(dk)).  Every other shape runs in fp64
+// (dh_attention_f64_fwd), as the reference computes it.
 Tensor* attention_impl(const char* name, int op, bool causal, Tensor* Q, Tensor* K, Tensor* V,
                        Tensor* bt, Tensor* st, Tensor* dt_) {
     if (!Q || !K || !V || !bt || !st || !dt_) return create_scalar(0.0);
@@ -259,11 +280,6 @@ Tensor* attention_impl(const char* name, int op, bool causal, Tensor* Q, Tensor*
         V->size != Q->size) {
         rt_error(name, "Q/K/V must hold batch*seq*dk = %d*%d*%d values (got %d, %d, %d)", B, S,
                  dk, Q->size, K->size, V->size);
-        return alloc_tensor(1, 1, 1, 1);
-    }
-    const int Dp = padded_dim(dk);
-    if (Dp < 0) {
-        rt_error(name, "head dim dk=%d above the 128 the GPU kernels hold", dk);
         return alloc_tensor(1, 1, 1, 1);
     }
     if (!hip_ready(name)) return alloc_tensor(1, 1, 1, 1);
@@ -275,6 +291,25 @@ Tensor* attention_impl(const char* name, int op, bool causal, Tensor* Q, Tensor*
     out->attn_S = S;
     out->attn_dk = dk;
     const size_t rows = (size_t)B * S, n = rows * dk;
+    if (!dh_flash_eligible(B, S, dk)) {
+        try {
+            Dev q(n * 8), k(n * 8), v(n * 8), o(n * 8);
+            upload_f64(Q->data, n, q);
+            upload_f64(K->data, n, k);
+            upload_f64(V->data, n, v);
+            need_buf(o);
+            need(dh_attention_f64_fwd(B, S, dk, 1.0 / std::sqrt((double)dk), causal ? 1 : 0,
+                                      q.d(), k.d(), v.d(), o.d()));
+            need(dh_memcpy_d2h(out->data, o.p, n * sizeof(double)));
+            out->f64_node = 1;
+        } catch (const Failure&) {
+            rt_error(name, "%s", dh_last_error());
+            tensor_decref(out);
+            return alloc_tensor(1, 1, 1, 1);
+        }
+        return out;
+    }
+    const int Dp = padded_dim(dk);
     const int dt = g_bf16 ? DH_BF16 : DH_F32;
     const size_t esz = dt == DH_BF16 ? 2 : 4;
     const float scale = (float)(1.0 / std::sqrt((double)dk));
@@ -322,6 +357,24 @@ void attention_backward(Tensor* t, bool causal) {
     Tensor *Q = t->parents[0], *K = t->parents[1], *V = t->parents[2];
     const int B = t->attn_B, S = t->attn_S, dk = t->attn_dk, Dp = padded_dim(dk);
     const size_t rows = (size_t)B * S, n = rows * dk;
+    if (t->f64_node) {
+        // fp64 forward: the fp64 backward (autograd.inc:675-778) from the host values, into
+        // separate device gradients added to the host grads one by one (Q, K, V may be one
+        // tensor, which then receives the sum, as the reference's "+=" leaves it).
+        flush_dgrad(t);
+        Dev q(n * 8), k(n * 8), v(n * 8), g(n * 8), dq(n * 8), dkk(n * 8), dv(n * 8);
+        upload_f64(Q->data, n, q);
+        upload_f64(K->data, n, k);
+        upload_f64(V->data, n, v);
+        upload_f64(t->grad, n, g);
+        need_buf(dq), need_buf(dkk), need_buf(dv);
+        need(dh_attention_f64_bwd(B, S, dk, 1.0 / std::sqrt((double)dk), causal ? 1 : 0, q.d(),
+                                  k.d(), v.d(), g.d(), dq.d(), dkk.d(), dv.d(), 0));
+        add_grad_f64(Q, dq, n);
+        add_grad_f64(K, dkk, n);
+        add_grad_f64(V, dv, n);
+        return;
+    }
     const int dt = g_bf16 ? DH_BF16 : DH_F32;
     const float scale = (float)(1.0 / std::sqrt((double)dk));
     if (Dp == dk) {
@@ -370,10 +423,24 @@ void attention_backward(Tensor* t, bool causal) {
 
 // ---- GEMM-family backward ------------------------------------------------------------------
 void matmul_backward(Tensor* t) {
-    // dA += dY B^T (NT), dB += A^T dY (TN) in fp32 on the device copies
-    // (runtime/ops/autograd.inc:91-125).
+    // dA += dY B^T (NT), dB += A^T dY (TN) (runtime/ops/autograd.inc:91-125): in fp64 from the
+    // host values when the forward ran in fp64, else in fp32 on the device copies.
     Tensor *A = t->lhs, *B = t->rhs;
     const int M = A->d0, K = A->d1, N = B->d1;
+    if (t->f64_node) {
+        flush_dgrad(t);
+        const size_t mk = (size_t)M * K, kn = (size_t)K * N, mn = (size_t)M * N;
+        Dev a(mk * 8), b(kn * 8), g(mn * 8), da(mk * 8), db(kn * 8);
+        upload_f64(A->data, mk, a);
+        upload_f64(B->data, kn, b);
+        upload_f64(t->grad, mn, g);
+        need_buf(da), need_buf(db);
+        need(dh_gemm_f64(0, 1, M, K, N, g.d(), N, b.d(), N, 0.0, da.d(), K));
+        need(dh_gemm_f64(1, 0, K, N, M, a.d(), K, g.d(), N, 0.0, db.d(), N));
+        add_grad_f64(A, da, mk);
+        add_grad_f64(B, db, kn);
+        return;
+    }
     const float* dy = grad_in(t);
     need(dh_gemm_f32(0, 1, M, K, N, dy, N, dev_data(B), N, 1.f, dgrad(A), K));
     need(dh_gemm_f32(1, 0, K, N, M, dev_data(A), K, dy, N, 1.f, dgrad(B), N));
@@ -1107,6 +1174,17 @@ Tensor* tensor_matmul(Tensor* a, Tensor* b) {
     const bool f32 = a->dtype == 1 && b->dtype == 1 && a->fdata && b->fdata;
     try {
         const size_t mk = (size_t)M * K, kn = (size_t)K * N, mn = (size_t)M * N;
+        if (!f32 && !dh_matmul_eligible(M, N)) {
+            // below the dispatch threshold: the reference's fp64 dgemm (elementwise.inc:1033-1040)
+            Dev da(mk * 8), db(kn * 8), dc(mn * 8);
+            upload_f64(a->data, mk, da);
+            upload_f64(b->data, kn, db);
+            need_buf(dc);
+            need(dh_gemm_f64(0, 0, M, N, K, da.d(), K, db.d(), N, 0.0, dc.d(), N));
+            need(dh_memcpy_d2h(c->data, dc.p, mn * sizeof(double)));
+            c->f64_node = 1;
+            return c;
+        }
         Dev dc(mn * 4);
         need_buf(dc);
         if (g_bf16 && !f32) {
@@ -1337,7 +1415,7 @@ Tensor* backward(Tensor* root) {
                 case DREAM_OP_FLASH:
                 case DREAM_OP_ATTN_CAUSAL:
                 case DREAM_OP_ATTN:
-                    if (t->dlse && hip_ready("backward(attention)"))
+                    if ((t->dlse || t->f64_node) && hip_ready("backward(attention)"))
                         attention_backward(t, t->op != DREAM_OP_ATTN);
                     break;
                 case DREAM_OP_SUM:
@@ -1399,6 +1477,10 @@ int dream_gpu_available(void) { return 0; }
 int dream_hip_available(void) { return dh_available(); }
 
 Tensor* gpu_selftest(void) {
+    // elementwise.inc:802-875.  The reference's shapes go through `@`, which at these sizes
+    // (M*N below the default threshold) runs fp64; the point of this test is the GPU kernels,
+    // so the fp32 matrix-core GEMM and the fp32 FlashAttention kernel are called directly on
+    // the same draws, under the reference's GPU gate (absolute sqrt(K) 1e-4).
     if (!dh_available()) {
         std::printf("=== gpu_selftest: no HIP device -- skipped ===\n");
         std::printf("  GPU: SKIP (CPU-only host; GPU kernels not exercised)\n");
@@ -1409,50 +1491,70 @@ Tensor* gpu_selftest(void) {
     std::uniform_real_distribution<double> dist(-1.0, 1.0);
     int pass = 0, total = 0;
     double worst = 0.0;
-    const int shapes[3][3] = {{256, 128, 256}, {300, 200, 257}, {512, 64, 300}};
-    for (const auto& s : shapes) {
-        Tensor* A = alloc_tensor(s[0], s[1], 1, 1);
-        Tensor* B = alloc_tensor(s[1], s[2], 1, 1);
-        for (int i = 0; i < A->size; ++i) A->data[i] = dist(rng());
-        for (int i = 0; i < B->size; ++i) B->data[i] = dist(rng());
-        Tensor* Cg = tensor_matmul(A, B);
-        std::vector<double> Cc((size_t)s[0] * s[2]);
-        ref_gemm(A->data, B->data, Cc.data(), s[0], s[1], s[2]);
-        double max_abs = 0.0;
-        for (size_t i = 0; i < Cc.size() && Cg->size == (int)Cc.size(); ++i)
-            max_abs = std::max(max_abs, std::fabs(Cg->data[i] - Cc[i]));
-        const double tol = std::sqrt((double)s[1]) * 1e-4;   // elementwise.inc:843-845
-        const bool ok = Cg->size == (int)Cc.size() && max_abs < tol;
-        std::printf("  matmul %dx%dx%d  max_abs=%.2e (tol %.1e)  %s\n", s[0], s[1], s[2], max_abs,
-                    tol, ok ? "PASS" : "FAIL");
-        worst = std::max(worst, max_abs);
+    auto to_dev32 = [](const std::vector<double>& h, Dev& d) {
+        std::vector<float> f(h.begin(), h.end());
+        need_buf(d);
+        need(dh_memcpy_h2d(d.p, f.data(), f.size() * sizeof(float)));
+    };
+    auto report = [&](bool ok, double err) {
+        worst = std::max(worst, err);
         ++total;
         pass += ok;
-        tensor_decref(A);
-        tensor_decref(B);
-        tensor_decref(Cg);
+    };
+    const int shapes[3][3] = {{256, 128, 256}, {300, 200, 257}, {512, 64, 300}};
+    for (const auto& sh : shapes) {
+        const int M = sh[0], K = sh[1], N = sh[2];
+        std::vector<double> A((size_t)M * K), B((size_t)K * N), Cc((size_t)M * N);
+        for (auto& v : A) v = dist(rng());
+        for (auto& v : B) v = dist(rng());
+        double max_abs = 1e30;
+        try {
+            Dev da(A.size() * 4), db(B.size() * 4), dc(Cc.size() * 4);
+            to_dev32(A, da);
+            to_dev32(B, db);
+            need_buf(dc);
+            need(dh_gemm_f32(0, 0, M, N, K, da.f(), K, db.f(), N, 0.f, dc.f(), N));
+            std::vector<float> Cg(Cc.size());
+            need(dh_memcpy_d2h(Cg.data(), dc.p, Cg.size() * 4));
+            ref_gemm(A.data(), B.data(), Cc.data(), M, K, N);
+            max_abs = 0.0;
+            for (size_t i = 0; i < Cc.size(); ++i)
+                max_abs = std::max(max_abs, std::fabs((double)Cg[i] - Cc[i]));
+        } catch (const Failure&) {
+            rt_error("gpu_selftest", "%s", dh_last_error());
+        }
+        const double tol = std::sqrt((double)K) * 1e-4;   // elementwise.inc:843-845
+        const bool ok = max_abs < tol;
+        std::printf("  matmul %dx%dx%d  max_abs=%.2e (tol %.1e)  %s\n", M, K, N, max_abs, tol,
+                    ok ? "PASS" : "FAIL");
+        report(ok, max_abs);
     }
     {   // causal flash attention on one slice, S=256, dk=64, against fp64
         const int S = 256, dkk = 64;
-        Tensor* Q = alloc_tensor(1, S * dkk, 1, 1);
-        Tensor* Kt = alloc_tensor(1, S * dkk, 1, 1);
-        Tensor* Vt = alloc_tensor(1, S * dkk, 1, 1);
-        for (Tensor* t : {Q, Kt, Vt})
-            for (int i = 0; i < t->size; ++i) t->data[i] = dist(rng());
-        Tensor *b1 = create_scalar(1), *s1 = create_scalar(S), *d1 = create_scalar(dkk);
-        Tensor* Og = dream_flash_attention(Q, Kt, Vt, b1, s1, d1, nullptr);
-        std::vector<double> Oc((size_t)S * dkk);
-        ref_causal_attention(Q->data, Kt->data, Vt->data, Oc.data(), S, dkk);
-        double max_abs = 0.0;
-        for (size_t i = 0; i < Oc.size() && Og->size == (int)Oc.size(); ++i)
-            max_abs = std::max(max_abs, std::fabs(Og->data[i] - Oc[i]));
-        const bool ok = Og->size == (int)Oc.size() && max_abs < 1e-4;
+        const size_t n = (size_t)S * dkk;
+        std::vector<double> Q(n), Kt(n), Vt(n), Oc(n);
+        for (auto* t : {&Q, &Kt, &Vt})
+            for (auto& v : *t) v = dist(rng());
+        double max_abs = 1e30;
+        try {
+            Dev q(n * 4), k(n * 4), v(n * 4), o(n * 4), lse(S * 4);
+            to_dev32(Q, q);
+            to_dev32(Kt, k);
+            to_dev32(Vt, v);
+            need_buf(o), need_buf(lse);
+            need(dh_flash_fwd(DH_F32, 1, S, dkk, 0.125f, 1, q.p, k.p, v.p, o.p, lse.f()));
+            std::vector<float> Og(n);
+            need(dh_memcpy_d2h(Og.data(), o.p, n * 4));
+            ref_causal_attention(Q.data(), Kt.data(), Vt.data(), Oc.data(), S, dkk);
+            max_abs = 0.0;
+            for (size_t i = 0; i < n; ++i) max_abs = std::max(max_abs, std::fabs((double)Og[i] - Oc[i]));
+        } catch (const Failure&) {
+            rt_error("gpu_selftest", "%s", dh_last_error());
+        }
+        const bool ok = max_abs < 1e-4;
         std::printf("  flash_attention S=%d dk=%d  max_abs=%.2e (tol 1.0e-04)  %s\n", S, dkk,
                     max_abs, ok ? "PASS" : "FAIL");
-        worst = std::max(worst, max_abs);
-        ++total;
-        pass += ok;
-        for (Tensor* t : {Q, Kt, Vt, b1, s1, d1, Og}) tensor_decref(t);
+        report(ok, max_abs);
     }
     std::printf("  GPU: %d/%d PASS (worst abs err %.2e)\n", pass, total, worst);
     std::fflush(stdout);
@@ -1465,6 +1567,9 @@ Tensor* gpu_selftest(void) {
 // with `as f32` operands -- against the fp64 naive product, under the reference's own GPU gate
 // (absolute sqrt(K) 1e-4, elementwise.inc:843-845); then the 512^3 throughput line.
 Tensor* gemm_selftest(void) {
+    // elementwise.inc:888-968: the same shapes, seed, draws and gates.  The fp64 shapes run the
+    // fp64 GEMM `@` takes below the threshold, the f32 shapes the fp32 GEMM of `as f32`
+    // operands; both against the naive fp64 product (the reference's gemm_ref_d).
     std::printf("=== gemm_selftest: GPU GEMM (the `@` path) vs naive fp64 reference ===\n");
     if (!dh_available()) {
         std::printf("  GEMM: SKIP (no HIP device: this runtime's `@` runs on the GPU)\n");
@@ -1473,65 +1578,85 @@ Tensor* gemm_selftest(void) {
     }
     rng().seed(20260707);
     std::uniform_real_distribution<double> dist(-1.0, 1.0);
-    std::uniform_real_distribution<float> fdist(-1.0f, 1.0f);
-    struct Shape {
-        int M, K, N;
-        bool f32;
-    };
-    const Shape shapes[] = {{1, 1, 1, false},     {1, 7, 1, false},     {5, 1, 9, false},
-                            {3, 4, 5, false},     {7, 13, 17, false},   {31, 33, 37, false},
-                            {64, 64, 64, false},  {65, 63, 66, false},  {128, 100, 96, false},
-                            {200, 50, 300, false}, {257, 129, 255, false}, {8, 16, 16, true},
-                            {7, 15, 13, true},    {9, 8, 17, true},     {1, 4, 1, true},
-                            {16, 32, 24, true},   {32, 16, 32, true}};
     int pass = 0, total = 0;
     double worst = 0.0;
-    for (const Shape& sh : shapes) {
-        Tensor* A = alloc_tensor(sh.M, sh.K, 1, 1);
-        Tensor* B = alloc_tensor(sh.K, sh.N, 1, 1);
-        for (int i = 0; i < A->size; ++i) A->data[i] = sh.f32 ? (double)fdist(rng()) : dist(rng());
-        for (int i = 0; i < B->size; ++i) B->data[i] = sh.f32 ? (double)fdist(rng()) : dist(rng());
-        if (sh.f32) {
-            dream_set_precision(A, 1);
-            dream_set_precision(B, 1);
+    const int shapes[11][3] = {{1, 1, 1},    {1, 7, 1},    {5, 1, 9},      {3, 4, 5},
+                               {7, 13, 17},  {31, 33, 37}, {64, 64, 64},   {65, 63, 66},
+                               {128, 100, 96}, {200, 50, 300}, {257, 129, 255}};
+    try {
+        for (const auto& sh : shapes) {
+            const int M = sh[0], K = sh[1], N = sh[2];
+            std::vector<double> A((size_t)M * K), B((size_t)K * N), C1((size_t)M * N),
+                C2((size_t)M * N);
+            for (auto& v : A) v = dist(rng());
+            for (auto& v : B) v = dist(rng());
+            Dev da(A.size() * 8), db(B.size() * 8), dc(C1.size() * 8);
+            upload_f64(A.data(), A.size(), da);
+            upload_f64(B.data(), B.size(), db);
+            need_buf(dc);
+            need(dh_gemm_f64(0, 0, M, N, K, da.d(), K, db.d(), N, 0.0, dc.d(), N));
+            need(dh_memcpy_d2h(C1.data(), dc.p, C1.size() * 8));
+            ref_gemm(A.data(), B.data(), C2.data(), M, K, N);
+            double mr = 0.0;
+            for (size_t i = 0; i < C1.size(); ++i)
+                mr = std::max(mr, std::fabs(C1[i] - C2[i]) / std::max(std::fabs(C2[i]), 1e-9));
+            const bool ok = mr < 1e-11;
+            std::printf("  %4dx%-4dx%-4d max_rel=%.2e  %s\n", M, K, N, mr, ok ? "PASS" : "FAIL");
+            worst = std::max(worst, mr);
+            ++total;
+            pass += ok;
         }
+        {   // throughput: the fp64 GEMM at 512^3, operands resident, best of 3
+            const int n = 512;
+            std::vector<double> A((size_t)n * n), B((size_t)n * n);
+            for (auto& v : A) v = dist(rng());
+            for (auto& v : B) v = dist(rng());
+            Dev da(A.size() * 8), db(B.size() * 8), dc(A.size() * 8);
+            upload_f64(A.data(), A.size(), da);
+            upload_f64(B.data(), B.size(), db);
+            need_buf(dc);
+            need(dh_sync());
+            double best = 1e30;
+            for (int rep = 0; rep < 3; ++rep) {
+                const auto t0 = std::chrono::steady_clock::now();
+                need(dh_gemm_f64(0, 0, n, n, n, da.d(), n, db.d(), n, 0.0, dc.d(), n));
+                need(dh_sync());
+                const auto t1 = std::chrono::steady_clock::now();
+                best = std::min(best, std::chrono::duration<double>(t1 - t0).count());
+            }
+            std::printf("  throughput: 512^3 in %.2f ms = %.1f GFLOPS (fp64 GEMM)\n", best * 1e3,
+                        2.0 * n * n * (double)n / best / 1e9);
+        }
+    } catch (const Failure&) {
+        rt_error("gemm_selftest", "%s", dh_last_error());
+    }
+    // f32 shapes: short K, so any tile-indexing bug shows (elementwise.inc:938-964)
+    const int fshapes[6][3] = {{8, 16, 16}, {7, 15, 13}, {9, 8, 17}, {1, 4, 1}, {16, 32, 24},
+                               {32, 16, 32}};
+    std::uniform_real_distribution<float> fdist(-1.0f, 1.0f);
+    for (const auto& sh : fshapes) {
+        const int M = sh[0], K = sh[1], N = sh[2];
+        Tensor* A = alloc_tensor(M, K, 1, 1);
+        Tensor* B = alloc_tensor(K, N, 1, 1);
+        for (int i = 0; i < A->size; ++i) A->data[i] = (double)fdist(rng());
+        for (int i = 0; i < B->size; ++i) B->data[i] = (double)fdist(rng());
+        dream_set_precision(A, 1);
+        dream_set_precision(B, 1);
         Tensor* C = tensor_matmul(A, B);
-        std::vector<double> R((size_t)sh.M * sh.N);
-        ref_gemm(A->data, B->data, R.data(), sh.M, sh.K, sh.N);
-        double max_abs = 0.0;
-        const bool shaped = C->size == (int)R.size();
+        std::vector<double> R((size_t)M * N);
+        ref_gemm(A->data, B->data, R.data(), M, K, N);
+        double mr = 0.0;
+        const bool shaped = C->size == (int)R.size() && C->fdata;
         for (size_t i = 0; shaped && i < R.size(); ++i)
-            max_abs = std::max(max_abs, std::fabs(C->data[i] - R[i]));
-        const double tol = std::sqrt((double)sh.K) * 1e-4;
-        const bool ok = shaped && max_abs < tol;
-        std::printf("  %s%4dx%-4dx%-4d max_abs=%.2e (tol %.1e)  %s\n", sh.f32 ? "f32 " : "",
-                    sh.M, sh.K, sh.N, max_abs, tol, ok ? "PASS" : "FAIL");
-        worst = std::max(worst, max_abs);
+            mr = std::max(mr, std::fabs((double)C->fdata[i] - R[i]) / std::max(std::fabs(R[i]), 1e-4));
+        const bool ok = shaped && mr < 2e-4;
+        std::printf("  f32 %dx%dx%d max_rel=%.2e  %s\n", M, K, N, mr, ok ? "PASS" : "FAIL");
+        worst = std::max(worst, mr);
         ++total;
         pass += ok;
         for (Tensor* t : {A, B, C}) tensor_decref(t);
     }
-    {   // throughput: 512^3 through `@`, best of 3 (host tensors in, host result out)
-        const int n = 512;
-        Tensor* A = alloc_tensor(n, n, 1, 1);
-        Tensor* B = alloc_tensor(n, n, 1, 1);
-        for (int i = 0; i < A->size; ++i) A->data[i] = dist(rng());
-        for (int i = 0; i < B->size; ++i) B->data[i] = dist(rng());
-        double best = 1e30;
-        for (int rep = 0; rep < 3; ++rep) {
-            ++A->version;   // time the whole builtin, operand upload included
-            const auto t0 = std::chrono::steady_clock::now();
-            Tensor* C = tensor_matmul(A, B);
-            const auto t1 = std::chrono::steady_clock::now();
-            best = std::min(best, std::chrono::duration<double>(t1 - t0).count());
-            tensor_decref(C);
-        }
-        std::printf("  throughput: 512^3 in %.2f ms = %.1f GFLOPS (`@` incl. copies)\n",
-                    best * 1e3, 2.0 * n * n * (double)n / best / 1e9);
-        tensor_decref(A);
-        tensor_decref(B);
-    }
-    std::printf("  GEMM: %d/%d PASS (worst abs err %.2e)\n", pass, total, worst);
+    std::printf("  GEMM: %d/%d PASS (worst rel err %.2e)\n", pass, total, worst);
     std::fflush(stdout);
     return create_scalar(pass == total ? 1.0 : 0.0);
 }
@@ -1660,7 +1785,7 @@ Tensor* dream_gpu_warmup(void) {
 }
 
 Tensor* flash_attention_selftest(void) {
-    std::printf("=== flash_attention_selftest: GPU flash == fp64 standard attention ===\n");
+    std::printf("=== flash_attention_selftest: flash == standard attention ===\n");
     if (!dh_available()) {
         std::printf("  FLASH_ATTN: SKIP (no HIP device)\n");
         return create_scalar(1.0);
@@ -1685,14 +1810,11 @@ Tensor* flash_attention_selftest(void) {
         Tensor* fla = dream_flash_attention(Q, K, V, bt, st, dt, blk);
         std::vector<double> ref((size_t)S * dkk);
         ref_causal_attention(Q->data, K->data, V->data, ref.data(), S, dkk);
-        double num = 0.0, den = 0.0;
-        for (size_t i = 0; i < ref.size() && fla->size == (int)ref.size(); ++i) {
-            num = std::max(num, std::fabs(fla->data[i] - ref[i]));
-            den = std::max(den, std::fabs(ref[i]));
-        }
-        const double mr = den > 0 ? num / den : num;
-        // fp32 GPU against fp64: normwise max relative error within 1e-5 * sqrt(S)
-        const bool ok = fla->size == (int)ref.size() && mr < 1e-5 * std::sqrt((double)S);
+        // B*S*S < 262144: flash_attention runs in fp64, so the reference's gate applies
+        double mr = 0.0;
+        for (size_t i = 0; i < ref.size() && fla->size == (int)ref.size(); ++i)
+            mr = std::max(mr, std::fabs(fla->data[i] - ref[i]) / std::max(std::fabs(ref[i]), 1e-9));
+        const bool ok = fla->size == (int)ref.size() && mr < 1e-9;
         std::printf("  S=%d dk=%d block=%d: max_rel=%.2e  %s\n", S, dkk, c[2], mr,
                     ok ? "PASS" : "FAIL");
         worst = std::max(worst, mr);

@@ -20,6 +20,7 @@ _i = ctypes.c_int
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
 _ll = ctypes.c_longlong
+_d = ctypes.c_double
 
 # name: (restype, argtypes) -- mirrors include/dream_hip.h
 _SIGS = {
@@ -53,6 +54,11 @@ _SIGS = {
                             _i, _vp, _i]),
     "dh_gemm_bf16_ex": (_i, [_i, _i, _i, _i, _i, _vp, _i, _ll, _vp, _i, _ll, _f, _vp, _i, _ll,
                              _i, _vp, _i]),
+    "dh_gemm_f64": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _d, _vp, _i]),
+    "dh_gemm_f64_ex": (_i, [_i, _i, _i, _i, _i, _d, _vp, _i, _ll, _vp, _i, _ll, _d, _vp, _i, _ll,
+                            _i]),
+    "dh_attention_f64_fwd": (_i, [_i, _i, _i, _d, _i, _vp, _vp, _vp, _vp]),
+    "dh_attention_f64_bwd": (_i, [_i, _i, _i, _d, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i]),
     "dh_flash_fwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp]),
     "dh_flash_bwd": (_i, [_i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp, _vp, _vp, _i]),
@@ -205,6 +211,25 @@ def gemm_ex(dtype, transA, transB, M, N, K, A, lda, sA, B, ldb, sB, beta, C, ldc
     check(fn(int(transA), int(transB), M, N, K, _p(A), lda, int(sA), _p(B), ldb, int(sB),
              float(beta), _p(C), ldc, int(sC), int(batch), _p(bias) if bias is not None else None,
              epi), f"dh_gemm_{dtype}_ex")
+
+
+def gemm_f64(transA, transB, M, N, K, A, lda, B, ldb, beta, C, ldc, alpha=1.0, sA=0, sB=0,
+             sC=0, batch=1):
+    """dh_gemm_f64_ex: fp64 GEMM in the reference dgemm's summation order."""
+    check(load().dh_gemm_f64_ex(int(transA), int(transB), M, N, K, float(alpha), _p(A), lda,
+                                int(sA), _p(B), ldb, int(sB), float(beta), _p(C), ldc, int(sC),
+                                int(batch)), "dh_gemm_f64_ex")
+
+
+def attention_f64_fwd(BH, S, D, scale, causal, Q, K, V, O):
+    check(load().dh_attention_f64_fwd(BH, S, D, float(scale), int(causal), _p(Q), _p(K), _p(V),
+                                      _p(O)), "dh_attention_f64_fwd")
+
+
+def attention_f64_bwd(BH, S, D, scale, causal, Q, K, V, dO, dQ, dK, dV, accumulate):
+    check(load().dh_attention_f64_bwd(BH, S, D, float(scale), int(causal), _p(Q), _p(K), _p(V),
+                                      _p(dO), _p(dQ), _p(dK), _p(dV), int(accumulate)),
+          "dh_attention_f64_bwd")
 
 
 def flash_fwd(dtype, BH, S, D, scale, causal, Q, K, V, O, LSE):

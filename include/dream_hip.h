@@ -141,6 +141,39 @@ int dh_gemm_bf16_ex(int transA, int transB, int M, int N, int K,
                     float beta, float* d_C, int ldc, long long strideC,
                     int batch, const float* d_bias, int epilogue);
 
+/* ---- fp64 (the reference's double-precision results) ---------------------------
+ * C[M x N] = alpha * (op(A) @ op(B)) + beta * C in fp64, same op / leading-dimension rules
+ * as dh_gemm_f32.  Replaces dream_gemm_d (runtime/ops/elementwise.inc:593-638), which the
+ * reference's `@` runs when M*N is below the dispatch threshold (elementwise.inc:1033-1040):
+ * every element is summed in the reference's order -- per 256-deep block of k (its KC) one
+ * fused multiply-add chain in k order started from zero, the blocks' sums added in k order
+ * -- so NN with alpha = 1, beta = 0 is bit-identical to the reference's fp64 `@`.  NT / TN
+ * with beta = 1 are the fp64 matmul backward (autograd.inc:91-125).  beta = 0 never reads C.
+ * _ex: batched, X_b = d_X + b * strideX (elements; zero shares an operand), batch <= 65535,
+ * C members must not overlap. */
+int dh_gemm_f64(int transA, int transB, int M, int N, int K,
+                const double* d_A, int lda, const double* d_B, int ldb,
+                double beta, double* d_C, int ldc);
+int dh_gemm_f64_ex(int transA, int transB, int M, int N, int K, double alpha,
+                   const double* d_A, int lda, long long strideA,
+                   const double* d_B, int ldb, long long strideB,
+                   double beta, double* d_C, int ldc, long long strideC, int batch);
+/* fp64 scaled dot-product attention in the reference layout (B, S*D), any head dim D:
+ * O = softmax(scale * Q K^T, causal mask j <= i when causal) V per slice -- the reference's
+ * dream_attention / dream_attention_causal (runtime/nn/training.inc:178-263), which it always
+ * computes in fp64, and its flash_attention outside B*S*S >= 262144 && dk <= 128 (the fp64
+ * loop of training.inc:366-399; same values up to rounding).  The backward
+ * (autograd.inc:675-778) recomputes the probabilities and adds (accumulate = 1) or writes
+ * dQ, dK, dV; any two of them may be one buffer, which then receives the sum of its
+ * gradients.  S x S score blocks (<= 256 MB each, by chunks of slices) come from the pool;
+ * S <= 46340.  scale must be positive. */
+int dh_attention_f64_fwd(int BH, int S, int D, double scale, int causal,
+                         const double* d_Q, const double* d_K, const double* d_V, double* d_O);
+int dh_attention_f64_bwd(int BH, int S, int D, double scale, int causal,
+                         const double* d_Q, const double* d_K, const double* d_V,
+                         const double* d_dO, double* d_dQ, double* d_dK, double* d_dV,
+                         int accumulate);
+
 /* ---- FlashAttention -----------------------------------------------------------
  * Q, K, V, O in the reference layout (B, S*dk): slice b (a batch x head pair)
  * starts at b*S*D, rows of D contiguous.  dtype DH_F32 or DH_BF16 for Q/K/V/dO;

@@ -8,8 +8,9 @@
  *     stolen (interop/dream.h:13-16);
  *   - errors print "RUNTIME ERROR in <op>: ..." to stderr and return a fresh 1x1 tensor
  *     (runtime/ops/elementwise.inc:972-989); nothing exits.
- * The GEMM and attention builtins compute on the GPU through include/dream_hip.h; this
- * runtime has no CPU GEMM or CPU attention.  Host-side builtins kept only to build
+ * The GEMM and attention builtins compute on the GPU through include/dream_hip.h, in fp64
+ * where the reference's dispatch computes fp64; this runtime has no CPU GEMM or CPU
+ * attention.  Host-side builtins kept only to build
  * programs around the hot path (ones, randn, sum, tensor_mul, ...) run on the host, as
  * the reference's own elementwise ops do.
  *
@@ -56,6 +57,8 @@ typedef struct Tensor {
     int grad_zero;             /* 1 while every host grad value is known to be 0   */
     float* dlse;               /* attention nodes: device per-row log-sum-exp (B*S) */
     int host_pinned;           /* bit 0: data, bit 1: grad are pinned pool buffers   */
+    int f64_node;              /* 1: the node's forward ran in fp64 (below the GPU
+                                * threshold), so its backward does too               */
 } Tensor;
 
 enum {
@@ -136,13 +139,22 @@ Tensor* dream_enable_fp16(void);   /* reduced-precision `@`: bf16 operands, fp32
 Tensor* dream_disable_fp16(void);
 
 /* ---- the hot path ---- */
-/* C = A @ B (runtime/ops/elementwise.inc:971-1213), graph node "matmul". */
+/* C = A @ B (runtime/ops/elementwise.inc:971-1213), graph node "matmul", with the
+ * reference's dispatch (elementwise.inc:1000-1040): both operands `as f32` -> fp32 GEMM;
+ * else M*N below the dispatch threshold (DREAM_GPU_THRESHOLD, default 262144) -> fp64 GEMM,
+ * bit-identical to the reference's dream_gemm_d; else the fp32 (bf16 after
+ * dream_enable_fp16) matrix-core GEMM, the reference's GPU branch.  All three run on the GPU;
+ * the node's backward runs in the precision of its forward. */
 Tensor* tensor_matmul(Tensor* a, Tensor* b);
-/* Causal FlashAttention (runtime/nn/training.inc:284-401); block_t may be NULL. */
+/* Causal FlashAttention (runtime/nn/training.inc:284-401); block_t may be NULL.  The
+ * reference's GPU rule B*S*S >= 262144 && dk <= 128 (training.inc:308, 336) selects the fp32
+ * (bf16) FlashAttention kernels; any other shape -- every dk > 128 included -- is computed in
+ * fp64, as the reference's CPU loop computes it. */
 Tensor* dream_flash_attention(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq,
                               Tensor* dk, Tensor* block);
-/* Standard attention, non-causal and causal (training.inc:178-263), computed by the
- * same FlashAttention kernels instead of materialising S x S scores. */
+/* Standard attention, non-causal and causal (training.inc:178-263).  The reference computes
+ * it in fp64 for every shape; here shapes under the flash rule above run on the FlashAttention
+ * kernels (no S x S scores), every other shape in fp64. */
 Tensor* dream_attention(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq, Tensor* dk);
 Tensor* dream_attention_causal(Tensor* Q, Tensor* K, Tensor* V, Tensor* batch, Tensor* seq,
                                Tensor* dk);
@@ -164,8 +176,13 @@ Tensor* dream_log_softmax(Tensor* x);
 Tensor* dream_layer_norm(Tensor* t);
 /* 2-D convolution of input (N, Cin*H*W) with kernel (Cout, Cin*KH*KW) plus a per-channel bias
  * (may be NULL) -> (N, Cout*OH*OW), scalars as 1x1 tensors: valid (runtime/nn/conv.inc:12-55)
- * and zero-padded / strided (conv.inc:119-178).  im2col + one batched GEMM; backward dX, dK
- * (autograd.inc:507-535; the reference computes no bias gradient, and neither does this). */
+ * and zero-padded / strided (conv.inc:119-178).  Implicit-GEMM kernels; backward dX, dK
+ * (autograd.inc:507-535; the reference computes no bias gradient, and neither does this).
+ * Divergence from the reference, on purpose: the reference's padded / strided node reuses the
+ * valid-convolution backward (autograd.inc:507-535 reads H, W, KH, KW only), which is correct
+ * for pad 0 and stride 1 alone; for pad > 0 or stride > 1 this backward computes the exact
+ * gradient of the padded / strided forward instead (pinned by finite differences), so dX and
+ * dK differ from the reference's values on the same inputs for those shapes. */
 Tensor* dream_conv2d(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h, Tensor* w,
                      Tensor* kh, Tensor* kw);
 Tensor* dream_conv2d_padded(Tensor* input, Tensor* kernel, Tensor* bias, Tensor* h, Tensor* w,
@@ -182,9 +199,11 @@ Tensor* backward(Tensor* root);
 int dream_gpu_available(void);
 /* 1 when the HIP backend can run the GEMM and attention builtins. */
 int dream_hip_available(void);
-/* gemm_selftest (elementwise.inc:888-968): the reference's 17 shapes, seed and draws through
- * `@` (the GPU GEMM; the 6 short-K shapes with `as f32` operands) against the naive fp64
- * product under the GPU gate sqrt(K) 1e-4; prints "GEMM: 17/17 PASS" like the reference. */
+/* gemm_selftest (elementwise.inc:888-968): the reference's 17 shapes, seed and draws; the 11
+ * fp64 shapes through the fp64 GEMM (dh_gemm_f64, what `@` runs below the threshold) against
+ * the naive fp64 product under the reference's gate (max relative error < 1e-11), the 6 f32
+ * shapes through the fp32 GEMM under its 2e-4; prints "GEMM: 17/17 PASS" like the
+ * reference. */
 Tensor* gemm_selftest(void);
 /* bf16_selftest (runtime/nn/training.inc:1978-2025): bf16 range and precision through the
  * device rounding (dh_convert), and the mixed-precision convergence check; prints
@@ -192,6 +211,9 @@ Tensor* gemm_selftest(void);
 Tensor* bf16_selftest(void);
 Tensor* gpu_selftest(void);
 Tensor* dream_gpu_warmup(void);
+/* flash_attention_selftest (training.inc:405-435): the reference's four configurations and
+ * seed; flash_attention (fp64 at these sizes) against the naive fp64 causal attention under
+ * the reference's gate (max relative error < 1e-9). */
 Tensor* flash_attention_selftest(void);
 
 #ifdef __cplusplus

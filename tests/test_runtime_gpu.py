@@ -69,15 +69,19 @@ def test_matmul_backward_matches_oracle(L):
 
 
 def test_bf16_mode_matmul(L):
+    # dream_enable_fp16 changes the reference's GPU branch only (elementwise.inc:1046-1071):
+    # at or above the threshold `@` takes bf16 operands; below it stays the fp64 dgemm.
     L.dream_enable_fp16()
     try:
         rng = np.random.default_rng(1)
-        A, B = rng.standard_normal((300, 520)), rng.standard_normal((520, 260))
+        A, B = rng.standard_normal((600, 520)), rng.standard_normal((520, 520))
         C = rt.read(L.tensor_matmul(rt.tensor(A), rt.tensor(B)))
         Ab = O.bf16_round(A.astype(np.float32)).astype(np.float64)
         Bb = O.bf16_round(B.astype(np.float32)).astype(np.float64)
         assert maxrel(C, Ab @ Bb) <= 2e-2
         assert maxrel(C, Ab @ Bb) <= 1e-5 * np.sqrt(520)
+        C = rt.read(L.tensor_matmul(rt.tensor(A[:300]), rt.tensor(B[:, :260])))
+        assert np.array_equal(C, O.gemm_d(A[:300], B[:, :260]))
     finally:
         L.dream_disable_fp16()
 
@@ -89,8 +93,11 @@ def _attn(L, fn, Q, K, V, B, S, dk, blk=None):
     return args, out
 
 
+# B*S*S below 262144 (fp64 path) and at or above it (the FlashAttention kernels, dk padded to
+# 32 / 64 / 128 where needed)
 @pytest.mark.parametrize("B,S,dk", [(1, 100, 24), (2, 64, 16), (4, 130, 64), (2, 33, 128),
-                                    (3, 70, 96)])
+                                    (3, 70, 96), (2, 400, 24), (1, 520, 96), (2, 384, 64),
+                                    (1, 512, 128)])
 def test_attention_builtins_vs_golden_math(L, B, S, dk):
     rng = np.random.default_rng(B * S + dk)
     Q, K, V, W = (rng.standard_normal((B, S * dk)) for _ in range(4))
@@ -237,8 +244,9 @@ def test_row_builtins_against_reference_golden(L, op):
 def test_device_copy_follows_in_place_writes(L):
     # A's device copy is reused by the second product only while A is unchanged: an index
     # assignment (tensor_set_element_2d bumps the version) must be seen by the next `@`.
+    # M*N = 512*512 is at the threshold, so these products run on the cached fp32 copies.
     rng = np.random.default_rng(3)
-    A0, B0 = rng.standard_normal((64, 32)), rng.standard_normal((32, 48))
+    A0, B0 = rng.standard_normal((512, 32)), rng.standard_normal((32, 512))
     a, b = rt.tensor(A0), rt.tensor(B0)
     c1 = rt.read(L.tensor_matmul(a, b))
     assert maxrel(c1, A0 @ B0) <= 1e-5 * np.sqrt(32)
@@ -253,11 +261,142 @@ def test_device_copy_follows_in_place_writes(L):
     assert maxrel(c3, A1 @ B0) <= 1e-5 * np.sqrt(32)
 
 
+def test_attention_device_copy_follows_in_place_writes(L):
+    # Same for attention on the FlashAttention kernels (B*S*S = 262144): a write to Q and a
+    # version bump must reach the next forward and backward.
+    B, S, dk = 1, 512, 64
+    rng = np.random.default_rng(12)
+    Q0, K0, V0, G = (rng.standard_normal((B, S * dk)) for _ in range(4))
+    q, k, v = (rt.tensor(x) for x in (Q0, K0, V0))
+    sc = lambda: [rt.scalar(B), rt.scalar(S), rt.scalar(dk)]  # noqa: E731
+    o1 = rt.read(L.dream_attention_causal(q, k, v, *sc()))
+    assert maxrel(o1, O.attention(Q0, K0, V0, B, S, dk, True)) <= 1e-5 * np.sqrt(S)
+    L.tensor_set_element_2d(q, rt.scalar(0), rt.scalar(dk * 300 + 5), rt.scalar(9.0))
+    Q1 = Q0.copy()
+    Q1[0, dk * 300 + 5] = 9.0
+    o = L.dream_attention_causal(q, k, v, *sc())
+    o2 = rt.read(o)
+    assert maxrel(o2, O.attention(Q1, K0, V0, B, S, dk, True)) <= 1e-5 * np.sqrt(S)
+    assert not np.allclose(o1, o2)
+    gq = _grads_through(L, o, G, q)[0]
+    assert maxrel(gq, O.attention_bwd(Q1, K0, V0, G, B, S, dk, True)[0]) <= 1e-5 * np.sqrt(S)
+
+
+# ---------------------------------------------------------------- the reference's dispatch
+@pytest.mark.parametrize("M,K,N", [(3, 4, 5), (200, 50, 300), (100, 1000, 100), (4096, 257, 10),
+                                   (511, 513, 511), (1, 3000, 1)])
+def test_matmul_below_threshold_is_the_reference_fp64(L, M, K, N):
+    # M*N < 262144: the reference's `@` runs dream_gemm_d (elementwise.inc:1033-1040).  The
+    # runtime's fp64 GEMM sums in the same order, so `@` returns the reference's values bit
+    # for bit (O.gemm_d is bit-identical to the reference build, tests/test_oracle.py), and
+    # its backward is the fp64 one of autograd.inc:91-125.
+    rng = np.random.default_rng(M + 3 * K + 7 * N)
+    A, B, W = rng.standard_normal((M, K)), rng.uniform(-1, 1, (K, N)), rng.standard_normal((M, N))
+    a, b = rt.tensor(A), rt.tensor(B)
+    c = L.tensor_matmul(a, b)
+    assert np.array_equal(rt.read(c), O.gemm_d(A, B))
+    ga, gb, _ = _grads_through(L, c, W, a, b)
+    dA, dB = O.matmul_bwd(A, B, W)
+    assert maxrel(ga, dA) <= 1e-13
+    assert maxrel(gb, dB) <= 1e-13
+
+
+def test_matmul_threshold_and_f32_operands_take_fp32(L):
+    # M*N = 262144 reaches the threshold: the fp32 matrix-core GEMM (the reference's GPU
+    # branch); `as f32` operands take the fp32 GEMM at any size (elementwise.inc:1000-1017).
+    rng = np.random.default_rng(21)
+    A, B = rng.standard_normal((512, 300)), rng.standard_normal((300, 512))
+    C = rt.read(L.tensor_matmul(rt.tensor(A), rt.tensor(B)))
+    ref = O.gemm_d(A, B)
+    assert maxrel(C, ref) <= 1e-5 * np.sqrt(300)
+    assert not np.array_equal(C, ref)
+    a, b = rt.tensor(A[:20, :30]), rt.tensor(B[:30, :20])
+    L.dream_set_precision(a, 1)
+    L.dream_set_precision(b, 1)
+    C = rt.read(L.tensor_matmul(a, b))
+    ref = O.gemm_d(A[:20, :30].astype(np.float32), B[:30, :20].astype(np.float32))
+    assert maxrel(C, ref) <= 1e-5 * np.sqrt(30)
+    assert not np.array_equal(C, ref)
+
+
+def _gc_run(L, fwd, leaves, W):
+    """The reference's gradcheck harness (training.inc:3856-3907): analytic gradients from
+    backward(sum(y * w)); numerical ones by central differences with eps = 1e-6 max(1, |x|),
+    written straight into each leaf's data as the reference writes them.  Returns max_rel."""
+    for t in leaves:
+        L.zero_grad(t)
+    w = rt.tensor(W)
+    y = fwd()
+    L.backward(L.sum(L.tensor_mul(y, w)))
+    ana = [rt.read(t, grad=True).ravel().copy() for t in leaves]
+
+    def num_loss():
+        yy = fwd()
+        s = float(np.dot(rt.read(yy).ravel(), W.ravel()))
+        rt.release(yy)
+        return s
+
+    max_rel, ana_abs, num_abs = 0.0, 0.0, 0.0
+    for t, g in zip(leaves, ana):
+        data = np.ctypeslib.as_array(t.contents.data, shape=(t.contents.size,))
+        for i in range(t.contents.size):
+            orig = data[i]
+            eps = 1e-6 * max(1.0, abs(orig))
+            data[i] = orig + eps
+            lp = num_loss()
+            data[i] = orig - eps
+            lm = num_loss()
+            data[i] = orig
+            gnum = (lp - lm) / (2 * eps)
+            ana_abs, num_abs = max(ana_abs, abs(g[i])), max(num_abs, abs(gnum))
+            max_rel = max(max_rel, abs(gnum - g[i]) / max(abs(gnum), abs(g[i]), 1e-6))
+    assert ana_abs > 1e-12 or num_abs > 1e-12     # the reference's degenerate guard
+    return max_rel
+
+
+def test_14_gradcheck_matmul_attention_entries(L):
+    # tests/14_gradcheck.dream's entries on the hot path, replayed through this runtime with
+    # the reference's harness, shapes, ranges and tolerance 1e-4: matmul 3x4 @ 4x5
+    # (training.inc:3933-3941), attention and attn_causal on Q, K, V of 1 x (4*8)
+    # (4180-4193, 4240-4252); flash_attention on the same shape as well.
+    rng = np.random.default_rng(20260706)
+    A, B = rng.uniform(-1, 1, (3, 4)), rng.uniform(-1, 1, (4, 5))
+    a, b = rt.tensor(A), rt.tensor(B)
+    mr = _gc_run(L, lambda: L.tensor_matmul(a, b), [a, b], rng.uniform(-1, 1, (3, 5)))
+    assert mr < 1e-4, f"matmul max_rel {mr:.2e}"
+    Q, K, V, W = (rng.uniform(-1, 1, (1, 32)) for _ in range(4))
+    q, k, v = rt.tensor(Q), rt.tensor(K), rt.tensor(V)
+    sc = lambda: [rt.scalar(1), rt.scalar(4), rt.scalar(8)]  # noqa: E731
+    for name, fwd in [("attention", lambda: L.dream_attention(q, k, v, *sc())),
+                      ("attn_causal", lambda: L.dream_attention_causal(q, k, v, *sc())),
+                      ("flash", lambda: L.dream_flash_attention(q, k, v, *sc(), rt.scalar(2)))]:
+        mr = _gc_run(L, fwd, [q, k, v], W)
+        assert mr < 1e-4, f"{name} max_rel {mr:.2e}"
+
+
+@pytest.mark.parametrize("B,S,dk", [(1, 40, 160), (2, 300, 256), (2, 400, 144)])
+def test_attention_builtins_head_dim_above_128(L, B, S, dk):
+    # dk > 128 is outside the reference's GPU rule (training.inc:336): all three builtins run
+    # in fp64, forward and backward, whatever B*S*S is.
+    rng = np.random.default_rng(B * S * dk)
+    Q, K, V, W = (rng.standard_normal((B, S * dk)) for _ in range(4))
+    for fn, causal, blk in [(L.dream_flash_attention, True, 64),
+                            (L.dream_attention_causal, True, None),
+                            (L.dream_attention, False, None)]:
+        args, o = _attn(L, fn, Q, K, V, B, S, dk, blk)
+        assert maxrel(rt.read(o).reshape(B, -1), O.attention(Q, K, V, B, S, dk, causal)) <= 1e-12
+        L.backward(L.sum(L.tensor_mul(o, rt.tensor(W))))
+        for t, r in zip(args, O.attention_bwd(Q, K, V, W, B, S, dk, causal)):
+            assert maxrel(rt.read(t, grad=True).reshape(B, -1), r) <= 1e-11
+
+
 def test_chained_gpu_graph_with_host_ops_gradients(L):
     # Gradients between GPU ops stay on the device; host ops in the middle (mul, add) must
     # see them.  loss = sum(layer_norm(softmax(((a*s) @ W) + c)) * G) against oracle/numpy.
+    # The product is 512 x 512 (at the threshold), so it runs on the device copies too.
     rng = np.random.default_rng(4)
-    A, S, W, Cb, G = (rng.standard_normal(sh) for sh in ((16, 24), (16, 24), (24, 40), (16, 40), (16, 40)))
+    A, S, W, Cb, G = (rng.standard_normal(sh) for sh in ((512, 24), (512, 24), (24, 512),
+                                                         (512, 512), (512, 512)))
     a, s, w, cb = (rt.tensor(x) for x in (A, S, W, Cb))
     h = L.tensor_mul(a, s)
     p = L.tensor_matmul(h, w)
