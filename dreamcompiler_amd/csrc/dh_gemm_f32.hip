@@ -836,6 +836,165 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
     return DH_OK;
 }
 
+// ---- skinny products: an output side of at most 16 (min(M, N) <= 16) ----------------------
+// Config 2's H W2 (4096 x 10, K 257) and dW2 = H^T dY (257 x 10, K 4096) move a few MB for
+// a few MFLOP: HBM- and latency-bound (a launch alone costs ~3.8 us on this stream).  The tiled
+// kernels stage 64- or 128-wide tiles through LDS for them and leave most of each tile empty.
+// Here a wave owns one 16 x 16 block of D = X Y (X: M x K, Y: K x N as the caller's op(A),
+// op(B), or the swapped pair for M <= 16) and streams its K range straight from global memory
+// into v_mfma_f32_16x16x4_f32: operand lane l holds X[i0 + l % 16][k] and Y[k][j0 + l % 16].
+// The order of k inside a product is free as long as X and Y agree, so in each 16-deep group
+// lane l takes k = k0 + 4 (l / 16) + j for MFMA j = 0..3 -- four consecutive k per lane, one
+// 16-byte span of a k-contiguous row.  A work-group of 4 waves splits one block's K range in four and
+// adds the partials through LDS in wave order; where that leaves the chip idle, K is cut
+// further over work-groups, with fp32 partials that splitk_reduce adds in a fixed order.
+// Reruns are bit-identical.
+// D register r of lane l is D[i0 + 4 (l / 16) + r][j0 + l % 16].
+template <bool TX, bool TY, int SK_WAVES>
+__global__ void __launch_bounds__(64 * SK_WAVES)
+gemm_f32_skinny_kernel(int M, int N, int K, const float* __restrict__ X, int ldx,
+                       const float* __restrict__ Y, int ldy, float beta, float* __restrict__ C,
+                       long long ldcr, long long ldcc, int mblocks, int nblocks, int Kc,
+                       int split_waves, float* __restrict__ part, long long part_ld,
+                       const float* __restrict__ bias, int epi) {
+    __shared__ f32x4 red[SK_WAVES][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // unit = (split s, m-block, n-block); split_waves: the waves share one unit's K range
+    const long long unit = split_waves ? (long long)blockIdx.x
+                                       : (long long)blockIdx.x * SK_WAVES + wave;
+    const long long units = (long long)mblocks * nblocks * ((K + Kc - 1) / Kc > 0 ? (K + Kc - 1) / Kc : 1);
+    if (unit >= units) return;   // whole waves only (split_waves grids have no spare units)
+    const int nb = (int)(unit % nblocks);
+    const int mb = (int)((unit / nblocks) % mblocks);
+    const int sidx = (int)(unit / ((long long)nblocks * mblocks));
+    const int i0 = mb * 16, j0 = nb * 16;
+    int kbeg = sidx * Kc, kend = min(K, kbeg + Kc);
+    if (split_waves) {
+        const int len = kend - kbeg;
+        const int kw = ((len + SK_WAVES - 1) / SK_WAVES + 15) & ~15;
+        kbeg = min(kend, kbeg + wave * kw);
+        kend = min(kend, kbeg + kw);
+    }
+    const int li = lane & 15, lk = 4 * (lane >> 4);
+    const int xi = i0 + li, yj = j0 + li;
+    const bool xin = xi < M, yin = yj < N;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    auto xat = [&](int k) { return TX ? X[(long long)k * ldx + xi] : X[(long long)xi * ldx + k]; };
+    auto yat = [&](int k) { return TY ? Y[(long long)yj * ldy + k] : Y[(long long)k * ldy + yj]; };
+    // Four 16-deep groups in flight: group g + 4 is loaded while group g runs.  Loads past kend
+    // read nothing and give zeros, whose products add exact zeros.
+    float xa[4][4], yb[4][4];
+    auto load = [&](int g, float (&xs)[4], float (&ys)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = kbeg + 16 * g + lk + j;
+            const bool kin = k < kend;
+            xs[j] = xin && kin ? xat(k) : 0.f;
+            ys[j] = yin && kin ? yat(k) : 0.f;
+        }
+    };
+#pragma unroll
+    for (int t = 0; t < 4; ++t) load(t, xa[t], yb[t]);
+    const int ngroups = (kend - kbeg + 15) >> 4;
+    for (int g = 0; g < ngroups; g += 4) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[t][j], yb[t][j], acc, 0, 0, 0);
+            load(g + 4 + t, xa[t], yb[t]);
+        }
+    }
+    if (split_waves) {
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
+        acc = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < SK_WAVES; ++w) acc += red[w][lane];
+    }
+    const int jj = j0 + li;
+    if (jj >= N) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int ii = i0 + lk + r;
+        if (ii >= M) continue;
+        // D[ii][jj] is C's element (ii, jj), or (jj, ii) when the operands were swapped
+        if (part) {
+            part[(long long)sidx * part_ld + ii * ldcr + jj * ldcc] = acc[r];
+            continue;
+        }
+        float* c = C + ii * ldcr + jj * ldcc;
+        const long long row = ldcc == 1 ? ii : jj, col = ldcc == 1 ? jj : ii;
+        float v = (beta == 0.f ? acc[r] : acc[r] + beta * *c) +
+                  (bias ? bias[(epi & DH_EPI_ROW_BIAS) ? row : col] : 0.f);
+        if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
+        *c = v;
+    }
+}
+
+// D = X Y with X = op(A), Y = op(B) (swap = false), or X = op(B)^T, Y = op(A)^T (swap = true:
+// M <= 16, so the short side lands on the 16 rows of a block) and C = D^T.  Returns
+// DH_ERR_UNSUPPORTED when the pool cannot give the split-K partials.
+template <bool TA, bool TB>
+int launch_skinny(int M, int N, int K, const float* A, int lda, const float* B, int ldb,
+                  float beta, float* C, int ldc, const Batch& bt) {
+    const bool swap = M <= 16 && N > 16;
+    const int DM = swap ? N : M, DN = swap ? M : N;
+    const long long ldcr = swap ? 1 : ldc, ldcc = swap ? ldc : 1;
+    const int mblocks = (DM + 15) / 16, nblocks = (DN + 15) / 16;
+    const long long mn_units = (long long)mblocks * nblocks;
+    const int cus = num_cus();
+    // Work-group shapes.  K above 64: the 4 waves of a work-group split one block's K range;
+    // K of 64 and less: each wave its own block.  Few blocks with a long K (config 2's
+    // dW2 = H^T dY: 17 blocks, K = 4096) split K over work-groups, chunks of at least 256, to
+    // about 4 work-groups per CU; their fp32 partials are added in order by splitk_reduce
+    // (18.3 -> 9.8 us).  Measured and rejected for that shape: one 16-wave work-group per block
+    // and no split (14.9 us: too few loads in flight per CU), and the reduction inside the
+    // launch by the last split to take an integer ticket (14.7-17.6 us: the device-scope
+    // release fence each split needs writes back its XCD's L2 under the others' streams).
+    const bool split_waves = K > 64;
+    const int W = 4;
+    int S = 1;
+    if (split_waves && mn_units < (long long)cus) {
+        long long sp = (4LL * cus + mn_units - 1) / mn_units;
+        sp = sp > K / 256 ? K / 256 : sp;
+        S = sp < 1 ? 1 : (int)sp;
+    }
+    const int Kc = S == 1 ? (K > 0 ? K : 1) : ((K + S - 1) / S + 15) & ~15;
+    S = K > 0 ? (K + Kc - 1) / Kc : 1;
+    const long long units = mn_units * S;
+    const long long wgs = split_waves ? units : (units + W - 1) / W;
+    if (wgs > 0x7fffffffLL) return set_error(DH_ERR_UNSUPPORTED, "dh_gemm_f32(skinny): grid");
+    float* part = nullptr;
+    if (S > 1) {
+        part = static_cast<float*>(dh_malloc((size_t)S * M * N * sizeof(float)));
+        if (!part) return DH_ERR_UNSUPPORTED;
+    }
+    const long long pr = swap ? 1 : N, pc = swap ? N : 1;   // partials are row-major M x N
+    hipStream_t s = stream();
+#define DH_SKINNY(TX, TY, X, LDX, Y, LDY, WV)                                                    \
+    gemm_f32_skinny_kernel<TX, TY, WV><<<(unsigned)wgs, 64 * WV, 0, s>>>(                         \
+        DM, DN, K, X, LDX, Y, LDY, beta, C, part ? pr : ldcr, part ? pc : ldcc, mblocks, nblocks, \
+        Kc, split_waves ? 1 : 0, part, (long long)M * N, bt.bias, bt.epi)
+    if (!swap) DH_SKINNY(TA, TB, A, lda, B, ldb, 4);
+    else DH_SKINNY(!TB, !TA, B, ldb, A, lda, 4);
+#undef DH_SKINNY
+    int st = check_launch("dh_gemm_f32(skinny)");
+    if (part) {
+        if (st == DH_OK) {
+            size_t blocks = ((size_t)M * N + 255) / 256;
+            if (blocks > (size_t)cus * 8) blocks = (size_t)cus * 8;
+            splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(part, S, M, N, beta, C, ldc, bt.bias,
+                                                           bt.epi);
+            st = check_launch("dh_gemm_f32(skinny reduce)");
+        }
+        dh_free(part);   // pooled; later users of the buffer are ordered on the stream
+    }
+    return st;
+}
+
 // Tile shape.  64 x 256 when M <= 64 (a 128-row tile would be at least half empty -- conv's
 // kernel @ im2col with few output channels, the bias gradient shapes), 256 x 64 when N <= 64,
 // else 128 x 128; but 64 x 64 tiles (one 32 x 32 block per wave, 8 waves per SIMD fit) when
@@ -869,6 +1028,13 @@ template <bool TA, bool TB>
 int launch(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta,
            float* C, int ldc, const Batch& bt) {
     const int cus = num_cus();
+    // Skinny products: a side of at most 16 rows or columns (measured on config 2: H W2 15.3 ->
+    // 5.8 us, dW2 = H^T dY 18.3 -> 9.8 us).  A short K alone (dH = dY W2^T, 4096 x 257, K 10)
+    // is write-bound and stays on the tiled kernels (5.8 us there, 8.3 us here).
+    if (bt.count == 1 && (M <= 16 || N <= 16)) {
+        const int st = launch_skinny<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+        if (st != DH_ERR_UNSUPPORTED) return st;   // no workspace: the tiled kernels below
+    }
     const long long t64 = (long long)((M + 63) / 64) * ((N + 63) / 64) * bt.count;
     if ((M <= 64 && N > 64) || (N <= 64 && M > 64)) {
         const long long tn = (long long)((M <= 64 ? N : M) + 255) / 256 * bt.count;

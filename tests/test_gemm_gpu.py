@@ -401,3 +401,69 @@ def test_fp32_64x64_two_waves_per_simd(Bt, M, N, K, ta, tb, row_bias):
     got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.5, relu=True, row_bias=row_bias,
                    seed=M + N + K + ta + 2 * tb + row_bias)
     assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+# Skinny products (a side <= 16): config 2's H W2 (4096 x 10, K 257), dW2 = H^T dY (257 x 10,
+# K 4096, split over work-groups) and dH = dY W2^T (4096 x 257, K 10); M <= 16 (operands
+# swapped, C written transposed); tails of every side; K = 0.
+SKINNY = [(4096, 10, 257), (257, 10, 4096), (4096, 257, 10), (10, 4096, 257), (16, 16, 16),
+          (1, 1, 1), (17, 5, 3), (5, 1000, 3000), (3000, 7, 64), (33, 2, 65), (2, 33, 1000),
+          (300, 16, 17), (1, 513, 33)]
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_fp32_skinny_products(M, N, K, ta, tb):
+    got, ref = _ex("f32", ta, tb, 1, M, N, K, beta=0.0, seed=M + 3 * N + 7 * K + ta + 2 * tb)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((K, M) if ta else (M, K))
+    B = rng.standard_normal((N, K) if tb else (K, N))
+    check_f32(gemm(f32(A), f32(B), bool(ta), bool(tb)), A.astype(np.float32).astype(np.float64),
+              B.astype(np.float32).astype(np.float64), K, bool(ta), bool(tb))
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 10, 257), (257, 10, 4096), (4096, 257, 10),
+                                   (10, 300, 700), (7, 9, 2000)])
+@pytest.mark.parametrize("relu,row_bias", [(False, False), (True, False), (True, True)])
+def test_fp32_skinny_epilogue(M, N, K, relu, row_bias):
+    got, ref = _ex("f32", 0, 0, 1, M, N, K, beta=-0.5, relu=relu, row_bias=row_bias,
+                   seed=M + N + K + relu)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_fp32_skinny_k_zero_and_reruns():
+    C0 = np.arange(30, dtype=np.float32).reshape(10, 3)
+    got = gemm(np.zeros((10, 0), np.float32), np.zeros((0, 3), np.float32), beta=0.5, C0=C0)
+    assert np.array_equal(got, 0.5 * C0)
+    a, _ = _ex("f32", 1, 0, 1, 257, 10, 4096, seed=5)
+    b, _ = _ex("f32", 1, 0, 1, 257, 10, 4096, seed=5)
+    assert np.array_equal(a, b)
+
+
+def test_fp32_skinny_split_k_many_launches():
+    # K split over work-groups with pooled partials added in a fixed order: 150 launches
+    # alternating two shapes with different block counts (the pool hands the partial buffers
+    # back and forth); every result must equal the first one bit for bit and the oracle
+    # within the fp32 bound.
+    rng = np.random.default_rng(77)
+    shapes = [(1, 0, 257, 10, 4096), (0, 1, 7, 600, 3000)]
+    DB = hip.DeviceBuffer
+    runs = []
+    for ta, tb, M, N, K in shapes:
+        A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+        ref = O.gemm_general_d(ta, tb, A.astype(np.float64), B.astype(np.float64))
+        runs.append((ta, tb, M, N, K, DB.from_numpy(A), DB.from_numpy(B), DB.empty((M, N), np.float32),
+                     A.shape[1], B.shape[1], ref))
+    first = [None, None]
+    for it in range(150):
+        x = it % 2
+        ta, tb, M, N, K, dA, dB, dC, lda, ldb, ref = runs[x]
+        hip.gemm_f32(ta, tb, M, N, K, dA, lda, dB, ldb, 0.0, dC, N)
+        got = dC.numpy()
+        if first[x] is None:
+            first[x] = got
+            assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+        else:
+            assert np.array_equal(got, first[x]), f"launch {it}"
