@@ -211,4 +211,24 @@ __device__ inline void xcd_tile_order(int bid, int nblocks, int tiles_m, int til
     tn = in / gsz;
 }
 
+// Work-group -> (slice bh, tile rank rr) for a grid of BH slices x n_t tiles per slice.
+// Work-groups are dealt round-robin to the 8 XCDs; when the slices split evenly over them,
+// XCD x takes the slices bh = x (mod 8) in groups of G and finishes one group before the
+// next, rank 0 (the caller's heaviest tile) first within a group: the few slices in flight
+// keep their operands in the XCD's L2.  G <= 0, or slices that do not split evenly: rank-major
+// over all slices (bh = bid mod BH).
+__device__ inline void slice_group_order(int bid, int BH, int n_t, int G, int& bh, int& rr) {
+    if (G <= 0 || (BH & 7)) {
+        bh = bid % BH;
+        rr = bid / BH;
+        return;
+    }
+    const int x = bid & 7, k = bid >> 3, spx = BH >> 3;
+    const int g = k / (G * n_t);
+    const int gsz = min(G, spx - g * G);
+    const int w = k - g * G * n_t;
+    rr = w / gsz;
+    bh = 8 * (g * G + w % gsz) + x;
+}
+
 }  // namespace dh

@@ -17,6 +17,8 @@
 // are staged through registers into row-major LDS.
 #include <mutex>
 
+#include <cstdlib>
+
 #include "dh_common.hpp"
 
 namespace dh {
@@ -183,7 +185,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
                      const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                      const uint16_t* __restrict__ dO, const float* __restrict__ L2,
                      const float* __restrict__ Dv, float* __restrict__ dK,
-                     float* __restrict__ dV, int accumulate, int kv_alias) {
+                     float* __restrict__ dV, int accumulate, int kv_alias, int group) {
     using T = BwTile<D, KV_BQ>;
     using R = BwTile<D, KV_KEYS>;                    // resident K, V of the work-group's keys
     constexpr int ND = D / 32, NTK = D / 16;
@@ -197,8 +199,8 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
     static_assert(KV_WAVES * 64 * 32 * ND * 4 / 2 <= KVRES + 2 * R::TILE, "reduction fits LDS");
     extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
-    const int bh = blockIdx.x % BH;
-    const int kt = blockIdx.x / BH;      // causal: small kt = longest query range, first
+    int bh, kt;                          // causal: small kt = longest query range, first
+    slice_group_order(blockIdx.x, BH, (S + KV_KEYS - 1) / KV_KEYS, group, bh, kt);
     const int kbase = kt * KV_KEYS;
     const size_t base = (size_t)bh * S * D;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -468,7 +470,8 @@ __global__ void __launch_bounds__(DQ_NT) __attribute__((amdgpu_waves_per_eu(2, 2
 bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __restrict__ Q,
                    const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                    const uint16_t* __restrict__ dO, const float* __restrict__ L2,
-                   const float* __restrict__ Dv, float* __restrict__ dQ, int accumulate) {
+                   const float* __restrict__ Dv, float* __restrict__ dQ, int accumulate,
+                   int group) {
     using T = BwTile<D, DQ_BN>;
     constexpr int ND = D / 32, NTK = D / 16;
     constexpr int STAGE = 2 * T::TILE;               // K tile, then V tile
@@ -477,8 +480,8 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
     extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
     const int n_qt = (S + DQ_ROWS - 1) / DQ_ROWS;
-    const int bh = blockIdx.x % BH;
-    const int rr = blockIdx.x / BH;
+    int bh, rr;
+    slice_group_order(blockIdx.x, BH, n_qt, group, bh, rr);
     const int qt = CAUSAL ? n_qt - 1 - rr : rr;
     const int q0 = qt * DQ_ROWS;
     const size_t base = (size_t)bh * S * D;
@@ -932,6 +935,18 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
              const void* dO, const float* L2, const float* Dv, float* dQ, float* dK, float* dV,
              int acc, int kv_alias, int acc_q) {
     const float sl2 = scale * 1.4426950408889634f;
+    // Each XCD walks its slices 4 at a time, heaviest tile first (slice_group_order): the Q, dO
+    // (dK/dV launch) and K, V (dQ launch) streams of a few slices stay in the XCD's L2.
+    // Config 4, same-box A/B (ms for the backward): rank-major over all slices 1.97; groups of
+    // 1 slice 1.99, 2: 1.91, 4: 1.89-1.91, 8: 1.91, 16: 1.97.  Tuning knobs override.
+    static const int group_kv = [] {
+        const char* e = std::getenv("DH_FLASH_BWD_GROUP_KV");
+        return e ? std::atoi(e) : 4;
+    }();
+    static const int group_q = [] {
+        const char* e = std::getenv("DH_FLASH_BWD_GROUP_Q");
+        return e ? std::atoi(e) : 4;
+    }();
     {
         auto kern = bwd_dkdv_bf16_kernel<D, CAUSAL>;
         const size_t lds = (size_t)KV_NSTAGE * (2 * BwTile<D, KV_BQ>::TILE + 2048) +
@@ -941,7 +956,8 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
         const int grid = BH * ((S + KV_KEYS - 1) / KV_KEYS);
         kern<<<grid, KV_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
                                              (const uint16_t*)K, (const uint16_t*)V,
-                                             (const uint16_t*)dO, L2, Dv, dK, dV, acc, kv_alias);
+                                             (const uint16_t*)dO, L2, Dv, dK, dV, acc, kv_alias,
+                                             group_kv);
         DH_TRY(check_launch("dh_flash_bwd(dK,dV bf16)"));
     }
     {
@@ -952,7 +968,7 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
         const int grid = BH * ((S + DQ_ROWS - 1) / DQ_ROWS);
         kern<<<grid, DQ_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
                                              (const uint16_t*)K, (const uint16_t*)V,
-                                             (const uint16_t*)dO, L2, Dv, dQ, acc_q);
+                                             (const uint16_t*)dO, L2, Dv, dQ, acc_q, group_q);
         DH_TRY(check_launch("dh_flash_bwd(dQ bf16)"));
     }
     return DH_OK;
