@@ -340,6 +340,122 @@ def runtime_mlp_metrics(steps=10, warmup=3):
 
 
 # --------------------------------------------------------------------------- CPU baseline
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _maxrel(got, ref):
+    return float(np.abs(got - ref).max() / max(float(np.abs(ref).max()), 1e-300))
+
+
+def parity_checks():
+    """Parity of every contract config on the GPU, checked on the CPU (part of the CPU leg):
+    the GPU result against an fp64 reference on the same inputs -- numpy's fp64 products for
+    the GEMMs, fp64 softmax attention for config 3, the CPU restatement of the reference
+    (oracle, sampled rows) for config 4 -- as the normwise max relative error beside the
+    contract's bound (fp32 1e-5 sqrt(K), bf16 2e-2)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    out = {}
+
+    def rec(name, err, tol, sample):
+        out[name] = {"gpu_maxrel": float(f"{err:.3e}"), "tol": float(f"{tol:.3e}"),
+                     "ok": bool(err <= tol), "sample": sample}
+
+    def gemm_gpu(dtype, A, B, ta=0, tb=0):
+        M = A.shape[1] if ta else A.shape[0]
+        K = A.shape[0] if ta else A.shape[1]
+        N = B.shape[0] if tb else B.shape[1]
+        dA, dB, dC = DB.from_numpy(A), DB.from_numpy(B), DB.empty((M, N), np.float32)
+        fn = hip.gemm_bf16 if dtype == "bf16" else hip.gemm_f32
+        fn(ta, tb, M, N, K, dA, A.shape[1], dB, B.shape[1], 0.0, dC, N)
+        C = dC.numpy()
+        for b in (dA, dB, dC):
+            b.free()
+        return C
+
+    def bf16(x):
+        u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+        return (((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFFFFFF) >> 16).astype(np.uint16)
+
+    def unbf16(b):
+        return (b.astype(np.uint32) << 16).view(np.float32)
+
+    rng = np.random.default_rng(42)
+    # config 1: fp32 1024^3, full product
+    A, B = (rng.standard_normal((1024, 1024), dtype=np.float32) for _ in range(2))
+    rec("C1_fp32_1024", _maxrel(gemm_gpu("f32", A, B), A.astype(np.float64) @ B.astype(np.float64)),
+        1e-5 * np.sqrt(1024), "full 1024 x 1024")
+    # config 2: the six products of the MLP set, full
+    worst, wtol = 0.0, 1.0
+    for name, ta, tb, M, N, K in MLP_SHAPES:
+        A = rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32)
+        B = rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32)
+        ref = (A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)
+        e, t = _maxrel(gemm_gpu("f32", A, B, ta, tb), ref), 1e-5 * np.sqrt(K)
+        if e / t > worst / wtol:
+            worst, wtol = e, t
+    rec("C2_mlp_set", worst, wtol, "six products in full; the one nearest its bound")
+    # config 5: bf16 8192^3 and fp32 4096^3 on sampled rows
+    for name, dtype, n, rows in (("C5_bf16_8192", "bf16", 8192, 16), ("C5_fp32_4096", "f32", 4096, 32)):
+        A, B = (rng.standard_normal((n, n), dtype=np.float32) for _ in range(2))
+        if dtype == "bf16":
+            A, B = bf16(A), bf16(B)
+            A64, B64 = unbf16(A).astype(np.float64), unbf16(B).astype(np.float64)
+        else:
+            A64, B64 = A.astype(np.float64), B.astype(np.float64)
+        C = gemm_gpu(dtype, A, B)
+        idx = rng.choice(n, rows, replace=False)
+        rec(name, _maxrel(C[idx], A64[idx] @ B64), 2e-2 if dtype == "bf16" else 1e-5 * np.sqrt(n),
+            f"{rows} random rows of {n}, all columns (fp64 on the {'bf16-rounded ' if dtype == 'bf16' else ''}inputs)")
+        del A, B, A64, B64, C
+    # config 3: fp32 causal flash B4 H6 S256 D64, full, against fp64 softmax attention
+    BH, S, D = 24, 256, 64
+    Q, K, V = (rng.standard_normal((BH, S * D), dtype=np.float32) * np.float32(0.5) for _ in range(3))
+    dq, dk, dv = (DB.from_numpy(x) for x in (Q, K, V))
+    dO, dL = DB.empty((BH, S * D), np.float32), DB.empty((BH, S), np.float32)
+    hip.flash_fwd(hip.F32, BH, S, D, 1.0 / np.sqrt(D), True, dq, dk, dv, dO, dL)
+    Og = dO.numpy().reshape(BH, S, D)
+    q, k, v = (x.astype(np.float64).reshape(BH, S, D) for x in (Q, K, V))
+    s = np.einsum("bid,bjd->bij", q, k) / np.sqrt(D)
+    s = np.where(np.tril(np.ones((S, S), bool))[None], s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    rec("C3_flash_fp32", _maxrel(Og, np.einsum("bij,bjd->bid", p, v)), 1e-5 * np.sqrt(S), "full")
+    # config 4: bf16 causal flash fwd + bwd at full size; O and dQ of 4 rows in each of 16
+    # slices from the CPU restatement (oracle attention_rows), fp64 on the bf16-rounded inputs
+    import _oracle  # noqa: E402  (test infrastructure: the checker of the CPU leg)
+    BH, S, D = 128, 4096, 128
+    Qb, Kb, Vb, Gb = (bf16(rng.standard_normal((BH, S * D), dtype=np.float32)) for _ in range(4))
+    bufs = [DB.from_numpy(x) for x in (Qb, Kb, Vb, Gb)]
+    dO, dL = DB.empty((BH, S * D), np.uint16), DB.empty((BH, S), np.float32)
+    grads = [DB.empty((BH, S * D), np.float32) for _ in range(3)]
+    sc = 1.0 / np.sqrt(D)
+    hip.flash_fwd(hip.BF16, BH, S, D, sc, True, bufs[0], bufs[1], bufs[2], dO, dL)
+    hip.flash_bwd(hip.BF16, BH, S, D, sc, True, bufs[0], bufs[1], bufs[2], dO, bufs[3], dL,
+                  grads[0], grads[1], grads[2], 0)
+    Og = unbf16(dO.numpy()).reshape(BH, S, D)
+    dQg = grads[0].numpy().reshape(BH, S, D)
+    sl = rng.choice(BH, 16, replace=False)
+    rows = np.stack([rng.choice(S, 4, replace=False) for _ in sl]).astype(np.int32)
+    f64 = [unbf16(x[sl]).astype(np.float64) for x in (Qb, Kb, Vb, Gb)]
+    Oref, dQref = _oracle.attention_rows(*f64, rows, len(sl), S, D, True)
+    rec("C4_flash_bf16_fwd_O", _maxrel(np.stack([Og[b][r] for b, r in zip(sl, rows)]), Oref), 2e-2,
+        "4 random rows in each of 16 random slices")
+    rec("C4_flash_bf16_bwd_dQ", _maxrel(np.stack([dQg[b][r] for b, r in zip(sl, rows)]), dQref), 2e-2,
+        "4 random rows in each of 16 random slices")
+    for b in bufs + grads + [dO, dL, dq, dk, dv]:
+        b.free()
+    hip.load().dh_pool_release()
+    return out
+
+
 def cpu_baseline_gemm(n=8192, rows=8192, reps=3):
     """The reference's CPU `@` on fp32 operands (`as f32` -> dream_gemm_f32, blocked 8x16
     AVX2 kernel, OpenMP over 128-row blocks, runtime/ops/elementwise.inc:689-738) on a
@@ -360,15 +476,20 @@ def cpu_baseline_gemm(n=8192, rows=8192, reps=3):
         kind = "port"
         A32, B32 = A.astype(np.float32), B.astype(np.float32)
         run = lambda: _oracle.gemm_f32(A32, B32)  # noqa: E731
-    best = 1e30
+    best, C = 1e30, None
     for _ in range(reps):
         t0 = time.perf_counter()
-        run()
+        C = run()
         best = min(best, time.perf_counter() - t0)
     gflops = 2.0 * rows * n * n / best / 1e9
+    idx = rng.choice(rows, 16, replace=False)   # the CPU result's own error, sampled rows
+    err = _maxrel(np.asarray(C, np.float64)[idx], A[idx] @ B)
     return {"value": round(gflops, 2), "unit": "GFLOP/s", "cores": threads, "kind": kind,
+            "cpu_model": cpu_model(),
+            "cpu_maxrel": float(f"{err:.3e}"),
             "sample": f"fp32 `@` (as f32) {rows}x{n} @ {n}x{n} (rows {rows}/{n} of the "
-                      f"workload), best of {reps}, {best:.2f} s, OMP threads {threads}"}
+                      f"workload), best of {reps}, {best:.2f} s, OMP threads {threads}; "
+                      f"cpu_maxrel: 16 random rows against fp64"}
 
 
 def cpu_baseline_flash(S=4096, D=128, slices=32):
@@ -625,6 +746,7 @@ def main():
             line["cpu_baseline_runtime_mlp_c2_step"] = cpu_baseline_mlp()
             line["cpu_baseline_workloads"] = cpu_baseline_workloads(
                 {k: v["ms"] for k, v in metrics.items() if isinstance(v, dict) and "ms" in v})
+            line["parity"] = parity_checks()
         except Exception as e:  # the CPU comparison must not hide the GPU result
             line["cpu_baseline"] = {"error": repr(e)}
     print(json.dumps(line), flush=True)

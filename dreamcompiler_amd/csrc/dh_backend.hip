@@ -63,8 +63,8 @@ void do_init() {
     }
     s.cus = s.prop.multiProcessorCount;
     s.status = DH_OK;
-    std::fprintf(stderr, "[dream] backend: HIP  (device: %s, %s, %d CUs)\n", s.prop.name,
-                 s.prop.gcnArchName, s.cus);
+    std::fprintf(stderr, "[dream] backend: HIP  (device: %s%s%s, %d CUs)\n", s.prop.name,
+                 s.prop.name[0] ? ", " : "", s.prop.gcnArchName, s.cus);
 }
 
 }  // namespace
@@ -158,7 +158,12 @@ int dh_device_info(char* name, int name_len, int* cus, int* xcds, int* sclk_mhz,
                    long long* hbm_bytes) {
     DH_TRY(ensure_init());
     const hipDeviceProp_t& p = st().prop;
-    if (name && name_len > 0) std::snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+    // Some driver stacks leave the marketing name empty (no amdgpu.ids table): name the chip
+    // by its architecture and CU count then.
+    if (name && name_len > 0) {
+        if (p.name[0]) std::snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+        else std::snprintf(name, name_len, "%s, %d CUs", p.gcnArchName, p.multiProcessorCount);
+    }
     if (cus) *cus = p.multiProcessorCount;
     if (xcds) *xcds = std::strncmp(p.gcnArchName, "gfx95", 5) == 0 ||
                               std::strncmp(p.gcnArchName, "gfx94", 5) == 0 ? 8 : 1;
