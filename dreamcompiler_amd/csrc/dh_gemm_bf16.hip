@@ -518,7 +518,10 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 
     const int tiles_m = M / 256, tiles_n = N / 256;
     int tm, tn;
-    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
+    // Each XCD's 32 tiles in flight form a 4 x 8 block (4 A panels, 8 B panels).  Same-box
+    // A/B at 8192^3 (NN, ms): groups of 4 tile rows 0.862-0.867, 8 rows (8 x 4 blocks)
+    // 0.879-0.881, 2: 0.893, 3: 0.889, 5: 0.894, 6: 0.885, 16: 0.903.
+    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 4, tm, tn);
     const int m0 = tm * 256, n0 = tn * 256;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
