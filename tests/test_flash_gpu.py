@@ -231,6 +231,31 @@ def test_bf16_fwd_bwd_grouped_slice_order(BH, causal):
     assert np.abs(lse - lse_ref).max() <= 1e-3 * np.sqrt(D)
 
 
+@pytest.mark.parametrize("BH,S,D", [(8, 300, 128), (8, 512, 128), (16, 1000, 64), (40, 1024, 32),
+                                    (72, 2048, 128), (24, 767, 64)])
+def test_bf16_causal_fwd_bwd_grouped_even_tiles(BH, S, D):
+    """Causal bf16 with BH % 8 == 0 (the XCD-grouped slice order, 4 slices per group; BH = 72
+    and 40 end on a short group) at q-tile counts from 2 to 8, S = 300, 1000, 767 leaving the
+    last tile ragged, every head dim.  Every slice and row in full against the fp64 oracle,
+    O and LSE, and the backward run on that O and LSE; a second run is bit-identical."""
+    Q, K, V, G = (bf16_bits(x) for x in inputs(BH, S, D, 5000 + BH + S + D))
+    Of, lse = flash_fwd(Q, K, V, BH, S, D, True, dtype="bf16")
+    Q64, K64, V64, G64 = (bits_to_f32(x).astype(np.float64) for x in (Q, K, V, G))
+    ref = O.attention(Q64, K64, V64, BH, S, D, True).reshape(BH, S, D)
+    for b in range(BH):
+        assert maxrel(Of.reshape(BH, S, D)[b], ref[b]) <= 2e-2, b
+    assert np.abs(lse - O.flash_lse(Q64, K64, BH, S, D, True)).max() <= 1e-3 * np.sqrt(D)
+    if S <= 1024:
+        grads = flash_bwd(Q, K, V, bf16_bits(Of), G, lse, BH, S, D, True, dtype="bf16")
+        refs = [r.reshape(BH, S, D) for r in _bwd_ref(Q64, K64, V64, G64, BH, S, D, True)]
+        for name, g, r in zip("QKV", grads, refs):
+            for b in range(BH):
+                assert maxrel(g.reshape(BH, S, D)[b], r[b]) <= 2e-2, (name, b)
+    # bit-identical on a second run (the schedule is static)
+    again, _ = flash_fwd(Q, K, V, BH, S, D, True, dtype="bf16")
+    assert np.array_equal(again, Of)
+
+
 @pytest.mark.timeout(600)
 def test_c4_bf16_fwd_bwd_full_size():
     """Config 4: B=8 H=16 (128 slices) S=4096 D=128, Q,K,V,dO ~ N(0,1) rounded to bf16,
