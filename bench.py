@@ -8,8 +8,9 @@ already resident in HBM.  The headline workload (`value`) is config 5 of the con
 bf16 GEMM C = A @ B, M = N = K = 8192, A, B ~ N(0,1) rounded to bf16, fp32 accumulate and
 output.  The same run also times fp32 GEMM 4096^3 (the fp32 MFMA figure of config 5), the
 causal FlashAttention forward and backward of config 4 (B8 H16 S4096 D128 bf16), config 3
-(fp32 causal flash B4 H6 S256 D64) and the config 2 MLP GEMM set; they are reported under
-"metrics".  Prints ONE JSON line.
+(fp32 causal flash B4 H6 S256 D64), the config 2 MLP GEMM set and the fp64 paths (`@` below
+the dispatch threshold, attention with dk = 256); they are reported under "metrics".
+Prints ONE JSON line.
 
 Timing: HIP events recorded on the library stream (the stream every kernel here is
 launched on) around K back-to-back launches, after W warm-up launches, with a stream
@@ -29,7 +30,7 @@ sys.path.insert(0, ROOT)
 from dreamcompiler_amd import hip  # noqa: E402
 
 DB = hip.DeviceBuffer
-PEAK = {"bf16": 2516.6, "fp32": 157.3}   # dense MFMA TFLOP/s, MI355X (256 CU x 2.4 GHz)
+PEAK = {"bf16": 2516.6, "fp32": 157.3, "fp64": 78.6}   # dense TFLOP/s, MI355X (256 CU x 2.4 GHz)
 HBM_PEAK_GBS = 8000.0
 
 
@@ -74,6 +75,37 @@ def gemm_workload(dtype, M, N, K, seed=0):
     flops = 2.0 * M * N * K
     alg_bytes = (M * K + K * N) * in_bytes + M * N * 4
     return step, flops, alg_bytes, [A, B, C]
+
+
+def gemm_f64_workload(M, N, K, seed=11):
+    """fp64 `@` below the dispatch threshold (M*N < 262144): dh_gemm_f64, the reference's
+    dgemm summation order (bit-identical results), on the fp64 VALU."""
+    rng = np.random.default_rng(seed)
+    A, B = DB.from_numpy(rng.standard_normal((M, K))), DB.from_numpy(rng.standard_normal((K, N)))
+    C = DB.empty((M, N), np.float64)
+
+    def step():
+        hip.gemm_f64(0, 0, M, N, K, A, K, B, N, 0.0, C, N)
+    return step, 2.0 * M * N * K, 8.0 * (M * K + K * N + M * N), [A, B, C]
+
+
+def attention_f64_workload(BH, S, D, causal, backward=False, seed=12):
+    """fp64 attention outside the flash rule (here dk > 128): dh_attention_f64_fwd / _bwd,
+    the standard form on fp64 GEMMs with the S x S scores in HBM.  FLOPs: the products
+    (forward 4 S^2 D per slice, backward 8 S^2 D), all S^2 scores computed even when causal."""
+    rng = np.random.default_rng(seed)
+    Q, K, V, G = (DB.from_numpy(rng.standard_normal((BH, S * D)) * 0.5) for _ in range(4))
+    O = DB.empty((BH, S * D), np.float64)
+    sc = 1.0 / np.sqrt(D)
+    if not backward:
+        def step():
+            hip.attention_f64_fwd(BH, S, D, sc, causal, Q, K, V, O)
+        return step, 4.0 * BH * S * S * D, 8.0 * 4 * BH * S * D, [Q, K, V, G, O]
+    dQ, dK, dV = (DB.empty((BH, S * D), np.float64) for _ in range(3))
+
+    def step():
+        hip.attention_f64_bwd(BH, S, D, sc, causal, Q, K, V, G, dQ, dK, dV, 0)
+    return step, 8.0 * BH * S * S * D, 8.0 * 7 * BH * S * D, [Q, K, V, G, O, dQ, dK, dV]
 
 
 def flash_workload(dtype, BH, S, D, causal, backward=False, seed=1):
@@ -232,6 +264,17 @@ WORKLOADS = {
                      "causal FlashAttention bwd B8 H16 S4096 D128 bf16 (config 4)"),
     "flash_fwd_c3": (flash_workload, dict(dtype="fp32", BH=24, S=256, D=64, causal=True),
                      "fp32", "causal FlashAttention fwd B4 H6 S256 D64 fp32 (config 3)"),
+    "gemm_f64_511": (gemm_f64_workload, dict(M=511, N=511, K=511), "fp64",
+                     "fp64 `@` 511^3 (below the dispatch threshold: the reference's dgemm "
+                     "order, bit-identical)"),
+    "gemm_f64_256x1024_k4096": (gemm_f64_workload, dict(M=256, N=1023, K=4096), "fp64",
+                                "fp64 `@` 256 x 4096 @ 4096 x 1023 (below the threshold, long K)"),
+    "attention_f64_d256_fwd": (attention_f64_workload, dict(BH=16, S=1024, D=256, causal=True),
+                               "fp64", "causal attention fwd B2 H8 S1024 dk=256 in fp64 "
+                                       "(outside the flash rule)"),
+    "attention_f64_d256_bwd": (attention_f64_workload, dict(BH=16, S=1024, D=256, causal=True,
+                                                            backward=True), "fp64",
+                               "causal attention bwd B2 H8 S1024 dk=256 in fp64"),
     "linear_relu_c2": (linear_workload, dict(N=4096, IN=784, OUT=257), "fp32",
                        "fused linear_relu X[4096x784] W[257x784]^T + b (config 2 layer 1), fp32"),
     "bmm_64x512": (bmm_workload, dict(Bt=64, M=512, N=512, K=512), "fp32",
@@ -616,6 +659,25 @@ def cpu_baseline_workloads(gpu_ms):
     L.backward(yc)
     record("conv2d_bwd_resnet_64x56x56", (time.perf_counter() - t0) * 1000.0, 64 / ni,
            f"{ni} of 64 images, fp64, backward(Y) of the conv, scaled by 64/{ni}")
+    # fp64 `@` below the threshold: the reference's dgemm on the full shapes
+    for name, (M, N, K) in (("gemm_f64_511", (511, 511, 511)),
+                            ("gemm_f64_256x1024_k4096", (256, 1023, 4096))):
+        Ag, Bg = rng.standard_normal((M, K)), rng.standard_normal((K, N))
+        ag, bg = R.tensor(Ag), R.tensor(Bg)
+        record(name, timed(lambda: L.tensor_decref(L.tensor_matmul(ag, bg))), 1,
+               "full shape, fp64 dgemm")
+    # causal attention, dk = 256 (fp64 on the reference's CPU for every shape): 1 of the 16
+    # slices, forward, and backward(O) of the attention node
+    q6, k6, v6 = (R.tensor(rng.standard_normal((1, 1024 * 256)) * 0.5) for _ in range(3))
+    sc6 = [R.scalar(v) for v in (1, 1024, 256)]
+    record("attention_f64_d256_fwd",
+           timed(lambda: L.tensor_decref(L.dream_attention_causal(q6, k6, v6, *sc6))), 16,
+           "1 of 16 slices, S=1024 dk=256, fp64, scaled by 16", 1)
+    o6 = L.dream_attention_causal(q6, k6, v6, *sc6)
+    t0 = time.perf_counter()
+    L.backward(o6)
+    record("attention_f64_d256_bwd", (time.perf_counter() - t0) * 1000.0, 16,
+           "1 of 16 slices, S=1024 dk=256, fp64, backward(O) only, scaled by 16", 1)
     # config 3 flash forward (fp64, single-threaded) on the whole config
     Q3, K3, V3 = (rng.standard_normal((24, 256 * 64)) * 0.5 for _ in range(3))
     record("flash_fwd_c3", timed(lambda: R.attention("flash", Q3, K3, V3, 24, 256, 64, 64)), 1,
@@ -729,7 +791,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if prec == "bf16" else "f64" if args.workload.startswith("ew_") else "f32",
+        "dtype": ("bf16" if prec == "bf16" else
+                  "f64" if prec == "fp64" or args.workload.startswith("ew_") else "f32"),
         "data": "synthetic N(0,1) inputs (numpy PCG64, seeded), resident in HBM",
         "config": {"workload": head["desc"], "name": args.workload},
         "roofline": roofline,

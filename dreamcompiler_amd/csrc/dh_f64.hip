@@ -9,12 +9,14 @@
 //
 // GEMM.  dream_gemm_d zeroes C and, per 256-deep k block (its KC), adds to every element the
 // sum of that block's products, each block's sum being one fused multiply-add chain in k
-// order started from zero (the 4x8 AVX2 micro-kernel, elementwise.inc:547-585).  Here each
-// lane owns a 4x4 block of outputs and runs exactly those chains with v_fma_f64 (IEEE fma,
-// round to nearest even, as _mm256_fmadd_pd), adding the chain to its running total at every
-// 256-boundary of k.  With beta = 0 and alpha = 1 the result is therefore bit-identical to the
-// reference's fp64 `@`.  FP64 FMA on the VALU runs at the chip's full fp64 rate (the same
-// 78.6 TFLOP/s as the fp64 matrix cores), so the kernel stays on plain FMA.
+// order started from zero (the 4x8 AVX2 micro-kernel, elementwise.inc:547-585).  Here the
+// fp64 matrix cores run exactly those chains: v_mfma_f64_16x16x4f64 performs the four
+// products of each output as sequential IEEE fused multiply-adds in k order (round to nearest
+// even, as _mm256_fmadd_pd), so an accumulator started from zero and fed the k-steps in order
+// is the chain; it is added to a running total at every 256-boundary of k.  With beta = 0 and
+// alpha = 1 the result is therefore bit-identical to the reference's fp64 `@`.  Grids too
+// small for the chip split K at those 256-boundaries and sum the block sums in k order in a
+// second launch, which keeps the identity.
 //
 // Attention.  The standard form of training.inc:178-263 on fp64 GEMMs: scores = Q K^T
 // (one batched NT product per chunk of slices), a row kernel applies the scale, the causal
@@ -29,92 +31,194 @@
 namespace dh {
 namespace {
 
-constexpr int F64_TILE = 32;     // 32 x 32 outputs per work-group
-constexpr int F64_KT = 16;       // k-step staged through LDS
-constexpr int F64_KC = 256;      // the reference's KC: chains restart every 256 k
-constexpr int F64_THREADS = 64;  // one wave; lane (tx, ty) in 8 x 8, outputs ty + 8i, tx + 8j
+constexpr int F64_KT = 16;        // k per LDS stage
+constexpr int F64_KC = 256;       // the reference's KC: chains restart every 256 k
+constexpr int F64_THREADS = 256;  // four waves as 2 x 2, each WB x WB blocks of 16 x 16
 
-template <int TA, int TB>
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <int WB>
+struct F64Cfg {
+    static constexpr int TILE = 32 * WB;                       // work-group tile side
+    static constexpr int NLD = TILE * F64_KT / F64_THREADS;    // A (and B) values per thread
+    // LDS copy of an operand tile in its global order, so the stores from global memory
+    // are conflict-free as well as the MFMA operand reads (16 consecutive rows or columns
+    // of one k, times 4 k, per wave):
+    //   k-contiguous (A untransposed, B transposed): [row][k], row pitch KT + 1 doubles;
+    //   row-contiguous (A transposed, B untransposed): [k][row], k pitch TILE + 16 doubles
+    //   (128 bytes past a multiple of the 256-byte bank sweep).
+    static constexpr int KP = F64_KT + 1, RP = TILE + 16;
+    static constexpr int SZ_K = TILE * KP, SZ_R = F64_KT * RP;
+};
+
+// One TILE x TILE output tile over the k range [kbeg, kend): all of K, or (split mode,
+// part != null) the single 256-deep block blockIdx.z, whose chain sum goes to the partial
+// buffer.  Products run on v_mfma_f64_16x16x4f64, which performs its four products of an
+// output as sequential IEEE fused multiply-adds in k order (a GPU probe over 7 M outputs --
+// integers, N(0,1), exponents over 2^+-30, subnormals, infinities and NaNs, 64-step chains --
+// found it bitwise equal to the fma chain), so each accumulator is exactly the reference's
+// chain.  Operand layout: lane l holds A[l % 16][k0 + l / 16] and B[k0 + l / 16][l % 16];
+// result register r holds D[l / 16 + 4 r][l % 16].  k past the range is zero in both
+// operands, and fma(0, 0, c) = c for every chain value (a chain started at +0 never holds
+// -0), so the padded k-steps of a last partial stage change nothing.  Stages of 16 k are
+// double-buffered in LDS; the next stage's global loads are issued before the current
+// stage's products.
+template <int TA, int TB, int WB>
 __global__ __launch_bounds__(F64_THREADS) void gemm_f64_kernel(
     int M, int N, int K, double alpha, const double* __restrict__ A, int lda, long long sA,
     const double* __restrict__ B, int ldb, long long sB, double beta, double* __restrict__ C,
-    int ldc, long long sC, int tilesN) {
-    __shared__ double As[F64_KT][F64_TILE + 1];
-    __shared__ double Bs[F64_KT][F64_TILE + 1];
-    const int t = threadIdx.x, tx = t & 7, ty = t >> 3;
+    int ldc, long long sC, int tilesN, double* __restrict__ part) {
+    using Cf = F64Cfg<WB>;
+    constexpr int TILE = Cf::TILE, NLD = Cf::NLD, KP = Cf::KP, RP = Cf::RP;
+    __shared__ double As[2][TA == 0 ? Cf::SZ_K : Cf::SZ_R];
+    __shared__ double Bs[2][TB == 1 ? Cf::SZ_K : Cf::SZ_R];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wr = 16 * WB * (wave & 1), wc = 16 * WB * (wave >> 1);   // wave's sub-tile
     const int tile = blockIdx.x;
-    const int m0 = (tile / tilesN) * F64_TILE, n0 = (tile % tilesN) * F64_TILE;
+    const int m0 = (tile / tilesN) * TILE, n0 = (tile % tilesN) * TILE;
     const long long b = blockIdx.y;
-    A += b * sA;
-    B += b * sB;
-    C += b * sC;
-
-    double tot[4][4], acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) tot[i][j] = acc[i][j] = 0.0;
-
-    for (int k0 = 0; k0 < K; k0 += F64_KT) {
-        const int kt = K - k0 < F64_KT ? K - k0 : F64_KT;
-        // A tile (32 rows m x 16 k) -> As[k][m]; reads run along the contiguous index.
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            int m, k;
-            if (TA == 0) { k = t & 15; m = (t >> 4) + 4 * r; }
-            else         { m = t & 31; k = (t >> 5) + 2 * r; }
-            const int gm = m0 + m, gk = k0 + k;
-            double v = 0.0;
-            if (gm < M && gk < K) v = TA == 0 ? A[(long long)gm * lda + gk] : A[(long long)gk * lda + gm];
-            As[k][m] = v;
-        }
-        // B tile (16 k x 32 cols n) -> Bs[k][n]
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            int n, k;
-            if (TB == 0) { n = t & 31; k = (t >> 5) + 2 * r; }
-            else         { k = t & 15; n = (t >> 4) + 4 * r; }
-            const int gn = n0 + n, gk = k0 + k;
-            double v = 0.0;
-            if (gn < N && gk < K) v = TB == 0 ? B[(long long)gk * ldb + gn] : B[(long long)gn * ldb + gk];
-            Bs[k][n] = v;
-        }
-        __syncthreads();
-        // Exactly kt products per chain: no padded products enter a sum.
-        for (int kk = 0; kk < kt; ++kk) {
-            double a[4], bb[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = As[kk][ty + 8 * i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bb[j] = Bs[kk][tx + 8 * j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fma(a[i], bb[j], acc[i][j]);
-        }
-        __syncthreads();
-        if ((k0 + F64_KT) % F64_KC == 0 || k0 + F64_KT >= K) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    tot[i][j] = tot[i][j] + acc[i][j];
-                    acc[i][j] = 0.0;
-                }
-        }
+    int kbeg = 0, kend = K;
+    if (part) {
+        kbeg = blockIdx.z * F64_KC;
+        kend = min(K, kbeg + F64_KC);
     }
+    const int ns = (kend - kbeg + F64_KT - 1) / F64_KT;
+
+    // Element (row, k) of an operand tile in LDS.
+    auto a_at = [&](int buf, int row, int k) -> double& {
+        return TA == 0 ? As[buf][row * KP + k] : As[buf][k * RP + row];
+    };
+    auto b_at = [&](int buf, int row, int k) -> double& {
+        return TB == 1 ? Bs[buf][row * KP + k] : Bs[buf][k * RP + row];
+    };
+    // This thread's NLD (row, k) positions per operand, read along the contiguous index
+    // (k-contiguous: 16 lanes per 128-byte row piece; row-contiguous: TILE lanes), with a
+    // loop-invariant pointer to k = kbeg + the position's k and the row's validity.
+    int arow[NLD], ak[NLD], brow[NLD], bk[NLD];
+    const double* ap[NLD];
+    const double* bp[NLD];
+    bool aok[NLD], bok[NLD];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int gm = m0 + ty + 8 * i;
-        if (gm >= M) continue;
+    for (int r = 0; r < NLD; ++r) {
+        if (TA == 0) { ak[r] = t & 15; arow[r] = (t >> 4) + 16 * r; }
+        else         { arow[r] = t % TILE; ak[r] = t / TILE + (F64_THREADS / TILE) * r; }
+        if (TB == 1) { bk[r] = t & 15; brow[r] = (t >> 4) + 16 * r; }
+        else         { brow[r] = t % TILE; bk[r] = t / TILE + (F64_THREADS / TILE) * r; }
+        const int gm = m0 + arow[r], gn = n0 + brow[r];
+        aok[r] = gm < M;
+        bok[r] = gn < N;
+        const long long ka = kbeg + ak[r], kb = kbeg + bk[r];
+        ap[r] = A + b * sA + (aok[r] ? (TA == 0 ? (long long)gm * lda + ka : ka * lda + gm) : 0);
+        bp[r] = B + b * sB + (bok[r] ? (TB == 1 ? (long long)gn * ldb + kb : kb * ldb + gn) : 0);
+    }
+    const long long astep = TA == 0 ? F64_KT : (long long)F64_KT * lda;   // pointer step per stage
+    const long long bstep = TB == 1 ? F64_KT : (long long)F64_KT * ldb;
+    double ra[NLD], rb[NLD];
+    auto fetch = [&](int s) {           // stage s: k = kbeg + 16 s + position
+        const int kleft = kend - kbeg - F64_KT * s;   // valid k in this stage (may exceed 16)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int gn = n0 + tx + 8 * j;
-            if (gn >= N) continue;
-            double* c = C + (long long)gm * ldc + gn;
-            const double v = alpha == 1.0 ? tot[i][j] : alpha * tot[i][j];
-            *c = beta == 0.0 ? v : beta * *c + v;
+        for (int r = 0; r < NLD; ++r) {
+            ra[r] = aok[r] && ak[r] < kleft ? ap[r][s * astep] : 0.0;
+            rb[r] = bok[r] && bk[r] < kleft ? bp[r][s * bstep] : 0.0;
         }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < NLD; ++r) {
+            a_at(buf, arow[r], ak[r]) = ra[r];
+            b_at(buf, brow[r], bk[r]) = rb[r];
+        }
+    };
+
+    f64x4 tot[WB][WB], acc[WB][WB];
+#pragma unroll
+    for (int i = 0; i < WB; ++i)
+#pragma unroll
+        for (int j = 0; j < WB; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tot[i][j][r] = acc[i][j][r] = 0.0;
+    auto step = [&](int buf, int k4) {
+        const int kr = 4 * k4 + (lane >> 4), c = lane & 15;
+        double a[WB], bb[WB];
+#pragma unroll
+        for (int i = 0; i < WB; ++i) a[i] = a_at(buf, wr + 16 * i + c, kr);
+#pragma unroll
+        for (int j = 0; j < WB; ++j) bb[j] = b_at(buf, wc + 16 * j + c, kr);
+#pragma unroll
+        for (int i = 0; i < WB; ++i)
+#pragma unroll
+            for (int j = 0; j < WB; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], bb[j], acc[i][j], 0, 0, 0);
+    };
+
+    // Every stage runs its four k-steps (zeros past kend), so the loop has no branch around
+    // the accumulators; a fetch past the last stage loads nothing and its stash lands in the
+    // buffer no later stage reads.  Blocks of 256 k (kbeg is a multiple of 256): the chain
+    // sum of each is added to tot in k order.
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int s = 0; s < ns;) {
+        const int s_end = min(ns, s + F64_KC / F64_KT);
+        for (; s < s_end; ++s) {
+            const int buf = s & 1;
+            fetch(s + 1);
+#pragma unroll
+            for (int k4 = 0; k4 < F64_KT / 4; ++k4) step(buf, k4);
+            stash(buf ^ 1);   // the buffer stage s - 1 read, released below
+            __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < WB; ++i)
+#pragma unroll
+            for (int j = 0; j < WB; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    tot[i][j][r] = tot[i][j][r] + acc[i][j][r];
+                    acc[i][j][r] = 0.0;
+                }
+    }
+    // lane l, register r of block (i, j): row wr + 16 i + l / 16 + 4 r, column wc + 16 j + l % 16
+    double* out = part ? part + ((long long)blockIdx.z * gridDim.y + b) * ((long long)M * N)
+                       : C + b * sC;
+    const long long ld = part ? N : ldc;
+#pragma unroll
+    for (int i = 0; i < WB; ++i)
+#pragma unroll
+        for (int j = 0; j < WB; ++j) {
+            const int gn = n0 + wc + 16 * j + (lane & 15);
+            if (gn >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gm = m0 + wr + 16 * i + (lane >> 4) + 4 * r;
+                if (gm >= M) continue;
+                double* c = out + (long long)gm * ld + gn;
+                if (part) {             // this block's chain sum, compact M x N per (block, member)
+                    *c = tot[i][j][r];
+                } else {
+                    const double v = alpha == 1.0 ? tot[i][j][r] : alpha * tot[i][j][r];
+                    *c = beta == 0.0 ? v : beta * *c + v;
+                }
+            }
+        }
+}
+
+// Split-K finish: C = alpha * (((0 + s_0) + s_1) + ...) over the per-block chain sums in k
+// order -- the reference's accumulation of its block sums into a zeroed C -- then beta.
+__global__ __launch_bounds__(256) void gemm_f64_reduce(int M, int N, int nkb, int batch,
+                                                       const double* __restrict__ part,
+                                                       double alpha, double beta,
+                                                       double* __restrict__ C, int ldc,
+                                                       long long sC) {
+    const long long mn = (long long)M * N, total = mn * batch;
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < total;
+         idx += (long long)gridDim.x * 256) {
+        const long long b = idx / mn, rem = idx - b * mn;
+        double tot = 0.0;
+        for (int z = 0; z < nkb; ++z) tot = tot + part[((long long)z * batch + b) * mn + rem];
+        double* c = C + b * sC + (rem / N) * (long long)ldc + rem % N;
+        const double v = alpha == 1.0 ? tot : alpha * tot;
+        *c = beta == 0.0 ? v : beta * *c + v;
     }
 }
 
@@ -167,20 +271,50 @@ __global__ __launch_bounds__(256) void attn_softmax_bwd_f64(const double* __rest
     for (int j = lane; j < S; j += 64) g[j] = j < n ? p[j] * (g[j] - rd) : 0.0;
 }
 
-int gemm_f64_launch(int transA, int transB, int M, int N, int K, double alpha, const double* A,
-                    int lda, long long sA, const double* B, int ldb, long long sB, double beta,
-                    double* C, int ldc, long long sC, int batch) {
-    const long long tilesM = (M + F64_TILE - 1) / F64_TILE, tilesN = (N + F64_TILE - 1) / F64_TILE;
-    const dim3 grid((unsigned)(tilesM * tilesN), (unsigned)batch);
+template <int WB>
+void launch_f64(int transA, int transB, dim3 grid, int M, int N, int K, double alpha,
+                const double* A, int lda, long long sA, const double* B, int ldb, long long sB,
+                double beta, double* C, int ldc, long long sC, int tilesN, double* part) {
 #define DH_F64_LAUNCH(TA, TB)                                                                  \
-    gemm_f64_kernel<TA, TB><<<grid, F64_THREADS, 0, stream()>>>(M, N, K, alpha, A, lda, sA, B, \
-                                                                ldb, sB, beta, C, ldc, sC,     \
-                                                                (int)tilesN)
+    gemm_f64_kernel<TA, TB, WB><<<grid, F64_THREADS, 0, stream()>>>(                           \
+        M, N, K, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tilesN, part)
     if (!transA && !transB) DH_F64_LAUNCH(0, 0);
     else if (!transA) DH_F64_LAUNCH(0, 1);
     else if (!transB) DH_F64_LAUNCH(1, 0);
     else DH_F64_LAUNCH(1, 1);
 #undef DH_F64_LAUNCH
+}
+
+int gemm_f64_launch(int transA, int transB, int M, int N, int K, double alpha, const double* A,
+                    int lda, long long sA, const double* B, int ldb, long long sB, double beta,
+                    double* C, int ldc, long long sC, int batch) {
+    // 64 x 64 tiles (2 x 2 blocks per wave) when they fill the chip twice over, else 32 x 32.
+    // Grids still too small split K at the reference's 256-deep block boundaries (one
+    // work-group per block, each block's chain sum stored, then summed in k order by
+    // gemm_f64_reduce), which leaves every result bit-identical.
+    const long long fill = 2LL * num_cus();
+    const int wb = ((M + 63) / 64) * (long long)((N + 63) / 64) * batch >= fill ? 2 : 1;
+    const long long tilesM = (M + 32 * wb - 1) / (32 * wb), tilesN = (N + 32 * wb - 1) / (32 * wb);
+    const long long nkb = ((long long)K + F64_KC - 1) / F64_KC;
+    const size_t pbytes = (size_t)nkb * batch * M * N * sizeof(double);
+    double* part = nullptr;
+    if (nkb > 1 && nkb <= 65535 && tilesM * tilesN * batch < fill && pbytes <= ((size_t)512 << 20))
+        part = static_cast<double*>(dh_malloc(pbytes));   // none: the unsplit grid
+    const dim3 grid((unsigned)(tilesM * tilesN), (unsigned)batch, part ? (unsigned)nkb : 1u);
+    if (wb == 2)
+        launch_f64<2>(transA, transB, grid, M, N, K, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc,
+                      sC, (int)tilesN, part);
+    else
+        launch_f64<1>(transA, transB, grid, M, N, K, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc,
+                      sC, (int)tilesN, part);
+    if (part) {
+        const long long total = (long long)M * N * batch;
+        long long blocks = (total + 255) / 256;
+        if (blocks > 8LL * num_cus()) blocks = 8LL * num_cus();
+        gemm_f64_reduce<<<(unsigned)blocks, 256, 0, stream()>>>(M, N, (int)nkb, batch, part,
+                                                                 alpha, beta, C, ldc, sC);
+        dh_free(part);   // pooled: stream order keeps the buffer alive for the queued work
+    }
     return check_launch("dh_gemm_f64");
 }
 
@@ -201,7 +335,7 @@ int check_gemm_f64(const char* op, int transA, int transB, int M, int N, int K, 
         return set_error(DH_ERR_INVALID, "%s: batch members of C overlap (strideC=%lld)", op, sC);
     if (batch > 65535)
         return set_error(DH_ERR_UNSUPPORTED, "%s: batch %d above 65535", op, batch);
-    const long long tiles = (long long)((M + F64_TILE - 1) / F64_TILE) * ((N + F64_TILE - 1) / F64_TILE);
+    const long long tiles = (long long)((M + 31) / 32) * ((N + 31) / 32);
     if (tiles > 0x7fffffffLL)
         return set_error(DH_ERR_UNSUPPORTED, "%s: %lld output tiles", op, tiles);
     return DH_OK;

@@ -44,7 +44,10 @@ def gemm64(A, B, transA=0, transB=0, beta=0.0, C0=None, alpha=1.0, pad=0):
 SHAPES = [(1, 1, 1), (1, 7, 1), (5, 1, 9), (3, 4, 5), (7, 13, 17), (31, 33, 37), (64, 64, 64),
           (65, 63, 66), (128, 100, 96), (200, 50, 300), (257, 129, 255), (4096, 257, 10),
           (100, 256, 70), (33, 257, 40), (70, 512, 33), (9, 1000, 130), (300, 2049, 7),
-          (511, 300, 511)]
+          (511, 300, 511),
+          # grids of >= 512 tiles: one work-group runs all of K (the others split K at the
+          # 256-deep blocks and sum the block sums in a second launch)
+          (1024, 600, 512), (700, 513, 800)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
@@ -98,6 +101,15 @@ def test_gemm_f64_batched_and_zero_k():
     C = dC.numpy()
     for b in range(Bt):
         assert np.array_equal(C[b], O.gemm_d(A[b], B[0]))
+    # 520 members of one tile each: a grid of >= 512 work-groups, K not split
+    Bt, M, K, N = 520, 19, 300, 23
+    A, B = rng.standard_normal((Bt, M, K)), rng.standard_normal((Bt, K, N))
+    dA, dB = DB.from_numpy(A), DB.from_numpy(B)
+    dC = DB.empty((Bt, M, N), np.float64)
+    hip.gemm_f64(0, 0, M, N, K, dA, K, dB, N, 0.0, dC, N, sA=M * K, sB=K * N, sC=M * N, batch=Bt)
+    C = dC.numpy()
+    for b in range(0, Bt, 37):
+        assert np.array_equal(C[b], O.gemm_d(A[b], B[b]))
     # K = 0: C = beta * C
     C0 = rng.standard_normal((4, 6))
     assert np.array_equal(gemm64(np.zeros((4, 0)), np.zeros((0, 6)), beta=0.5, C0=C0), 0.5 * C0)
