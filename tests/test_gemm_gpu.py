@@ -390,14 +390,16 @@ def test_fp32_64x64_tiles(Bt, M, N, K, ta, tb):
 
 
 @pytest.mark.parametrize("Bt,M,N,K", [(1, 1000, 1000, 300), (1, 999, 1001, 257), (2, 512, 900, 512),
-                                      (1, 1024, 960, 1000)])
+                                      (1, 1024, 960, 1000), (1, 1000, 1000, 256), (1, 960, 1000, 1300)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("row_bias", [False, True])
 def test_fp32_64x64_two_waves_per_simd(Bt, M, N, K, ta, tb, row_bias):
     # At most one 64 x 64 tile per CU (256 on MI355X) and K >= 256: the 8-wave kernel, two
     # waves per 32 x 32 block splitting each 32-wide k-slice and reducing through LDS.
     # Ragged M / N, K not a multiple of 32 (300, 1000) or of 4 (257: scalar loads), batched,
-    # all layouts, beta and either bias orientation with ReLU.
+    # all layouts, beta and either bias orientation with ReLU.  K = 256, 512, 1000 and 1300
+    # (8, 16, 32 and 41 slices) keep four slices in flight, 1300 with three zero slices in its
+    # last group of four; the others two.
     got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.5, relu=True, row_bias=row_bias,
                    seed=M + N + K + ta + 2 * tb + row_bias)
     assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
