@@ -94,6 +94,32 @@ struct Slice {
             }
         }
     }
+    // The same copy into a 64-wide, unpadded k-major tile whose element (k, t) sits at
+    // k * 64 + swz64(k, t): for 32-wide slices (8 float4 per row of a k-contiguous operand) the
+    // padded layout puts rows kq and kq + 4 of a transposing store on the same banks, and the
+    // two k-rows of an MFMA operand read (lanes 0-31 row k, 32-63 row k + 1) on overlapping
+    // ones.  swz64 flips bit 5 of t on odd k (the two rows of a read fall in opposite bank
+    // halves) and bits 3-5 by (k / 4) % 8 (the 8 k-quads of a store on distinct banks); it
+    // keeps runs of 4 aligned t together, so the row copies stay 16-byte stores.
+    __device__ static int swz64(int k, int t) { return t ^ (32 * (k & 1)) ^ (8 * ((k >> 2) & 7)); }
+    __device__ void store_swz(float* lds, int tid) const {
+        static_assert(TILE == 64, "64-wide tiles");
+#pragma unroll
+        for (int r = 0; r < CH; ++r) {
+            const int f = tid + r * NT;
+            if (KCONTIG) {
+                const int t = f / (BKT / 4), kq = f % (BKT / 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int k = 4 * kq + e;
+                    lds[k * 64 + swz64(k, t)] = v[r][e];
+                }
+            } else {
+                const int k = f / (TILE / 4), tq = f % (TILE / 4);
+                *reinterpret_cast<f32x4*>(&lds[k * 64 + swz64(k, 4 * tq)]) = v[r];
+            }
+        }
+    }
 };
 
 // Work-group tile TBM x TBN (128 x 128, or 64 x 256 / 256 x 64 for products with M or N at
@@ -238,9 +264,9 @@ gemm_f32_ks_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     A += blockIdx.y * sA;
     B += blockIdx.y * sB;
     C += blockIdx.y * sC;
-    constexpr int T = 64, LDS_A = T + 4, LDS_B = T + 4;
-    __shared__ __attribute__((aligned(16))) float As[2][KS_BK * LDS_A];
-    __shared__ __attribute__((aligned(16))) float Bs[2][KS_BK * LDS_B];
+    constexpr int T = 64;   // tiles k-major, 64 floats per k-row, swizzled (Slice::swz64)
+    __shared__ __attribute__((aligned(16))) float As[2][KS_BK * T];
+    __shared__ __attribute__((aligned(16))) float Bs[2][KS_BK * T];
 
     const int tiles_m = (M + T - 1) / T, tiles_n = (N + T - 1) / T;
     int tm, tn;
@@ -265,15 +291,17 @@ gemm_f32_ks_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
             sa[q].fetch(A, lda, m0, q * KS_BK, M, K, tid);
             sb[q].fetch(B, ldb, n0, q * KS_BK, N, K, tid);
         }
-        sa[0].store(As[0], LDS_A, tid);
-        sb[0].store(Bs[0], LDS_B, tid);
+        sa[0].store_swz(As[0], tid);
+        sb[0].store_swz(Bs[0], tid);
         __syncthreads();
     }
+    using SA = Slice<!TA, VA, T, KS_BK, KS_NT>;
     auto mma = [&](const float* as, const float* bs) {   // this wave's half of a k-slice
 #pragma unroll
         for (int kk = 0; kk < KS_BK / 2; kk += 2) {
-            const float av = as[(kh0 + kk + h) * LDS_A + wm + l32];
-            const float bv = bs[(kh0 + kk + h) * LDS_B + wn + l32];
+            const int k = kh0 + kk + h;
+            const float av = as[k * T + SA::swz64(k, wm + l32)];
+            const float bv = bs[k * T + SA::swz64(k, wn + l32)];
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
         }
     };
@@ -284,8 +312,8 @@ gemm_f32_ks_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
         sa[cur].fetch(A, lda, m0, (kt + PF) * KS_BK, M, K, tid);
         sb[cur].fetch(B, ldb, n0, (kt + PF) * KS_BK, N, K, tid);
         mma(As[lb], Bs[lb]);
-        sa[nxt].store(As[lb ^ 1], LDS_A, tid);
-        sb[nxt].store(Bs[lb ^ 1], LDS_B, tid);
+        sa[nxt].store_swz(As[lb ^ 1], tid);
+        sb[nxt].store_swz(Bs[lb ^ 1], tid);
         __syncthreads();
     };
     if (nk == 1) {
