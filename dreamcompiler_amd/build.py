@@ -89,7 +89,7 @@ def build(verbose=False, jobs=None):
         tmp = rt_so + ".tmp"
         # The reference runtime's own host flags (src/main.cpp:994): -ffast-math also fixes
         # how libstdc++'s normal_distribution evaluates, so randn streams match the reference.
-        _run([HIPCC, "-std=c++17", "-O3", "-ffast-math", "-mavx2", "-mfma", "-fno-math-errno", "-fPIC", "-shared",
+        _run([HIPCC, "-std=c++17", "-O3", "-ffast-math", "-mavx2", "-mfma", "-fno-math-errno", "-fPIC", "-shared", "-pthread",
               "-I" + os.path.join(ROOT, "include"),
               *[os.path.join(CSRC, s) for s in rt], "-L" + LIBDIR, "-ldream_hip",
               "-Wl,-rpath,$ORIGIN", "-o", tmp], verbose)

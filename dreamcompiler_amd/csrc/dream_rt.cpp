@@ -24,6 +24,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <random>
+#include <thread>
 #include <unordered_set>
 #include <vector>
 
@@ -36,6 +37,27 @@ bool g_bf16 = false;   // dream_enable_fp16(): reduced-precision `@`
 std::mt19937& rng() {
     static std::mt19937 g(std::random_device{}());
     return g;
+}
+
+// body(i0, i1) over [0, n) in chunks on up to 16 host threads, for host loops over large
+// tensors whose iterations are independent (each writes only its own elements), so the
+// result does not depend on the split.  Small ranges run inline.
+template <typename F>
+void par_for(size_t n, F body) {
+    constexpr size_t kMin = size_t(1) << 20;
+    const unsigned hw = std::thread::hardware_concurrency();
+    const size_t nt = std::min<size_t>({n / kMin, hw ? hw : 1, 16});
+    if (nt <= 1) {
+        body(size_t(0), n);
+        return;
+    }
+    std::vector<std::thread> th;
+    th.reserve(nt - 1);
+    const size_t step = (n + nt - 1) / nt;
+    for (size_t k = 1; k < nt; ++k)
+        th.emplace_back([=] { body(std::min(n, k * step), std::min(n, (k + 1) * step)); });
+    body(size_t(0), std::min(n, step));
+    for (auto& x : th) x.join();
 }
 
 void rt_error(const char* op, const char* fmt, ...) {
@@ -190,7 +212,11 @@ void flush_dgrad(Tensor* t) {
     } else {
         std::vector<float> h(n);
         need(dh_memcpy_d2h(h.data(), t->dgrad, n * sizeof(float)));
-        for (size_t i = 0; i < n; ++i) t->grad[i] += (double)h[i];
+        double* g = t->grad;
+        const float* hp = h.data();
+        par_for(n, [=](size_t i0, size_t i1) {
+            for (size_t i = i0; i < i1; ++i) g[i] += (double)hp[i];
+        });
     }
     dh_free(t->dgrad);
     t->dgrad = nullptr;
@@ -1418,12 +1444,29 @@ Tensor* backward(Tensor* root) {
                     if ((t->dlse || t->f64_node) && hip_ready("backward(attention)"))
                         attention_backward(t, t->op != DREAM_OP_ATTN);
                     break;
-                case DREAM_OP_SUM:
+                case DREAM_OP_SUM: {
                     host_grad(t);
-                    for (int j = 0; j < t->lhs->size; ++j) t->lhs->grad[j] += t->grad[0];
+                    double* lg = t->lhs->grad;
+                    const double g0 = t->grad[0];
+                    par_for((size_t)t->lhs->size, [=](size_t j0, size_t j1) {
+                        for (size_t j = j0; j < j1; ++j) lg[j] += g0;
+                    });
                     break;
+                }
                 case DREAM_OP_MUL:
                     host_grad(t);
+                    if (t->lhs->size == t->size && t->rhs->size == t->size && t->lhs != t->rhs) {
+                        // same shapes, distinct operands: every j updates its own elements
+                        double *lg = t->lhs->grad, *rg = t->rhs->grad;
+                        const double *ld = t->lhs->data, *rd = t->rhs->data, *g = t->grad;
+                        par_for((size_t)t->size, [=](size_t j0, size_t j1) {
+                            for (size_t j = j0; j < j1; ++j) {
+                                lg[j] += g[j] * rd[j];
+                                rg[j] += g[j] * ld[j];
+                            }
+                        });
+                        break;
+                    }
                     for (int j = 0; j < t->size; ++j) {
                         const double g = t->grad[j];
                         t->lhs->grad[j % t->lhs->size] += g * t->rhs->data[j % t->rhs->size];

@@ -113,6 +113,50 @@ def test_attention_builtins_vs_golden_math(L, B, S, dk):
             assert maxrel(rt.read(t, grad=True).reshape(B, -1), r) <= tol, kind
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("bf16", [False, True])
+def test_c4_flash_builtin_full_size(L, bf16):
+    """Config 4 through the builtins: dream_flash_attention(Q, K, V, 128, 4096, 128, 64) on fp64
+    host tensors (B8 x H16 slices), then backward(sum(O * W)), in the default precision (fp32
+    FlashAttention kernels) and with dream_enable_fp16 (bf16 kernels; inputs and W pre-rounded
+    to bf16 so the oracle sees the device's values).  O, dQ, dK, dV of 6 random slices in full
+    against the fp64 oracle; on every slice causal row 0 of O = V_0 and sum_j dV_j = sum_i W_i
+    (rows of P sum to one)."""
+    B, S, dk = 128, 4096, 128
+    rng = np.random.default_rng(44 + bf16)
+    X = [rng.standard_normal((B, S * dk)) for _ in range(4)]
+    if bf16:
+        X = [O.bf16_round(x.astype(np.float32)).astype(np.float64) for x in X]
+        L.dream_enable_fp16()
+    try:
+        Q, K, V, W = X
+        args, o = _attn(L, L.dream_flash_attention, Q, K, V, B, S, dk, 64)
+        Og = rt.read(o).reshape(B, S, dk)
+        w = rt.tensor(W)
+        m = L.tensor_mul(o, w)
+        loss = L.sum(m)
+        r = L.backward(loss)
+        grads = [rt.read(t, grad=True).reshape(B, S, dk) for t in args]
+        rt.release(r, loss, m, w, o, *args)
+    finally:
+        if bf16:
+            L.dream_disable_fp16()
+    tol = 2e-2 if bf16 else 1e-5 * np.sqrt(S)
+    V3, W3 = V.reshape(B, S, dk), W.reshape(B, S, dk)
+    assert np.allclose(Og[:, 0], V3[:, 0], rtol=0, atol=tol * np.abs(V3[:, 0]).max())
+    dVsum, Wsum = grads[2].sum(axis=1), W3.sum(axis=1)
+    assert np.abs(dVsum - Wsum).max() <= tol * np.abs(W3).sum(axis=1).max()
+    sl = rng.choice(B, 6, replace=False)
+    sub = lambda x: np.ascontiguousarray(x.reshape(B, S * dk)[sl])  # noqa: E731
+    rO = O.attention(sub(Q), sub(K), sub(V), len(sl), S, dk, True).reshape(-1, S, dk)
+    refs = [r.reshape(-1, S, dk) for r in
+            O.attention_bwd(sub(Q), sub(K), sub(V), sub(W), len(sl), S, dk, True)]
+    for i, b in enumerate(sl):
+        assert maxrel(Og[b], rO[i]) <= tol, ("O", b)
+        for name, g, r in zip(("dQ", "dK", "dV"), grads, refs):
+            assert maxrel(g[b], r[i]) <= tol, (name, b)
+
+
 def test_26_flash_backward_matches_standard(L):
     # tests/26_flash_backward.dream: sum|dQ| of flash vs attention_causal, S=32, dk=16, Bc=8
     L.dream_set_seed(rt.scalar(5))
