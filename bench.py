@@ -773,6 +773,10 @@ def main():
     ap.add_argument("--only", action="store_true",
                     help="time only --workload (for profiling runs); no extra metrics")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only time the vendor library on the headline shape (hipBLASLt through "
+                         "torch.mm, bf16 8192^3, fp32 out) under the same --warmup / --steps, "
+                         "after the same kind of idle gap the bench has before its launches")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain device copies of 1 GiB (dh_convert F32->F32), the "
                          "known-size reference for rocprof FETCH_SIZE / WRITE_SIZE")
@@ -781,6 +785,28 @@ def main():
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         sys.exit(2)
+    if args.vendor:   # before this library loads: torch brings its own HIP runtime
+        import torch
+        n = 8192
+        a = torch.randn(n, n, device="cuda").to(torch.bfloat16)
+        b = torch.randn(n, n, device="cuda").to(torch.bfloat16)
+        torch.cuda.synchronize()
+        time.sleep(2.0)   # the GPU idles while bench.py generates its inputs on the host
+        for _ in range(args.warmup):
+            torch.mm(a, b, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            torch.mm(a, b, out_dtype=torch.float32)
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        print(json.dumps({"vendor": "hipBLASLt via torch.mm, bf16 8192^3, fp32 out",
+                          "warmup": args.warmup, "steps": args.steps, "ms": round(ms, 5),
+                          "tflops": round(2.0 * n ** 3 / ms / 1e9, 1)}), flush=True)
+        return
+
     if not hip.available():
         raise SystemExit("bench.py: no usable HIP device: " + hip.load().dh_last_error().decode())
 
