@@ -774,9 +774,11 @@ def main():
                     help="time only --workload (for profiling runs); no extra metrics")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--vendor", action="store_true",
-                    help="only time the vendor library on the headline shape (hipBLASLt through "
-                         "torch.mm, bf16 8192^3, fp32 out) under the same --warmup / --steps, "
-                         "after the same kind of idle gap the bench has before its launches")
+                    help="only time the vendor libraries: hipBLASLt through torch.mm on the "
+                         "headline shape (bf16 8192^3, fp32 out) after the same kind of idle gap "
+                         "the bench has before its launches, then config 4's causal attention "
+                         "forward and backward through torch's scaled_dot_product_attention "
+                         "backends, under the same --warmup / --steps")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain device copies of 1 GiB (dh_convert F32->F32), the "
                          "known-size reference for rocprof FETCH_SIZE / WRITE_SIZE")
@@ -802,9 +804,50 @@ def main():
         t1.record()
         torch.cuda.synchronize()
         ms = t0.elapsed_time(t1) / args.steps
-        print(json.dumps({"vendor": "hipBLASLt via torch.mm, bf16 8192^3, fp32 out",
-                          "warmup": args.warmup, "steps": args.steps, "ms": round(ms, 5),
-                          "tflops": round(2.0 * n ** 3 / ms / 1e9, 1)}), flush=True)
+        out = {"vendor": "hipBLASLt via torch.mm, bf16 8192^3, fp32 out",
+               "warmup": args.warmup, "steps": args.steps, "ms": round(ms, 5),
+               "tflops": round(2.0 * n ** 3 / ms / 1e9, 1)}
+        del a, b
+        # config 4 through torch's scaled_dot_product_attention, each backend it offers here
+        import torch.nn.functional as F
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        Bt, H, S, D = 8, 16, 4096, 128
+        q, k, v = (torch.randn(Bt, H, S, D, device="cuda", dtype=torch.bfloat16,
+                               requires_grad=True) for _ in range(3))
+        g = torch.randn(Bt, H, S, D, device="cuda", dtype=torch.bfloat16)
+        fwd_flops = 4.0 * Bt * H * D * S * (S + 1) / 2
+
+        def timed(fn, steps):
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0.record()
+            for _ in range(steps):
+                fn()
+            t1.record()
+            torch.cuda.synchronize()
+            return t0.elapsed_time(t1) / steps
+
+        attn = {}
+        for name, be in (("flash", SDPBackend.FLASH_ATTENTION),
+                         ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+            try:
+                with sdpa_kernel(be):
+                    f_ms = timed(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True),
+                                 args.steps)
+                    o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+
+                    def bwd():
+                        q.grad = k.grad = v.grad = None
+                        o.backward(g, retain_graph=True)
+                    b_ms = timed(bwd, max(5, args.steps // 2))
+                attn[name] = {"fwd_ms": round(f_ms, 4), "fwd_tflops": round(fwd_flops / f_ms / 1e9, 1),
+                              "bwd_ms": round(b_ms, 4),
+                              "bwd_tflops": round(2.5 * fwd_flops / b_ms / 1e9, 1)}
+            except Exception as e:  # a backend this torch build does not offer
+                attn[name] = {"error": repr(e)[:200]}
+        out["sdpa_c4_causal_bf16"] = attn
+        print(json.dumps(out), flush=True)
         return
 
     if not hip.available():
