@@ -3,11 +3,14 @@
 // Gradients of O = softmax(Q K^T * scale) V (causal or not) given O and the row LSE
 // saved by the forward: P is recomputed as exp(S * scale - LSE) instead of the
 // reference's two extra recompute passes for (m, l) and D_i
-// (runtime/ops/autograd.inc:779-840).  Three launches, no floating-point atomics, so
-// every run gives bit-identical gradients:
+// (runtime/ops/autograd.inc:779-840).  No floating-point atomics, so every run gives
+// bit-identical gradients.  fp32, three launches:
 //   1. Dvec_i = dO_i . O_i                                   (one pass over O, dO)
 //   2. per key tile:   dV += P^T dO,  dK += scale * dS^T Q    (dS = P o (dP - Dvec))
 //   3. per query tile: dQ += scale * dS K                     (S and dP recomputed)
+// bf16, two: the per-query-tile launch runs first and forms Dvec_i (and LSE_i log2 e) from
+// the dO row it holds anyway and the O row, stores them, and the per-key-tile launch reads
+// them.
 // MFMA layouts: in launch 2 the scores are formed as S = Q K^T so the lane index is the
 // key (the row of dK / dV); in launch 3 as S^T = K Q^T so the lane index is the query.
 // Either way the product that consumes P or dS takes it straight from the score
@@ -35,30 +38,30 @@ __device__ inline uint32_t cvt_pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));   // RNE
 }
 
-// dK/dV epilogue store of one lane's 4 columns.  kv_alias: dK and dV are the same buffer
-// (K and V are one tensor, e.g. attention(q, q, q)); it then receives dK + dV (+ its old
-// contents), the sum the reference's per-input "+=" leaves there (autograd.inc:693-728).
-__device__ inline void store_dkdv(float* dk, float* dv, f32x4 a, f32x4 b, int accumulate,
+// dK/dV epilogue store of one lane's 4 columns; acc_k / acc_v: add to the buffer's contents.
+// kv_alias: dK and dV are the same buffer (K and V are one tensor, e.g. attention(q, q, q));
+// it then receives dK + dV (+ its contents with acc_k), the sum the reference's per-input
+// "+=" leaves there (autograd.inc:693-728).
+__device__ inline void store_dkdv(float* dk, float* dv, f32x4 a, f32x4 b, int acc_k, int acc_v,
                                   int kv_alias) {
     if (kv_alias) {
         a += b;
-        if (accumulate) a += *reinterpret_cast<const f32x4*>(dk);
+        if (acc_k) a += *reinterpret_cast<const f32x4*>(dk);
         *reinterpret_cast<f32x4*>(dk) = a;
         return;
     }
-    if (accumulate) {
-        a += *reinterpret_cast<const f32x4*>(dk);
-        b += *reinterpret_cast<const f32x4*>(dv);
-    }
+    if (acc_k) a += *reinterpret_cast<const f32x4*>(dk);
+    if (acc_v) b += *reinterpret_cast<const f32x4*>(dv);
     *reinterpret_cast<f32x4*>(dk) = a;
     *reinterpret_cast<f32x4*>(dv) = b;
 }
 
 // ---------------------------------------------------------------------------------
-// 1. Dvec = rowsum(dO * O).  16 lanes per row, each reading its D / 16 consecutive
-//    elements of O and of dO as one vector (4 to 32 bytes; the entry point requires
-//    16-byte aligned tensors and D is a multiple of 32); work-groups stride over the
-//    16-row groups so that a large BH * S does not launch one tiny work-group per group.
+// 1. Dvec = rowsum(dO * O) (fp32; the bf16 dQ launch forms it itself).  16 lanes per row,
+//    each reading its D / 16 consecutive elements of O and of dO as one vector (4 to 32
+//    bytes; the entry point requires 16-byte aligned tensors and D is a multiple of 32);
+//    work-groups stride over the 16-row groups so that a large BH * S does not launch one
+//    tiny work-group per group.
 // ---------------------------------------------------------------------------------
 template <int NDW>
 __device__ inline void load_dw(const uint32_t* __restrict__ p, uint32_t (&w)[NDW]) {
@@ -80,8 +83,7 @@ __device__ inline void load_dw(const uint32_t* __restrict__ p, uint32_t (&w)[NDW
 
 template <typename T, int D>
 __global__ void __launch_bounds__(NT)
-dvec_kernel(int rows, const T* __restrict__ O, const T* __restrict__ dO, float* __restrict__ Dv,
-            const float* __restrict__ LSE, float* __restrict__ L2) {
+dvec_kernel(int rows, const T* __restrict__ O, const T* __restrict__ dO, float* __restrict__ Dv) {
     constexpr int NDW = D * (int)sizeof(T) / 4 / 16;   // dwords per lane
     static_assert(NDW == 1 || NDW == 2 || NDW % 4 == 0, "lane chunk of 4, 8 or 16n bytes");
     const int sub = threadIdx.x & 15;
@@ -108,10 +110,7 @@ dvec_kernel(int rows, const T* __restrict__ O, const T* __restrict__ dO, float* 
         acc += dpp_quad_xor2(acc);
         acc += dpp_half_mirror(acc);
         acc += dpp_row_mirror(acc);
-        if (row < rows && sub == 0) {
-            Dv[row] = acc;
-            if (L2) L2[row] = LSE[row] * 1.4426950408889634f;   // log2-domain LSE (bf16 kernels)
-        }
+        if (row < rows && sub == 0) Dv[row] = acc;
     }
 }
 
@@ -185,7 +184,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
                      const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                      const uint16_t* __restrict__ dO, const float* __restrict__ L2,
                      const float* __restrict__ Dv, float* __restrict__ dK,
-                     float* __restrict__ dV, int accumulate, int kv_alias, int group) {
+                     float* __restrict__ dV, int acc_k, int acc_v, int kv_alias, int group) {
     using T = BwTile<D, KV_BQ>;
     using R = BwTile<D, KV_KEYS>;                    // resident K, V of the work-group's keys
     constexpr int ND = D / 32, NTK = D / 16;
@@ -449,7 +448,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
             f32x4 a = {dkacc[d][4 * q] * scale, dkacc[d][4 * q + 1] * scale,
                        dkacc[d][4 * q + 2] * scale, dkacc[d][4 * q + 3] * scale};
             f32x4 b = {dvacc[d][4 * q], dvacc[d][4 * q + 1], dvacc[d][4 * q + 2], dvacc[d][4 * q + 3]};
-            store_dkdv(dkr + col, dvr + col, a, b, accumulate, kv_alias);
+            store_dkdv(dkr + col, dvr + col, a, b, acc_k, acc_v, kv_alias);
         }
 }
 
@@ -469,9 +468,9 @@ template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(DQ_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __restrict__ Q,
                    const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-                   const uint16_t* __restrict__ dO, const float* __restrict__ L2,
-                   const float* __restrict__ Dv, float* __restrict__ dQ, int accumulate,
-                   int group) {
+                   const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO,
+                   const float* __restrict__ LSE, float* __restrict__ L2,
+                   float* __restrict__ Dv, float* __restrict__ dQ, int accumulate, int group) {
     using T = BwTile<D, DQ_BN>;
     constexpr int ND = D / 32, NTK = D / 16;
     constexpr int STAGE = 2 * T::TILE;               // K tile, then V tile
@@ -516,19 +515,33 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
         }
     };
 
-    // Q and dO rows of this lane's query as B operands: Q[i][16t + 8h .. +7].
+    // Q and dO rows of this lane's query as B operands: Q[i][16t + 8h .. +7].  The same
+    // elements of O give the lane half of Dvec_i = dO_i . O_i; the two halves (lanes l and
+    // l ^ 32) are added, and Dvec_i and LSE_i log2(e) are stored for the dK/dV launch.
     bf16x8 qf[NTK], gf[NTK];
     float lse2, dvi;
     {
         const int ic = min(i, S - 1);
+        float part = 0.f;
 #pragma unroll
         for (int t = 0; t < NTK; ++t) {
             const size_t off = base + (size_t)ic * D + 16 * t + 8 * h;
+            const u32x4 g4 = *reinterpret_cast<const u32x4*>(dO + off);
+            const u32x4 o4 = *reinterpret_cast<const u32x4*>(O + off);
             qf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(Q + off));
-            gf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(dO + off));
+            gf[t] = __builtin_bit_cast(bf16x8, g4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                part += __uint_as_float(o4[e] << 16) * __uint_as_float(g4[e] << 16);
+                part += __uint_as_float(o4[e] & 0xffff0000u) * __uint_as_float(g4[e] & 0xffff0000u);
+            }
         }
-        lse2 = L2[(size_t)bh * S + ic];
-        dvi = Dv[(size_t)bh * S + ic];
+        dvi = part + xor32(part);
+        lse2 = LSE[(size_t)bh * S + ic] * 1.4426950408889634f;
+        if (h == 0 && i < S) {
+            Dv[(size_t)bh * S + i] = dvi;
+            L2[(size_t)bh * S + i] = lse2;
+        }
 #pragma unroll
         for (int t = 0; t < NTK; ++t)
             asm volatile("" ::"v"(__builtin_bit_cast(u32x4, qf[t])), "v"(__builtin_bit_cast(u32x4, gf[t])));
@@ -808,7 +821,7 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
                        dkacc[d][4 * q + 2] * scale, dkacc[d][4 * q + 3] * scale};
             f32x4 b = {dvacc[d][4 * q], dvacc[d][4 * q + 1], dvacc[d][4 * q + 2],
                        dvacc[d][4 * q + 3]};
-            store_dkdv(dkr + col, dvr + col, a, b, accumulate, kv_alias);
+            store_dkdv(dkr + col, dvr + col, a, b, accumulate, accumulate, kv_alias);
         }
 }
 
@@ -930,10 +943,14 @@ int set_lds(Kern kern, size_t bytes, bool& done) {
     return DH_OK;
 }
 
+// dQ launch first (it also stores Dvec and LSE log2 e into Dv and L2), then dK/dV.  A gradient
+// buffer shared with dQ is added to by the dK/dV launch, so shared buffers receive the sum.
 template <int D, bool CAUSAL>
 int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const void* V,
-             const void* dO, const float* L2, const float* Dv, float* dQ, float* dK, float* dV,
-             int acc, int kv_alias, int acc_q) {
+             const void* O, const void* dO, const float* LSE, float* L2, float* Dv, float* dQ,
+             float* dK, float* dV, int acc) {
+    const int kv_alias = dK == dV;
+    const int acc_k = acc || dK == dQ, acc_v = acc || dV == dQ;
     const float sl2 = scale * 1.4426950408889634f;
     // Each XCD walks its slices 4 at a time, heaviest tile first (slice_group_order): the Q, dO
     // (dK/dV launch) and K, V (dQ launch) streams of a few slices stay in the XCD's L2.
@@ -948,6 +965,18 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
         return e ? std::atoi(e) : 4;
     }();
     {
+        auto kern = bwd_dq_bf16_kernel<D, CAUSAL>;
+        const size_t lds = (size_t)DQ_NSTAGE * 2 * BwTile<D, DQ_BN>::TILE;
+        static bool done = false;
+        DH_TRY(set_lds(kern, lds, done));
+        const int grid = BH * ((S + DQ_ROWS - 1) / DQ_ROWS);
+        kern<<<grid, DQ_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
+                                             (const uint16_t*)K, (const uint16_t*)V,
+                                             (const uint16_t*)O, (const uint16_t*)dO, LSE, L2, Dv,
+                                             dQ, acc, group_q);
+        DH_TRY(check_launch("dh_flash_bwd(dQ bf16)"));
+    }
+    {
         auto kern = bwd_dkdv_bf16_kernel<D, CAUSAL>;
         const size_t lds = (size_t)KV_NSTAGE * (2 * BwTile<D, KV_BQ>::TILE + 2048) +
                            2 * BwTile<D, KV_KEYS>::TILE;
@@ -956,20 +985,9 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
         const int grid = BH * ((S + KV_KEYS - 1) / KV_KEYS);
         kern<<<grid, KV_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
                                              (const uint16_t*)K, (const uint16_t*)V,
-                                             (const uint16_t*)dO, L2, Dv, dK, dV, acc, kv_alias,
-                                             group_kv);
+                                             (const uint16_t*)dO, L2, Dv, dK, dV, acc_k, acc_v,
+                                             kv_alias, group_kv);
         DH_TRY(check_launch("dh_flash_bwd(dK,dV bf16)"));
-    }
-    {
-        auto kern = bwd_dq_bf16_kernel<D, CAUSAL>;
-        const size_t lds = (size_t)DQ_NSTAGE * 2 * BwTile<D, DQ_BN>::TILE;
-        static bool done = false;
-        DH_TRY(set_lds(kern, lds, done));
-        const int grid = BH * ((S + DQ_ROWS - 1) / DQ_ROWS);
-        kern<<<grid, DQ_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
-                                             (const uint16_t*)K, (const uint16_t*)V,
-                                             (const uint16_t*)dO, L2, Dv, dQ, acc_q, group_q);
-        DH_TRY(check_launch("dh_flash_bwd(dQ bf16)"));
     }
     return DH_OK;
 }
@@ -1004,11 +1022,11 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
 }
 
 template <typename T, int D>
-int run_dvec(int rows, const void* O, const void* dO, float* Dv, const float* LSE, float* L2) {
+int run_dvec(int rows, const void* O, const void* dO, float* Dv) {
     // eight work-groups (32 waves) per CU, each striding over 16-row groups
     const int groups = (rows + NT / 16 - 1) / (NT / 16);
     const int grid = groups < 8 * num_cus() ? groups : 8 * num_cus();
-    dvec_kernel<T, D><<<grid, NT, 0, stream()>>>(rows, (const T*)O, (const T*)dO, Dv, LSE, L2);
+    dvec_kernel<T, D><<<grid, NT, 0, stream()>>>(rows, (const T*)O, (const T*)dO, Dv);
     return check_launch("dh_flash_bwd(Dvec)");
 }
 
@@ -1019,11 +1037,10 @@ int dispatch(int dtype, int causal, int BH, int S, float scale, const void* Q, c
     const int rows = BH * S;
     if (dtype == DH_BF16) {
         float* L2 = Dv + rows;                       // second half of the scratch
-        DH_TRY((run_dvec<uint16_t, D>(rows, O, dO, Dv, LSE, L2)));
-        return causal ? run_bf16<D, true>(BH, S, scale, Q, K, V, dO, L2, Dv, dQ, dK, dV, acc, kv_alias, acc_q)
-                      : run_bf16<D, false>(BH, S, scale, Q, K, V, dO, L2, Dv, dQ, dK, dV, acc, kv_alias, acc_q);
+        return causal ? run_bf16<D, true>(BH, S, scale, Q, K, V, O, dO, LSE, L2, Dv, dQ, dK, dV, acc)
+                      : run_bf16<D, false>(BH, S, scale, Q, K, V, O, dO, LSE, L2, Dv, dQ, dK, dV, acc);
     }
-    DH_TRY((run_dvec<float, D>(rows, O, dO, Dv, LSE, nullptr)));
+    DH_TRY((run_dvec<float, D>(rows, O, dO, Dv)));
     return causal ? run_f32<D, true>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc, kv_alias, acc_q)
                   : run_f32<D, false>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc, kv_alias, acc_q);
 }
@@ -1063,9 +1080,9 @@ int check_bwd_args(int dtype, int BH, int S, int D, const void* Q, const void* K
     return DH_OK;
 }
 
-// The three or four launches over caller-supplied scratch Dv (BH*S floats, twice that for
-// bf16).  The dK/dV launch runs before the dQ launch on the same stream, so a dQ buffer shared
-// with dK or dV accumulates onto what that launch stored.
+// The launches over caller-supplied scratch Dv (BH*S floats, twice that for bf16).  fp32: the
+// dK/dV launch runs before the dQ launch on the same stream, so a dQ buffer shared with dK or
+// dV accumulates onto what that launch stored; bf16: the other way round (run_bf16).
 int run_bwd(int dtype, int BH, int S, int D, float scale, int causal, const void* Q,
             const void* K, const void* V, const void* O, const void* dO, const float* LSE,
             float* dQ, float* dK, float* dV, int accumulate, float* Dv) {
@@ -1153,8 +1170,8 @@ extern "C" int dh_flash_bwd_noalloc(int dtype, int BH, int S, int D, float scale
     if (BH == 0 || S == 0) return DH_OK;
     float* Dv = nullptr;
     DH_TRY(scratch_address(&Dv));
-    // Every Dvec / LSE*log2(e) entry the later launches read is written by the Dvec launch of
-    // this call first, so nothing is cleared.
+    // Every Dvec / LSE*log2(e) entry the later launches read is written earlier in this call
+    // (by the Dvec launch, or for bf16 by the dQ launch), so nothing is cleared.
     return run_bwd(dtype, BH, S, D, scale, causal, Q, K, V, O, dO, LSE, dQ, dK, dV, accumulate,
                    Dv);
 }
