@@ -262,6 +262,12 @@ WORKLOADS = {
     "flash_bwd_c4": (flash_workload, dict(dtype="bf16", BH=128, S=4096, D=128, causal=True,
                                           backward=True), "bf16",
                      "causal FlashAttention bwd B8 H16 S4096 D128 bf16 (config 4)"),
+    "flash_fwd_c4_fp32": (flash_workload, dict(dtype="fp32", BH=128, S=4096, D=128, causal=True),
+                          "fp32", "causal FlashAttention fwd B8 H16 S4096 D128 fp32 (the default "
+                                  "precision's kernels at config 4's shape)"),
+    "flash_bwd_c4_fp32": (flash_workload, dict(dtype="fp32", BH=128, S=4096, D=128, causal=True,
+                                               backward=True), "fp32",
+                          "causal FlashAttention bwd B8 H16 S4096 D128 fp32"),
     "flash_fwd_c3": (flash_workload, dict(dtype="fp32", BH=24, S=256, D=64, causal=True),
                      "fp32", "causal FlashAttention fwd B4 H6 S256 D64 fp32 (config 3)"),
     "gemm_f64_511": (gemm_f64_workload, dict(M=511, N=511, K=511), "fp64",
