@@ -345,9 +345,10 @@ struct FastOperand {
 // [256 rows][64 k] = 32 KB; 16-byte chunk c of row r at position c ^ ((r >> 1) & 7): the 16
 // rows of one b128 pass fall on 8 even and 8 odd rows, so the 16-byte units they read are
 // all different (conflict free).  DMA block b = rows 8b .. 8b+7, 8 lanes x 16 B per row;
-// 4 waves x 8 blocks per double stage.
+// 32 blocks per double stage, 32 / WAVES per wave.
+template <int WAVES>
 struct DeepKOperand {
-    static constexpr int PER = 8;
+    static constexpr int PER = 32 / WAVES;
     static constexpr int PARTS = 1;
     static constexpr int ELEMS = 256 * 64;   // elements of one double stage
     uint32_t off[PER];                        // byte offsets from the operand base, pair 0
@@ -488,13 +489,13 @@ __device__ inline void wait_dma_stages(int n) {
     }
 }
 
-// WAVES = 4 (default): 2 x 2 waves of 128 x 128 (one wave per SIMD, 256 accumulators in
-// AGPRs), reads and DMA issues interleaved op by op.  Under the chip's power cap it runs
-// 2-3% faster than
-// WAVES = 8: 2 x 4 waves of 128 x 64 (two waves per SIMD, 128 accumulators each, so one
-// wave's MFMAs cover the other's barrier and LDS-read gaps), which reads 1.5x the LDS
-// fragment bytes per matrix-core op.
-template <bool TA, bool TB, int WAVES>
+// WAVES = 4 (TN, TT): 2 x 2 waves of 128 x 128 (one wave per SIMD, 256 accumulators in
+// AGPRs), reads and DMA issues interleaved op by op.
+// WAVES = 8 (NN, NT): 2 x 4 waves of 128 x 64 (two waves per SIMD, 128 accumulators each, so
+// one wave's MFMAs cover the other's barrier and LDS-read gaps), which reads 1.5x the LDS
+// fragment bytes per matrix-core op.  DEEP8: a k-contiguous A in 64-k double stages on 8
+// waves (the launch's default for NN and NT; off only through the tuning knob).
+template <bool TA, bool TB, int WAVES, bool DEEP8>
 __global__ void __launch_bounds__(64 * WAVES)
 gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
                       const uint16_t* __restrict__ B, int ldb, float beta, float* __restrict__ C,
@@ -508,11 +509,12 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     constexpr int WN_CNT = WAVES / 2;                 // waves along N
     constexpr int FM = 4, FN = 4 / (WAVES / 4);       // 128 x (128 or 64) per wave
     // Ring of FAST_NSTAGE stages, each an A tile then a B tile.  Stage kt + 3 is fetched
-    // while stage kt is consumed, so every DMA has three stages of MFMA work to land.  The
-    // one-wave-per-SIMD form with a k-contiguous A (NN, NT) instead holds A in 3 double stages
-    // of 64 k and B in 4 stages of 32 k: 96 + 64 = 160 KB.
-    constexpr bool DEEP_A = WAVES == 4 && !TA;
-    constexpr int RING = DEEP_A ? 3 * DeepKOperand::ELEMS + FAST_NSTAGE * FAST_TILE
+    // while stage kt is consumed, so every DMA has three stages of MFMA work to land.  With a
+    // k-contiguous A (NN, NT; on 4 waves, or on 8 with DEEP8) A is instead held in 3 double
+    // stages of 64 k and B in 4 stages of 32 k: 96 + 64 = 160 KB.
+    constexpr bool DEEP_A = !TA && (WAVES == 4 || DEEP8);
+    using DK = DeepKOperand<WAVES>;
+    constexpr int RING = DEEP_A ? 3 * DK::ELEMS + FAST_NSTAGE * FAST_TILE
                                 : FAST_NSTAGE * 2 * FAST_TILE;
     __shared__ __attribute__((aligned(16))) uint16_t ring[RING];
 
@@ -549,17 +551,17 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
         // into a slot nobody reads any more), so the counts are constant: at the barrier of
         // stage kt, stage kt+1 must have landed while the 24 (kt even) or 16 (kt odd) younger
         // loads may still be in flight.
-        DeepKOperand da;
+        DK da;
         da.init(lda, M, m0, wave, lane);
         const u32x4 rsa = make_rsrc(A, da.bytes), rsb = make_rsrc(B, ob.bytes);
         uint16_t* const ring_a = ring;
-        uint16_t* const ring_b = ring + 3 * DeepKOperand::ELEMS;
+        uint16_t* const ring_b = ring + 3 * DK::ELEMS;
         const int npair = (nk + 1) / 2;
-        auto a_slot = [&](int p) { return ring_a + (p % 3) * DeepKOperand::ELEMS; };
+        auto a_slot = [&](int p) { return ring_a + (p % 3) * DK::ELEMS; };
         auto b_slot = [&](int st) { return ring_b + (st % FAST_NSTAGE) * FAST_TILE; };
         auto a_dma = [&](int p, uint32_t& base, uint32_t& soff) {
-            base = __builtin_amdgcn_readfirstlane(lds_addr(a_slot(p)) + 1024u * DeepKOperand::PER * wave);
-            soff = __builtin_amdgcn_readfirstlane((uint32_t)min(p, npair - 1) * DeepKOperand::STEP);
+            base = __builtin_amdgcn_readfirstlane(lds_addr(a_slot(p)) + 1024u * DK::PER * wave);
+            soff = __builtin_amdgcn_readfirstlane((uint32_t)min(p, npair - 1) * DK::STEP);
         };
         auto b_dma = [&](int st, uint32_t& base, uint32_t& soff) {
             base = __builtin_amdgcn_readfirstlane(lds_addr(b_slot(st)) + 1024u * OB::PER * wave);
@@ -569,7 +571,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
             uint32_t base, soff;
             a_dma(p, base, soff);
 #pragma unroll
-            for (int t = 0; t < DeepKOperand::PER; ++t) da.issue_one(rsa, soff, base, t);
+            for (int t = 0; t < DK::PER; ++t) da.issue_one(rsa, soff, base, t);
         };
         auto issue_b = [&](int st) {
             uint32_t base, soff;
@@ -577,18 +579,21 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 #pragma unroll
             for (int t = 0; t < OB::PER; ++t) ob.issue_one(rsb, soff, base, t);
         };
-        static_assert(OB::PER == 4 && DeepKOperand::PER == 8, "vmcnt constants below");
+        // vmcnt constants below: 4 waves issue 8 A blocks per pair and 4 B blocks per stage,
+        // 8 waves half as many
+        static_assert(OB::PER == 16 / WAVES && DK::PER == 32 / WAVES, "vmcnt constants below");
         issue_a(0);
         issue_b(0);
         issue_b(1);
         issue_a(1);
         issue_b(2);
-        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        if constexpr (WAVES == 4) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
         __syncthreads();
         asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(epi));
         s16x4 f0a[FM][2], f0b[FN][2], f1a[FM][2], f1b[FN][2];
 #pragma unroll
-        for (int x = 0; x < FM; ++x) DeepKOperand::part(a_slot(0), wm + 32 * x, 0, lane, 0, f0a[x]);
+        for (int x = 0; x < FM; ++x) DK::part(a_slot(0), wm + 32 * x, 0, lane, 0, f0a[x]);
 #pragma unroll
         for (int x = 0; x < FN; ++x)
 #pragma unroll
@@ -600,13 +605,18 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
             uint32_t ba = 0, sa = 0, bb, sb;
             if (EVEN) a_dma(kt / 2 + 2, ba, sa);
             b_dma(kt + 3, bb, sb);
-            step_deep<DeepKOperand, OB, FM, FN, EVEN ? DeepKOperand::PER : 0, OB::PER>(
+            step_deep<DK, OB, FM, FN, EVEN ? DK::PER : 0, OB::PER>(
                 f0a, f0b, acc, a_slot(kt / 2), 2 * (kt & 1) + 1, b_slot(kt), 1, wm, wn, lane, f1a,
                 f1b, da, ob, rsa, rsb, sa, sb, ba, bb);
-            if (EVEN) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(24)" ::: "memory");
-            else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(16)" ::: "memory");
+            if constexpr (WAVES == 4) {
+                if (EVEN) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(24)" ::: "memory");
+                else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(16)" ::: "memory");
+            } else {
+                if (EVEN) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(12)" ::: "memory");
+                else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(8)" ::: "memory");
+            }
             __syncthreads();
-            step_deep<DeepKOperand, OB, FM, FN, 0, 0>(
+            step_deep<DK, OB, FM, FN, 0, 0>(
                 f1a, f1b, acc, a_slot((kt + 1) / 2), 2 * ((kt + 1) & 1), b_slot(kt + 1), 0, wm, wn,
                 lane, f0a, f0b, da, ob, rsa, rsb, 0u, 0u, 0u, 0u);
         };
@@ -622,7 +632,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
             ++kt;
         }
         // last stage kt = nk - 1: k-step 1 from its slots, then its MFMAs
-        step_deep<DeepKOperand, OB, FM, FN, 0, 0>(f0a, f0b, acc, a_slot(kt / 2), 2 * (kt & 1) + 1,
+        step_deep<DK, OB, FM, FN, 0, 0>(f0a, f0b, acc, a_slot(kt / 2), 2 * (kt & 1) + 1,
                                                   b_slot(kt), 1, wm, wn, lane, f1a, f1b, da, ob,
                                                   rsa, rsb, 0u, 0u, 0u, 0u);
 #pragma unroll
@@ -789,16 +799,24 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
 template <bool TA, bool TB>
 int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
                 float beta, float* C, int ldc, const Batch& bt) {
-    // Default: 8 waves (two per SIMD) for NN, 4 (one per SIMD) for the other layouts -- with
-    // the non-temporal epilogue, NN at 8192^3 ran 1301-1305 TFLOP/s on 8 waves against
-    // 1283-1289 on 4 on one box and equal on another (same-box A/Bs), while NT / TN / TT stay
-    // faster on 4.
+    // Default: 8 waves (two per SIMD) with A in 64-k double stages for a k-contiguous A (NN,
+    // NT), 4 waves (one per SIMD) for TN and TT.  Same-box A/B at 8192^3 (ms): NN 0.803 (8
+    // waves, 64-k A) / 0.860 (8 waves, 32-k A) / 0.85-0.87 (4 waves, 64-k A); NT 0.795 / 0.857
+    // / 0.836; TN 0.865 on 8 waves against 0.838 on 4, TT 0.865 against 0.860.  The 32-k
+    // stages fetch half an L2 line per row of a k-contiguous operand (the next stage fetches
+    // the other half again): 40% more L2 requests than the vendor library for the same bytes.
     static const int env_waves = [] {
         const char* e = std::getenv("DH_GEMM_BF16_WAVES");   // tuning knob: 4 or 8
         return e ? (std::atoi(e) == 8 ? 8 : 4) : 0;
     }();
-    const int waves = env_waves ? env_waves : (!TA && !TB ? 8 : 4);
-    auto kern = waves == 4 ? gemm_bf16_fast_kernel<TA, TB, 4> : gemm_bf16_fast_kernel<TA, TB, 8>;
+    const int waves = env_waves ? env_waves : (!TA ? 8 : 4);
+    static const bool deep8 = [] {
+        const char* e = std::getenv("DH_GEMM_BF16_DEEP8");   // tuning knob: 0 or 1
+        return !e || std::atoi(e) != 0;
+    }();
+    auto kern = waves == 4 ? gemm_bf16_fast_kernel<TA, TB, 4, false>
+              : deep8      ? gemm_bf16_fast_kernel<TA, TB, 8, true>
+                           : gemm_bf16_fast_kernel<TA, TB, 8, false>;
     for (int b0 = 0; b0 < bt.count; b0 += 65535) {   // gridDim.y = batch member
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
         kern<<<dim3((M / 256) * (N / 256), nb), 64 * waves, 0, stream()>>>(
