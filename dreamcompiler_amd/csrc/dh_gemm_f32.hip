@@ -59,8 +59,8 @@ __device__ inline f32x4 load4(const float* __restrict__ p, int ld, int rows, int
 // TILE = tile extent along the non-k dimension (64, 128 or 256).  The k-major LDS rows are
 // padded by 4 floats, which puts the 4 k-rows a transposing store of a 16-wide slice touches
 // 16 banks apart (conflict-free); an MFMA operand read (k-rows k and k + 1 in the two lane
-// halves) overlaps on 28 banks.  An XOR swizzle that removes that (store_swz) measured +1%
-// at 4096^3 but -3% for 64 x 512^3 batched products here: it breaks the paired ds_read2 /
+// halves) overlaps on 28 banks.  An XOR swizzle like store_swz's for these tiles measured +1%
+// at 4096^3 but -3% for 64 x 512^3 batched products: it breaks the paired ds_read2 /
 // ds_write2 forms the padded layout gets.
 template <bool KCONTIG, bool VEC, int TILE, int BKT = BK, int NT = NTHREADS>
 struct Slice {
