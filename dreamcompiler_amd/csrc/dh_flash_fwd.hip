@@ -399,6 +399,9 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
         mx = step(st, sa, sb, mx);
         if (st + 1 < nst) mx = step(st + 1, sb, sa, mx);
     }
+    // The last steps' look-ahead blocks (re-reads past the last stage) land before the
+    // work-group can end and its LDS go to another one; issued a stage ago, they have.
+    wait_vmcnt<0>();
 
     // Epilogue: lane (i, h) holds O^T[d][i] for d = 32 dt + 8 q + 4 h + (0..3).
     const int i = r0 + l32;
