@@ -379,12 +379,15 @@ def test_fp32_narrow_tiles(Bt, M, N, K, ta, tb, row_bias):
 
 
 @pytest.mark.parametrize("Bt,M,N,K", [(1, 1024, 1024, 1024), (1, 1000, 777, 100), (2, 520, 700, 33),
-                                      (1, 4096, 257, 784), (1, 700, 900, 7)])
+                                      (1, 4096, 257, 784), (1, 700, 900, 7), (1, 784, 257, 4096),
+                                      (1, 300, 200, 2048)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_fp32_64x64_tiles(Bt, M, N, K, ta, tb):
     # Products whose 128 x 128 grid is under one tile per CU run on 64 x 64 tiles (one 32 x 32
     # MFMA block per wave): config 1, ragged edges, batched, config 2's first layer, a single
-    # k-slice (K = 7); beta and a per-column bias with ReLU through the epilogue.
+    # k-slice (K = 7), and split-K grids whose 128-wide tiles would be mostly padding (config
+    # 2's dW1, 784 x 257 with K = 4096; 300 x 200); beta and a per-column bias with ReLU
+    # through the epilogue (the split-K reduce applies it).
     got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.5, relu=True, seed=M + N + K + ta + 2 * tb)
     assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
 
