@@ -539,25 +539,31 @@ flash_fwd_f32_kernel(int BH, int S, float scale_log2, const float* __restrict__ 
                 sacc[kb][r] = s;
                 mx = fmaxf(mx, s);
             }
-        mx = fmaxf(mx, xor32(mx));
-        const float m_new = fmaxf(m, mx);
-        const float corr = fast_exp2(m - m_new);
-        m = m_new;
+        // Lazy rescaling, as in the bf16 kernel: the running max m moves (and O, l are
+        // rescaled) only when some row of the wave sees a block max above m + RESCALE_TH;
+        // p = exp2(s - m) <= 2^RESCALE_TH otherwise.  The first stage always moves it.
+        if (__any(mx > m + RESCALE_TH)) {                // wave-uniform
+            mx = fmaxf(mx, xor32(mx));
+            const float m_new = fmaxf(m, mx);
+            const float corr = fast_exp2(m - m_new);
+            m = m_new;
+            l *= corr;
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+        }
         float sum = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(sacc[kb][r] - m_new);
+                const float p = fast_exp2(sacc[kb][r] - m);
                 sacc[kb][r] = p;
                 sum += p;
             }
         sum += xor32(sum);
-        l = l * corr + sum;
-#pragma unroll
-        for (int d = 0; d < ND; ++d)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+        l += sum;
         // O^T[d][i] += sum_j V[j][d] P[i][j]; MFMA r pairs key 8(r/4) + 4h + r%4 per half.
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
