@@ -16,8 +16,9 @@
 //   4-deep LDS ring filled by direct-to-LDS DMA (no staging registers); both stay
 //   row-major, V being read with the transposing ds_read_b64_tr_b16.  Q fragments live in
 //   registers for the whole kernel.
-// fp32 kernel (v_mfma_f32_32x32x2_f32): same structure with 32 rows per wave and K, V
-//   both [key][d] in LDS.
+// fp32 kernel (v_mfma_f32_32x32x2_f32): 32 rows per wave, K and V both [key][d] in a
+//   two-stage LDS ring filled through registers; 8 waves (two per SIMD, 256 rows) when that
+//   grid fills the chip, else 4 (128 rows).
 // Causal work-groups are launched heaviest-first (longest key range) and all
 //   q-tiles of one slice land on the same XCD, which shares that slice's K/V in L2.
 #include <cmath>
@@ -424,18 +425,18 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
 // ---------------------------------------------------------------------------------
 // fp32
 // ---------------------------------------------------------------------------------
-template <int D>
+template <int D, int THREADS = NT>
 struct F32Stage {
     static constexpr int LS = D + 4;                  // row stride (floats)
     static constexpr int ELEMS = BN * LS;
-    static constexpr int CH = BN * D / 4 / NT;        // float4 chunks per thread per tensor
+    static constexpr int CH = BN * D / 4 / THREADS;   // float4 chunks per thread per tensor
     f32x4 k[CH], v[CH];
 
     __device__ void fetch(const float* __restrict__ Kg, const float* __restrict__ Vg, int j0,
                           int S, int tid) {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            const int f = tid + c * NT;
+            const int f = tid + c * THREADS;
             const int key = f / (D / 4), dq = f % (D / 4);
             const int j = j0 + key;
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -446,7 +447,7 @@ struct F32Stage {
     __device__ void store(float* ks, float* vs, int tid) const {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            const int f = tid + c * NT;
+            const int f = tid + c * THREADS;
             const int key = f / (D / 4), dq = f % (D / 4);
             *reinterpret_cast<f32x4*>(&ks[key * LS + 4 * dq]) = k[c];
             *reinterpret_cast<f32x4*>(&vs[key * LS + 4 * dq]) = v[c];
@@ -454,13 +455,17 @@ struct F32Stage {
     }
 };
 
-template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(NT)
+// WAVES = 8: two waves per SIMD on one 256-row tile (the other wave fills each one's
+// softmax and barrier gaps; each K/V stage feeds twice the rows; 250 VGPRs at D = 128).
+// WAVES = 4: one wave per SIMD on 128 rows, for grids the 256-row tiles would leave short of
+// one round of the CUs.
+template <int D, bool CAUSAL, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WAVES / 4, WAVES / 4)))
 flash_fwd_f32_kernel(int BH, int S, float scale_log2, const float* __restrict__ Q,
                      const float* __restrict__ K, const float* __restrict__ V,
                      float* __restrict__ O, float* __restrict__ LSE) {
-    using St = F32Stage<D>;
-    constexpr int ROWS_WG = 128, ND = D / 32, NDQ = D / 4;
+    using St = F32Stage<D, 64 * WAVES>;
+    constexpr int ROWS_WG = 32 * WAVES, ND = D / 32, NDQ = D / 4;
     extern __shared__ __attribute__((aligned(16))) float fsm[];
     float* const kbuf = fsm;
     float* const vbuf = fsm + 2 * St::ELEMS;
@@ -809,8 +814,19 @@ int launch_f32(int BH, int S, float sl2, const void* Q, const void* K, const voi
                                                           (float*)O, LSE);
         return check_launch("dh_flash_fwd(f32 split)");
     }
-    auto kern = flash_fwd_f32_kernel<D, CAUSAL>;
+    // 256-row tiles on 8 waves when they fill at least one round of the CUs (config 4's
+    // shape: 5.48 -> 4.53 ms, same box), else 128-row tiles on 4 waves.
     const size_t lds = 4 * F32Stage<D>::ELEMS * sizeof(float);
+    const int grid8 = BH * ((S + 255) / 256);
+    if (grid8 >= num_cus()) {
+        auto kern = flash_fwd_f32_kernel<D, CAUSAL, 8>;
+        static bool done8 = false;
+        DH_TRY(set_lds(kern, lds, done8));
+        kern<<<grid8, 512, lds, stream()>>>(BH, S, sl2, (const float*)Q, (const float*)K,
+                                            (const float*)V, (float*)O, LSE);
+        return check_launch("dh_flash_fwd(f32, 8 waves)");
+    }
+    auto kern = flash_fwd_f32_kernel<D, CAUSAL, 4>;
     static bool done = false;
     DH_TRY(set_lds(kern, lds, done));
     kern<<<grid, NT, lds, stream()>>>(BH, S, sl2, (const float*)Q, (const float*)K,

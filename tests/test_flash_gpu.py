@@ -56,12 +56,14 @@ def test_fp32_fwd_shapes(S, D, causal):
         assert np.allclose(got.reshape(BH, S, D)[:, 0], V.reshape(BH, S, D)[:, 0], atol=1e-6)
 
 
+@pytest.mark.parametrize("BH,S", [(130, 257), (64, 520)])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
-def test_fp32_fwd_wide_grid(D, causal):
-    # 130 slices x 257 rows fill the chip with 128-row work-groups (the small-grid split
-    # kernel covers the 3-slice shapes above); ragged last block, fp64 oracle.
-    BH, S = 130, 257
+def test_fp32_fwd_wide_grid(BH, S, D, causal):
+    # Grids that fill the chip (the small-grid split kernel covers the 3-slice shapes above):
+    # 130 slices x 257 rows take 256-row work-groups on 8 waves (a one-row last tile), 64 x 520
+    # 128-row work-groups on 4 waves (its 256-row grid, 192, is short of one round of the
+    # CUs); ragged last blocks, fp64 oracle.
     Q, K, V = inputs(BH, S, D, 1000 + D + causal, n=3)
     got, lse = flash_fwd(Q, K, V, BH, S, D, causal)
     Q64, K64, V64 = (x.astype(np.float64) for x in (Q, K, V))
