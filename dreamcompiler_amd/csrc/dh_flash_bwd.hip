@@ -676,16 +676,16 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
 // D + 4): the per-key / per-query operands of the 32x32x2 MFMA are single floats, so
 // a row-major tile read at column 32*db + l32 already yields the "transposed" operand.
 // ---------------------------------------------------------------------------------
-template <int D>
+template <int D, int THREADS = NT>
 struct Tile32 {
     static constexpr int LS = D + 4;
     static constexpr int ELEMS = RB * LS;
     static constexpr int CH = RB * D / 4;           // float4 chunks per tile
-    f32x4 v[(CH + NT - 1) / NT];
+    f32x4 v[(CH + THREADS - 1) / THREADS];
     __device__ void fetch(const float* __restrict__ g, int r0, int S, int tid) {
 #pragma unroll
-        for (int c = 0; c < (CH + NT - 1) / NT; ++c) {
-            const int f = tid + c * NT;
+        for (int c = 0; c < (CH + THREADS - 1) / THREADS; ++c) {
+            const int f = tid + c * THREADS;
             const int row = f / (D / 4), dq = f % (D / 4);
             v[c] = (f < CH && r0 + row < S)
                        ? *reinterpret_cast<const f32x4*>(g + (size_t)(r0 + row) * D + 4 * dq)
@@ -694,8 +694,8 @@ struct Tile32 {
     }
     __device__ void store(float* lds, int tid) const {
 #pragma unroll
-        for (int c = 0; c < (CH + NT - 1) / NT; ++c) {
-            const int f = tid + c * NT;
+        for (int c = 0; c < (CH + THREADS - 1) / THREADS; ++c) {
+            const int f = tid + c * THREADS;
             if (f < CH) *reinterpret_cast<f32x4*>(&lds[(f / (D / 4)) * LS + 4 * (f % (D / 4))]) = v[c];
         }
     }
@@ -825,21 +825,21 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
         }
 }
 
-template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(NT)
+template <int D, bool CAUSAL, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WAVES / 4, WAVES / 4)))
 bwd_dq_f32_kernel(int BH, int S, float scale, float sl2, const float* __restrict__ Q,
                   const float* __restrict__ K, const float* __restrict__ V,
                   const float* __restrict__ dO, const float* __restrict__ LSE,
                   const float* __restrict__ Dv, float* __restrict__ dQ, int accumulate) {
-    using Tl = Tile32<D>;
-    constexpr int ND = D / 32, NDQ = D / 4;
+    using Tl = Tile32<D, 64 * WAVES>;
+    constexpr int ND = D / 32, NDQ = D / 4, ROWS = 32 * WAVES;
     extern __shared__ __attribute__((aligned(16))) float fsm[];
 
-    const int n_qt = (S + 127) / 128;
+    const int n_qt = (S + ROWS - 1) / ROWS;
     const int bh = blockIdx.x % BH;
     const int rr = blockIdx.x / BH;
     const int qt = CAUSAL ? n_qt - 1 - rr : rr;
-    const int qbase = qt * 128;
+    const int qbase = qt * ROWS;
     const size_t base = (size_t)bh * S * D;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
@@ -863,7 +863,7 @@ bwd_dq_f32_kernel(int BH, int S, float scale, float sl2, const float* __restrict
 #pragma unroll
         for (int r = 0; r < 16; ++r) dqacc[d][r] = 0.f;
 
-    const int kend = CAUSAL ? min(S, qbase + 128) : S;
+    const int kend = CAUSAL ? min(S, qbase + ROWS) : S;
     const int nst = (kend + RB - 1) / RB;
     Tl tk, tv;
     auto fetch = [&](int st) {
@@ -1009,8 +1009,21 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
                                                 (const float*)dO, LSE, Dv, dK, dV, acc, kv_alias);
         DH_TRY(check_launch("dh_flash_bwd(dK,dV f32)"));
     }
+    // dQ: 8 waves (two per SIMD) on 256-query tiles when that grid fills at least one round
+    // of the CUs, else 4 waves on 128 (the same rule as the fp32 forward).
+    const int tiles8 = (S + 255) / 256;
+    if (BH * tiles8 >= num_cus()) {
+        auto kern = bwd_dq_f32_kernel<D, CAUSAL, 8>;
+        static bool done8 = false;
+        DH_TRY(set_lds(kern, lds, done8));
+        kern<<<BH * tiles8, 512, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,
+                                                  (const float*)K, (const float*)V,
+                                                  (const float*)dO, LSE, Dv, dQ, acc_q);
+        DH_TRY(check_launch("dh_flash_bwd(dQ f32, 8 waves)"));
+        return DH_OK;
+    }
     {
-        auto kern = bwd_dq_f32_kernel<D, CAUSAL>;
+        auto kern = bwd_dq_f32_kernel<D, CAUSAL, 4>;
         static bool done = false;
         DH_TRY(set_lds(kern, lds, done));
         kern<<<BH * tiles, NT, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,

@@ -72,6 +72,24 @@ def test_fp32_fwd_wide_grid(BH, S, D, causal):
     assert np.abs(lse - ref_lse(Q, K, BH, S, D, causal)).max() <= tol
 
 
+@pytest.mark.parametrize("BH,S", [(130, 257), (64, 520)])
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fp32_bwd_wide_grid(BH, S, D, causal):
+    # Grids that fill the chip: 130 x 257 takes the dQ launch on 256-query tiles (8 waves, a
+    # one-row last tile), 64 x 520 on 128-query tiles (4 waves); every slice against the
+    # fp64 standard-attention backward.
+    Q, K, V, G = inputs(BH, S, D, 2000 + D + causal)
+    Of, lse = flash_fwd(Q, K, V, BH, S, D, causal)
+    grads = flash_bwd(Q, K, V, Of, G, lse, BH, S, D, causal)
+    refs = _bwd_ref(Q, K, V, G, BH, S, D, causal)
+    tol = 1e-5 * np.sqrt(S)
+    for name, g, r in zip("QKV", grads, refs):
+        g3, r3 = g.reshape(BH, S, D), r.reshape(BH, S, D)
+        for b in range(BH):
+            assert maxrel(g3[b], r3[b]) <= tol, (name, b)
+
+
 @pytest.mark.parametrize("S", [1, 64, 100, 257, 520])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
