@@ -57,10 +57,11 @@ def _run(cmd, verbose):
 # Per-source additions.  dh_flash_fwd: the softmax takes row maxima of matrix-core
 # results; with NaNs honoured, IEEE-mode max first quiets each operand (one extra VALU
 # op per score).  The reference runtime itself is built with -ffast-math.
-# dh_flash_bwd, dh_f64: matrix-core results in arch VGPRs.  The kernels fit there, and the
-# accumulator-register form made the allocator shuttle the accumulators between register
-# files every stage (dK/dV; the fp64 GEMM's chain and block-sum registers).
-SRC_FLAGS = {"dh_flash_fwd.hip": ["-fno-honor-nans"],
+# dh_flash_fwd, dh_flash_bwd, dh_f64: matrix-core results in arch VGPRs.  The kernels fit
+# there, and the accumulator-register form made the allocator shuttle the accumulators
+# between register files every stage (dK/dV; the fp64 GEMM's chain and block-sum registers;
+# the fp32 forward's one-wave forms, config 3 15.0 -> 14.8 us).
+SRC_FLAGS = {"dh_flash_fwd.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=true"],
              "dh_flash_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
              "dh_f64.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
 
