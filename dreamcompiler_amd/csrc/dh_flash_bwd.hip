@@ -672,9 +672,10 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
 }
 
 // ---------------------------------------------------------------------------------
-// fp32 variants (v_mfma_f32_32x32x2_f32).  All LDS tiles row-major [row][d] (stride
-// D + 4): the per-key / per-query operands of the 32x32x2 MFMA are single floats, so
-// a row-major tile read at column 32*db + l32 already yields the "transposed" operand.
+// fp32 variants (v_mfma_f32_16x16x4_f32 for dK/dV, v_mfma_f32_32x32x2_f32 for dQ).  All
+// LDS tiles row-major [row][d] (stride D + 4): the per-key / per-query operands of the fp32
+// MFMAs are single floats, so a row-major tile read at a column already yields the
+// "transposed" operand.
 // ---------------------------------------------------------------------------------
 template <int D, int THREADS = NT>
 struct Tile32 {
@@ -701,15 +702,25 @@ struct Tile32 {
     }
 };
 
+// fp32 dK/dV.  Work-group: 128 keys, 8 waves of 16 keys, each wave's K and V rows in
+// registers (D / 2 floats per lane each) and its dK/dV accumulators too (D / 2 each); Q, dO
+// and each stage's LSE*log2(e) and Dvec stream through a register-staged LDS double buffer
+// of 32-query stages, one barrier per stage.  16 keys per wave (v_mfma_f32_16x16x4_f32 rather
+// than 32 on 32x32x2) halve the per-wave registers, so two waves share each SIMD at
+// D = 128 (234 VGPRs) and four at D <= 64 (two work-groups per CU).  MFMA layouts (lane l: l16 = l % 16, g = l / 16): operands A[m = l16][k = g] and
+// B[k = g][n = l16]; result register i of lane l is row 4 g + i, column l16.  S = Q K^T and
+// dP = dO V^T per 16-query block qb come out with lane = key j and register i = query
+// 16 qb + 4 g + i, and P, dS feed dV^T += dO^T P, dK^T += Q^T dS straight from those
+// registers: k-step (qb, i) pairs lane group g with query 16 qb + 4 g + i.
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(NT)
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 4, D == 128 ? 2 : 4)))
 bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restrict__ Q,
-                    const float* __restrict__ K, const float* __restrict__ V,
-                    const float* __restrict__ dO, const float* __restrict__ LSE,
-                    const float* __restrict__ Dv, float* __restrict__ dK,
-                    float* __restrict__ dV, int accumulate, int kv_alias) {
-    using Tl = Tile32<D>;
-    constexpr int ND = D / 32, NDQ = D / 4;
+                       const float* __restrict__ K, const float* __restrict__ V,
+                       const float* __restrict__ dO, const float* __restrict__ LSE,
+                       const float* __restrict__ Dv, float* __restrict__ dK,
+                       float* __restrict__ dV, int accumulate, int kv_alias) {
+    using Tl = Tile32<D, 512>;
+    constexpr int NB = D / 16, NDQ = D / 4, QB = RB / 16;
     extern __shared__ __attribute__((aligned(16))) float fsm[];
     __shared__ __attribute__((aligned(16))) float s_lse[2][RB], s_dv[2][RB];
 
@@ -718,24 +729,21 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
     const int kbase = kt * 128;
     const size_t base = (size_t)bh * S * D;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l32 = lane & 31, h = lane >> 5;
-    const int k0 = kbase + 32 * wave;
-    const int j = k0 + l32;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int k0 = kbase + 16 * wave;
+    const int j = k0 + l16;
 
-    float kf[NDQ][2], vf[NDQ][2];
+    // B operand of d-step u: K[j][4u + g], V[j][4u + g]
+    float kf[NDQ], vf[NDQ];
 #pragma unroll
-    for (int u = 0; u < NDQ; ++u)
+    for (int u = 0; u < NDQ; ++u) {
+        const size_t off = base + (size_t)j * D + 4 * u + g;
+        kf[u] = j < S ? K[off] : 0.f;
+        vf[u] = j < S ? V[off] : 0.f;
+    }
+    f32x4 dkacc[NB], dvacc[NB];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const size_t off = base + (size_t)j * D + 4 * u + 2 * h + s;
-            kf[u][s] = j < S ? K[off] : 0.f;
-            vf[u][s] = j < S ? V[off] : 0.f;
-        }
-    f32x16 dkacc[ND], dvacc[ND];
-#pragma unroll
-    for (int d = 0; d < ND; ++d)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dkacc[d][r] = dvacc[d][r] = 0.f;
+    for (int b = 0; b < NB; ++b) dkacc[b] = dvacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int qstart = CAUSAL ? kbase : 0;
     const int nst = qstart < S ? (S - qstart + RB - 1) / RB : 0;
@@ -773,38 +781,42 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
         if (!(CAUSAL && i0 + RB - 1 < k0)) {
             const float* qs = fsm + cur * 2 * Tl::ELEMS;
             const float* gs = qs + Tl::ELEMS;
-            f32x16 s, dp;
+            f32x4 s[QB], dp[QB];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+            for (int qb = 0; qb < QB; ++qb) s[qb] = dp[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < NDQ; ++u)
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int c = 4 * u + 2 * h + e;
-                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(qs[l32 * Tl::LS + c], kf[u][e], s, 0, 0, 0);
-                    dp = __builtin_amdgcn_mfma_f32_32x32x2f32(gs[l32 * Tl::LS + c], vf[u][e], dp, 0, 0, 0);
+                for (int qb = 0; qb < QB; ++qb) {
+                    const int a = (16 * qb + l16) * Tl::LS + 4 * u + g;
+                    s[qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(qs[a], kf[u], s[qb], 0, 0, 0);
+                    dp[qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(gs[a], vf[u], dp[qb], 0, 0, 0);
                 }
-            float p[16], ds[16];
+            float p[QB][4], ds[QB][4];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int il = 8 * (r >> 2) + 4 * h + (r & 3);
-                const int i = i0 + il;
-                const bool ok = i < S && j < S && (!CAUSAL || j <= i);
-                p[r] = ok ? fast_exp2(s[r] * sl2 - s_lse[cur][il]) : 0.f;
-                ds[r] = p[r] * (dp[r] - s_dv[cur][il]);
-            }
-            // dV^T[d][j] += sum_i dO[i][d] P[i][j]; MFMA r pairs query 8(r/4)+4h+r%4 per half
+            for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int il = 8 * (r >> 2) + 4 * h + (r & 3);
-#pragma unroll
-                for (int d = 0; d < ND; ++d) {
-                    dvacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(gs[il * Tl::LS + 32 * d + l32],
-                                                                    p[r], dvacc[d], 0, 0, 0);
-                    dkacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(qs[il * Tl::LS + 32 * d + l32],
-                                                                    ds[r], dkacc[d], 0, 0, 0);
+                for (int r = 0; r < 4; ++r) {
+                    const int il = 16 * qb + 4 * g + r;
+                    const int i = i0 + il;
+                    const bool ok = i < S && j < S && (!CAUSAL || j <= i);
+                    p[qb][r] = ok ? fast_exp2(s[qb][r] * sl2 - s_lse[cur][il]) : 0.f;
+                    ds[qb][r] = p[qb][r] * (dp[qb][r] - s_dv[cur][il]);
                 }
-            }
+            // dV^T[d][j] += sum_i dO[i][d] P[i][j], d = 16 b + (row of the result)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = (16 * qb + 4 * g + r) * Tl::LS + l16;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        dvacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(gs[row + 16 * b], p[qb][r],
+                                                                        dvacc[b], 0, 0, 0);
+                        dkacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(qs[row + 16 * b], ds[qb][r],
+                                                                        dkacc[b], 0, 0, 0);
+                    }
+                }
         }
         if (more) store(cur ^ 1);
         __syncthreads();
@@ -812,17 +824,13 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
     if (j >= S) return;
     float* dkr = dK + base + (size_t)j * D;
     float* dvr = dV + base + (size_t)j * D;
+    // lane (j, g) holds dK^T[d][j], dV^T[d][j] for d = 16 b + 4 g + (0..3)
 #pragma unroll
-    for (int d = 0; d < ND; ++d)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int col = 32 * d + 8 * q + 4 * h;
-            f32x4 a = {dkacc[d][4 * q] * scale, dkacc[d][4 * q + 1] * scale,
-                       dkacc[d][4 * q + 2] * scale, dkacc[d][4 * q + 3] * scale};
-            f32x4 b = {dvacc[d][4 * q], dvacc[d][4 * q + 1], dvacc[d][4 * q + 2],
-                       dvacc[d][4 * q + 3]};
-            store_dkdv(dkr + col, dvr + col, a, b, accumulate, accumulate, kv_alias);
-        }
+    for (int b = 0; b < NB; ++b) {
+        const int col = 16 * b + 4 * g;
+        store_dkdv(dkr + col, dvr + col, dkacc[b] * scale, dvacc[b], accumulate, accumulate,
+                   kv_alias);
+    }
 }
 
 template <int D, bool CAUSAL, int WAVES>
@@ -1004,9 +1012,9 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
         auto kern = bwd_dkdv_f32_kernel<D, CAUSAL>;
         static bool done = false;
         DH_TRY(set_lds(kern, lds, done));
-        kern<<<BH * tiles, NT, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,
-                                                (const float*)K, (const float*)V,
-                                                (const float*)dO, LSE, Dv, dK, dV, acc, kv_alias);
+        kern<<<BH * tiles, 512, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,
+                                                 (const float*)K, (const float*)V,
+                                                 (const float*)dO, LSE, Dv, dK, dV, acc, kv_alias);
         DH_TRY(check_launch("dh_flash_bwd(dK,dV f32)"));
     }
     // dQ: 8 waves (two per SIMD) on 256-query tiles when that grid fills at least one round
