@@ -9,8 +9,8 @@
 //   2. per key tile:   dV += P^T dO,  dK += scale * dS^T Q    (dS = P o (dP - Dvec))
 //   3. per query tile: dQ += scale * dS K                     (S and dP recomputed)
 // bf16, two: the per-query-tile launch runs first and forms Dvec_i (and LSE_i log2 e) from
-// the dO row it holds anyway and the O row, stores them, and the per-key-tile launch reads
-// them.
+// the dO row it holds anyway and the O row, stores -Dvec_i and LSE_i log2 e, and the
+// per-key-tile launch reads them.
 // MFMA layouts: in launch 2 the scores are formed as S = Q K^T so the lane index is the
 // key (the row of dK / dV); in launch 3 as S^T = K Q^T so the lane index is the query.
 // Either way the product that consumes P or dS takes it straight from the score
@@ -297,10 +297,11 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
     // One stage, one MFMA per chunk, chunks fenced by sched_barrier(0) and operands read
     // one chunk ahead:
     //   S = Q K^T (NTK MFMAs);
-    //   dP = dO V^T (NTK MFMAs), each chunk also exponentiating 16 / NTK scores of S, so
-    //     the exponentials run while the matrix cores work;
+    //   dP - Dvec = dO V^T - Dvec (NTK MFMAs whose chain starts from -Dvec), each chunk also
+    //     exponentiating 16 / NTK scores of S, so the exponentials run while the matrix
+    //     cores work;
     //   the mask (a branch, taken on diagonal and tail stages only);
-    //   dS = P o (dP - Dvec) and the bf16 packing of P, dS for k-step 0;
+    //   dS = P o (dP - Dvec) (one multiply) and the bf16 packing of P, dS for k-step 0;
     //   dV^T += dO^T P, dK^T += Q^T dS for k-step 0 (2 ND MFMAs), the chunks also packing
     //     k-step 1; then the same MFMAs for k-step 1.
     // k-step kk pairs queries 16 kk + 4 h + (0..3) and + 8: score registers 8 kk .. + 7.
@@ -321,12 +322,19 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
         auto trf = [&](int kk, int s) {
             return tr_operand((s & 1 ? qt : gt) + 16 * kk * T::ROWB, tofs0[s >> 1], tofs1[s >> 1]);
         };
+        // dP's chain starts from -Dvec (stored negated), so it ends as dP - Dvec.
         f32x16 sc, dp;
+        f32x4 l4[4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
-        f32x4 l4[4], d4[4];
+        for (int q = 0; q < 4; ++q) {
+            l4[q] = *reinterpret_cast<const f32x4*>(vec + 8 * q + 4 * h);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(vec + 256 + 8 * q + 4 * h);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) l4[q] = *reinterpret_cast<const f32x4*>(vec + 8 * q + 4 * h);
+            for (int e = 0; e < 4; ++e) {
+                sc[4 * q + e] = 0.f;
+                dp[4 * q + e] = d4[e];
+            }
+        }
         // operands of S/dP MFMA i (i < NTK: S, else dP), read two chunks ahead
         auto opa = [&](int i) { return rowf(i < NTK ? qt : gt, i % NTK); };
         auto opb = [&](int i) { return keyf(i % NTK, i < NTK ? 0 : 1); };
@@ -351,9 +359,6 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
             if (t + 1 == NTK) {
                 ta[0] = trf(0, 0);
                 ta[1] = trf(0, 1);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    d4[q] = *reinterpret_cast<const f32x4*>(vec + 256 + 8 * q + 4 * h);
             }
             dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, dp, 0, 0, 0);
 #pragma unroll
@@ -378,8 +383,8 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
         uint32_t pk[8], pd[8];
         auto pack = [&](int u) {
             const int r = 2 * u;
-            const float ds0 = p[r] * (dp[r] - d4[r >> 2][r & 3]);
-            const float ds1 = p[r + 1] * (dp[r + 1] - d4[r >> 2][(r + 1) & 3]);
+            const float ds0 = p[r] * dp[r];
+            const float ds1 = p[r + 1] * dp[r + 1];
             pk[u] = cvt_pk_bf16(p[r], p[r + 1]);
             pd[u] = cvt_pk_bf16(ds0, ds1);
             asm volatile("" : "+v"(pk[u]), "+v"(pd[u]));
@@ -517,7 +522,7 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
 
     // Q and dO rows of this lane's query as B operands: Q[i][16t + 8h .. +7].  The same
     // elements of O give the lane half of Dvec_i = dO_i . O_i; the two halves (lanes l and
-    // l ^ 32) are added, and Dvec_i and LSE_i log2(e) are stored for the dK/dV launch.
+    // l ^ 32) are added, and -Dvec_i and LSE_i log2(e) are stored for the dK/dV launch.
     bf16x8 qf[NTK], gf[NTK];
     float lse2, dvi;
     {
@@ -539,7 +544,7 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
         dvi = part + xor32(part);
         lse2 = LSE[(size_t)bh * S + ic] * 1.4426950408889634f;
         if (h == 0 && i < S) {
-            Dv[(size_t)bh * S + i] = dvi;
+            Dv[(size_t)bh * S + i] = -dvi;       // negated: the dK/dV launch's dP chain starts from it
             L2[(size_t)bh * S + i] = lse2;
         }
 #pragma unroll
