@@ -15,7 +15,8 @@
 //   rows per wave, 256 per work-group.  K and V stream in stages of 64 keys through a
 //   4-deep LDS ring filled by direct-to-LDS DMA (no staging registers); both stay
 //   row-major, V being read with the transposing ds_read_b64_tr_b16.  Q fragments live in
-//   registers for the whole kernel.
+//   registers for the whole kernel.  Grids of at most two rounds take 4-wave work-groups
+//   (128 rows, two per CU) with two-slot K and V rings instead.
 // fp32 kernel (v_mfma_f32_32x32x2_f32): 32 rows per wave, K and V both [key][d] in a
 //   two-stage LDS ring filled through registers; 8 waves (two per SIMD, 256 rows) when that
 //   grid fills the chip, else 4 (128 rows).
@@ -37,10 +38,7 @@ __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // ---------------------------------------------------------------------------------
 // bf16
 // ---------------------------------------------------------------------------------
-constexpr int BF_WAVES = 8;                 // two waves per SIMD
-constexpr int BF_NT = 64 * BF_WAVES;
-constexpr int BF_ROWS = 32 * BF_WAVES;      // query rows per work-group (32 per wave)
-constexpr int BF_NSTAGE = 4;                // LDS ring depth, in stages of BN keys
+constexpr int BF_NSTAGE = 4;                // 8-wave LDS ring depth, in stages of BN keys
 
 // One stage = a K tile then a V tile, each BN key rows of D bf16 kept row-major, moved
 // by direct-to-LDS DMA in 1 KB blocks (64 lanes x 16 bytes).  The 16-byte chunk c of key
@@ -49,7 +47,7 @@ constexpr int BF_NSTAGE = 4;                // LDS ring depth, in stages of BN k
 //    rows over all 64 banks;
 //  V is read with ds_read_b64_tr_b16 (4 consecutive rows x 64 bytes per pass): vswz
 //    spreads those 4 rows over all 64 banks.
-template <int D>
+template <int D, int W>
 struct BfTile {
     static constexpr int CH = D / 8;                  // 16-byte chunks per key row
     static constexpr int ROWB = 2 * D;                // bytes per key row
@@ -57,9 +55,20 @@ struct BfTile {
     static constexpr int STAGE = 2 * TILE;
     static constexpr int NBLK = TILE / 1024;          // DMA blocks per tile
     static constexpr int RPB = 1024 / ROWB;           // key rows per DMA block
-    static constexpr int PER = 2 * NBLK / BF_WAVES;   // DMA blocks per wave per stage
+    static constexpr int PER = 2 * NBLK / W;          // DMA blocks per wave per stage
     static constexpr int RW = 256 / ROWB;             // key rows per 256-byte bank sweep
-    static_assert(PER >= 1 && 2 * NBLK == PER * BF_WAVES, "stage must split over the waves");
+    static_assert(PER >= 1 && 2 * NBLK == PER * W, "stage must split over the waves");
+    // Ring layout.  8 waves: BF_NSTAGE slots of one K and one V tile, refilled 3 stages
+    // ahead.  4 waves (two work-groups per CU, 64 KB each): two K slots, then two V slots;
+    // after barrier st the waves refill K(st + 2) into K(st)'s slot (last read by step
+    // st - 1, which formed the scores of st) and V(st + 1) into V(st - 1)'s slot.
+    static constexpr int LDS = W == 8 ? BF_NSTAGE * STAGE : 4 * TILE;
+    __device__ static uint32_t kslot(int st) {
+        return W == 8 ? (st % BF_NSTAGE) * STAGE : (st & 1) * TILE;
+    }
+    __device__ static uint32_t vslot(int st) {
+        return W == 8 ? (st % BF_NSTAGE) * STAGE + TILE : (2 + (st & 1)) * TILE;
+    }
     __device__ static int kswz(int j) { return (j * CH / 16) % CH; }
     __device__ static int vswz(int j) { return 4 * ((j / RW) % (4 / RW)); }
 };
@@ -105,27 +114,27 @@ __device__ inline void bf_order(int BH, int n_qt, int& bh, int& rr) {
     bh = 8 * (g * G + w % gsz) + x;
 }
 
-// One work-group = 8 waves x 32 query rows.  Per stage of 64 keys a wave computes
+// One work-group = W waves x 32 query rows.  Per stage of 64 keys a wave computes
 // S^T = K Q^T (2 x D/16 MFMAs, K from LDS, Q from registers), the online softmax on its
 // 32 scores per lane, and O^T += V^T P^T (2 x 2 x D/32 MFMAs, V through transpose reads,
 // P straight from the score registers).  The running max m is kept on raw scores (scale
 // > 0), so p = exp2(s * sl2 - m * sl2) is one FMA and one exp; the row sum l is taken
 // over the bf16-rounded p that the PV product uses (v_dot2_f32_bf16 with (1, 1)), per
 // lane half, and combined once at the end.
-template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(BF_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int D, bool CAUSAL, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2)))
 flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
                       const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                       uint16_t* __restrict__ O, float* __restrict__ LSE) {
-    using T = BfTile<D>;
-    constexpr int NTK = D / 16, ND = D / 32;
+    using T = BfTile<D, W>;
+    constexpr int NTK = D / 16, ND = D / 32, ROWS = 32 * W;
     extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
-    const int n_qt = (S + BF_ROWS - 1) / BF_ROWS;
+    const int n_qt = (S + ROWS - 1) / ROWS;
     int bh, rr;
     bf_order<CAUSAL>(BH, n_qt, bh, rr);
     const int qt = CAUSAL ? n_qt - 1 - rr : rr;
-    const int q0 = qt * BF_ROWS;
+    const int q0 = qt * ROWS;
     const size_t base = (size_t)bh * S * D;
     const uint16_t* Qg = Q + base;
     const uint16_t* Kg = K + base;
@@ -137,9 +146,9 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     const int r0 = q0 + 32 * wave;                 // first query row of this wave
     const uint32_t ring_lds = lds_addr(ring);
 
-    const int kend = CAUSAL ? min(S, q0 + BF_ROWS) : S;
+    const int kend = CAUSAL ? min(S, q0 + ROWS) : S;
     const int nst = (kend + BN - 1) / BN;
-    // DMA work of this wave: blocks wave, wave + 8, ... of the stage (K tile first).
+    // DMA work of this wave: blocks wave, wave + W, ... of the stage (K tile first).
     // Loads go through a buffer resource per stage (base = key row j0, range = the rows
     // left in the slice), so each lane's byte offset is loop-invariant and rows at or past
     // S arrive as zeros (masked keys; zero V rows meet p = 0).
@@ -147,26 +156,30 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     bool dk[T::PER];
 #pragma unroll
     for (int q = 0; q < T::PER; ++q) {
-        const int gb = wave + BF_WAVES * q;
+        const int gb = wave + W * q;
         const int tile = gb / T::NBLK, b = gb % T::NBLK;
         const int row = b * T::RPB + lane / T::CH, pos = lane % T::CH;
         dk[q] = tile == 0;
-        dlds[q] = tile * T::TILE + b * 1024;
+        dlds[q] = b * 1024;
         dvoff[q] = row * T::ROWB + 16 * (pos ^ (tile == 0 ? T::kswz(row) : T::vswz(row)));
     }
-    // DMA block q of stage st into ring slot st % BF_NSTAGE.  A stage at or past nst is
-    // never computed: its slot is free, and the load re-reads key rows from 0 (in bounds,
+    // DMA block q (of K stage sk or V stage sv) into its ring slot.  A stage at or past nst
+    // is never computed: its slot is free, and the load re-reads key rows from 0 (in bounds,
     // cached) so that callers need no branch.
-    auto issue_one = [&](int st, int q) {
+    auto issue_one = [&](int sk, int sv, int q) {
+        const int st = dk[q] ? sk : sv;
         const int j0 = st < nst ? st * BN : 0;
-        const uint32_t sb = ring_lds + (st % BF_NSTAGE) * T::STAGE;
+        const uint32_t sb = ring_lds + (dk[q] ? T::kslot(st) : T::vslot(st));
         const u32x4 rs = make_rsrc((dk[q] ? Kg : Vg) + (size_t)j0 * D, (uint32_t)(S - j0) * T::ROWB);
         lds_dma16_buf(dvoff[q], rs, __builtin_amdgcn_readfirstlane(sb + dlds[q]));
     };
-    auto issue = [&](int st) {
+    auto issue = [&](int sk, int sv) {
 #pragma unroll
-        for (int q = 0; q < T::PER; ++q) issue_one(st, q);
+        for (int q = 0; q < T::PER; ++q) issue_one(sk, sv, q);
     };
+    // stages refilled after barrier st
+    auto ahead_k = [](int st) { return W == 8 ? st + BF_NSTAGE - 1 : st + 2; };
+    auto ahead_v = [](int st) { return W == 8 ? st + BF_NSTAGE - 1 : st + 1; };
 
     // Q fragments (B operand of S^T = K Q^T): lane (i, h) holds Q[i][16t + 8h .. +7].
     bf16x8 qf[NTK];
@@ -217,14 +230,15 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     // run unconditionally: past the last stage they read a stale, in-bounds ring slot and
     // the result is discarded.
     auto sync = [&](int st) {
-        // stages <= st + 1 must have landed; st + 2 may still be in flight
-        if (st + 2 < nst) wait_vmcnt<T::PER>();
+        // stages <= st + 1 must have landed; st + 2 may still be in flight (8 waves; with
+        // 4, everything issued a step ago is needed now)
+        if (W == 8 && st + 2 < nst) wait_vmcnt<T::PER>();
         else wait_vmcnt<0>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
     };
     auto scores = [&](int st, f32x16 (&sacc)[2]) {
-        const uint8_t* kt = ring + (st % BF_NSTAGE) * T::STAGE;
+        const uint8_t* kt = ring + T::kslot(st);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -290,8 +304,8 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
         constexpr int QB = D == 128 ? 10 : D == 64 ? 12 : 16;   // pairs exponentiated in B
         constexpr int J0 = 16 - QB;            // first C chunk free of exponentials
         constexpr int KPF = 4;                 // K fragments in flight
-        const uint8_t* kt = ring + ((st + 1) % BF_NSTAGE) * T::STAGE;
-        const uint8_t* vt = ring + (st % BF_NSTAGE) * T::STAGE + T::TILE;
+        const uint8_t* kt = ring + T::kslot(st + 1);
+        const uint8_t* vt = ring + T::vslot(st);
         auto kfrag = [&](int i) {
             return *reinterpret_cast<const bf16x8*>(kt + kofs[i >> 1] + 32 * (i & 1) * T::ROWB);
         };
@@ -329,11 +343,11 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
             else if (i + KPF - NS < 2) vread(i + KPF - NS, va[i + KPF - NS]);
 #pragma unroll
             for (int q = QB * i / NS; q < QB * (i + 1) / NS; ++q) expo(q);
-            if ((i & 1) && (i >> 1) < T::PER) issue_one(st + BF_NSTAGE - 1, i >> 1);
+            if ((i & 1) && (i >> 1) < T::PER) issue_one(ahead_k(st), ahead_v(st), i >> 1);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int q = NS / 2; q < T::PER; ++q) issue_one(st + BF_NSTAGE - 1, q);
+        for (int q = NS / 2; q < T::PER; ++q) issue_one(ahead_k(st), ahead_v(st), q);
         float tmax[8];
 #pragma unroll
         for (int j = 0; j < NP; ++j) {
@@ -374,20 +388,28 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     auto step = [&](int st, f32x16 (&cur)[2], f32x16 (&nxt)[2], float mx_cur) -> float {
         sync(st);
         if (st >= wlast) {                     // no rows left here: only the DMA share
-            issue(st + BF_NSTAGE - 1);
+            issue(ahead_k(st), ahead_v(st));
             return 0.f;
         }
         rescale(mx_cur);
         return overlap(st, cur, nxt);
     };
 
+    if constexpr (W == 8) {
 #pragma unroll
-    for (int st = 0; st < BF_NSTAGE - 1; ++st)
-        if (st < nst) issue(st);
-    // prologue: S(0) and its max
-    if (nst > 2) wait_vmcnt<2 * T::PER>();              // stage 0 landed, 1 and 2 may fly
-    else if (nst == 2) wait_vmcnt<T::PER>();
-    else wait_vmcnt<0>();
+        for (int st = 0; st < BF_NSTAGE - 1; ++st)
+            if (st < nst) issue(st, st);
+        // prologue: S(0) and its max
+        if (nst > 2) wait_vmcnt<2 * T::PER>();          // stage 0 landed, 1 and 2 may fly
+        else if (nst == 2) wait_vmcnt<T::PER>();
+        else wait_vmcnt<0>();
+    } else {
+        static_assert(W == 8 || T::NBLK % 4 == 0, "4 waves: blocks q < PER / 2 are K's");
+        issue(0, 0);                                    // K(0), V(0)
+#pragma unroll
+        for (int q = 0; q < T::PER / 2; ++q) issue_one(1, 0, q);   // K(1)
+        wait_vmcnt<0>();
+    }
     __builtin_amdgcn_s_barrier();
     f32x16 sa[2], sb[2];
     float mx = 0.f;
@@ -787,17 +809,30 @@ int set_lds(Kern kern, size_t bytes, bool& done) {
     return DH_OK;
 }
 
+template <int D, bool CAUSAL, int W>
+int launch_bf16_w(int BH, int S, float sl2, const void* Q, const void* K, const void* V, void* O,
+                  float* LSE) {
+    auto kern = flash_fwd_bf16_kernel<D, CAUSAL, W>;
+    const size_t lds = BfTile<D, W>::LDS;
+    static bool done = false;
+    DH_TRY(set_lds(kern, lds, done));
+    const int grid = BH * ((S + 32 * W - 1) / (32 * W));
+    kern<<<grid, 64 * W, lds, stream()>>>(BH, S, sl2, (const uint16_t*)Q, (const uint16_t*)K,
+                                         (const uint16_t*)V, (uint16_t*)O, LSE);
+    return check_launch("dh_flash_fwd(bf16)");
+}
+
 template <int D, bool CAUSAL>
 int launch_bf16(int BH, int S, float sl2, const void* Q, const void* K, const void* V, void* O,
                 float* LSE) {
-    auto kern = flash_fwd_bf16_kernel<D, CAUSAL>;
-    const size_t lds = (size_t)BF_NSTAGE * BfTile<D>::STAGE;
-    static bool done = false;
-    DH_TRY(set_lds(kern, lds, done));
-    const int grid = BH * ((S + BF_ROWS - 1) / BF_ROWS);
-    kern<<<grid, BF_NT, lds, stream()>>>(BH, S, sl2, (const uint16_t*)Q, (const uint16_t*)K,
-                                      (const uint16_t*)V, (uint16_t*)O, LSE);
-    return check_launch("dh_flash_fwd(bf16)");
+    // 4-wave work-groups (two per CU) when the 256-row grid fills at most two rounds of the
+    // CUs: twice the work-groups, and each CU's two run their prologues and epilogues apart.
+    // Same box: (BH, S, D) = (32, 2048, 128) causal 0.0604 -> 0.0512 ms, (16, 4096, 64)
+    // 0.0834 -> 0.0816; at config 4's 8 rounds a wash (0.5427 / 0.5410 causal, 0.9637 /
+    // 0.9694 non-causal), the doubled K/V staging per row taking back what the overlap gives.
+    if (BH * ((S + 255) / 256) <= 2 * num_cus())
+        return launch_bf16_w<D, CAUSAL, 4>(BH, S, sl2, Q, K, V, O, LSE);
+    return launch_bf16_w<D, CAUSAL, 8>(BH, S, sl2, Q, K, V, O, LSE);
 }
 
 template <int D, bool CAUSAL>

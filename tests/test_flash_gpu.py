@@ -110,6 +110,23 @@ def test_bf16_fwd_shapes(S, D, causal):
     assert np.abs(lse - O.flash_lse(Q64, K64, BH, S, D, causal)).max() <= 1e-3 * np.sqrt(D)
 
 
+@pytest.mark.parametrize("BH,S", [(520, 257), (516, 130)])
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_bf16_fwd_wide_grid(BH, S, D, causal):
+    # Grids past two rounds of the CUs take the 8-wave forward (the small shapes above, the
+    # 4-wave one): 520 slices x 257 rows in the XCD-grouped slice order with a one-row last
+    # tile, 516 x 130 in rank-major order; every slice against fp64.
+    Q, K, V = (bf16_bits(x) for x in inputs(BH, S, D, 5000 + D + causal, n=3))
+    got, lse = flash_fwd(Q, K, V, BH, S, D, causal, dtype="bf16")
+    Q64, K64, V64 = (bits_to_f32(x).astype(np.float64) for x in (Q, K, V))
+    ref = O.attention(Q64, K64, V64, BH, S, D, causal).reshape(BH, S, D)
+    g3 = got.reshape(BH, S, D)
+    for b in range(BH):
+        assert maxrel(g3[b], ref[b]) <= 2e-2, b
+    assert np.abs(lse - O.flash_lse(Q64, K64, BH, S, D, causal)).max() <= 1e-3 * np.sqrt(D)
+
+
 def _bwd_ref(Q, K, V, dO, BH, S, D, causal):
     args = [x.astype(np.float64) for x in (Q, K, V, dO)]
     return O.attention_bwd(*args, BH, S, D, causal)
