@@ -712,26 +712,33 @@ struct Tile32 {
 // and each stage's LSE*log2(e) and Dvec stream through a register-staged LDS double buffer
 // of 32-query stages, one barrier per stage.  16 keys per wave (v_mfma_f32_16x16x4_f32 rather
 // than 32 on 32x32x2) halve the per-wave registers, so two waves share each SIMD at
-// D = 128 (234 VGPRs) and four at D <= 64 (two work-groups per CU).  MFMA layouts (lane l: l16 = l % 16, g = l / 16): operands A[m = l16][k = g] and
+// D = 128 (234 VGPRs) and four at D <= 64 (two work-groups per CU).  Grids short of a round
+// of the CUs take W = 4, 2 or 1 waves (64, 32, 16 keys) per work-group instead; with fewer
+// threads staging each tile, the 1- and 2-wave forms get the whole register file.
+// MFMA layouts (lane l: l16 = l % 16, g = l / 16): operands A[m = l16][k = g] and
 // B[k = g][n = l16]; result register i of lane l is row 4 g + i, column l16.  S = Q K^T and
 // dP = dO V^T per 16-query block qb come out with lane = key j and register i = query
 // 16 qb + 4 g + i, and P, dS feed dV^T += dO^T P, dK^T += Q^T dS straight from those
 // registers: k-step (qb, i) pairs lane group g with query 16 qb + 4 g + i.
-template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 4, D == 128 ? 2 : 4)))
+template <int D, int W>
+constexpr int dkdv_f32_wpe() { return W == 8 ? (D == 128 ? 2 : 4) : W == 4 ? 2 : 1; }
+
+template <int D, bool CAUSAL, int W>
+__global__ void __launch_bounds__(64 * W)
+__attribute__((amdgpu_waves_per_eu(dkdv_f32_wpe<D, W>(), dkdv_f32_wpe<D, W>())))
 bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restrict__ Q,
                        const float* __restrict__ K, const float* __restrict__ V,
                        const float* __restrict__ dO, const float* __restrict__ LSE,
                        const float* __restrict__ Dv, float* __restrict__ dK,
                        float* __restrict__ dV, int accumulate, int kv_alias) {
-    using Tl = Tile32<D, 512>;
+    using Tl = Tile32<D, 64 * W>;
     constexpr int NB = D / 16, NDQ = D / 4, QB = RB / 16;
     extern __shared__ __attribute__((aligned(16))) float fsm[];
     __shared__ __attribute__((aligned(16))) float s_lse[2][RB], s_dv[2][RB];
 
     const int bh = blockIdx.x % BH;
     const int kt = blockIdx.x / BH;
-    const int kbase = kt * 128;
+    const int kbase = kt * 16 * W;
     const size_t base = (size_t)bh * S * D;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
@@ -839,7 +846,8 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
 }
 
 template <int D, bool CAUSAL, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WAVES / 4, WAVES / 4)))
+__global__ void __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(WAVES >= 4 ? WAVES / 4 : 1, WAVES >= 4 ? WAVES / 4 : 1)))
 bwd_dq_f32_kernel(int BH, int S, float scale, float sl2, const float* __restrict__ Q,
                   const float* __restrict__ K, const float* __restrict__ V,
                   const float* __restrict__ dO, const float* __restrict__ LSE,
@@ -1005,46 +1013,62 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
     return DH_OK;
 }
 
+template <int D, bool CAUSAL, int W>
+int launch_dkdv_f32(int BH, int S, float scale, float sl2, const void* Q, const void* K,
+                    const void* V, const void* dO, const float* LSE, const float* Dv, float* dK,
+                    float* dV, int acc, int kv_alias, size_t lds) {
+    auto kern = bwd_dkdv_f32_kernel<D, CAUSAL, W>;
+    static bool done = false;
+    DH_TRY(set_lds(kern, lds, done));
+    kern<<<BH * ((S + 16 * W - 1) / (16 * W)), 64 * W, lds, stream()>>>(
+        BH, S, scale, sl2, (const float*)Q, (const float*)K, (const float*)V, (const float*)dO,
+        LSE, Dv, dK, dV, acc, kv_alias);
+    return check_launch("dh_flash_bwd(dK,dV f32)");
+}
+
+template <int D, bool CAUSAL, int W>
+int launch_dq_f32(int BH, int S, float scale, float sl2, const void* Q, const void* K,
+                  const void* V, const void* dO, const float* LSE, const float* Dv, float* dQ,
+                  int acc_q, size_t lds) {
+    auto kern = bwd_dq_f32_kernel<D, CAUSAL, W>;
+    static bool done = false;
+    DH_TRY(set_lds(kern, lds, done));
+    kern<<<BH * ((S + 32 * W - 1) / (32 * W)), 64 * W, lds, stream()>>>(
+        BH, S, scale, sl2, (const float*)Q, (const float*)K, (const float*)V, (const float*)dO,
+        LSE, Dv, dQ, acc_q);
+    return check_launch("dh_flash_bwd(dQ f32)");
+}
+
+// Waves per work-group: the most (8 at most) whose grid of `rows`-per-wave tiles still fills
+// one round of the CUs, else 1.
+inline int f32_waves(int BH, int S, int rows) {
+    int w = 8;
+    while (w > 1 && (long long)BH * ((S + rows * w - 1) / (rows * w)) < num_cus()) w /= 2;
+    return w;
+}
+
 template <int D, bool CAUSAL>
 int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void* V,
             const void* dO, const float* LSE, const float* Dv, float* dQ, float* dK, float* dV,
             int acc, int kv_alias, int acc_q) {
     using Tl = Tile32<D>;
     const float sl2 = scale * 1.4426950408889634f;
-    const int tiles = (S + 127) / 128;
     const size_t lds = 2 * 2 * Tl::ELEMS * sizeof(float);
-    {
-        auto kern = bwd_dkdv_f32_kernel<D, CAUSAL>;
-        static bool done = false;
-        DH_TRY(set_lds(kern, lds, done));
-        kern<<<BH * tiles, 512, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,
-                                                 (const float*)K, (const float*)V,
-                                                 (const float*)dO, LSE, Dv, dK, dV, acc, kv_alias);
-        DH_TRY(check_launch("dh_flash_bwd(dK,dV f32)"));
+    // dK/dV: 16 keys per wave (8 waves, 128 keys, when that grid fills the CUs).
+    switch (f32_waves(BH, S, 16)) {
+    case 8: DH_TRY((launch_dkdv_f32<D, CAUSAL, 8>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dK, dV, acc, kv_alias, lds))); break;
+    case 4: DH_TRY((launch_dkdv_f32<D, CAUSAL, 4>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dK, dV, acc, kv_alias, lds))); break;
+    case 2: DH_TRY((launch_dkdv_f32<D, CAUSAL, 2>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dK, dV, acc, kv_alias, lds))); break;
+    default: DH_TRY((launch_dkdv_f32<D, CAUSAL, 1>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dK, dV, acc, kv_alias, lds)));
     }
-    // dQ: 8 waves (two per SIMD) on 256-query tiles when that grid fills at least one round
-    // of the CUs, else 4 waves on 128 (the same rule as the fp32 forward).
-    const int tiles8 = (S + 255) / 256;
-    if (BH * tiles8 >= num_cus()) {
-        auto kern = bwd_dq_f32_kernel<D, CAUSAL, 8>;
-        static bool done8 = false;
-        DH_TRY(set_lds(kern, lds, done8));
-        kern<<<BH * tiles8, 512, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,
-                                                  (const float*)K, (const float*)V,
-                                                  (const float*)dO, LSE, Dv, dQ, acc_q);
-        DH_TRY(check_launch("dh_flash_bwd(dQ f32, 8 waves)"));
-        return DH_OK;
+    // dQ: 32 queries per wave (8 waves, two per SIMD, on 256-query tiles when that grid fills
+    // the CUs; the same rule as the fp32 forward, continued down to 1 wave).
+    switch (f32_waves(BH, S, 32)) {
+    case 8: return launch_dq_f32<D, CAUSAL, 8>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dQ, acc_q, lds);
+    case 4: return launch_dq_f32<D, CAUSAL, 4>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dQ, acc_q, lds);
+    case 2: return launch_dq_f32<D, CAUSAL, 2>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dQ, acc_q, lds);
+    default: return launch_dq_f32<D, CAUSAL, 1>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dQ, acc_q, lds);
     }
-    {
-        auto kern = bwd_dq_f32_kernel<D, CAUSAL, 4>;
-        static bool done = false;
-        DH_TRY(set_lds(kern, lds, done));
-        kern<<<BH * tiles, NT, lds, stream()>>>(BH, S, scale, sl2, (const float*)Q,
-                                                (const float*)K, (const float*)V,
-                                                (const float*)dO, LSE, Dv, dQ, acc_q);
-        DH_TRY(check_launch("dh_flash_bwd(dQ f32)"));
-    }
-    return DH_OK;
 }
 
 template <typename T, int D>

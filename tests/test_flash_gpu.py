@@ -73,13 +73,15 @@ def test_fp32_fwd_wide_grid(BH, S, D, causal):
     assert np.abs(lse - ref_lse(Q, K, BH, S, D, causal)).max() <= tol
 
 
-@pytest.mark.parametrize("BH,S", [(130, 257), (64, 520), (300, 2), (256, 3)])
+@pytest.mark.parametrize("BH,S", [(130, 257), (64, 520), (300, 2), (256, 3), (64, 256), (32, 256)])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 def test_fp32_bwd_wide_grid(BH, S, D, causal):
     # Grids that fill the chip: 130 x 257 takes the dQ launch on 256-query tiles (8 waves, a
     # one-row last tile), 64 x 520 on 128-query tiles (4 waves), many two- and three-row
-    # slices the 8-wave launch with one mostly padding stage.  The whole tensor meets the
+    # slices the 8-wave launch with one mostly padding stage; 64 x 256 and 32 x 256 the
+    # smaller work-groups of both launches (dK/dV on 4 and 2 waves, dQ on 2 and 1), as
+    # grids short of a round take them.  The whole tensor meets the
     # normwise bar; each slice, so that a misplaced tile cannot hide behind the others,
     # meets it relative to the size of the terms it sums (for two keys dQ_1 is
     # scale P10 P11 (dP10 - dP11)(K0 - K1), which cancellation can make far smaller than
