@@ -15,8 +15,8 @@
 //   rows per wave, 256 per work-group.  K and V stream in stages of 64 keys through a
 //   4-deep LDS ring filled by direct-to-LDS DMA (no staging registers); both stay
 //   row-major, V being read with the transposing ds_read_b64_tr_b16.  Q fragments live in
-//   registers for the whole kernel.  Grids of at most two rounds take 4-wave work-groups
-//   (128 rows, two per CU) with two-slot K and V rings instead.
+//   registers for the whole kernel.  All grids but non-causal ones past six rounds of the
+//   CUs take 4-wave work-groups (128 rows, two per CU) with two-slot K and V rings instead.
 // fp32 kernel (v_mfma_f32_32x32x2_f32): 32 rows per wave, K and V both [key][d] in a
 //   two-stage LDS ring filled through registers; 8 waves (two per SIMD, 256 rows) when that
 //   grid fills the chip, else 4 (128 rows).
@@ -825,14 +825,14 @@ int launch_bf16_w(int BH, int S, float sl2, const void* Q, const void* K, const 
 template <int D, bool CAUSAL>
 int launch_bf16(int BH, int S, float sl2, const void* Q, const void* K, const void* V, void* O,
                 float* LSE) {
-    // 4-wave work-groups (two per CU) when the 256-row grid fills at most two rounds of the
-    // CUs: twice the work-groups, and each CU's two run their prologues and epilogues apart.
-    // Same box: (BH, S, D) = (32, 2048, 128) causal 0.0604 -> 0.0512 ms, (16, 4096, 64)
-    // 0.0834 -> 0.0816; at config 4's 8 rounds a wash (0.5427 / 0.5410 causal, 0.9637 /
-    // 0.9694 non-causal), the doubled K/V staging per row taking back what the overlap gives.
-    if (BH * ((S + 255) / 256) <= 2 * num_cus())
-        return launch_bf16_w<D, CAUSAL, 4>(BH, S, sl2, Q, K, V, O, LSE);
-    return launch_bf16_w<D, CAUSAL, 8>(BH, S, sl2, Q, K, V, O, LSE);
+    // 4-wave work-groups (two per CU): twice the work-groups, and each CU's two run their
+    // prologues and epilogues apart.  Same box, 8-wave / 4-wave time: 1.5 to 6 rounds of the
+    // CUs 1.00-1.16 (D = 64: 1.09-1.11); at 8 rounds causal 1.003-1.007, non-causal
+    // 0.986-0.999, where the doubled K/V staging per row takes back what the overlap gives.
+    // So 8-wave work-groups only for non-causal grids past six rounds.
+    if (!CAUSAL && (long long)BH * ((S + 255) / 256) > 6LL * num_cus())
+        return launch_bf16_w<D, CAUSAL, 8>(BH, S, sl2, Q, K, V, O, LSE);
+    return launch_bf16_w<D, CAUSAL, 4>(BH, S, sl2, Q, K, V, O, LSE);
 }
 
 template <int D, bool CAUSAL>
