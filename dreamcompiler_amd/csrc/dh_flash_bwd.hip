@@ -458,19 +458,20 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
 }
 
 // ---------------------------------------------------------------------------------
-// 3. dQ (bf16).  Work-group: 8 waves x 32 queries (two waves per SIMD); 64-key stages of
-//    K and V through a 4-deep LDS ring.  S^T = K Q^T and dP^T = V dO^T come out with
+// 3. dQ (bf16).  Work-group: W waves x 32 queries; 64-key stages of K and V through a
+//    4-deep LDS ring on 8 waves (two per SIMD), a 2-deep one (64 KB at D = 128, two
+//    work-groups per CU) on 4: stage st + 1 is issued after barrier st into the slot stage
+//    st - 1 left, and each barrier waits for all.  S^T = K Q^T and dP^T = V dO^T come out with
 //    lane = query; dS^T feeds dQ^T += K^T dS^T straight from the registers, K^T through
 //    transpose reads of the same K tile.
 // ---------------------------------------------------------------------------------
-constexpr int DQ_WAVES = 8;
-constexpr int DQ_NT = 64 * DQ_WAVES;
-constexpr int DQ_ROWS = 32 * DQ_WAVES;
 constexpr int DQ_BN = 64;
-constexpr int DQ_NSTAGE = 4;
 
-template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(DQ_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int W>
+constexpr int dq_nstage() { return W == 8 ? 4 : 2; }
+
+template <int D, bool CAUSAL, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __restrict__ Q,
                    const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
                    const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO,
@@ -479,6 +480,7 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
     using T = BwTile<D, DQ_BN>;
     constexpr int ND = D / 32, NTK = D / 16;
     constexpr int STAGE = 2 * T::TILE;               // K tile, then V tile
+    constexpr int DQ_WAVES = W, DQ_ROWS = 32 * W, DQ_NSTAGE = dq_nstage<W>();
     constexpr int PER = 2 * T::NBLK / DQ_WAVES;
     static_assert(PER >= 1 && PER * DQ_WAVES == 2 * T::NBLK, "stage must split over the waves");
     extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
@@ -964,6 +966,22 @@ int set_lds(Kern kern, size_t bytes, bool& done) {
     return DH_OK;
 }
 
+template <int D, bool CAUSAL, int W>
+int launch_dq_bf16(int BH, int S, float scale, float sl2, const void* Q, const void* K,
+                   const void* V, const void* O, const void* dO, const float* LSE, float* L2,
+                   float* Dv, float* dQ, int acc, int group) {
+    auto kern = bwd_dq_bf16_kernel<D, CAUSAL, W>;
+    const size_t lds = (size_t)dq_nstage<W>() * 2 * BwTile<D, DQ_BN>::TILE;
+    static bool done = false;
+    DH_TRY(set_lds(kern, lds, done));
+    const int grid = BH * ((S + 32 * W - 1) / (32 * W));
+    kern<<<grid, 64 * W, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
+                                         (const uint16_t*)K, (const uint16_t*)V,
+                                         (const uint16_t*)O, (const uint16_t*)dO, LSE, L2, Dv, dQ,
+                                         acc, group);
+    return check_launch("dh_flash_bwd(dQ bf16)");
+}
+
 // dQ launch first (it also stores Dvec and LSE log2 e into Dv and L2), then dK/dV.  A gradient
 // buffer shared with dQ is added to by the dK/dV launch, so shared buffers receive the sum.
 template <int D, bool CAUSAL>
@@ -985,18 +1003,15 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
         const char* e = std::getenv("DH_FLASH_BWD_GROUP_Q");
         return e ? std::atoi(e) : 4;
     }();
-    {
-        auto kern = bwd_dq_bf16_kernel<D, CAUSAL>;
-        const size_t lds = (size_t)DQ_NSTAGE * 2 * BwTile<D, DQ_BN>::TILE;
-        static bool done = false;
-        DH_TRY(set_lds(kern, lds, done));
-        const int grid = BH * ((S + DQ_ROWS - 1) / DQ_ROWS);
-        kern<<<grid, DQ_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
-                                             (const uint16_t*)K, (const uint16_t*)V,
-                                             (const uint16_t*)O, (const uint16_t*)dO, LSE, L2, Dv,
-                                             dQ, acc, group_q);
-        DH_TRY(check_launch("dh_flash_bwd(dQ bf16)"));
-    }
+    // dQ on 4-wave work-groups (128 queries, two per CU, a two-stage ring) except D = 128 grids
+    // of between one and four rounds of the 256-query tiles.  Same box, 8-wave / 4-wave time:
+    // config 4 1.007-1.009, (16, 4096, 128) causal 1.072, (16, 2048, 64) causal 1.233,
+    // (128, 2048, 64) 1.024; (32, 4096, 128) causal 0.980-0.985, (64, 2048, 128) 1.002.
+    const long long grid8 = (long long)BH * ((S + 255) / 256);
+    if (D == 128 && grid8 > num_cus() && grid8 < 4LL * num_cus())
+        DH_TRY((launch_dq_bf16<D, CAUSAL, 8>(BH, S, scale, sl2, Q, K, V, O, dO, LSE, L2, Dv, dQ, acc, group_q)));
+    else
+        DH_TRY((launch_dq_bf16<D, CAUSAL, 4>(BH, S, scale, sl2, Q, K, V, O, dO, LSE, L2, Dv, dQ, acc, group_q)));
     {
         auto kern = bwd_dkdv_bf16_kernel<D, CAUSAL>;
         const size_t lds = (size_t)KV_NSTAGE * (2 * BwTile<D, KV_BQ>::TILE + 2048) +
