@@ -185,7 +185,7 @@ def test_fp32_bwd(S, D, causal):
             assert maxrel(g, r) <= tol
 
 
-@pytest.mark.parametrize("S", [64, 100, 257])
+@pytest.mark.parametrize("S", [1, 33, 64, 100, 257])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 def test_bf16_bwd(S, D, causal):
@@ -195,7 +195,12 @@ def test_bf16_bwd(S, D, causal):
     grads = flash_bwd(Q, K, V, bf16_bits(Of), G, lse, BH, S, D, causal, dtype="bf16")
     refs = _bwd_ref(*(bits_to_f32(x) for x in (Q, K, V, G)), BH, S, D, causal)
     for name, g, r in zip("QKV", grads, refs):
-        assert maxrel(g, r) <= 2e-2, name
+        if np.abs(r).max() < 1e-12:
+            # S = 1: dS = P (dP - Dvec) with Dvec = dP exactly, so dQ = dK = 0; the GPU keeps
+            # fp32 rounding residue of the O(1) terms dP and Dvec.
+            assert np.abs(g).max() <= 2e-2, name
+        else:
+            assert maxrel(g, r) <= 2e-2, name
 
 
 def test_fwd_rejects_non_positive_scale():
