@@ -19,7 +19,7 @@
 //   CUs take 4-wave work-groups (128 rows, two per CU) with two-slot K and V rings instead.
 // fp32 kernel (v_mfma_f32_32x32x2_f32): 32 rows per wave, K and V both [key][d] in a
 //   two-stage LDS ring filled through registers; 8 waves (two per SIMD, 256 rows) when that
-//   grid fills the chip, else 4 (128 rows).
+//   grid fills the chip (non-causal: 5/8 of it), else 4 (128 rows).
 // Causal work-groups are launched heaviest-first (longest key range) and all
 //   q-tiles of one slice land on the same XCD, which shares that slice's K/V in L2.
 #include <cmath>
@@ -852,8 +852,13 @@ int launch_f32(int BH, int S, float sl2, const void* Q, const void* K, const voi
     // 256-row tiles on 8 waves when they fill at least one round of the CUs (config 4's
     // shape: 5.48 -> 4.53 ms, same box), else 128-row tiles on 4 waves.
     const size_t lds = 4 * F32Stage<D>::ELEMS * sizeof(float);
+    // 8 waves when their grid fills the CUs, and for non-causal grids from 5/8 of a round
+    // (same box, 8-wave against 4-wave at 0.62-0.94 rounds: (48, 1024, 128) 0.290 / 0.343 ms,
+    // (40, 1024, 64) 0.160 / 0.196, (60, 1024, 32) 0.101 / 0.131; at half a round, and for
+    // causal grids under one round, 4 waves stay faster: (32, 1024, 32) 0.096 / 0.065,
+    // (64, 520, 128) causal 0.144 / 0.089).
     const int grid8 = BH * ((S + 255) / 256);
-    if (grid8 >= num_cus()) {
+    if (grid8 >= num_cus() || (!CAUSAL && 8 * grid8 >= 5 * num_cus())) {
         auto kern = flash_fwd_f32_kernel<D, CAUSAL, 8>;
         static bool done8 = false;
         DH_TRY(set_lds(kern, lds, done8));

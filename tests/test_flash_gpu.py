@@ -62,9 +62,10 @@ def test_fp32_fwd_shapes(S, D, causal):
 def test_fp32_fwd_wide_grid(BH, S, D, causal):
     # Grids that fill the chip (the small-grid split kernel covers the 3-slice shapes above):
     # 130 slices x 257 rows take 256-row work-groups on 8 waves (a one-row last tile), 64 x 520
-    # 128-row work-groups on 4 waves (its 256-row grid, 192, is short of one round of the
-    # CUs); many one- and three-row slices take the 8-wave kernel with a single, mostly
-    # padding stage; ragged last blocks, fp64 oracle.
+    # causal 128-row work-groups on 4 waves (its 256-row grid, 192, is short of one round of
+    # the CUs; non-causal takes 8 waves from 5/8 of a round); many one- and three-row slices
+    # take the 8-wave kernel with a single, mostly padding stage; ragged last blocks, fp64
+    # oracle.
     Q, K, V = inputs(BH, S, D, 1000 + D + causal, n=3)
     got, lse = flash_fwd(Q, K, V, BH, S, D, causal)
     Q64, K64, V64 = (x.astype(np.float64) for x in (Q, K, V))
