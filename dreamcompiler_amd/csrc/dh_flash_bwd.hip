@@ -1077,8 +1077,12 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
     default: DH_TRY((launch_dkdv_f32<D, CAUSAL, 1>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dK, dV, acc, kv_alias, lds)));
     }
     // dQ: 32 queries per wave (8 waves, two per SIMD, on 256-query tiles when that grid fills
-    // the CUs; the same rule as the fp32 forward, continued down to 1 wave).
-    switch (f32_waves(BH, S, 32)) {
+    // the CUs, continued down to 1 wave; as in the fp32 forward, non-causal grids take 8 waves
+    // from 5/8 of a round: same box, whole backward (48, 1024, 128) 1.052 -> 1.035 ms,
+    // (40, 1024, 64) 0.542 -> 0.504, (60, 1024, 32) 0.314 -> 0.283, (40, 1536, 128) 1.540 ->
+    // 1.513).
+    const bool nc8 = !CAUSAL && 8LL * BH * ((S + 255) / 256) >= 5LL * num_cus();
+    switch (nc8 ? 8 : f32_waves(BH, S, 32)) {
     case 8: return launch_dq_f32<D, CAUSAL, 8>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dQ, acc_q, lds);
     case 4: return launch_dq_f32<D, CAUSAL, 4>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dQ, acc_q, lds);
     case 2: return launch_dq_f32<D, CAUSAL, 2>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dQ, acc_q, lds);
