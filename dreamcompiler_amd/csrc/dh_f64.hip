@@ -27,6 +27,7 @@
 #include "dh_common.hpp"
 
 #include <math.h>
+#include <cstdlib>
 
 namespace dh {
 namespace {
@@ -226,15 +227,17 @@ __global__ __launch_bounds__(256) void gemm_f64_reduce(int M, int N, int nkb, in
 // slice; x_j = s_j * scale over the row's visible keys (j <= i when causal), then
 // p_j = exp(x_j - max x) / sum exp(x - max x), and exact zeros for masked keys
 // (training.inc:193-201, 240-247).  One wave per row.
+// P holds `rows` score rows of S keys: consecutive groups of R rows are query rows
+// row0 .. row0 + R - 1 of a slice (R = S, row0 = 0 for whole slices).
 __global__ __launch_bounds__(256) void attn_softmax_f64(double* __restrict__ P, int S,
-                                                        long long rows, double scale,
-                                                        int causal) {
+                                                        long long rows, int R, int row0,
+                                                        double scale, int causal) {
     // x = s * scale is rounded before the subtraction, as the reference stores it first.
 #pragma clang fp contract(off)
     const long long r = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
     const int lane = threadIdx.x & 63;
-    const int i = (int)(r % S);
+    const int i = row0 + (int)(r % R);
     const int n = causal ? i + 1 : S;
     double* row = P + r * (long long)S;
     double mx = -1e30;
@@ -256,11 +259,12 @@ __global__ __launch_bounds__(256) void attn_softmax_f64(double* __restrict__ P, 
 // autograd.inc:711-714, 758-761).
 __global__ __launch_bounds__(256) void attn_softmax_bwd_f64(const double* __restrict__ P,
                                                             double* __restrict__ dP, int S,
-                                                            long long rows, int causal) {
+                                                            long long rows, int R, int row0,
+                                                            int causal) {
     const long long r = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
     const int lane = threadIdx.x & 63;
-    const int i = (int)(r % S);
+    const int i = row0 + (int)(r % R);
     const int n = causal ? i + 1 : S;
     const double* p = P + r * (long long)S;
     double* g = dP + r * (long long)S;
@@ -341,14 +345,31 @@ int check_gemm_f64(const char* op, int transA, int transB, int M, int N, int K, 
     return DH_OK;
 }
 
-// Slices per chunk so that one S x S fp64 score buffer stays within 256 MB.
-int attn_chunk(int BH, int S) {
+// Bytes one fp64 score buffer may take: 256 MB (DH_ATTN_F64_SCORE_BYTES overrides it, for
+// tests of the row-block path at small S).
+size_t attn_budget() {
+    const char* e = std::getenv("DH_ATTN_F64_SCORE_BYTES");
+    const long long v = e && *e ? std::atoll(e) : 0;
+    return v > 0 ? (size_t)v : ((size_t)256 << 20);
+}
+
+// Work per pass over the scores: `chunk` whole slices of S x S scores when one slice fits the
+// budget, else (chunk = 1) blocks of `rows` query rows of one slice, rows x S scores each.
+struct AttnPass {
+    int chunk, rows;
+};
+AttnPass attn_pass(int BH, int S) {
+    const size_t budget = attn_budget();
     const size_t per = (size_t)S * S * sizeof(double);
-    size_t c = ((size_t)256 << 20) / (per ? per : 1);
-    if (c < 1) c = 1;
-    if (c > (size_t)BH) c = BH;
-    if (c > 65535) c = 65535;
-    return (int)c;
+    if (per <= budget) {
+        size_t c = budget / (per ? per : 1);
+        if (c > (size_t)BH) c = BH;
+        if (c > 65535) c = 65535;
+        return {(int)c, S};
+    }
+    size_t r = budget / ((size_t)S * sizeof(double));
+    if (r < 1) r = 1;
+    return {1, (int)r};
 }
 
 int check_attn_f64(const char* op, int BH, int S, int D) {
@@ -361,8 +382,16 @@ int check_attn_f64(const char* op, int BH, int S, int D) {
     return DH_OK;
 }
 
-void launch_softmax(double* P, int S, long long rows, double scale, int causal) {
-    attn_softmax_f64<<<(unsigned)((rows + 3) / 4), 256, 0, stream()>>>(P, S, rows, scale, causal);
+void launch_softmax(double* P, int S, long long rows, int R, int row0, double scale,
+                    int causal) {
+    attn_softmax_f64<<<(unsigned)((rows + 3) / 4), 256, 0, stream()>>>(P, S, rows, R, row0,
+                                                                      scale, causal);
+}
+
+void launch_softmax_bwd(const double* P, double* G, int S, long long rows, int R, int row0,
+                        int causal) {
+    attn_softmax_bwd_f64<<<(unsigned)((rows + 3) / 4), 256, 0, stream()>>>(P, G, S, rows, R,
+                                                                          row0, causal);
 }
 
 }  // namespace
@@ -398,22 +427,30 @@ int dh_attention_f64_fwd(int BH, int S, int D, double scale, int causal, const d
         return set_error(DH_ERR_INVALID, "dh_attention_f64_fwd: null pointer");
     if (!(scale > 0.0) || !isfinite(scale))
         return set_error(DH_ERR_INVALID, "dh_attention_f64_fwd: scale must be positive and finite");
-    const int chunk = attn_chunk(BH, S);
-    const long long SD = (long long)S * D, SS = (long long)S * S;
-    double* P = static_cast<double*>(dh_malloc((size_t)chunk * SS * sizeof(double)));
-    if (!P) return set_error(DH_ERR_OOM, "dh_attention_f64_fwd: %d score blocks of %d x %d", chunk, S, S);
+    const AttnPass ps = attn_pass(BH, S);
+    const long long SD = (long long)S * D;
+    const long long RS = (long long)ps.rows * S;   // scores per slice and pass
+    double* P = static_cast<double*>(dh_malloc((size_t)ps.chunk * RS * sizeof(double)));
+    if (!P)
+        return set_error(DH_ERR_OOM, "dh_attention_f64_fwd: %d score blocks of %d x %d",
+                         ps.chunk, ps.rows, S);
     int st = DH_OK;
-    for (int b0 = 0; b0 < BH && st == DH_OK; b0 += chunk) {
-        const int nb = BH - b0 < chunk ? BH - b0 : chunk;
-        const long long off = (long long)b0 * SD;
-        // scores = Q K^T
-        st = gemm_f64_launch(0, 1, S, S, D, 1.0, d_Q + off, D, SD, d_K + off, D, SD, 0.0, P, S, SS, nb);
-        if (st != DH_OK) break;
-        launch_softmax(P, S, (long long)nb * S, scale, causal);
-        st = check_launch("dh_attention_f64_fwd");
-        if (st != DH_OK) break;
-        // O = P V
-        st = gemm_f64_launch(0, 0, S, D, S, 1.0, P, S, SS, d_V + off, D, SD, 0.0, d_O + off, D, SD, nb);
+    for (int b0 = 0; b0 < BH && st == DH_OK; b0 += ps.chunk) {
+        const int nb = BH - b0 < ps.chunk ? BH - b0 : ps.chunk;
+        for (int r0 = 0; r0 < S && st == DH_OK; r0 += ps.rows) {
+            const int nr = S - r0 < ps.rows ? S - r0 : ps.rows;
+            const long long off = (long long)b0 * SD, qoff = off + (long long)r0 * D;
+            // scores of query rows r0 .. r0 + nr - 1 = Q K^T
+            st = gemm_f64_launch(0, 1, nr, S, D, 1.0, d_Q + qoff, D, SD, d_K + off, D, SD, 0.0,
+                                 P, S, RS, nb);
+            if (st != DH_OK) break;
+            launch_softmax(P, S, (long long)nb * nr, nr, r0, scale, causal);
+            st = check_launch("dh_attention_f64_fwd");
+            if (st != DH_OK) break;
+            // O = P V
+            st = gemm_f64_launch(0, 0, nr, D, S, 1.0, P, S, RS, d_V + off, D, SD, 0.0,
+                                 d_O + qoff, D, SD, nb);
+        }
     }
     dh_free(P);   // pooled: stream order keeps the buffer alive for the queued work
     return st;
@@ -429,7 +466,7 @@ int dh_attention_f64_bwd(int BH, int S, int D, double scale, int causal, const d
         return set_error(DH_ERR_INVALID, "dh_attention_f64_bwd: null pointer");
     if (!(scale > 0.0) || !isfinite(scale))
         return set_error(DH_ERR_INVALID, "dh_attention_f64_bwd: scale must be positive and finite");
-    const long long SD = (long long)S * D, SS = (long long)S * S;
+    const long long SD = (long long)S * D;
     const size_t gbytes = (size_t)BH * SD * sizeof(double);
     // Shared gradient buffers (one tensor passed as several of Q, K, V) receive the sum of
     // their gradients: every product below adds into its output, after one clearing pass.
@@ -441,37 +478,46 @@ int dh_attention_f64_bwd(int BH, int S, int D, double scale, int causal, const d
             if (!seen) DH_TRY(dh_memset(outs[x], 0, gbytes));
         }
     }
-    const int chunk = attn_chunk(BH, S);
-    double* P = static_cast<double*>(dh_malloc((size_t)chunk * SS * sizeof(double)));
-    double* G = static_cast<double*>(dh_malloc((size_t)chunk * SS * sizeof(double)));
+    const AttnPass ps = attn_pass(BH, S);
+    const long long RS = (long long)ps.rows * S;   // scores per slice and pass
+    double* P = static_cast<double*>(dh_malloc((size_t)ps.chunk * RS * sizeof(double)));
+    double* G = static_cast<double*>(dh_malloc((size_t)ps.chunk * RS * sizeof(double)));
     if (!P || !G) {
         if (P) dh_free(P);
         if (G) dh_free(G);
-        return set_error(DH_ERR_OOM, "dh_attention_f64_bwd: %d score blocks of %d x %d", chunk, S, S);
+        return set_error(DH_ERR_OOM, "dh_attention_f64_bwd: %d score blocks of %d x %d",
+                         ps.chunk, ps.rows, S);
     }
     int st = DH_OK;
-    for (int b0 = 0; b0 < BH && st == DH_OK; b0 += chunk) {
-        const int nb = BH - b0 < chunk ? BH - b0 : chunk;
+    for (int b0 = 0; b0 < BH && st == DH_OK; b0 += ps.chunk) {
+        const int nb = BH - b0 < ps.chunk ? BH - b0 : ps.chunk;
         const long long off = (long long)b0 * SD;
         const double *Q = d_Q + off, *K = d_K + off, *V = d_V + off, *dO = d_dO + off;
-        // P recomputed from Q, K exactly as the forward computes it
-        st = gemm_f64_launch(0, 1, S, S, D, 1.0, Q, D, SD, K, D, SD, 0.0, P, S, SS, nb);
-        if (st != DH_OK) break;
-        launch_softmax(P, S, (long long)nb * S, scale, causal);
-        if ((st = check_launch("dh_attention_f64_bwd")) != DH_OK) break;
-        // dV += P^T dO
-        st = gemm_f64_launch(1, 0, S, D, S, 1.0, P, S, SS, dO, D, SD, 1.0, d_dV + off, D, SD, nb);
-        if (st != DH_OK) break;
-        // dP = dO V^T, then dS in its place
-        st = gemm_f64_launch(0, 1, S, S, D, 1.0, dO, D, SD, V, D, SD, 0.0, G, S, SS, nb);
-        if (st != DH_OK) break;
-        attn_softmax_bwd_f64<<<(unsigned)(((long long)nb * S + 3) / 4), 256, 0, stream()>>>(
-            P, G, S, (long long)nb * S, causal);
-        if ((st = check_launch("dh_attention_f64_bwd")) != DH_OK) break;
-        // dQ += scale dS K ;  dK += scale dS^T Q
-        st = gemm_f64_launch(0, 0, S, D, S, scale, G, S, SS, K, D, SD, 1.0, d_dQ + off, D, SD, nb);
-        if (st != DH_OK) break;
-        st = gemm_f64_launch(1, 0, S, D, S, scale, G, S, SS, Q, D, SD, 1.0, d_dK + off, D, SD, nb);
+        // Query rows r0 .. r0 + nr - 1 per pass (whole slices when they fit the budget).
+        for (int r0 = 0; r0 < S && st == DH_OK; r0 += ps.rows) {
+            const int nr = S - r0 < ps.rows ? S - r0 : ps.rows;
+            const long long ro = (long long)r0 * D;
+            // P recomputed from Q, K exactly as the forward computes it
+            st = gemm_f64_launch(0, 1, nr, S, D, 1.0, Q + ro, D, SD, K, D, SD, 0.0, P, S, RS, nb);
+            if (st != DH_OK) break;
+            launch_softmax(P, S, (long long)nb * nr, nr, r0, scale, causal);
+            if ((st = check_launch("dh_attention_f64_bwd")) != DH_OK) break;
+            // dV += P^T dO
+            st = gemm_f64_launch(1, 0, S, D, nr, 1.0, P, S, RS, dO + ro, D, SD, 1.0, d_dV + off,
+                                 D, SD, nb);
+            if (st != DH_OK) break;
+            // dP = dO V^T, then dS in its place
+            st = gemm_f64_launch(0, 1, nr, S, D, 1.0, dO + ro, D, SD, V, D, SD, 0.0, G, S, RS, nb);
+            if (st != DH_OK) break;
+            launch_softmax_bwd(P, G, S, (long long)nb * nr, nr, r0, causal);
+            if ((st = check_launch("dh_attention_f64_bwd")) != DH_OK) break;
+            // dQ += scale dS K ;  dK += scale dS^T Q
+            st = gemm_f64_launch(0, 0, nr, D, S, scale, G, S, RS, K, D, SD, 1.0,
+                                 d_dQ + off + ro, D, SD, nb);
+            if (st != DH_OK) break;
+            st = gemm_f64_launch(1, 0, S, D, nr, scale, G, S, RS, Q + ro, D, SD, 1.0,
+                                 d_dK + off, D, SD, nb);
+        }
     }
     dh_free(P);
     dh_free(G);

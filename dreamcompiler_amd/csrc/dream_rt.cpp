@@ -24,6 +24,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <random>
+#include <system_error>
 #include <thread>
 #include <unordered_set>
 #include <vector>
@@ -41,7 +42,8 @@ std::mt19937& rng() {
 
 // body(i0, i1) over [0, n) in chunks on up to 16 host threads, for host loops over large
 // tensors whose iterations are independent (each writes only its own elements), so the
-// result does not depend on the split.  Small ranges run inline.
+// result does not depend on the split.  Small ranges run inline.  A thread that cannot be
+// created (resource limits) leaves its chunk, and the ones after it, to the calling thread.
 template <typename F>
 void par_for(size_t n, F body) {
     constexpr size_t kMin = size_t(1) << 20;
@@ -54,9 +56,16 @@ void par_for(size_t n, F body) {
     std::vector<std::thread> th;
     th.reserve(nt - 1);
     const size_t step = (n + nt - 1) / nt;
-    for (size_t k = 1; k < nt; ++k)
-        th.emplace_back([=] { body(std::min(n, k * step), std::min(n, (k + 1) * step)); });
+    size_t k = 1;
+    for (; k < nt; ++k) {
+        try {
+            th.emplace_back([=] { body(std::min(n, k * step), std::min(n, (k + 1) * step)); });
+        } catch (const std::system_error&) {
+            break;
+        }
+    }
     body(size_t(0), std::min(n, step));
+    for (; k < nt; ++k) body(std::min(n, k * step), std::min(n, (k + 1) * step));
     for (auto& x : th) x.join();
 }
 
@@ -793,6 +802,20 @@ Tensor* dream_randn(Tensor* d0, Tensor* d1) {
     return t;
 }
 
+// dropout(x, keep) (runtime/io/builtins.inc:151-163): one fp32 uniform draw on [0, 1) from the
+// shared generator per element, in element order; a draw below keep keeps x / keep, else 0.
+// Host op, like the reference's: the draws define the mask, so the stream must be the same.
+Tensor* dream_dropout(Tensor* t, Tensor* keep_rate) {
+    if (!t || !keep_rate) return create_scalar(0.0);
+    const float rate = (float)keep_rate->data[0];
+    Tensor* c = alloc_tensor(t->d0, t->d1, t->d2, t->d3);
+    std::uniform_real_distribution<float> dist(0.f, 1.f);
+    for (int i = 0; i < t->size; ++i) c->data[i] = dist(rng()) < rate ? t->data[i] / rate : 0.0;
+    c->keep = (double)rate;
+    set_graph(c, t, nullptr, DREAM_OP_DROPOUT);
+    return c;
+}
+
 Tensor* sum(Tensor* a) {
     Tensor* c = alloc_tensor(1, 1, 1, 1);
     double s = 0.0;
@@ -1496,6 +1519,13 @@ Tensor* backward(Tensor* root) {
                     host_grad(t);
                     unary_backward(t);
                     break;
+                case DREAM_OP_DROPOUT: {   // autograd.inc:472-482: kept elements, times 1/keep
+                    host_grad(t);
+                    const double inv = (t->keep > 0.0 && t->keep <= 1.0) ? 1.0 / t->keep : 1.0;
+                    for (int j = 0; j < t->lhs->size; ++j)
+                        if (t->data[j] != 0.0) t->lhs->grad[j] += t->grad[j] * inv;
+                    break;
+                }
                 default:
                     break;
             }

@@ -25,7 +25,7 @@ TP = ctypes.POINTER(TensorHead)
 _SIGS = {
     "alloc_tensor": [ctypes.c_int] * 4, "create_scalar": [ctypes.c_double],
     "tensor_incref": [TP], "tensor_decref": [TP], "ones": [TP, TP],
-    "dream_set_seed": [TP], "dream_randn": [TP, TP], "sum": [TP],
+    "dream_set_seed": [TP], "dream_randn": [TP, TP], "sum": [TP], "dream_dropout": [TP, TP],
     "tensor_add": [TP, TP], "tensor_mul": [TP, TP], "tensor_get_grad": [TP],
     "zero_grad": [TP], "dream_set_precision": [TP, ctypes.c_int], "dream_to_float32": [TP],
     "dream_enable_fp16": [], "dream_disable_fp16": [], "tensor_matmul": [TP, TP],

@@ -165,8 +165,9 @@ int dh_gemm_f64_ex(int transA, int transB, int M, int N, int K, double alpha,
  * loop of training.inc:366-399; same values up to rounding).  The backward
  * (autograd.inc:675-778) recomputes the probabilities and adds (accumulate = 1) or writes
  * dQ, dK, dV; any two of them may be one buffer, which then receives the sum of its
- * gradients.  S x S score blocks (<= 256 MB each, by chunks of slices) come from the pool;
- * S <= 46340.  scale must be positive. */
+ * gradients.  Score buffers come from the pool, at most 256 MB each: whole S x S blocks
+ * by chunks of slices while one slice fits, else blocks of query rows of one slice
+ * (rows x S); the backward takes two.  S <= 46340.  scale must be positive. */
 int dh_attention_f64_fwd(int BH, int S, int D, double scale, int causal,
                          const double* d_Q, const double* d_K, const double* d_V, double* d_O);
 int dh_attention_f64_bwd(int BH, int S, int D, double scale, int causal,

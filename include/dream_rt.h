@@ -59,6 +59,7 @@ typedef struct Tensor {
     int host_pinned;           /* bit 0: data, bit 1: grad are pinned pool buffers   */
     int f64_node;              /* 1: the node's forward ran in fp64 (below the GPU
                                 * threshold), so its backward does too               */
+    double keep;               /* dropout nodes: the keep rate (bwd_name)            */
 } Tensor;
 
 enum {
@@ -70,7 +71,8 @@ enum {
      * logical not, floor/ceil/round, clip) */
     DREAM_OP_SUB, DREAM_OP_DIV, DREAM_OP_MINIMUM, DREAM_OP_MAXIMUM, DREAM_OP_POW,
     DREAM_OP_RELU, DREAM_OP_EXP, DREAM_OP_LOG, DREAM_OP_SQRT, DREAM_OP_ABS, DREAM_OP_SIGMOID,
-    DREAM_OP_TANH, DREAM_OP_SIN, DREAM_OP_COS, DREAM_OP_TAN, DREAM_OP_ATAN, DREAM_OP_NO_GRAD
+    DREAM_OP_TANH, DREAM_OP_SIN, DREAM_OP_COS, DREAM_OP_TAN, DREAM_OP_ATAN, DREAM_OP_NO_GRAD,
+    DREAM_OP_DROPOUT
 };
 
 /* ---- tensors (runtime/core/tensor.inc:143-303) ---- */
@@ -82,6 +84,7 @@ Tensor* ones(Tensor* d0, Tensor* d1);                      /* elementwise.inc:2 
 Tensor* dream_set_seed(Tensor* seed);                      /* elementwise.inc:35-40 */
 Tensor* dream_randn(Tensor* d0, Tensor* d1);               /* elementwise.inc:48-54 */
 Tensor* sum(Tensor* a);                                    /* elementwise.inc:56    */
+Tensor* dream_dropout(Tensor* t, Tensor* keep_rate);       /* builtins.inc:151-163  */
 /* ---- elementwise ops (elementwise.inc:276-336, 1254-1270; math_extra.inc:1-10;
  * builtins.inc:85-87), the reference's runGPU / runGPUUnary path (backend/gpu.inc:637-716).
  * Binary: C's dims are the per-dim maxima of the operands', each operand read through

@@ -59,7 +59,8 @@ class RefRuntime:
                             ("dream_softmax", 1), ("dream_log_softmax", 1),
                             ("dream_layer_norm", 1), ("dream_linear", 3),
                             ("dream_linear_relu", 3), ("dream_bmm", 6),
-                            ("dream_set_seed", 1), ("dream_randn", 2),
+                            ("dream_set_seed", 1), ("dream_randn", 2), ("dream_dropout", 2),
+                            ("tensor_get_grad", 1),
                             ("dream_kaiming_init", 2), ("gemm_selftest", 0),
                             ("flash_attention_selftest", 0), ("tensor_decref", 1),
                             ("zero_grad", 1), ("dream_conv2d", 7),

@@ -210,7 +210,8 @@ def test_attention_f64_backward_shared_gradient_buffer():
 
 def test_attention_f64_chunks_over_slices():
     # S = 3000: one 72 MB score block per slice, so 3 slices run as one chunk of 3; S = 6000
-    # gives 288 MB per slice, one slice per chunk.  Checked on sampled rows of every slice.
+    # gives 288 MB per slice, above the 256 MB budget: one slice at a time in blocks of 5592
+    # query rows (and a last block of 408).  Checked on sampled rows of every slice.
     for B, S, D in [(3, 3000, 8), (2, 6000, 4)]:
         rng = np.random.default_rng(S)
         Q, K, V, G = (rng.standard_normal((B, S * D)) for _ in range(4))
@@ -219,3 +220,26 @@ def test_attention_f64_chunks_over_slices():
         Orow, _ = O.attention_rows(Q, K, V, G, rows, B, S, D, True)
         for b in range(B):
             assert maxrel(got[b, rows[b]], Orow[b]) <= 1e-12
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_f64_query_row_blocks(causal, monkeypatch):
+    """Slices whose S x S scores exceed the score budget run in blocks of query rows (a
+    rows x S buffer each), so no buffer exceeds the budget at any S.  The budget is lowered
+    (DH_ATTN_F64_SCORE_BYTES, read at each call) to 100 rows x S x 8 bytes so small shapes take
+    that path: blocks of 100 query rows and a ragged last block, forward and backward (fresh,
+    accumulating, and one buffer for dQ, dK and dV) against the oracle."""
+    B, S, D = 2, 330, 160
+    monkeypatch.setenv("DH_ATTN_F64_SCORE_BYTES", str(100 * S * 8))
+    rng = np.random.default_rng(330 + causal)
+    Q, K, V, G = (rng.standard_normal((B, S * D)) for _ in range(4))
+    assert maxrel(attn64(Q, K, V, B, S, D, causal), O.attention(Q, K, V, B, S, D, causal)) <= 1e-12
+    ref = O.attention_bwd(Q, K, V, G, B, S, D, causal)
+    for g, r in zip(attn64_bwd(Q, K, V, G, B, S, D, causal), ref):
+        assert maxrel(g, r) <= 1e-11
+    init = [rng.standard_normal((B, S * D)) for _ in range(3)]
+    acc = attn64_bwd(Q, K, V, G, B, S, D, causal, accumulate=True, init=init)
+    for g, r, i in zip(acc, ref, init):
+        assert maxrel(g, r + i) <= 1e-11
+    shared = sum(O.attention_bwd(Q, Q, Q, G, B, S, D, causal))
+    assert maxrel(attn64_bwd(Q, Q, Q, G, B, S, D, causal, alias=True)[0], shared) <= 1e-11

@@ -55,3 +55,30 @@ def test_host_builtins_and_refcounts():
     assert rt.read(s)[0, 0] == 6.0
     L.backward(s)
     assert np.all(rt.read(o, grad=True) == 2.0)   # d/do sum(o*o) = 2o
+
+
+def test_dropout_matches_reference_build():
+    """dream_dropout (runtime/io/builtins.inc:151-163) and its backward (autograd.inc:472-482):
+    the same fp32 uniform draws from the shared generator as the reference build, so the mask,
+    the kept values x / keep and the gradient (1 / keep on kept elements) are bit-identical.
+    Host-only: no GPU work."""
+    import pytest
+    import _ref_runtime
+    if not _ref_runtime.available():
+        pytest.skip("oracle/_ref not built (needs /root/reference)")
+    R = _ref_runtime.RefRuntime()
+    L = rt.load()
+    X = np.random.default_rng(3).standard_normal((37, 53))
+    out = []
+    for lib, tensor, read in ((L, rt.tensor, rt.read), (R.L, R.tensor, R.read)):
+        lib.dream_set_seed(lib.create_scalar(31337.0))
+        x = tensor(X)
+        d = lib.dream_dropout(x, lib.create_scalar(0.8))
+        lib.backward(lib.sum(lib.tensor_mul(d, tensor(X))))   # upstream gradient X
+        out.append((read(d), read(x, grad=True)))
+    (d_ours, g_ours), (d_ref, g_ref) = out
+    assert np.array_equal(d_ours, d_ref) and np.array_equal(g_ours, g_ref)
+    kept = d_ref != 0
+    assert 0.7 < kept.mean() < 0.9
+    # x / keep (the -ffast-math build may form it as x * (1 / keep): one rounding apart)
+    assert np.allclose(d_ref[kept], X[kept] / np.float64(np.float32(0.8)), rtol=4e-16, atol=0)

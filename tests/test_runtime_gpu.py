@@ -187,6 +187,99 @@ def test_15_18_25_selftests(L, capfd):
     assert "FLASH_ATTN: 4/4 PASS" in out           # tests/25_flash_attention.dream
 
 
+def _run_16_determinism(lib, scalar, read):
+    """One run_once() of tests/16_determinism.dream:6-16 through a runtime's builtins: returns
+    loss[0] + sum(grad(W)) * 7.0 and the pieces it is made of."""
+    A = lib.dream_randn(scalar(160), scalar(160))
+    W = lib.dream_randn(scalar(160), scalar(160))
+    h = lib.relu(lib.tensor_matmul(A, W))            # 160 x 160: the fp64 `@` (dgemm order)
+    d = lib.dream_dropout(h, scalar(0.8))
+    q = lib.dream_randn(scalar(1), scalar(128))
+    at = lib.dream_attention(q, q, q, scalar(1.0), scalar(4.0), scalar(32.0))   # self-attention
+    loss = lib.tensor_add(lib.sum(d), lib.tensor_mul(lib.sum(at), scalar(3.0)))
+    lib.backward(loss)
+    gW = read(W, grad=True)
+    sW = read(lib.sum(lib.tensor_get_grad(W)))[0, 0]
+    f = read(loss)[0, 0] + sW * 7.0
+    return f, read(loss)[0, 0], gW, read(q, grad=True), read(at)
+
+
+def test_determinism_16_as_written(L):
+    """tests/16_determinism.dream replayed through the builtins as written: set_seed(31337);
+    randn 160 x 160 `@` (below the GPU threshold: fp64 on the GPU in dgemm's order), relu,
+    dropout(h, 0.8), randn(1, 128), attention(q, q, q, 1, 4, 32) (one tensor as Q, K and V, so
+    its gradient is dQ + dK + dV), loss = sum(d) + sum(at) * 3, backward; twice, bit-identical
+    (DETERMINISM: PASS).  Against the reference build's CPU runtime (oracle/_ref, when present)
+    on the same program: the loss, grad(W) and grad(q) to 1e-12 (the fp64 products differ from
+    the reference's loops only in summation order)."""
+    runs = []
+    for _ in range(2):
+        L.dream_set_seed(rt.scalar(31337))
+        runs.append(_run_16_determinism(L, rt.scalar, rt.read))
+    f1, f2 = runs[0][0], runs[1][0]
+    assert f1 - f2 == 0.0                                       # DETERMINISM: PASS
+    for a, b in zip(runs[0][1:], runs[1][1:]):
+        assert np.array_equal(a, b)
+    import _ref_runtime
+    if not _ref_runtime.available():
+        pytest.skip("oracle/_ref not built: bit-exact repeat checked, reference values not")
+    R = _ref_runtime.RefRuntime()
+    R.L.dream_set_seed(R.scalar(31337))
+    ref = _run_16_determinism(R.L, R.scalar, R.read)
+    assert abs(runs[0][1] - ref[1]) <= 1e-12 * abs(ref[1])       # loss
+    assert maxrel(runs[0][2], ref[2]) <= 1e-12                   # grad(W)
+    assert maxrel(runs[0][3], ref[3]) <= 1e-12                   # grad(q) = dQ + dK + dV
+    assert maxrel(runs[0][4], ref[4]) <= 1e-12                   # attention output
+    assert abs(f1 - ref[0]) <= 1e-12 * (abs(ref[1]) + 7.0 * np.abs(ref[2]).sum())
+
+
+def _shared_grad_err(g, parts):
+    """Normwise error of a gradient that is a sum of terms, against the scale of the terms
+    (the sum itself may cancel)."""
+    ref = sum(parts)
+    return float(np.abs(g - ref).max() / max(sum(np.abs(p) for p in parts).max(), 1e-30))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("kind", ["flash", "causal", "plain"])
+def test_self_attention_shared_gradient_buffers(L, kind, bf16):
+    """attention(q, q, q) and attention(q, kv, kv) at a FlashAttention shape (B*S*S >= 262144,
+    dk = 64) through the builtins and backward(sum(O * W)): the tensor passed as several
+    operands receives the sum of their gradients, as the reference's "+=" into one grad buffer
+    leaves it (autograd.inc:690-728, 779-840) -- the kernels' shared-gradient path reached
+    through the runtime, in the default precision (fp32 kernels) and with dream_enable_fp16
+    (bf16 kernels; inputs and W pre-rounded to bf16 so the oracle sees the device's values)."""
+    B, S, dk = 2, 384, 64
+    causal = kind != "plain"
+    fn = {"flash": L.dream_flash_attention, "causal": L.dream_attention_causal,
+          "plain": L.dream_attention}[kind]
+    rng = np.random.default_rng(160 + 2 * bf16 + (kind == "plain"))
+    X, KV, W = (rng.standard_normal((B, S * dk)) for _ in range(3))
+    if bf16:
+        X, KV, W = (O.bf16_round(a.astype(np.float32)).astype(np.float64) for a in (X, KV, W))
+        L.dream_enable_fp16()
+    tol = 2e-2 if bf16 else 1e-5 * np.sqrt(S)
+    sc = lambda: [rt.scalar(B), rt.scalar(S), rt.scalar(dk)]  # noqa: E731
+    try:
+        # q as Q, K and V
+        q, w = rt.tensor(X), rt.tensor(W)
+        o = fn(q, q, q, *sc())
+        assert maxrel(rt.read(o).reshape(B, -1), O.attention(X, X, X, B, S, dk, causal)) <= tol
+        L.backward(L.sum(L.tensor_mul(o, w)))
+        dQ, dK, dV = O.attention_bwd(X, X, X, W, B, S, dk, causal)
+        assert _shared_grad_err(rt.read(q, grad=True).reshape(B, -1), (dQ, dK, dV)) <= tol
+        # q as Q, kv as K and V
+        q, kv = rt.tensor(X), rt.tensor(KV)
+        o = fn(q, kv, kv, *sc())
+        L.backward(L.sum(L.tensor_mul(o, w)))
+        dQ, dK, dV = O.attention_bwd(X, KV, KV, W, B, S, dk, causal)
+        assert maxrel(rt.read(q, grad=True).reshape(B, -1), dQ) <= tol
+        assert _shared_grad_err(rt.read(kv, grad=True).reshape(B, -1), (dK, dV)) <= tol
+    finally:
+        if bf16:
+            L.dream_disable_fp16()
+
+
 def test_determinism_16(L):
     # tests/16_determinism.dream: bit-exact repeat of matmul, attention and backward
     def run():
