@@ -259,7 +259,8 @@ def test_self_attention_shared_gradient_buffers(L, kind, bf16):
         X, KV, W = (O.bf16_round(a.astype(np.float32)).astype(np.float64) for a in (X, KV, W))
         L.dream_enable_fp16()
     tol = 2e-2 if bf16 else 1e-5 * np.sqrt(S)
-    sc = lambda: [rt.scalar(B), rt.scalar(S), rt.scalar(dk)]  # noqa: E731
+    sc = lambda: ([rt.scalar(B), rt.scalar(S), rt.scalar(dk)]  # noqa: E731
+                  + ([rt.scalar(64)] if kind == "flash" else []))
     try:
         # q as Q, K and V
         q, w = rt.tensor(X), rt.tensor(W)
