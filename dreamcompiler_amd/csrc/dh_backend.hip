@@ -278,6 +278,45 @@ int dh_memcpy_h2d(void* d, const void* h, size_t n) {
 int dh_memcpy_d2h(void* h, const void* d, size_t n) {
     return copy(h, d, n, hipMemcpyDeviceToHost, "dh_memcpy_d2h");
 }
+void* dh_event_create(void) {
+    if (ensure_init() != DH_OK) return nullptr;
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        set_error(DH_ERR_HIP, "dh_event_create: %s", hipGetErrorString(e));
+        return nullptr;
+    }
+    return (void*)ev;
+}
+int dh_event_record(void* ev) {
+    DH_TRY(ensure_init());
+    if (!ev) return set_error(DH_ERR_INVALID, "dh_event_record: null event");
+    hipError_t e = hipEventRecord((hipEvent_t)ev, stream());
+    if (e != hipSuccess) return set_error(DH_ERR_HIP, "dh_event_record: %s", hipGetErrorString(e));
+    return DH_OK;
+}
+int dh_event_wait(void* ev) {
+    DH_TRY(ensure_init());
+    if (!ev) return set_error(DH_ERR_INVALID, "dh_event_wait: null event");
+    hipError_t e = hipEventSynchronize((hipEvent_t)ev);
+    if (e != hipSuccess) return set_error(DH_ERR_HIP, "dh_event_wait: %s", hipGetErrorString(e));
+    return DH_OK;
+}
+int dh_event_destroy(void* ev) {
+    if (!ev) return DH_OK;
+    hipError_t e = hipEventDestroy((hipEvent_t)ev);
+    if (e != hipSuccess) return set_error(DH_ERR_HIP, "dh_event_destroy: %s", hipGetErrorString(e));
+    return DH_OK;
+}
+int dh_memcpy_d2h_async(void* h, const void* d, size_t n) {
+    DH_TRY(ensure_init());
+    if (n == 0) return DH_OK;
+    if (!h || !d) return set_error(DH_ERR_INVALID, "dh_memcpy_d2h_async: null pointer");
+    hipError_t e = hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, stream());
+    if (e != hipSuccess)
+        return set_error(DH_ERR_HIP, "dh_memcpy_d2h_async: %s", hipGetErrorString(e));
+    return DH_OK;
+}
 int dh_memcpy_d2d(void* d, const void* s, size_t n) {
     return copy(d, s, n, hipMemcpyDeviceToDevice, "dh_memcpy_d2d");
 }

@@ -17,6 +17,9 @@
 #include "../../include/dream_rt.h"
 
 #include <algorithm>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
@@ -40,33 +43,104 @@ std::mt19937& rng() {
     return g;
 }
 
-// body(i0, i1) over [0, n) in chunks on up to 16 host threads, for host loops over large
-// tensors whose iterations are independent (each writes only its own elements), so the
-// result does not depend on the split.  Small ranges run inline.  A thread that cannot be
-// created (resource limits) leaves its chunk, and the ones after it, to the calling thread.
+// Host worker threads for par_for, started on first use and kept for the process (creating
+// threads per loop cost 10-50 us each, a large part of the short loops of a training step).
+// A thread that cannot be created leaves the pool smaller; with none the caller does all.
+class HostPool {
+public:
+    static HostPool& get() {
+        static HostPool p;
+        return p;
+    }
+    int workers() const { return (int)th_.size(); }
+    // job(k) for k in [0, nk) on the workers and the calling thread; returns when all ran.
+    template <typename F>
+    void run(size_t nk, const F& job) {
+        std::unique_lock<std::mutex> lk(mu_);
+        job_ = [&job](size_t k) { job(k); };
+        nk_ = nk;
+        next_ = 0;
+        left_ = nk;
+        ++gen_;
+        lk.unlock();
+        cv_.notify_all();
+        work();
+        lk.lock();
+        done_.wait(lk, [&] { return left_ == 0; });
+        job_ = nullptr;
+    }
+
+private:
+    HostPool() {
+        const unsigned hw = std::thread::hardware_concurrency();
+        const unsigned n = std::min(hw ? hw : 1u, 16u) - 1;
+        for (unsigned k = 0; k < n; ++k) {
+            try {
+                th_.emplace_back([this] { loop(); });
+            } catch (const std::system_error&) {
+                break;
+            }
+        }
+    }
+    ~HostPool() {
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto& t : th_) t.join();
+    }
+    void work() {   // take chunks until none is left
+        for (;;) {
+            size_t k;
+            {
+                std::lock_guard<std::mutex> g(mu_);
+                if (next_ >= nk_) return;
+                k = next_++;
+            }
+            job_(k);
+            std::lock_guard<std::mutex> g(mu_);
+            if (--left_ == 0) done_.notify_all();
+        }
+    }
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+                if (stop_) return;
+                seen = gen_;
+            }
+            work();
+        }
+    }
+    std::mutex mu_;
+    std::condition_variable cv_, done_;
+    std::vector<std::thread> th_;
+    std::function<void(size_t)> job_;
+    size_t nk_ = 0, next_ = 0, left_ = 0;
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+};
+
+// body(i0, i1) over [0, n) in chunks on the host pool (up to 16 threads), for host loops
+// over large tensors whose iterations are independent (each writes only its own elements),
+// so the result does not depend on the split.  Small ranges run inline.
 template <typename F>
 void par_for(size_t n, F body) {
-    constexpr size_t kMin = size_t(1) << 20;
-    const unsigned hw = std::thread::hardware_concurrency();
-    const size_t nt = std::min<size_t>({n / kMin, hw ? hw : 1, 16});
-    if (nt <= 1) {
+    constexpr size_t kMin = size_t(1) << 18;
+    const size_t nt = std::min<size_t>(n / kMin, 16);
+    if (nt <= 1 || HostPool::get().workers() == 0) {
         body(size_t(0), n);
         return;
     }
-    std::vector<std::thread> th;
-    th.reserve(nt - 1);
-    const size_t step = (n + nt - 1) / nt;
-    size_t k = 1;
-    for (; k < nt; ++k) {
-        try {
-            th.emplace_back([=] { body(std::min(n, k * step), std::min(n, (k + 1) * step)); });
-        } catch (const std::system_error&) {
-            break;
-        }
-    }
-    body(size_t(0), std::min(n, step));
-    for (; k < nt; ++k) body(std::min(n, k * step), std::min(n, (k + 1) * step));
-    for (auto& x : th) x.join();
+    const size_t chunks = nt * 2;   // a little slack for uneven thread start
+    const size_t step = (n + chunks - 1) / chunks;
+    HostPool::get().run(chunks, [&](size_t k) {
+        const size_t i0 = std::min(n, k * step), i1 = std::min(n, (k + 1) * step);
+        if (i0 < i1) body(i0, i1);
+    });
 }
 
 void rt_error(const char* op, const char* fmt, ...) {
@@ -124,7 +198,10 @@ double* host_buffer(size_t n, bool zero, bool& pinned) {
     pinned = false;
     if (bytes >= PIN_MIN_BYTES && dh_available()) {
         if (void* p = dh_host_alloc(bytes)) {
-            if (zero) std::memset(p, 0, bytes);
+            if (zero) {
+                double* d = static_cast<double*>(p);
+                par_for(n, [=](size_t i0, size_t i1) { std::fill(d + i0, d + i1, 0.0); });
+            }
             pinned = true;
             return static_cast<double*>(p);
         }
@@ -140,9 +217,85 @@ void release_host(double* p, bool pinned) {
 Tensor* new_tensor(int d0, int d1, int d2, int d3, bool zero_data);
 Tensor* alloc_result(int d0, int d1, int d2, int d3);
 
+// ---- transfers ---------------------------------------------------------------------------
+// Every value crossing PCIe in fp32 form goes as fp32 (half the bytes of fp64): fp64 host
+// values are rounded to fp32 on the host threads (the same round-to-nearest-even as the
+// device conversion) into pinned staging memory and uploaded; fp32 device values come home
+// into pinned staging and are widened (exactly) on the host threads.
+struct Stage {   // pinned host staging of n floats from the backend's pool (else plain memory)
+    float* p = nullptr;
+    bool pinned = false;
+    explicit Stage(size_t n) {
+        if (n * sizeof(float) >= PIN_MIN_BYTES) p = static_cast<float*>(dh_host_alloc(n * sizeof(float)));
+        pinned = p != nullptr;
+        if (!p) p = static_cast<float*>(std::malloc(std::max<size_t>(n, 1) * sizeof(float)));
+        if (!p) throw Failure{};
+    }
+    ~Stage() {
+        if (pinned) dh_host_free(p);
+        else std::free(p);
+    }
+    Stage(const Stage&) = delete;
+    Stage& operator=(const Stage&) = delete;
+};
+
+// device fp32 dst[0..n) = (float) host src[0..n)
+void upload_as_f32(float* dst, const double* src, size_t n) {
+    Stage st(n);
+    float* sp = st.p;
+    par_for(n, [=](size_t i0, size_t i1) {
+        for (size_t i = i0; i < i1; ++i) sp[i] = (float)src[i];
+    });
+    need(dh_memcpy_h2d(dst, sp, n * sizeof(float)));
+    need(dh_sync());   // the copy reads the staging memory asynchronously
+}
+
+// Events on the library stream, created once and reused (mark where one copy of several
+// ends, so the host can widen it while the later ones are still in flight).
+void* copy_event(size_t k) {
+    static std::vector<void*> evs;
+    while (evs.size() <= k) {
+        void* e = dh_event_create();
+        if (!e) throw Failure{};
+        evs.push_back(e);
+    }
+    return evs[k];
+}
+
+// host dst[i] = (or +=) (double) src[i] for i in [i0, i1), on the host pool
+void widen(double* dst, const float* src, size_t n, bool add) {
+    if (add) {
+        par_for(n, [=](size_t i0, size_t i1) {
+            for (size_t i = i0; i < i1; ++i) dst[i] += (double)src[i];
+        });
+    } else {
+        par_for(n, [=](size_t i0, size_t i1) {
+            for (size_t i = i0; i < i1; ++i) dst[i] = (double)src[i];
+        });
+    }
+}
+
+// host dst[0..n) = (or +=) (double) device fp32 src[0..n).  The copy comes home in chunks
+// of 32 MB, each widened on the host pool while the next ones are still being copied.
+void download_f32(double* dst, const float* src, size_t n, bool add) {
+    constexpr size_t kChunk = size_t(1) << 23;
+    Stage st(n);
+    const size_t nch = (n + kChunk - 1) / kChunk;
+    for (size_t c = 0; c < nch; ++c) {
+        const size_t off = c * kChunk, len = std::min(kChunk, n - off);
+        need(dh_memcpy_d2h_async(st.p + off, src + off, len * sizeof(float)));
+        need(dh_event_record(copy_event(c)));
+    }
+    for (size_t c = 0; c < nch; ++c) {
+        const size_t off = c * kChunk, len = std::min(kChunk, n - off);
+        need(dh_event_wait(copy_event(c)));
+        widen(dst + off, st.p + off, len, add);
+    }
+}
+
 // ---- device residency ------------------------------------------------------------------
-// fp32 device copy of t->data (t->size values), uploaded (fp64 -> fp32 on the device) only
-// when there is none or `data` changed since (version).
+// fp32 device copy of t->data (t->size values), uploaded only when there is none or `data`
+// changed since (version).
 const float* dev_data(Tensor* t) {
     if (t->dev && t->dev_version == t->version) return t->dev;
     const size_t n = (size_t)t->size;
@@ -150,24 +303,38 @@ const float* dev_data(Tensor* t) {
         t->dev = static_cast<float*>(dh_malloc(n * sizeof(float)));
         if (!t->dev) throw Failure{};
     }
-    Dev tmp(n * sizeof(double));
-    need_buf(tmp);
-    need(dh_memcpy_h2d(tmp.p, t->data, n * sizeof(double)));
-    need(dh_convert(t->dev, DH_F32, tmp.p, DH_F64, n));
+    upload_as_f32(t->dev, t->data, n);
     t->dev_version = t->version;
+    t->dev_exact = 0;
     return t->dev;
+}
+
+// fp64 device copy of t->data for the fp64 elementwise kernels: kept while `version` does
+// not change; rebuilt on the device from the fp32 copy when data is exactly that copy
+// widened (a GPU result), else uploaded.
+const double* dev_data64(Tensor* t) {
+    if (t->dev64 && t->dev64_version == t->version) return t->dev64;
+    const size_t n = (size_t)t->size;
+    if (!t->dev64) {
+        t->dev64 = static_cast<double*>(dh_malloc(n * sizeof(double)));
+        if (!t->dev64) throw Failure{};
+    }
+    if (t->dev && t->dev_version == t->version && t->dev_exact)
+        need(dh_convert(t->dev64, DH_F64, t->dev, DH_F32, n));
+    else
+        need(dh_memcpy_h2d(t->dev64, t->data, n * sizeof(double)));
+    t->dev64_version = t->version;
+    return t->dev64;
 }
 
 // A device fp32 result holding t's values becomes t's device copy, and is copied home.
 void adopt_result(Tensor* t, Dev& d) {
     const size_t n = (size_t)t->size;
-    Dev tmp(n * sizeof(double));
-    need_buf(tmp);
-    need(dh_convert(tmp.p, DH_F64, d.p, DH_F32, n));
-    need(dh_memcpy_d2h(t->data, tmp.p, n * sizeof(double)));
+    download_f32(t->data, d.f(), n, false);
     if (t->dev) dh_free(t->dev);
     t->dev = static_cast<float*>(d.release());
     t->dev_version = t->version;
+    t->dev_exact = 1;
 }
 
 // bf16 operand built on the device from the fp32 copy (round to nearest even, the rule of
@@ -188,55 +355,92 @@ float* dgrad(Tensor* t) {
 }
 
 // The complete incoming gradient of node t for a GPU backward op (every consumer of t has
-// run): host contributions move into t->dgrad, which holds the whole gradient until
-// backward() adds it into the host grad.
-float* grad_in(Tensor* t) {
-    float* g = dgrad(t);
-    if (!t->grad_zero) {
+// run), as a device fp32 buffer.  t->dgrad holds only device contributions and the host part
+// stays in t->grad (fp64, as the reference keeps it); when there is a host part it is
+// uploaded and, if t->dgrad exists too, added to a copy of it, and the final flush adds
+// t->dgrad into the host part.  An op that rewrites the gradient in place (linear_relu's
+// mask, which the reference applies to the node's own gradient) gets t->dgrad holding the
+// whole gradient instead: the host part is moved over and cleared, and the flush writes the
+// rewritten values back.
+struct GradIn {
+    Dev tmp{0};
+    float* p = nullptr;
+    GradIn(Tensor* t, bool in_place) {
         const size_t n = (size_t)t->size;
-        Dev h(n * sizeof(double)), f(n * sizeof(float));
-        need_buf(h);
+        if (t->grad_zero) {
+            p = dgrad(t);
+            return;
+        }
+        if (in_place) {
+            p = dgrad(t);
+            Dev f(n * sizeof(float));
+            need_buf(f);
+            upload_as_f32(f.f(), t->grad, n);
+            need(dh_axpy(p, f.f(), 1.f, n));
+            double* hg = t->grad;
+            par_for(n, [=](size_t i0, size_t i1) { std::fill(hg + i0, hg + i1, 0.0); });
+            t->grad_zero = 1;
+            return;
+        }
+        Dev f(n * sizeof(float));
         need_buf(f);
-        need(dh_memcpy_h2d(h.p, t->grad, n * sizeof(double)));
-        need(dh_convert(f.p, DH_F32, h.p, DH_F64, n));
-        need(dh_axpy(g, f.f(), 1.f, n));
-        need(dh_sync());   // a pinned source is read asynchronously: finish before clearing it
-        std::fill(t->grad, t->grad + n, 0.0);
-        t->grad_zero = 1;
+        upload_as_f32(f.f(), t->grad, n);
+        if (t->dgrad) need(dh_axpy(f.f(), t->dgrad, 1.f, n));
+        p = f.f();
+        std::swap(tmp.p, f.p);
     }
-    return g;
-}
+};
 
 // Host grad += device grad, and the device grad is released (also makes t->grad complete for
 // a host backward op).
 void flush_dgrad(Tensor* t) {
     if (!t->dgrad) return;
-    const size_t n = (size_t)t->size;
-    if (t->grad_zero) {
-        // host grad all zero: the device gradient, widened to fp64 on the device, is the result
-        Dev d(n * sizeof(double));
-        need_buf(d);
-        need(dh_convert(d.p, DH_F64, t->dgrad, DH_F32, n));
-        need(dh_memcpy_d2h(t->grad, d.p, n * sizeof(double)));
-    } else {
-        std::vector<float> h(n);
-        need(dh_memcpy_d2h(h.data(), t->dgrad, n * sizeof(float)));
-        double* g = t->grad;
-        const float* hp = h.data();
-        par_for(n, [=](size_t i0, size_t i1) {
-            for (size_t i = i0; i < i1; ++i) g[i] += (double)hp[i];
-        });
-    }
+    // host grad all zero: the widened device gradient is the result, else it is added
+    download_f32(t->grad, t->dgrad, (size_t)t->size, !t->grad_zero);
     dh_free(t->dgrad);
     t->dgrad = nullptr;
     t->grad_zero = 0;
+}
+
+// flush_dgrad for every tensor of `order` holding a device gradient: all copies queued
+// into one pinned staging buffer, each tensor widened (or added) on the host pool as soon as
+// its own copy has landed, while the later copies are still in flight.
+void flush_all(const std::vector<Tensor*>& order) {
+    std::vector<Tensor*> fl;
+    size_t total = 0;
+    for (Tensor* t : order)
+        if (t->dgrad) {
+            fl.push_back(t);
+            total += (size_t)t->size;
+        }
+    if (fl.empty()) return;
+    Stage st(total);
+    size_t off = 0;
+    for (size_t k = 0; k < fl.size(); ++k) {
+        need(dh_memcpy_d2h_async(st.p + off, fl[k]->dgrad, (size_t)fl[k]->size * sizeof(float)));
+        need(dh_event_record(copy_event(k)));
+        off += (size_t)fl[k]->size;
+    }
+    off = 0;
+    for (size_t k = 0; k < fl.size(); ++k) {
+        Tensor* t = fl[k];
+        const size_t n = (size_t)t->size;
+        need(dh_event_wait(copy_event(k)));
+        widen(t->grad, st.p + off, n, !t->grad_zero);
+        off += n;
+        dh_free(t->dgrad);
+        t->dgrad = nullptr;
+        t->grad_zero = 0;
+    }
 }
 
 void drop_device(Tensor* t) {
     if (t->dev) dh_free(t->dev);
     if (t->dgrad) dh_free(t->dgrad);
     if (t->dlse) dh_free(t->dlse);
+    if (t->dev64) dh_free(t->dev64);
     t->dev = t->dgrad = t->dlse = nullptr;
+    t->dev64 = nullptr;
 }
 
 void set_graph(Tensor* c, Tensor* l, Tensor* r, int op) {
@@ -414,7 +618,8 @@ void attention_backward(Tensor* t, bool causal) {
     const float scale = (float)(1.0 / std::sqrt((double)dk));
     if (Dp == dk) {
         // dO, O, Q, K, V as device copies; dQ, dK, dV accumulate into the device gradients.
-        float* g = grad_in(t);
+        GradIn gi(t, false);
+        const float* g = gi.p;
         if (dt == DH_F32) {
             need(dh_flash_bwd(dt, B, S, dk, scale, causal ? 1 : 0, dev_data(Q), dev_data(K),
                               dev_data(V), dev_data(t), g, t->dlse, dgrad(Q), dgrad(K), dgrad(V),
@@ -476,7 +681,8 @@ void matmul_backward(Tensor* t) {
         add_grad_f64(B, db, kn);
         return;
     }
-    const float* dy = grad_in(t);
+    GradIn gi(t, false);
+    const float* dy = gi.p;
     need(dh_gemm_f32(0, 1, M, K, N, dy, N, dev_data(B), N, 1.f, dgrad(A), K));
     need(dh_gemm_f32(1, 0, K, N, M, dev_data(A), K, dy, N, 1.f, dgrad(B), N));
 }
@@ -486,7 +692,8 @@ void linear_backward(Tensor* t, bool relu) {
     // dX += dY W (NN); dW += dY^T X (TN).
     Tensor *x = t->parents[0], *W = t->parents[1], *b = t->parents[2];
     const int N = x->d0, in = x->d1, out = W->d0;
-    float* dy = grad_in(t);
+    GradIn gi(t, relu);   // linear_relu masks its node's gradient in place
+    float* dy = gi.p;
     need(dh_linear_bias_grad(relu ? dev_data(t) : nullptr, dy, dgrad(b), N, out, relu ? 1 : 0, 1));
     need(dh_gemm_f32(0, 0, N, in, out, dy, out, dev_data(W), in, 1.f, dgrad(x), in));
     need(dh_gemm_f32(1, 0, out, in, N, dy, out, dev_data(x), in, 1.f, dgrad(W), in));
@@ -496,7 +703,8 @@ void bmm_backward(Tensor* t) {
     // autograd.inc:549-574: gA += G B^T, gB += A^T G per batch member.
     Tensor *a = t->lhs, *b = t->rhs;
     const int Bt = t->bmm_B, M = t->bmm_M, K = t->bmm_K, N = t->bmm_N;
-    const float* g = grad_in(t);
+    GradIn gi(t, false);
+    const float* g = gi.p;
     need(dh_gemm_f32_ex(0, 1, M, K, N, g, N, (long long)M * N, dev_data(b), N, (long long)K * N,
                         1.f, dgrad(a), K, (long long)M * K, Bt, nullptr, 0));
     need(dh_gemm_f32_ex(1, 0, K, N, M, dev_data(a), K, (long long)M * K, g, N, (long long)M * N,
@@ -519,7 +727,8 @@ void row_backward(Tensor* t) {
     Tensor* x = t->lhs;
     int R, C;
     row_shape(x, t->op, R, C);
-    const float* g = grad_in(t);
+    GradIn gi(t, false);
+    const float* g = gi.p;
     if (t->op == DREAM_OP_LAYER_NORM)
         need(dh_layer_norm_bwd(dev_data(x), dev_data(t), g, dgrad(x), R, C, 1));
     else
@@ -576,7 +785,8 @@ void conv_backward(Tensor* t) {
     const ConvDims d = conv_dims(t);
     Tensor *x = t->lhs, *k = t->rhs;
     const size_t K = d.K(), NP = (size_t)d.N * d.P();
-    const float* go = grad_in(t);
+    GradIn gi(t, false);
+    const float* go = gi.p;
     need(dh_conv2d_bwd_filter(go, dev_data(x), dgrad(k), d.N, d.Cin, d.H, d.W, d.Cout, d.KH,
                               d.KW, d.pad, d.stride, 1));
     if (d.stride == 1 && d.pad <= d.KH - 1 && d.pad <= d.KW - 1) {
@@ -931,6 +1141,14 @@ static void keep_dev32(Tensor* c, Dev& d32) {
     if (c->dev) dh_free(c->dev);
     c->dev = static_cast<float*>(d32.release());
     c->dev_version = c->version;
+    c->dev_exact = 0;
+}
+
+// ... and the fp64 result itself its fp64 device copy.
+static void keep_dev64(Tensor* c, Dev& d64) {
+    if (c->dev64) dh_free(c->dev64);
+    c->dev64 = static_cast<double*>(d64.release());
+    c->dev64_version = c->version;
 }
 
 // c = op(a, b) over c's dims; false (error printed) when the shapes do not broadcast or the
@@ -947,6 +1165,21 @@ static bool elementwise_binary(const char* name, int op, Tensor* a, Tensor* b, T
     }
     const long long n = c->size;
     if (n <= elemwise_cpu_max()) {
+        // Operands of C's own shape (index i) or single values (index 0) need no index
+        // decomposition: the same elements as the general loop below.
+        auto whole = [&](const Tensor* x) {
+            return x->d0 == cd[0] && x->d1 == cd[1] && x->d2 == cd[2] && x->d3 == cd[3];
+        };
+        if ((whole(a) || a->size == 1) && (whole(b) || b->size == 1)) {
+            const double *ad = a->data, *bd = b->data;
+            const size_t sa = a->size == 1 && !whole(a) ? 0 : 1;
+            const size_t sb = b->size == 1 && !whole(b) ? 0 : 1;
+            double* cdat = c->data;
+            par_for((size_t)n, [=](size_t i0, size_t i1) {
+                for (size_t i = i0; i < i1; ++i) cdat[i] = host_bin(op, ad[i * sa], bd[i * sb]);
+            });
+            return true;
+        }
         for (long long i = 0; i < n; ++i) {
             long long r = i, ia = 0, ib = 0;
             for (int k = 3; k >= 0; --k) {
@@ -961,14 +1194,15 @@ static bool elementwise_binary(const char* name, int op, Tensor* a, Tensor* b, T
     }
     if (!hip_ready(name)) return false;
     try {
-        Dev da((size_t)a->size * 8), db((size_t)b->size * 8), dc((size_t)n * 8), d32((size_t)n * 4);
-        need_buf(da), need_buf(db), need_buf(dc), need_buf(d32);
-        need(dh_memcpy_h2d(da.p, a->data, (size_t)a->size * 8));
-        need(dh_memcpy_h2d(db.p, b->data, (size_t)b->size * 8));
-        need(dh_binary(op, DH_F64, da.p, (size_t)a->size, as, db.p, (size_t)b->size, bs, dc.p, cd,
+        Dev dc((size_t)n * 8), d32((size_t)n * 4);
+        need_buf(dc), need_buf(d32);
+        const double* da = dev_data64(a);
+        const double* db = dev_data64(b);
+        need(dh_binary(op, DH_F64, da, (size_t)a->size, as, db, (size_t)b->size, bs, dc.p, cd,
                        d32.f()));
         need(dh_memcpy_d2h(c->data, dc.p, (size_t)n * 8));
         keep_dev32(c, d32);
+        keep_dev64(c, dc);
     } catch (const Failure&) {
         rt_error(name, "%s", dh_last_error());
         return false;
@@ -979,17 +1213,21 @@ static bool elementwise_binary(const char* name, int op, Tensor* a, Tensor* b, T
 static bool elementwise_unary(const char* name, int op, Tensor* a, Tensor* c, double lo, double hi) {
     const long long n = a->size;
     if (n <= elemwise_cpu_max()) {
-        for (long long i = 0; i < n; ++i) c->data[i] = host_un(op, a->data[i], lo, hi);
+        const double* ad = a->data;
+        double* cdat = c->data;
+        par_for((size_t)n, [=](size_t i0, size_t i1) {
+            for (size_t i = i0; i < i1; ++i) cdat[i] = host_un(op, ad[i], lo, hi);
+        });
         return true;
     }
     if (!hip_ready(name)) return false;
     try {
-        Dev da((size_t)n * 8), dc((size_t)n * 8), d32((size_t)n * 4);
-        need_buf(da), need_buf(dc), need_buf(d32);
-        need(dh_memcpy_h2d(da.p, a->data, (size_t)n * 8));
-        need(dh_unary(op, DH_F64, da.p, dc.p, (size_t)n, lo, hi, d32.f()));
+        Dev dc((size_t)n * 8), d32((size_t)n * 4);
+        need_buf(dc), need_buf(d32);
+        need(dh_unary(op, DH_F64, dev_data64(a), dc.p, (size_t)n, lo, hi, d32.f()));
         need(dh_memcpy_d2h(c->data, dc.p, (size_t)n * 8));
         keep_dev32(c, d32);
+        keep_dev64(c, dc);
     } catch (const Failure&) {
         rt_error(name, "%s", dh_last_error());
         return false;
@@ -1101,7 +1339,10 @@ Tensor* zero_grad(Tensor* t) {
         rt_error("zero_grad", "tensor is null");
         return nullptr;
     }
-    if (!t->grad_zero) std::fill(t->grad, t->grad + t->size, 0.0);   // else already all zero
+    if (!t->grad_zero) {   // else already all zero
+        double* g = t->grad;
+        par_for((size_t)t->size, [=](size_t i0, size_t i1) { std::fill(g + i0, g + i1, 0.0); });
+    }
     if (t->dgrad) dh_free(t->dgrad);
     t->dgrad = nullptr;
     t->grad_zero = 1;
@@ -1439,6 +1680,23 @@ Tensor* backward(Tensor* root) {
         if (t->lhs) t->lhs->grad_zero = 0;
         if (t->rhs) t->rhs->grad_zero = 0;
     };
+    // DREAM_TRACE_BACKWARD=1: each node's op code, size and time (device work waited for)
+    // on stderr.
+    static const bool trace = [] {
+        const char* e = std::getenv("DREAM_TRACE_BACKWARD");
+        return e && *e && *e != '0';
+    }();
+    auto now = [] { return std::chrono::steady_clock::now(); };
+    auto t_last = now();
+    auto stamp = [&](const char* what, int op, int size) {
+        if (!trace) return;
+        if (dh_available()) dh_sync();
+        const auto t1 = now();
+        std::fprintf(stderr, "[backward] %-8s op %2d size %9d  %8.3f ms\n", what, op, size,
+                     std::chrono::duration<double, std::milli>(t1 - t_last).count());
+        t_last = t1;
+    };
+    stamp("start", 0, root->size);
     for (int x = (int)order.size() - 1; x >= 0; --x) {
         Tensor* t = order[x];
         try {
@@ -1532,13 +1790,21 @@ Tensor* backward(Tensor* root) {
         } catch (const Failure&) {
             rt_error("backward", "%s", dh_last_error());
         }
+        stamp("node", t->op, t->size);
     }
-    // Every gradient back on the host (the reference's grad buffers are host memory).
-    for (Tensor* t : order) {
-        try {
-            flush_dgrad(t);
-        } catch (const Failure&) {
-            rt_error("backward", "%s", dh_last_error());
+    // Every gradient back on the host (the reference's grad buffers are host memory): all
+    // device gradients queued home into one pinned staging buffer, one wait, then widened
+    // (or added) on the host threads.
+    try {
+        flush_all(order);
+        stamp("flush", -1, 0);
+    } catch (const Failure&) {
+        rt_error("backward", "%s", dh_last_error());
+        for (Tensor* t : order) {
+            try {
+                flush_dgrad(t);
+            } catch (const Failure&) {
+            }
         }
     }
     return create_scalar(1.0);

@@ -39,6 +39,11 @@ _SIGS = {
     "dh_host_free": (_i, [_vp]),
     "dh_memcpy_h2d": (_i, [_vp, _vp, _sz]),
     "dh_memcpy_d2h": (_i, [_vp, _vp, _sz]),
+    "dh_memcpy_d2h_async": (_i, [_vp, _vp, _sz]),
+    "dh_event_create": (_vp, []),
+    "dh_event_record": (_i, [_vp]),
+    "dh_event_wait": (_i, [_vp]),
+    "dh_event_destroy": (_i, [_vp]),
     "dh_memcpy_d2d": (_i, [_vp, _vp, _sz]),
     "dh_memset": (_i, [_vp, _i, _sz]),
     "dh_sync": (_i, []),

@@ -76,7 +76,11 @@ int dh_pool_release(void);
 void* dh_host_alloc(size_t bytes);
 int dh_host_free(void* h_ptr);
 int dh_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes);
-int dh_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes);
+int dh_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes);   /* returns when the data is home */
+/* D2H copy queued on the stream without waiting (HostBuf's download, gpu.inc:177-196, made
+ * asynchronous): the data is home after the next dh_sync.  Several of them into one pinned
+ * buffer cost one wait instead of one each. */
+int dh_memcpy_d2h_async(void* h_dst, const void* d_src, size_t bytes);
 int dh_memcpy_d2d(void* d_dst, const void* d_src, size_t bytes);
 int dh_memset(void* d_dst, int value, size_t bytes);
 int dh_sync(void);                         /* synchronous: waits for the stream */
@@ -86,6 +90,13 @@ int dh_set_stream(void* hip_stream);       /* NULL restores the library stream  
 /* ---- timing on the library stream ----------------------------------------- */
 int dh_timer_start(void);
 int dh_timer_stop(float* ms);              /* synchronous */
+/* Events on the library stream, so a host thread can wait for part of the queued work (one
+ * copy of several) instead of all of it: the copies home of a backward overlap the host's
+ * widening of the ones already landed. */
+void* dh_event_create(void);               /* NULL on failure (dh_last_error) */
+int dh_event_record(void* event);          /* marks the work queued so far */
+int dh_event_wait(void* event);            /* host waits until that work is done */
+int dh_event_destroy(void* event);
 
 /* ---- conversions (replaces HostBuf fromDouble/toDouble, gpu.inc:177-196) ----
  * dst[i] = convert(src[i]) for n elements.  Supported pairs: F64->F32, F32->F64,

@@ -60,6 +60,10 @@ typedef struct Tensor {
     int f64_node;              /* 1: the node's forward ran in fp64 (below the GPU
                                 * threshold), so its backward does too               */
     double keep;               /* dropout nodes: the keep rate (bwd_name)            */
+    int dev_exact;             /* 1: data is exactly the widened `dev` (a GPU result), so
+                                * the fp64 values can be rebuilt on the device from it  */
+    double* dev64;             /* device fp64 copy of data (elementwise operands), or NULL */
+    int dev64_version;
 } Tensor;
 
 enum {
