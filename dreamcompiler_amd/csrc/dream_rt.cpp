@@ -17,6 +17,7 @@
 #include "../../include/dream_rt.h"
 
 #include <algorithm>
+#include <atomic>
 #include <condition_variable>
 #include <functional>
 #include <mutex>
@@ -54,23 +55,27 @@ public:
     }
     int workers() const { return (int)th_.size(); }
     // job(k) for k in [0, nk) on the workers and the calling thread; returns when all ran.
+    // The job state is guarded by mu_, so a worker that wakes late simply finds no chunk left
+    // (or helps with the next job).  Not reentrant: a job must not call run() itself.
     template <typename F>
     void run(size_t nk, const F& job) {
-        std::unique_lock<std::mutex> lk(mu_);
-        job_ = [&job](size_t k) { job(k); };
-        nk_ = nk;
-        next_ = 0;
-        left_ = nk;
-        ++gen_;
-        lk.unlock();
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            job_ = [&job](size_t k) { job(k); };
+            nk_ = nk;
+            next_ = 0;
+            left_.store(nk, std::memory_order_relaxed);
+            gen_.fetch_add(1, std::memory_order_release);
+        }
         cv_.notify_all();
         work();
-        lk.lock();
-        done_.wait(lk, [&] { return left_ == 0; });
+        while (left_.load(std::memory_order_acquire) != 0) cpu_relax();
+        std::lock_guard<std::mutex> g(mu_);
         job_ = nullptr;
     }
 
 private:
+    static void cpu_relax() { __builtin_ia32_pause(); }
     HostPool() {
         const unsigned hw = std::thread::hardware_concurrency();
         const unsigned n = std::min(hw ? hw : 1u, 16u) - 1;
@@ -86,41 +91,54 @@ private:
         {
             std::lock_guard<std::mutex> g(mu_);
             stop_ = true;
+            gen_.fetch_add(1, std::memory_order_release);
         }
         cv_.notify_all();
         for (auto& t : th_) t.join();
     }
-    void work() {   // take chunks until none is left
+    void work() {   // claim chunks until none is left
         for (;;) {
+            std::function<void(size_t)>* job;
             size_t k;
             {
                 std::lock_guard<std::mutex> g(mu_);
                 if (next_ >= nk_) return;
                 k = next_++;
+                job = &job_;
             }
-            job_(k);
-            std::lock_guard<std::mutex> g(mu_);
-            if (--left_ == 0) done_.notify_all();
+            (*job)(k);   // job_ stays set until every claimed chunk is done (left_ == 0)
+            left_.fetch_sub(1, std::memory_order_acq_rel);
         }
     }
     void loop() {
         uint64_t seen = 0;
         for (;;) {
+            // A training step issues many short loops back to back: spin for ~100 us before
+            // sleeping, so the next one does not wait for a wake-up.
+            const auto t0 = std::chrono::steady_clock::now();
+            for (int it = 0; gen_.load(std::memory_order_acquire) == seen; ++it) {
+                cpu_relax();
+                if ((it & 255) == 255 &&
+                    std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(100)) {
+                    std::unique_lock<std::mutex> lk(mu_);
+                    cv_.wait(lk, [&] { return gen_.load(std::memory_order_acquire) != seen; });
+                }
+            }
+            seen = gen_.load(std::memory_order_acquire);
             {
-                std::unique_lock<std::mutex> lk(mu_);
-                cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+                std::lock_guard<std::mutex> g(mu_);
                 if (stop_) return;
-                seen = gen_;
             }
             work();
         }
     }
     std::mutex mu_;
-    std::condition_variable cv_, done_;
+    std::condition_variable cv_;
     std::vector<std::thread> th_;
     std::function<void(size_t)> job_;
-    size_t nk_ = 0, next_ = 0, left_ = 0;
-    uint64_t gen_ = 0;
+    size_t nk_ = 0, next_ = 0;
+    std::atomic<size_t> left_{0};
+    std::atomic<uint64_t> gen_{0};
     bool stop_ = false;
 };
 
@@ -151,6 +169,24 @@ void rt_error(const char* op, const char* fmt, ...) {
     va_end(ap);
     std::fprintf(stderr, "\n");
     std::fflush(stderr);
+}
+
+// DREAM_TRACE=1: host-side time between trace points inside the builtins, on stderr (where
+// the time of a builtin goes besides its kernels and copies).
+bool trace_on() {
+    static const bool on = [] {
+        const char* e = std::getenv("DREAM_TRACE");
+        return e && *e && *e != '0';
+    }();
+    return on;
+}
+void tpoint(const char* what) {
+    if (!trace_on()) return;
+    static auto last = std::chrono::steady_clock::now();
+    const auto now = std::chrono::steady_clock::now();
+    std::fprintf(stderr, "[trace] %-24s %9.1f us\n", what,
+                 std::chrono::duration<double, std::micro>(now - last).count());
+    last = now;
 }
 
 // Device buffer from the backend pool, returned on scope exit unless released.
@@ -226,7 +262,9 @@ struct Stage {   // pinned host staging of n floats from the backend's pool (els
     float* p = nullptr;
     bool pinned = false;
     explicit Stage(size_t n) {
-        if (n * sizeof(float) >= PIN_MIN_BYTES) p = static_cast<float*>(dh_host_alloc(n * sizeof(float)));
+        // pinned at every size: a copy to or from pageable memory is staged synchronously by
+        // the HIP runtime (~0.1 ms even for a few KB)
+        p = static_cast<float*>(dh_host_alloc(std::max<size_t>(n, 1) * sizeof(float)));
         pinned = p != nullptr;
         if (!p) p = static_cast<float*>(std::malloc(std::max<size_t>(n, 1) * sizeof(float)));
         if (!p) throw Failure{};
@@ -279,17 +317,22 @@ void widen(double* dst, const float* src, size_t n, bool add) {
 // of 32 MB, each widened on the host pool while the next ones are still being copied.
 void download_f32(double* dst, const float* src, size_t n, bool add) {
     constexpr size_t kChunk = size_t(1) << 23;
+    tpoint("download: entry");
     Stage st(n);
+    tpoint("download: stage");
     const size_t nch = (n + kChunk - 1) / kChunk;
     for (size_t c = 0; c < nch; ++c) {
         const size_t off = c * kChunk, len = std::min(kChunk, n - off);
         need(dh_memcpy_d2h_async(st.p + off, src + off, len * sizeof(float)));
         need(dh_event_record(copy_event(c)));
     }
+    tpoint("download: queued");
     for (size_t c = 0; c < nch; ++c) {
         const size_t off = c * kChunk, len = std::min(kChunk, n - off);
         need(dh_event_wait(copy_event(c)));
+        tpoint("download: waited");
         widen(dst + off, st.p + off, len, add);
+        tpoint("download: widened");
     }
 }
 
@@ -949,7 +992,9 @@ Tensor* new_tensor(int d0, int d1, int d2, int d3, bool zero_data) {
     Tensor* t = (Tensor*)std::calloc(1, sizeof(Tensor));
     bool pd, pg;
     t->data = host_buffer(size, zero_data, pd);
+    tpoint("new_tensor: data");
     t->grad = host_buffer(size, true, pg);
+    tpoint("new_tensor: grad");
     t->host_pinned = (pd ? 1 : 0) | (pg ? 2 : 0);
     t->size = size;
     t->d0 = d0;
@@ -1536,7 +1581,9 @@ static Tensor* linear_impl(Tensor* x, Tensor* W, Tensor* b, bool relu) {
         return alloc_tensor(1, 1, 1, 1);
     }
     if (!hip_ready("linear")) return alloc_tensor(1, 1, 1, 1);
+    tpoint("linear: entry");
     Tensor* y = alloc_result(N, out, 1, 1);
+    tpoint("linear: alloc");
     set_graph(y, x, W, relu ? DREAM_OP_LINEAR_RELU : DREAM_OP_LINEAR);
     set_parents(y, x, W, b);
     try {
@@ -1544,7 +1591,9 @@ static Tensor* linear_impl(Tensor* x, Tensor* W, Tensor* b, bool relu) {
         need_buf(d);
         need(dh_gemm_f32_ex(0, 1, N, out, in, dev_data(x), in, 0, dev_data(W), in, 0, 0.f, d.f(),
                             out, 0, 1, dev_data(b), relu ? DH_EPI_RELU : 0));
+        tpoint("linear: launched");
         adopt_result(y, d);
+        tpoint("linear: adopted");
     } catch (const Failure&) {
         rt_error("linear", "%s", dh_last_error());
         tensor_decref(y);

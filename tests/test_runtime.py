@@ -82,3 +82,23 @@ def test_dropout_matches_reference_build():
     assert 0.7 < kept.mean() < 0.9
     # x / keep (the -ffast-math build may form it as x * (1 / keep): one rounding apart)
     assert np.allclose(d_ref[kept], X[kept] / np.float64(np.float32(0.8)), rtol=4e-16, atol=0)
+
+
+def test_host_pool_loops_match_numpy():
+    """Host elementwise loops large enough to run on the runtime's worker pool (same-shape,
+    scalar and broadcast operands, and a unary op), many times in a row: every element as
+    numpy computes it (the split over threads cannot change any value)."""
+    L = rt.load()
+    rng = np.random.default_rng(7)
+    A, B = rng.standard_normal((1500, 2000)), rng.standard_normal((1500, 2000))
+    row, s = rng.standard_normal((1, 2000)), np.array([[2.5]])
+    a, b, r, sc = rt.tensor(A), rt.tensor(B), rt.tensor(row), rt.tensor(s)
+    for _ in range(20):
+        for x, y, ref in ((a, b, A * B), (a, sc, A * 2.5), (a, r, A * row)):
+            c = L.tensor_mul(x, y)
+            assert np.array_equal(rt.read(c), ref)
+            rt.release(c)
+        c = L.dream_exp(a)
+        assert np.allclose(rt.read(c), np.exp(A), rtol=4e-16, atol=0)
+        rt.release(c)
+    rt.release(a, b, r, sc)
