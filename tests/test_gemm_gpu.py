@@ -270,3 +270,215 @@ def test_bf16_fast_path_knob_variants(env):
                        capture_output=True, text=True, timeout=110)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.count("variant") == 16, r.stdout
+
+def _ex(dtype, ta, tb, Bt, M, N, K, beta=0.0, bias=True, relu=False, share=None, seed=0,
+        row_bias=False):
+    """Run dh_gemm_*_ex on random inputs; returns (got, ref) as (Bt, M, N) arrays."""
+    rng = np.random.default_rng(seed)
+    shA = (K, M) if ta else (M, K)
+    shB = (N, K) if tb else (K, N)
+    A = rng.standard_normal((1 if share == "A" else Bt,) + shA).astype(np.float32)
+    B = rng.standard_normal((1 if share == "B" else Bt,) + shB).astype(np.float32)
+    C0 = rng.standard_normal((Bt, M, N)).astype(np.float32)
+    b = rng.standard_normal(M if row_bias else N).astype(np.float32) if bias else None
+    if dtype == "bf16":
+        A, B = bf16_bits(A), bf16_bits(B)
+        A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    else:
+        A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    opA = np.swapaxes(A64, 1, 2) if ta else A64
+    opB = np.swapaxes(B64, 1, 2) if tb else B64
+    ref = np.matmul(opA, opB) + beta * C0.astype(np.float64)
+    if bias:
+        ref = ref + (b.astype(np.float64)[:, None] if row_bias else b.astype(np.float64))
+    if relu:
+        ref = np.maximum(ref, 0.0)
+    DB = hip.DeviceBuffer
+    dA, dB, dC = DB.from_numpy(A), DB.from_numpy(B), DB.from_numpy(C0)
+    dbias = DB.from_numpy(b) if bias else None
+    sA = 0 if share == "A" else shA[0] * shA[1]
+    sB = 0 if share == "B" else shB[0] * shB[1]
+    hip.gemm_ex(dtype, ta, tb, M, N, K, dA, shA[1], sA, dB, shB[1], sB, beta, dC, N, M * N, Bt,
+                dbias, relu, row_bias)
+    got = dC.numpy()
+    for x in (dA, dB, dC, dbias):
+        if x is not None:
+            x.free()
+    return got, ref
+
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("relu", [False, True])
+def test_gemm_ex_batched_bias_relu(dtype, ta, tb, relu):
+    Bt, M, N, K = 3, 70, 50, 33
+    got, ref = _ex(dtype, ta, tb, Bt, M, N, K, beta=0.5, relu=relu, seed=ta + 2 * tb + 4 * relu)
+    tol = (1e-5 * np.sqrt(K)) if dtype == "f32" else 2e-2
+    assert maxrel(got, ref) <= tol
+
+
+@pytest.mark.parametrize("share", ["A", "B"])
+def test_gemm_ex_shared_operand(share):
+    got, ref = _ex("f32", 0, 0, 4, 40, 36, 20, share=share, seed=7)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(20)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1)])
+@pytest.mark.parametrize("relu", [False, True])
+def test_gemm_ex_bf16_fast_path_batched(ta, tb, relu):
+    # 16 members of 1024 x 1024 = 256 tiles of 256 x 256: the direct-to-LDS fast path with
+    # gridDim.y batches, the bias / ReLU epilogue form.
+    Bt, M, N, K = 16, 1024, 1024, 64
+    got, ref = _ex("bf16", ta, tb, Bt, M, N, K, relu=relu, seed=40 + ta + 2 * relu)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)      # exact bf16 products, fp32 sums
+
+
+def test_gemm_ex_rejects_overlapping_batches():
+    DB = hip.DeviceBuffer
+    a, b, c = DB(4 * 64), DB(4 * 64), DB(4 * 64)
+    with pytest.raises(hip.DreamHipError):
+        hip.gemm_ex("f32", 0, 0, 4, 4, 4, a, 4, 16, b, 4, 16, 0.0, c, 4, 8, 2)
+    with pytest.raises(hip.DreamHipError):
+        hip.gemm_ex("bf16", 0, 0, 4, 4, 4, a, 4, -16, b, 4, 16, 0.0, c, 4, 16, 2)
+
+
+def test_linear_reference_golden_vectors():
+    # Y = X W^T + b (NT with the bias epilogue), and with ReLU, against the reference build's
+    # own dream_linear / dream_linear_relu outputs.
+    import os
+    G = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
+    X, W, b = (G["linear_" + c].astype(np.float32) for c in "XWb")
+    N_, K_ = X.shape
+    O_ = W.shape[0]
+    DB = hip.DeviceBuffer
+    for relu, key in ((False, "linear_Y"), (True, "linear_relu_Y")):
+        dX, dW, db, dY = DB.from_numpy(X), DB.from_numpy(W), DB.from_numpy(b.ravel()), \
+            DB.empty((N_, O_), np.float32)
+        hip.gemm_ex("f32", 0, 1, N_, O_, K_, dX, K_, 0, dW, K_, 0, 0.0, dY, O_, 0, 1, db, relu)
+        assert maxrel(dY.numpy(), G[key]) <= 1e-5 * np.sqrt(K_)
+
+
+@pytest.mark.parametrize("M,N,K", [(40, 33, 5000), (300, 200, 2048), (784, 257, 4096), (257, 10, 4096)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_fp32_split_k_skinny_long_k(M, N, K, ta, tb):
+    # Few output tiles and a long contraction take the split-K path (K chunks as gridDim.y
+    # members, a ragged last chunk of its own, an ordered reduction with beta / bias / ReLU).
+    got, ref = _ex("f32", ta, tb, 1, M, N, K, beta=0.5, relu=bool(ta), seed=M + K + ta)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_fp32_split_k_bit_identical_reruns():
+    a, _ = _ex("f32", 1, 0, 1, 784, 257, 4096, seed=3)
+    b, _ = _ex("f32", 1, 0, 1, 784, 257, 4096, seed=3)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("Bt,M,N,K", [(3, 40, 300, 70), (2, 300, 50, 129), (1, 64, 4096, 576),
+                                      (1, 4096, 10, 784), (4, 1, 513, 33), (1, 64, 40000, 40),
+                                      (1, 40000, 48, 40)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("row_bias", [False, True])
+def test_fp32_narrow_tiles(Bt, M, N, K, ta, tb, row_bias):
+    # M <= 64 takes 64 x 256 work-group tiles, N <= 64 256 x 64 -- or 64 x 64 when those grids
+    # are small (the first five shapes); the last two keep the wide tiles.  Batched, split-K
+    # and the epilogue with either bias orientation go through the same shapes.
+    got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.25, relu=row_bias, row_bias=row_bias,
+                   seed=M + N + K + ta + 2 * tb)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+@pytest.mark.parametrize("Bt,M,N,K", [(1, 1024, 1024, 1024), (1, 1000, 777, 100), (2, 520, 700, 33),
+                                      (1, 4096, 257, 784), (1, 700, 900, 7), (1, 784, 257, 4096),
+                                      (1, 300, 200, 2048)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_fp32_64x64_tiles(Bt, M, N, K, ta, tb):
+    # Products whose 128 x 128 grid is under one tile per CU run on 64 x 64 tiles (one 32 x 32
+    # MFMA block per wave): config 1, ragged edges, batched, config 2's first layer, a single
+    # k-slice (K = 7), and split-K grids whose 128-wide tiles would be mostly padding (config
+    # 2's dW1, 784 x 257 with K = 4096; 300 x 200); beta and a per-column bias with ReLU
+    # through the epilogue (the split-K reduce applies it).
+    got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.5, relu=True, seed=M + N + K + ta + 2 * tb)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+@pytest.mark.parametrize("Bt,M,N,K", [(1, 1000, 1000, 300), (1, 999, 1001, 257), (2, 512, 900, 512),
+                                      (1, 1024, 960, 1000), (1, 1000, 1000, 256), (1, 960, 1000, 1300)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("row_bias", [False, True])
+def test_fp32_64x64_two_waves_per_simd(Bt, M, N, K, ta, tb, row_bias):
+    # At most one 64 x 64 tile per CU (256 on MI355X) and K >= 256: the 8-wave kernel, two
+    # waves per 32 x 32 block splitting each 32-wide k-slice and reducing through LDS.
+    # Ragged M / N, K not a multiple of 32 (300, 1000) or of 4 (257: scalar loads), batched,
+    # all layouts, beta and either bias orientation with ReLU.  K = 256, 512, 1000 and 1300
+    # (8, 16, 32 and 41 slices) keep four slices in flight, 1300 with three zero slices in its
+    # last group of four; the others two.
+    got, ref = _ex("f32", ta, tb, Bt, M, N, K, beta=0.5, relu=True, row_bias=row_bias,
+                   seed=M + N + K + ta + 2 * tb + row_bias)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+# Skinny products (a side <= 16): config 2's H W2 (4096 x 10, K 257), dW2 = H^T dY (257 x 10,
+# K 4096, split over work-groups) and dH = dY W2^T (4096 x 257, K 10); M <= 16 (operands
+# swapped, C written transposed); tails of every side; K = 0.
+SKINNY = [(4096, 10, 257), (257, 10, 4096), (4096, 257, 10), (10, 4096, 257), (16, 16, 16),
+          (1, 1, 1), (17, 5, 3), (5, 1000, 3000), (3000, 7, 64), (33, 2, 65), (2, 33, 1000),
+          (300, 16, 17), (1, 513, 33)]
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_fp32_skinny_products(M, N, K, ta, tb):
+    got, ref = _ex("f32", ta, tb, 1, M, N, K, beta=0.0, seed=M + 3 * N + 7 * K + ta + 2 * tb)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((K, M) if ta else (M, K))
+    B = rng.standard_normal((N, K) if tb else (K, N))
+    check_f32(gemm(f32(A), f32(B), bool(ta), bool(tb)), A.astype(np.float32).astype(np.float64),
+              B.astype(np.float32).astype(np.float64), K, bool(ta), bool(tb))
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 10, 257), (257, 10, 4096), (4096, 257, 10),
+                                   (10, 300, 700), (7, 9, 2000)])
+@pytest.mark.parametrize("relu,row_bias", [(False, False), (True, False), (True, True)])
+def test_fp32_skinny_epilogue(M, N, K, relu, row_bias):
+    got, ref = _ex("f32", 0, 0, 1, M, N, K, beta=-0.5, relu=relu, row_bias=row_bias,
+                   seed=M + N + K + relu)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_fp32_skinny_k_zero_and_reruns():
+    C0 = np.arange(30, dtype=np.float32).reshape(10, 3)
+    got = gemm(np.zeros((10, 0), np.float32), np.zeros((0, 3), np.float32), beta=0.5, C0=C0)
+    assert np.array_equal(got, 0.5 * C0)
+    a, _ = _ex("f32", 1, 0, 1, 257, 10, 4096, seed=5)
+    b, _ = _ex("f32", 1, 0, 1, 257, 10, 4096, seed=5)
+    assert np.array_equal(a, b)
+
+
+def test_fp32_skinny_split_k_many_launches():
+    # K split over work-groups with pooled partials added in a fixed order: 150 launches
+    # alternating two shapes with different block counts (the pool hands the partial buffers
+    # back and forth); every result must equal the first one bit for bit and the oracle
+    # within the fp32 bound.
+    rng = np.random.default_rng(77)
+    shapes = [(1, 0, 257, 10, 4096), (0, 1, 7, 600, 3000)]
+    DB = hip.DeviceBuffer
+    runs = []
+    for ta, tb, M, N, K in shapes:
+        A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+        ref = O.gemm_general_d(ta, tb, A.astype(np.float64), B.astype(np.float64))
+        runs.append((ta, tb, M, N, K, DB.from_numpy(A), DB.from_numpy(B), DB.empty((M, N), np.float32),
+                     A.shape[1], B.shape[1], ref))
+    first = [None, None]
+    for it in range(150):
+        x = it % 2
+        ta, tb, M, N, K, dA, dB, dC, lda, ldb, ref = runs[x]
+        hip.gemm_f32(ta, tb, M, N, K, dA, lda, dB, ldb, 0.0, dC, N)
+        got = dC.numpy()
+        if first[x] is None:
+            first[x] = got
+            assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+        else:
+            assert np.array_equal(got, first[x]), f"launch {it}"
