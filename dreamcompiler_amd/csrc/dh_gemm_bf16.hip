@@ -518,7 +518,7 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
                                 : FAST_NSTAGE * 2 * FAST_TILE;
     __shared__ __attribute__((aligned(16))) uint16_t ring[RING];
 
-    const int tiles_m = M / 256, tiles_n = N / 256;
+    const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
     int tm, tn;
     // Each XCD's 32 tiles in flight form a 4 x 8 block (4 A panels, 8 B panels).  Same-box
     // A/B at 8192^3 (NN, ms): groups of 4 tile rows 0.862-0.867, 8 rows (8 x 4 blocks)
@@ -755,6 +755,42 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     mfma_block<FM, FN>(f1a, f1b, acc);
     }
 
+    // K % 32 tail (the DMA stages cover k < 32 nk): one or two 16-k steps whose operands come
+    // straight from global memory, zero at k >= K (and m >= M, n >= N on edge tiles) -- no
+    // value from outside the operands' rows enters the sums.  Lane (l32, h) supplies
+    // op(A)[m][k] and op(B)[k][n] for k = k16 + 8 h + e.
+    for (int k16 = 32 * nk; k16 < K; k16 += 16) {
+        bf16x8 ta[FM], tb[FN];
+        const int kb = k16 + 8 * h;
+#pragma unroll
+        for (int a = 0; a < FM; ++a) {
+            const int m = m0 + wm + 32 * a + l32;
+            s16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int k = kb + e;
+                v[e] = (m < M && k < K)
+                           ? (short)(TA ? A[(size_t)k * lda + m] : A[(size_t)m * lda + k])
+                           : (short)0;
+            }
+            ta[a] = __builtin_bit_cast(bf16x8, v);
+        }
+#pragma unroll
+        for (int b = 0; b < FN; ++b) {
+            const int n = n0 + wn + 32 * b + l32;
+            s16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int k = kb + e;
+                v[e] = (n < N && k < K)
+                           ? (short)(TB ? B[(size_t)n * ldb + k] : B[(size_t)k * ldb + n])
+                           : (short)0;
+            }
+            tb[b] = __builtin_bit_cast(bf16x8, v);
+        }
+        mfma_block<FM, FN>(ta, tb, acc);
+    }
+
     // Register r of block (a, b) is C[32 a + 8 (r / 4) + 4 (lane / 32) + r % 4][32 b + lane % 32]
     // (relative to the wave's tile): each store instruction writes two 128-byte row pieces,
     // non-temporally -- C is not read again here, and streaming it past the caches leaves them
@@ -765,6 +801,31 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     auto at = [&](int a, int b, int r) {
         return cw + (size_t)(32 * a + 8 * (r >> 2) + (r & 3)) * ldc + 32 * b;
     };
+    if (m0 + 256 > M || n0 + 256 > N) {
+        // Edge tile of a ragged shape: rows >= M and columns >= N hold products of the
+        // zeros (or neighbouring values) the loads returned past the operands' extents and
+        // are not stored; bias indices are clamped so nothing outside C or the bias is read.
+        const int row0 = m0 + wm + 4 * h, col0 = n0 + wn + l32;
+        const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS);
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b) {
+                const int col = col0 + 32 * b;
+                const float bcol = bias && !row_bias ? bias[min(col, N - 1)] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = row0 + 32 * a + 8 * (r >> 2) + (r & 3);
+                    if (row >= M || col >= N) continue;
+                    float* c = at(a, b, r);
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
+                              (row_bias ? bias[row] : bcol);
+                    if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
+                    __builtin_nontemporal_store(v, c);
+                }
+            }
+        return;
+    }
     if (beta == 0.f && !bias && !(epi & DH_EPI_RELU)) {
 #pragma unroll
         for (int a = 0; a < FM; ++a)
@@ -819,7 +880,7 @@ int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t*
                            : gemm_bf16_fast_kernel<TA, TB, 8, false>;
     for (int b0 = 0; b0 < bt.count; b0 += 65535) {   // gridDim.y = batch member
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
-        kern<<<dim3((M / 256) * (N / 256), nb), 64 * waves, 0, stream()>>>(
+        kern<<<dim3(((M + 255) / 256) * ((N + 255) / 256), nb), 64 * waves, 0, stream()>>>(
             M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB, ldb, beta, C + b0 * bt.sC, ldc, bt.sA,
             bt.sB, bt.sC, bt.bias, bt.epi);
         DH_TRY(check_launch("dh_gemm_bf16(fast)"));
@@ -828,21 +889,84 @@ int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t*
 }
 
 template <bool TA, bool TB>
-int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
-           float beta, float* C, int ldc, const Batch& bt) {
-    // 16-byte operand rows: aligned bases, leading dimensions and batch strides in multiples
-    // of 8 elements.
+int launch_general(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
+                   float beta, float* C, int ldc, const Batch& bt) {
     const bool va = ((uintptr_t)A % 16 == 0) && (lda % 8 == 0) && (bt.sA % 8 == 0);
     const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 8 == 0) && (bt.sB % 8 == 0);
-    const long long a_elems = (long long)(TA ? K : M) * lda, b_elems = (long long)(TB ? N : K) * ldb;
-    if (va && vb && M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K > 0 &&
-        (long long)(M / 256) * (N / 256) * bt.count >= num_cus() && a_elems < (1LL << 31) &&
-        b_elems < (1LL << 31))
-        return launch_fast<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
     if (va && vb) return launch_vec<TA, TB, true, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
     if (va) return launch_vec<TA, TB, true, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
     if (vb) return launch_vec<TA, TB, false, true>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
     return launch_vec<TA, TB, false, false>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+}
+
+// Rows of cols bf16 values at leading dimension ld -> rows at ldo (a multiple of 8, dst
+// 16-byte aligned), zero-filled to ldo: 16 bytes per thread and store, grid-stride.
+__global__ __launch_bounds__(256) void copy_rows_bf16(const uint16_t* __restrict__ src, int ld,
+                                                     uint16_t* __restrict__ dst, int ldo,
+                                                     int rows, int cols) {
+    const int chunks = ldo / 8;
+    const long long total = (long long)rows * chunks;
+    for (long long x = (long long)blockIdx.x * 256 + threadIdx.x; x < total;
+         x += (long long)gridDim.x * 256) {
+        const int r = (int)(x / chunks), c = (int)(x - (long long)r * chunks) * 8;
+        const uint16_t* sp = src + (size_t)r * ld + c;
+        s16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = c + e < cols ? (short)sp[e] : (short)0;
+        *reinterpret_cast<s16x8*>(dst + (size_t)r * ldo + c) = v;
+    }
+}
+
+// A stored operand (rows x cols, leading dimension ld) copied to pool memory with 16-byte
+// aligned rows (leading dimension cols rounded up to 8, zero-padded).
+uint16_t* aligned_copy(const uint16_t* src, int rows, int cols, int ld, int& ld_out) {
+    ld_out = (cols + 7) & ~7;
+    uint16_t* d = static_cast<uint16_t*>(dh_malloc((size_t)rows * ld_out * sizeof(uint16_t)));
+    if (!d) return nullptr;
+    const long long total = (long long)rows * (ld_out / 8);
+    long long blocks = (total + 255) / 256;
+    if (blocks > 8LL * num_cus()) blocks = 8LL * num_cus();
+    copy_rows_bf16<<<(unsigned)blocks, 256, 0, stream()>>>(src, ld, d, ld_out, rows, cols);
+    if (check_launch("dh_gemm_bf16(aligned copy)") != DH_OK) {
+        dh_free(d);
+        return nullptr;
+    }
+    return d;
+}
+
+template <bool TA, bool TB>
+int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
+           float beta, float* C, int ldc, const Batch& bt) {
+    // The direct-to-LDS path needs 16-byte operand rows (aligned bases, leading dimensions
+    // and batch strides in multiples of 8 elements) and at least one round of 256 x 256 tiles.
+    // Ragged M and N are edge tiles of it, a K that is not a multiple of 32 ends with the
+    // kernel's masked tail steps (a DMA'd k-contiguous tile would read the next row's values,
+    // possibly non-finite, past K); rows that are not 16-byte aligned are copied to aligned
+    // ones first (one product: a pass over the operand, where the general kernel on such
+    // rows takes ~5-10x the fast path's time).
+    const long long tiles = (long long)((M + 255) / 256) * ((N + 255) / 256) * bt.count;
+    const int K32 = K - K % 32;
+    const long long a_bytes = 2LL * ((TA ? K : M) + 255) * lda,
+                    b_bytes = 2LL * ((TB ? N : K) + 255) * ldb;
+    if (K32 == 0 || tiles < num_cus() || a_bytes >= (1LL << 32) || b_bytes >= (1LL << 32))
+        return launch_general<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    const bool va = ((uintptr_t)A % 16 == 0) && (lda % 8 == 0) && (bt.sA % 8 == 0);
+    const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 8 == 0) && (bt.sB % 8 == 0);
+    if (!va || !vb) {
+        if (bt.count > 1) return launch_general<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+        int la = lda, lb = ldb;
+        uint16_t* a2 = va ? nullptr : aligned_copy(A, TA ? K : M, TA ? M : K, lda, la);
+        uint16_t* b2 = vb ? nullptr : aligned_copy(B, TB ? N : K, TB ? K : N, ldb, lb);
+        int st;
+        if ((!va && !a2) || (!vb && !b2))
+            st = launch_general<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+        else
+            st = launch<TA, TB>(M, N, K, a2 ? a2 : A, la, b2 ? b2 : B, lb, beta, C, ldc, bt);
+        if (a2) dh_free(a2);   // pooled: stream order keeps them alive for the queued work
+        if (b2) dh_free(b2);
+        return st;
+    }
+    return launch_fast<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 
 }  // namespace

@@ -482,3 +482,70 @@ def test_fp32_skinny_split_k_many_launches():
             assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
         else:
             assert np.array_equal(got, first[x]), f"launch {it}"
+
+
+# Ragged shapes on the direct-to-LDS bf16 path (at least one round of 256 x 256 tiles): edge
+# tiles for M, N; the last K % 32 on the general kernel; unaligned leading dimensions copied to
+# aligned rows first.
+RAGGED = [(4000, 4000, 256), (4000, 4000, 300), (4095, 4097, 100), (3900, 4352, 33),
+          (4352, 3841, 1000)]
+
+
+@pytest.mark.parametrize("M,N,K", RAGGED)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_ragged_fast_path(M, N, K, ta, tb):
+    rng = np.random.default_rng(M + 3 * N + 7 * K + 11 * ta + 13 * tb)
+    A = bf16_bits(rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32))
+    C0 = rng.standard_normal((M, N), dtype=np.float32)
+    got = gemm(A, B, bool(ta), bool(tb), beta=-0.5, C0=C0, dtype="bf16")
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    opA, opB = (A64.T if ta else A64), (B64.T if tb else B64)
+    rows = np.sort(np.concatenate([rng.choice(M, 40, replace=False), [0, M - 1]]))
+    ref = opA[rows] @ opB - 0.5 * C0[rows].astype(np.float64)
+    assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(K)
+    # every element, through the row and column sums (the edge tiles included)
+    _rowcol_sums_check(got + 0.5 * C0, opA, opB, 1e-5)
+
+
+@pytest.mark.parametrize("ldpad", [1, 3, 4])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_bf16_unaligned_rows_take_aligned_copies(ldpad, ta, tb):
+    # leading dimensions that are not multiples of 8 elements (rows not 16-byte aligned)
+    M, N, K = 4100, 4000, 264
+    rng = np.random.default_rng(ldpad + 5 * ta)
+    A = bf16_bits(rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32))
+    got = gemm(A, B, bool(ta), bool(tb), dtype="bf16", ldpad=ldpad, ldcpad=0)
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    opA, opB = (A64.T if ta else A64), (B64.T if tb else B64)
+    rows = np.sort(rng.choice(M, 40, replace=False))
+    assert maxrel(got[rows], opA[rows] @ opB) <= 1e-5 * np.sqrt(K)
+    _rowcol_sums_check(got, opA, opB, 1e-5)
+
+
+@pytest.mark.parametrize("relu", [False, True])
+def test_bf16_ragged_epilogue_bias_relu(relu):
+    # column bias and ReLU on ragged edge tiles, and applied once when K has a tail
+    for M, N, K in ((4000, 4000, 300), (4095, 4097, 256)):
+        got, ref = _ex("bf16", 0, 1, 1, M, N, K, beta=0.25, bias=True, relu=relu, seed=M + K)
+        assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_bf16_ragged_k_tail_keeps_nonfinite_values_in_their_row():
+    # A NaN in the last column of A row i and an Inf in row i+1: only C rows i and i+1 may be
+    # non-finite (the k-tail of row i must not read row i+1's values, nor the reverse).
+    M, N, K = 4000, 4000, 300
+    rng = np.random.default_rng(5)
+    Af = rng.standard_normal((M, K), dtype=np.float32)
+    Af[1000, K - 1] = np.nan
+    Af[1001, 0] = np.inf
+    A = bf16_bits(Af)
+    B = bf16_bits(rng.standard_normal((K, N), dtype=np.float32))
+    got = gemm(A, B, dtype="bf16")
+    bad = np.where(~np.isfinite(got).all(axis=1))[0]
+    assert set(bad.tolist()) == {1000, 1001}
+    ok = np.isfinite(got).all(axis=1)
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    rows = np.where(ok)[0][::97]
+    assert maxrel(got[rows], A64[rows] @ B64) <= 1e-5 * np.sqrt(K)
