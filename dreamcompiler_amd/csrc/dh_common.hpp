@@ -211,24 +211,39 @@ __device__ inline void xcd_tile_order(int bid, int nblocks, int tiles_m, int til
     tn = in / gsz;
 }
 
-// Work-group -> (slice bh, tile rank rr) for a grid of BH slices x n_t tiles per slice.
-// Work-groups are dealt round-robin to the 8 XCDs; when the slices split evenly over them,
-// XCD x takes the slices bh = x (mod 8) in groups of G and finishes one group before the
-// next, rank 0 (the caller's heaviest tile) first within a group: the few slices in flight
-// keep their operands in the XCD's L2.  G <= 0, or slices that do not split evenly: rank-major
-// over all slices (bh = bid mod BH).
+// Work-group -> (slice bh, tile rank rr) for BH slices x n_t tiles per slice.  Work-groups are
+// dealt round-robin to the 8 XCDs; XCD x takes the slices bh = x (mod 8) in groups of G and
+// finishes one group before the next, rank 0 (the caller's heaviest tile) first within a
+// group: the few slices in flight keep their operands in the XCD's L2.  The grid then has
+// slice_grid(BH, n_t) = 8 ceil(BH / 8) n_t work-groups: when 8 does not divide BH an XCD
+// holds ceil or floor of BH / 8 slices, and its work-groups past its last tile get bh = -1
+// (nothing to do).  G <= 0: rank-major over all slices (bh = bid mod BH) on a grid of
+// BH n_t, for BH that slice_grouping() declines.
 __device__ inline void slice_group_order(int bid, int BH, int n_t, int G, int& bh, int& rr) {
-    if (G <= 0 || (BH & 7)) {
+    if (G <= 0) {
         bh = bid % BH;
         rr = bid / BH;
         return;
     }
-    const int x = bid & 7, k = bid >> 3, spx = BH >> 3;
+    const int x = bid & 7, k = bid >> 3, spx = (BH - x + 7) >> 3;
+    if (k >= spx * n_t) {
+        bh = -1;
+        rr = 0;
+        return;
+    }
     const int g = k / (G * n_t);
     const int gsz = min(G, spx - g * G);
     const int w = k - g * G * n_t;
     rr = w / gsz;
     bh = 8 * (g * G + w % gsz) + x;
 }
+
+// Whether to group slices by XCD: always when 8 divides BH; otherwise when the XCDs' unequal
+// slice counts leave at most ~6% of the work's time with XCDs idle (rank-major order costs
+// ~13% at config 4's shape with BH = 127 or 131: every XCD fetches every slice's operands).
+inline bool slice_grouping(int BH) {
+    return (BH & 7) == 0 || 100LL * BH >= 94LL * 8 * ((BH + 7) / 8);
+}
+inline long long slice_grid(int BH, int n_t) { return 8LL * ((BH + 7) / 8) * n_t; }
 
 }  // namespace dh

@@ -200,6 +200,7 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
 
     int bh, kt;                          // causal: small kt = longest query range, first
     slice_group_order(blockIdx.x, BH, (S + KV_KEYS - 1) / KV_KEYS, group, bh, kt);
+    if (bh < 0) return;                  // padding of an XCD with one slice fewer
     const int kbase = kt * KV_KEYS;
     const size_t base = (size_t)bh * S * D;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -488,6 +489,7 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
     const int n_qt = (S + DQ_ROWS - 1) / DQ_ROWS;
     int bh, rr;
     slice_group_order(blockIdx.x, BH, n_qt, group, bh, rr);
+    if (bh < 0) return;                  // padding of an XCD with one slice fewer
     const int qt = CAUSAL ? n_qt - 1 - rr : rr;
     const int q0 = qt * DQ_ROWS;
     const size_t base = (size_t)bh * S * D;
@@ -974,11 +976,13 @@ int launch_dq_bf16(int BH, int S, float scale, float sl2, const void* Q, const v
     const size_t lds = (size_t)dq_nstage<W>() * 2 * BwTile<D, DQ_BN>::TILE;
     static bool done = false;
     DH_TRY(set_lds(kern, lds, done));
-    const int grid = BH * ((S + 32 * W - 1) / (32 * W));
-    kern<<<grid, 64 * W, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
-                                         (const uint16_t*)K, (const uint16_t*)V,
-                                         (const uint16_t*)O, (const uint16_t*)dO, LSE, L2, Dv, dQ,
-                                         acc, group);
+    const int n_qt = (S + 32 * W - 1) / (32 * W);
+    if (!slice_grouping(BH)) group = 0;
+    const long long grid = group > 0 ? slice_grid(BH, n_qt) : (long long)BH * n_qt;
+    kern<<<(unsigned)grid, 64 * W, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
+                                                   (const uint16_t*)K, (const uint16_t*)V,
+                                                   (const uint16_t*)O, (const uint16_t*)dO, LSE,
+                                                   L2, Dv, dQ, acc, group);
     return check_launch("dh_flash_bwd(dQ bf16)");
 }
 
@@ -1018,11 +1022,13 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
                            2 * BwTile<D, KV_KEYS>::TILE;
         static bool done = false;
         DH_TRY(set_lds(kern, lds, done));
-        const int grid = BH * ((S + KV_KEYS - 1) / KV_KEYS);
-        kern<<<grid, KV_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
-                                             (const uint16_t*)K, (const uint16_t*)V,
-                                             (const uint16_t*)dO, L2, Dv, dK, dV, acc_k, acc_v,
-                                             kv_alias, group_kv);
+        const int n_kt = (S + KV_KEYS - 1) / KV_KEYS;
+        const int gkv = slice_grouping(BH) ? group_kv : 0;
+        const long long grid = gkv > 0 ? slice_grid(BH, n_kt) : (long long)BH * n_kt;
+        kern<<<(unsigned)grid, KV_NT, lds, stream()>>>(BH, S, scale, sl2, (const uint16_t*)Q,
+                                                       (const uint16_t*)K, (const uint16_t*)V,
+                                                       (const uint16_t*)dO, L2, Dv, dK, dV,
+                                                       acc_k, acc_v, kv_alias, gkv);
         DH_TRY(check_launch("dh_flash_bwd(dK,dV bf16)"));
     }
     return DH_OK;

@@ -91,27 +91,20 @@ __device__ inline float dot2_bf16(uint32_t p, uint32_t q, float acc) {
                                            acc, false);
 }
 
-// Work-group -> (slice bh, q-tile rank rr; rank 0 = longest causal key range).  Work-groups
-// are dealt round-robin to the 8 XCDs.  When the slices split evenly, XCD x takes the
-// slices bh = x (mod 8) in groups of G and finishes one group before the next, heaviest
-// q-tile first within a group: the few slices in flight keep their K and V in the XCD's
-// L2, and G = 4 causal slices hold enough work that the last, longest tiles of a group
-// do not trail.  Otherwise: heaviest q-tile of every slice first.
+// Work-group -> (slice bh, q-tile rank rr; rank 0 = longest causal key range), by
+// slice_group_order: each XCD walks its slices G at a time (G = 4 causal slices hold enough
+// work that the last, longest tiles of a group do not trail), heaviest q-tile first within a
+// group, so the slices in flight keep their K and V in the XCD's L2.  A grid of exactly
+// BH n_qt work-groups with 8 not dividing BH is the rank-major fallback (slice_grouping).
 template <bool CAUSAL>
 __device__ inline void bf_order(int BH, int n_qt, int& bh, int& rr) {
     const int bid = blockIdx.x;
-    if (BH & 7) {
+    if ((BH & 7) && (long long)gridDim.x == (long long)BH * n_qt) {
         bh = bid % BH;
         rr = bid / BH;
         return;
     }
-    constexpr int G = CAUSAL ? 4 : 1;
-    const int x = bid & 7, k = bid >> 3, spx = BH >> 3;
-    const int g = k / (G * n_qt);
-    const int gsz = min(G, spx - g * G);
-    const int w = k - g * G * n_qt;
-    rr = w / gsz;
-    bh = 8 * (g * G + w % gsz) + x;
+    slice_group_order(bid, BH, n_qt, CAUSAL ? 4 : 1, bh, rr);
 }
 
 // One work-group = W waves x 32 query rows.  Per stage of 64 keys a wave computes
@@ -133,6 +126,7 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     const int n_qt = (S + ROWS - 1) / ROWS;
     int bh, rr;
     bf_order<CAUSAL>(BH, n_qt, bh, rr);
+    if (bh < 0) return;                  // padding of an XCD with one slice fewer
     const int qt = CAUSAL ? n_qt - 1 - rr : rr;
     const int q0 = qt * ROWS;
     const size_t base = (size_t)bh * S * D;
@@ -816,9 +810,11 @@ int launch_bf16_w(int BH, int S, float sl2, const void* Q, const void* K, const 
     const size_t lds = BfTile<D, W>::LDS;
     static bool done = false;
     DH_TRY(set_lds(kern, lds, done));
-    const int grid = BH * ((S + 32 * W - 1) / (32 * W));
-    kern<<<grid, 64 * W, lds, stream()>>>(BH, S, sl2, (const uint16_t*)Q, (const uint16_t*)K,
-                                         (const uint16_t*)V, (uint16_t*)O, LSE);
+    const int n_qt = (S + 32 * W - 1) / (32 * W);
+    const long long grid = slice_grouping(BH) ? slice_grid(BH, n_qt) : (long long)BH * n_qt;
+    kern<<<(unsigned)grid, 64 * W, lds, stream()>>>(BH, S, sl2, (const uint16_t*)Q,
+                                                   (const uint16_t*)K, (const uint16_t*)V,
+                                                   (uint16_t*)O, LSE);
     return check_launch("dh_flash_fwd(bf16)");
 }
 

@@ -336,6 +336,26 @@ def test_bf16_causal_fwd_bwd_grouped_even_tiles(BH, S, D):
     assert np.array_equal(again, Of)
 
 
+@pytest.mark.parametrize("BH,S,D", [(31, 300, 128), (33, 520, 64), (63, 200, 32)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_bf16_padded_slice_grid(BH, S, D, causal):
+    """BH not a multiple of 8 but large enough that slices are still grouped by XCD: the grid
+    is padded to 8 ceil(BH / 8) slices and the work-groups past an XCD's last slice do
+    nothing.  Every slice in full against the fp64 oracle (a slice computed twice or not at
+    all would show), forward, LSE and backward."""
+    Q, K, V, G = (bf16_bits(x) for x in inputs(BH, S, D, 7000 + BH + S + causal))
+    Of, lse = flash_fwd(Q, K, V, BH, S, D, causal, dtype="bf16")
+    grads = flash_bwd(Q, K, V, bf16_bits(Of), G, lse, BH, S, D, causal, dtype="bf16")
+    Q64, K64, V64, G64 = (bits_to_f32(x).astype(np.float64) for x in (Q, K, V, G))
+    ref = O.attention(Q64, K64, V64, BH, S, D, causal).reshape(BH, S, D)
+    refs = [r.reshape(BH, S, D) for r in _bwd_ref(Q64, K64, V64, G64, BH, S, D, causal)]
+    for b in range(BH):
+        assert maxrel(Of.reshape(BH, S, D)[b], ref[b]) <= 2e-2, b
+        for name, g, r in zip("QKV", grads, refs):
+            assert maxrel(g.reshape(BH, S, D)[b], r[b]) <= 2e-2, (name, b)
+    assert np.abs(lse - O.flash_lse(Q64, K64, BH, S, D, causal)).max() <= 1e-3 * np.sqrt(D)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_bf16_bwd_wide_grid(causal):
     """88 slices x 520 rows at D = 128: a dQ grid of 264 256-query tiles, the band that keeps
