@@ -14,6 +14,10 @@ int ensure_init();                 // DH_OK or DH_ERR_NO_DEVICE
 hipStream_t stream();
 int check_launch(const char* what);   // hipGetLastError after a launch
 int num_cus();
+// C = beta C + sum_s part[s] (+ bias, then ReLU: the DH_EPI_* epilogue) over S fp32 partials
+// of M x N (part[s] at part + s M N), added in a fixed order; defined in dh_gemm_f32.hip.
+int splitk_reduce_launch(const float* part, int S, int M, int N, float beta, float* C, int ldc,
+                         const float* bias, int epi);
 
 #define DH_TRY(expr)                      \
     do {                                  \

@@ -257,12 +257,17 @@ int launch_vec(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* 
 // fragments of the next k-step are read while the matrix cores run the current one.
 // ---------------------------------------------------------------------------------
 
-template <bool KCONTIG, int WAVES>
+template <bool KCONTIG, int WAVES, int T = 256>
 struct FastOperand {
-    // One 32-k stage of a 256-wide operand tile is 16 KB = 16 DMA blocks of 1 KB; wave w
-    // issues blocks PER*w .. PER*w + PER-1.  Per-lane element offsets at k0 = 0 and the
-    // per-stage step.
-    static constexpr int PER = 16 / WAVES;
+    // One 32-k stage of a T-wide operand tile (T = 256 or 128) is T / 16 DMA blocks of 1 KB;
+    // wave w issues blocks PER*w .. PER*w + PER-1.  Per-lane element offsets at k0 = 0 and
+    // the per-stage step.
+    static constexpr int NBLK = T / 16;
+    static constexpr int PER = NBLK / WAVES;
+    static constexpr int KPB = 512 / T;    // k rows of an mn-contiguous tile per DMA block
+    static constexpr int CPR = T / 8;      // 16-byte chunks in one of those rows
+    static constexpr int CPR_LOG = T == 256 ? 5 : 4;
+    static_assert(T == 256 || T == 128, "tile widths");
     uint32_t off[PER];     // byte offsets from the operand base at stage 0
     uint32_t step;         // bytes per stage
     uint32_t bytes;        // operand extent (rows x ld x 2 < 2^32, checked by the host)
@@ -275,9 +280,9 @@ struct FastOperand {
                 const int row = 16 * b + (lane >> 2);
                 const int c = (lane & 3) ^ ((lane >> 4) & 3);   // = p ^ ((row >> 2) & 3)
                 off[t] = 2u * ((uint32_t)(t0 + row) * ld + 8 * c);
-            } else {                           // block b = k rows 2b, 2b+1 of [32 k][t]
-                const int k = 2 * b + (lane >> 5);
-                const int c = (lane & 31) ^ (4 * (k & 3));
+            } else {                           // block b = k rows KPB b .. of [32 k][T]
+                const int k = KPB * b + (lane >> CPR_LOG);
+                const int c = (lane & (CPR - 1)) ^ (4 * (k & 3));
                 off[t] = 2u * ((uint32_t)k * ld + t0 + 8 * c);
             }
         }
@@ -300,7 +305,7 @@ struct FastOperand {
             const int row = o + (lane & 31);
             const int p = (2 * kk + h) ^ ((row >> 2) & 3);
             return *reinterpret_cast<const bf16x8*>(lds + row * 32 + 8 * p);
-        } else {                               // [32][256]: chunk c of row k at c ^ 4 (k % 4)
+        } else {                               // [32][T]: chunk c of row k at c ^ 4 (k % 4)
             const int G = (lane & 31) >> 4, i = lane & 15;
             const int n = o + 16 * G + 4 * (i & 3);
             s16x4 r[2];
@@ -308,7 +313,7 @@ struct FastOperand {
             for (int q = 0; q < 2; ++q) {
                 const int k = 16 * kk + 8 * h + 4 * q + (i >> 2);
                 const int p = (n >> 3) ^ (4 * (k & 3));
-                r[q] = ds_read_tr(lds + k * 256 + 8 * p + 4 * ((n >> 2) & 1));
+                r[q] = ds_read_tr(lds + k * T + 8 * p + 4 * ((n >> 2) & 1));
             }
             return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7));
         }
@@ -330,7 +335,7 @@ struct FastOperand {
             const int n = o + 16 * G + 4 * (i & 3);
             const int k = 16 * kk + 8 * h + 4 * q + (i >> 2);
             const int p = (n >> 3) ^ (4 * (k & 3));
-            f[q] = ds_read_tr(lds + k * 256 + 8 * p + 4 * ((n >> 2) & 1));
+            f[q] = ds_read_tr(lds + k * T + 8 * p + 4 * ((n >> 2) & 1));
         }
     }
     // DMA block t of this wave's share of a stage (see issue()).
@@ -381,14 +386,15 @@ struct DeepKOperand {
 constexpr int FAST_TILE = 256 * 32;   // elements of one operand stage (32 k)
 constexpr int FAST_NSTAGE = 4;        // LDS ring: 4 x (A + B) x 16 KB = 128 KB
 
-// Fragments of one 16-k step for the wave's FM x FN block of 32 x 32 MFMA tiles.
-template <typename OA, typename OB, int FM, int FN>
+// Fragments of one 16-k step for the wave's FM x FN block of 32 x 32 MFMA tiles (the stage's
+// B tile BOFF elements after its A tile).
+template <typename OA, typename OB, int FM, int FN, int BOFF = FAST_TILE>
 __device__ inline void load_frags(const uint16_t* st, int kk, int wm, int wn, int lane,
                                   bf16x8 (&fa)[FM], bf16x8 (&fb)[FN]) {
 #pragma unroll
     for (int x = 0; x < FM; ++x) fa[x] = OA::frag(st, wm + 32 * x, kk, lane);
 #pragma unroll
-    for (int x = 0; x < FN; ++x) fb[x] = OB::frag(st + FAST_TILE, wn + 32 * x, kk, lane);
+    for (int x = 0; x < FN; ++x) fb[x] = OB::frag(st + BOFF, wn + 32 * x, kk, lane);
 }
 
 template <int FM, int FN>
@@ -486,6 +492,119 @@ __device__ inline void wait_dma_stages(int n) {
         if (n >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
         else if (n == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+}
+
+// K % 32 tail (the DMA stages cover k < 32 nk): one or two 16-k steps whose operands come
+// straight from global memory, zero at k >= K (and m >= M, n >= N on edge tiles) -- no
+// value from outside the operands' rows enters the sums.  Lane (l32, h) supplies
+// op(A)[m][k] and op(B)[k][n] for k = k16 + 8 h + e; mw, nw: the wave's first row and column.
+template <bool TA, bool TB, int FM, int FN>
+__device__ inline void k_tail(int M, int N, int K, int nk, const uint16_t* __restrict__ A,
+                              int lda, const uint16_t* __restrict__ B, int ldb, int mw, int nw,
+                              int lane, f32x16 (&acc)[FM][FN]) {
+    const int l32 = lane & 31, h = lane >> 5;
+    for (int k16 = 32 * nk; k16 < K; k16 += 16) {
+        bf16x8 ta[FM], tb[FN];
+        const int kb = k16 + 8 * h;
+#pragma unroll
+        for (int a = 0; a < FM; ++a) {
+            const int m = mw + 32 * a + l32;
+            s16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int k = kb + e;
+                v[e] = (m < M && k < K)
+                           ? (short)(TA ? A[(size_t)k * lda + m] : A[(size_t)m * lda + k])
+                           : (short)0;
+            }
+            ta[a] = __builtin_bit_cast(bf16x8, v);
+        }
+#pragma unroll
+        for (int b = 0; b < FN; ++b) {
+            const int n = nw + 32 * b + l32;
+            s16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int k = kb + e;
+                v[e] = (n < N && k < K)
+                           ? (short)(TB ? B[(size_t)n * ldb + k] : B[(size_t)k * ldb + n])
+                           : (short)0;
+            }
+            tb[b] = __builtin_bit_cast(bf16x8, v);
+        }
+        mfma_block<FM, FN>(ta, tb, acc);
+    }
+}
+
+// Register r of block (a, b) is C[32 a + 8 (r / 4) + 4 (lane / 32) + r % 4][32 b + lane % 32]
+// (relative to the wave's tile): each store instruction writes two 128-byte row pieces,
+// non-temporally -- C is not read again here, and streaming it past the caches leaves them
+// to the A / B panels (8192^3: +3.2%, measured A/B on one box; the flash kernels' narrower
+// output pieces lost 8-9% the same way, so they store normally).
+// One uniform branch on the epilogue form keeps each form straight-line code.
+template <int FM, int FN, int T>
+__device__ inline void store_tile(int M, int N, float beta, float* __restrict__ C, int ldc,
+                                  const float* __restrict__ bias, int epi, int m0, int n0, int wm,
+                                  int wn, int lane, const f32x16 (&acc)[FM][FN]) {
+    const int l32 = lane & 31, h = lane >> 5;
+    float* cw = C + (size_t)(m0 + wm + 4 * h) * ldc + n0 + wn + l32;
+    auto at = [&](int a, int b, int r) {
+        return cw + (size_t)(32 * a + 8 * (r >> 2) + (r & 3)) * ldc + 32 * b;
+    };
+    if (m0 + T > M || n0 + T > N) {
+        // Edge tile of a ragged shape: rows >= M and columns >= N hold products of the
+        // zeros (or neighbouring values) the loads returned past the operands' extents and
+        // are not stored; bias indices are clamped so nothing outside C or the bias is read.
+        const int row0 = m0 + wm + 4 * h, col0 = n0 + wn + l32;
+        const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS);
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b) {
+                const int col = col0 + 32 * b;
+                const float bcol = bias && !row_bias ? bias[min(col, N - 1)] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = row0 + 32 * a + 8 * (r >> 2) + (r & 3);
+                    if (row >= M || col >= N) continue;
+                    float* c = at(a, b, r);
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
+                              (row_bias ? bias[row] : bcol);
+                    if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
+                    __builtin_nontemporal_store(v, c);
+                }
+            }
+        return;
+    }
+    if (beta == 0.f && !bias && !(epi & DH_EPI_RELU)) {
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) __builtin_nontemporal_store(acc[a][b][r], at(a, b, r));
+    } else {
+        // C = acc + beta C + bias (by column, or by row with DH_EPI_ROW_BIAS), then max(., 0)
+        // with DH_EPI_RELU (NaN passes).
+        const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS);
+        float bv[FN];
+#pragma unroll
+        for (int b = 0; b < FN; ++b)
+            bv[b] = bias && !row_bias ? bias[n0 + wn + 32 * b + l32] : 0.f;
+        const float* brow = row_bias ? bias + m0 + wm + 4 * h : nullptr;
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float* c = at(a, b, r);
+                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
+                              (row_bias ? brow[32 * a + 8 * (r >> 2) + (r & 3)] : bv[b]);
+                    if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
+                    __builtin_nontemporal_store(v, c);
+                }
     }
 }
 
@@ -755,106 +874,94 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     mfma_block<FM, FN>(f1a, f1b, acc);
     }
 
-    // K % 32 tail (the DMA stages cover k < 32 nk): one or two 16-k steps whose operands come
-    // straight from global memory, zero at k >= K (and m >= M, n >= N on edge tiles) -- no
-    // value from outside the operands' rows enters the sums.  Lane (l32, h) supplies
-    // op(A)[m][k] and op(B)[k][n] for k = k16 + 8 h + e.
-    for (int k16 = 32 * nk; k16 < K; k16 += 16) {
-        bf16x8 ta[FM], tb[FN];
-        const int kb = k16 + 8 * h;
-#pragma unroll
-        for (int a = 0; a < FM; ++a) {
-            const int m = m0 + wm + 32 * a + l32;
-            s16x8 v;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int k = kb + e;
-                v[e] = (m < M && k < K)
-                           ? (short)(TA ? A[(size_t)k * lda + m] : A[(size_t)m * lda + k])
-                           : (short)0;
-            }
-            ta[a] = __builtin_bit_cast(bf16x8, v);
-        }
-#pragma unroll
-        for (int b = 0; b < FN; ++b) {
-            const int n = n0 + wn + 32 * b + l32;
-            s16x8 v;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int k = kb + e;
-                v[e] = (n < N && k < K)
-                           ? (short)(TB ? B[(size_t)n * ldb + k] : B[(size_t)k * ldb + n])
-                           : (short)0;
-            }
-            tb[b] = __builtin_bit_cast(bf16x8, v);
-        }
-        mfma_block<FM, FN>(ta, tb, acc);
-    }
+    k_tail<TA, TB, FM, FN>(M, N, K, nk, A, lda, B, ldb, m0 + wm, n0 + wn, lane, acc);
+    store_tile<FM, FN, 256>(M, N, beta, C, ldc, bias, epi, m0, n0, wm, wn, lane, acc);
+}
 
-    // Register r of block (a, b) is C[32 a + 8 (r / 4) + 4 (lane / 32) + r % 4][32 b + lane % 32]
-    // (relative to the wave's tile): each store instruction writes two 128-byte row pieces,
-    // non-temporally -- C is not read again here, and streaming it past the caches leaves them
-    // to the A / B panels (8192^3: +3.2%, measured A/B on one box; the flash kernels' narrower
-    // output pieces lost 8-9% the same way, so they store normally).
-    // One uniform branch on the epilogue form keeps each form straight-line code.
-    float* cw = C + (size_t)(m0 + wm + 4 * h) * ldc + n0 + wn + l32;
-    auto at = [&](int a, int b, int r) {
-        return cw + (size_t)(32 * a + 8 * (r >> 2) + (r & 3)) * ldc + 32 * b;
-    };
-    if (m0 + 256 > M || n0 + 256 > N) {
-        // Edge tile of a ragged shape: rows >= M and columns >= N hold products of the
-        // zeros (or neighbouring values) the loads returned past the operands' extents and
-        // are not stored; bias indices are clamped so nothing outside C or the bias is read.
-        const int row0 = m0 + wm + 4 * h, col0 = n0 + wn + l32;
-        const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS);
+// ---------------------------------------------------------------------------------
+// Mid-size path: 128 x 128 tiles for shapes whose 256 x 256 tiles leave the CUs short of one
+// round (2048^3: 64 tiles of 256 against 256 of 128).  The fast path's direct-to-LDS ring in
+// 32-k stages of 128-wide tiles (8 KB per operand and stage, four stages = 64 KB, so two
+// work-groups fit a CU); 4 waves as 2 x 2 of 64 x 64 (2 x 2 MFMA blocks each), the same
+// software pipeline as the 8-wave fast loop: DMA of stage kt+3 | reads of k-step 1 | MFMAs
+// of k-step 0 | wait + barrier | reads of stage kt+1's k-step 0 | MFMAs of k-step 1.  Same
+// contract for ragged shapes (edge tiles, masked K tail) as the fast path.
+// ---------------------------------------------------------------------------------
+constexpr int MID_TILE = 128 * 32;    // elements of one operand stage (32 k)
+constexpr int MID_NSTAGE = 4;         // LDS ring: 4 x (A + B) x 8 KB = 64 KB
+
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(256)
+gemm_bf16_mid_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
+                     const uint16_t* __restrict__ B, int ldb, float beta, float* __restrict__ C,
+                     int ldc, long long sA, long long sB, long long sC,
+                     const float* __restrict__ bias, int epi) {
+    A += blockIdx.y * sA;   // batch member blockIdx.y
+    B += blockIdx.y * sB;
+    C += blockIdx.y * sC;
+    using OA = FastOperand<!TA, 4, 128>;
+    using OB = FastOperand<TB, 4, 128>;
+    constexpr int FM = 2, FN = 2;
+    __shared__ __attribute__((aligned(16))) uint16_t ring[MID_NSTAGE * 2 * MID_TILE];
+
+    const int tiles_m = (M + 127) / 128, tiles_n = (N + 127) / 128;
+    int tm, tn;
+    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 4, tm, tn);
+    const int m0 = tm * 128, n0 = tn * 128;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+
+    OA oa;
+    OB ob;
+    oa.init(lda, TA ? K : M, m0, wave, lane);
+    ob.init(ldb, TB ? N : K, n0, wave, lane);
+
+    f32x16 acc[FM][FN];
 #pragma unroll
-        for (int a = 0; a < FM; ++a)
-#pragma unroll
-            for (int b = 0; b < FN; ++b) {
-                const int col = col0 + 32 * b;
-                const float bcol = bias && !row_bias ? bias[min(col, N - 1)] : 0.f;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = row0 + 32 * a + 8 * (r >> 2) + (r & 3);
-                    if (row >= M || col >= N) continue;
-                    float* c = at(a, b, r);
-                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
-                              (row_bias ? bias[row] : bcol);
-                    if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
-                    __builtin_nontemporal_store(v, c);
-                }
-            }
-        return;
-    }
-    if (beta == 0.f && !bias && !(epi & DH_EPI_RELU)) {
-#pragma unroll
-        for (int a = 0; a < FM; ++a)
-#pragma unroll
-            for (int b = 0; b < FN; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) __builtin_nontemporal_store(acc[a][b][r], at(a, b, r));
-    } else {
-        // C = acc + beta C + bias (by column, or by row with DH_EPI_ROW_BIAS), then max(., 0)
-        // with DH_EPI_RELU (NaN passes).
-        const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS);
-        float bv[FN];
+    for (int a = 0; a < FM; ++a)
 #pragma unroll
         for (int b = 0; b < FN; ++b)
-            bv[b] = bias && !row_bias ? bias[n0 + wn + 32 * b + l32] : 0.f;
-        const float* brow = row_bias ? bias + m0 + wm + 4 * h : nullptr;
 #pragma unroll
-        for (int a = 0; a < FM; ++a)
-#pragma unroll
-            for (int b = 0; b < FN; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float* c = at(a, b, r);
-                    float v = (beta == 0.f ? acc[a][b][r] : acc[a][b][r] + beta * *c) +
-                              (row_bias ? brow[32 * a + 8 * (r >> 2) + (r & 3)] : bv[b]);
-                    if (epi & DH_EPI_RELU) v = v < 0.f ? 0.f : v;
-                    __builtin_nontemporal_store(v, c);
-                }
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    const int nk = K / 32;   // >= 1 (the host sends K < 32 elsewhere)
+    auto stage_ptr = [&](int kt) { return ring + (kt % MID_NSTAGE) * 2 * MID_TILE; };
+    auto issue = [&](int kt) {
+        uint16_t* st = stage_ptr(kt);
+        oa.issue(A, kt, st, wave);
+        ob.issue(B, kt, st + MID_TILE, wave);
+    };
+    const int pre = nk < MID_NSTAGE - 1 ? nk : MID_NSTAGE - 1;
+    for (int s = 0; s < pre; ++s) issue(s);
+    static_assert(OA::PER == 2 && OB::PER == 2, "wait_dma_stages<4>: 4 loads per stage");
+    wait_dma_stages<2 * OA::PER>(pre - 1);
+    __syncthreads();
+    asm volatile("" ::"s"(C), "s"(ldc), "s"(beta), "s"(bias), "s"(epi));
+    bf16x8 f0a[FM], f0b[FN], f1a[FM], f1b[FN];
+    load_frags<OA, OB, FM, FN, MID_TILE>(stage_ptr(0), 0, wm, wn, lane, f0a, f0b);
+    for (int kt = 0; kt < nk - 1; ++kt) {
+        if (kt + MID_NSTAGE - 1 < nk) issue(kt + MID_NSTAGE - 1);
+        load_frags<OA, OB, FM, FN, MID_TILE>(stage_ptr(kt), 1, wm, wn, lane, f1a, f1b);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_block<FM, FN>(f0a, f0b, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        const int ahead = min(nk - 1, kt + MID_NSTAGE - 1) - (kt + 1);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wait_dma_stages<2 * OA::PER>(ahead);
+        __syncthreads();
+        load_frags<OA, OB, FM, FN, MID_TILE>(stage_ptr(kt + 1), 0, wm, wn, lane, f0a, f0b);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_block<FM, FN>(f1a, f1b, acc);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    load_frags<OA, OB, FM, FN, MID_TILE>(stage_ptr(nk - 1), 1, wm, wn, lane, f1a, f1b);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_block<FM, FN>(f0a, f0b, acc);
+    mfma_block<FM, FN>(f1a, f1b, acc);
+
+    k_tail<TA, TB, FM, FN>(M, N, K, nk, A, lda, B, ldb, m0 + wm, n0 + wn, lane, acc);
+    store_tile<FM, FN, 128>(M, N, beta, C, ldc, bias, epi, m0, n0, wm, wn, lane, acc);
 }
 
 template <bool TA, bool TB>
@@ -886,6 +993,61 @@ int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t*
         DH_TRY(check_launch("dh_gemm_bf16(fast)"));
     }
     return DH_OK;
+}
+
+template <bool TA, bool TB>
+int launch_mid_grid(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
+                    float beta, float* C, int ldc, const Batch& bt) {
+    for (int b0 = 0; b0 < bt.count; b0 += 65535) {   // gridDim.y = batch member
+        const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
+        gemm_bf16_mid_kernel<TA, TB><<<dim3(((M + 127) / 128) * ((N + 127) / 128), nb), 256, 0,
+                                       stream()>>>(
+            M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB, ldb, beta, C + b0 * bt.sC, ldc, bt.sA,
+            bt.sB, bt.sC, bt.bias, bt.epi);
+        DH_TRY(check_launch("dh_gemm_bf16(mid)"));
+    }
+    return DH_OK;
+}
+
+// One product whose 128 x 128 tiles fill at most half the CUs with a long contraction (weight
+// gradients, K = the batch; 512 x 512 x 8192) splits K into S chunks of Kc (a multiple of 32,
+// the last chunk taking the rest) run as batch members of the same kernel, each writing an fp32
+// partial, which splitk_reduce_launch adds in a fixed order (reruns stay bit-identical) with
+// beta, the bias and ReLU.  The partials cost 8 S M N bytes of HBM traffic, so S aims at only
+// 2 work-groups per CU, at most 16 chunks of at least 256, and K below 2048 is not split
+// (1024^3: 13.4 us unsplit against 27.7 us in 8 chunks; 512^2 x 8192: 79 us unsplit, 34 us in
+// 32 chunks).
+template <bool TA, bool TB>
+int launch_mid(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
+               float beta, float* C, int ldc, const Batch& bt) {
+    const int tiles = ((M + 127) / 128) * ((N + 127) / 128);
+    const int cus = num_cus();
+    static const bool split_on = [] {
+        const char* e = std::getenv("DH_GEMM_BF16_SPLITK");   // tuning knob: 0 or 1
+        return !e || std::atoi(e) != 0;
+    }();
+    if (split_on && bt.count == 1 && 2 * tiles <= cus && K >= 2048) {
+        int S = 2 * cus / tiles;
+        S = S > 16 ? 16 : S;
+        S = S > K / 256 ? K / 256 : S;
+        const int Kc = K / S / 32 * 32;
+        float* part = static_cast<float*>(dh_malloc((size_t)S * M * N * sizeof(float)));
+        if (part) {
+            const long long MN = (long long)M * N;
+            const Batch pb{TA ? (long long)Kc * lda : Kc, TB ? Kc : (long long)Kc * ldb, MN, S - 1,
+                           nullptr, 0};
+            int st = launch_mid_grid<TA, TB>(M, N, Kc, A, lda, B, ldb, 0.f, part, N, pb);
+            if (st == DH_OK)
+                st = launch_mid_grid<TA, TB>(M, N, K - (S - 1) * Kc, A + (S - 1) * pb.sA, lda,
+                                             B + (S - 1) * pb.sB, ldb, 0.f, part + (S - 1) * MN, N,
+                                             Batch{0, 0, 0, 1, nullptr, 0});
+            if (st == DH_OK) st = splitk_reduce_launch(part, S, M, N, beta, C, ldc, bt.bias, bt.epi);
+            dh_free(part);   // pooled; later users of the buffer are ordered on the stream
+            return st;
+        }
+        // no workspace: the one-pass grid
+    }
+    return launch_mid_grid<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 
 template <bool TA, bool TB>
@@ -937,23 +1099,31 @@ uint16_t* aligned_copy(const uint16_t* src, int rows, int cols, int ld, int& ld_
 template <bool TA, bool TB>
 int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
            float beta, float* C, int ldc, const Batch& bt) {
-    // The direct-to-LDS path needs 16-byte operand rows (aligned bases, leading dimensions
-    // and batch strides in multiples of 8 elements) and at least one round of 256 x 256 tiles.
-    // Ragged M and N are edge tiles of it, a K that is not a multiple of 32 ends with the
-    // kernel's masked tail steps (a DMA'd k-contiguous tile would read the next row's values,
-    // possibly non-finite, past K); rows that are not 16-byte aligned are copied to aligned
-    // ones first (one product: a pass over the operand, where the general kernel on such
-    // rows takes ~5-10x the fast path's time).
+    // The direct-to-LDS paths need 16-byte operand rows (aligned bases, leading dimensions
+    // and batch strides in multiples of 8 elements): 256 x 256 tiles when they make at least
+    // one round of the CUs, else 128 x 128 (DH_GEMM_BF16_MID=0 sends those shapes to the
+    // general kernel instead).  Ragged M and N are edge tiles, a K that is not a multiple of
+    // 32 ends with the kernels' masked tail steps (a DMA'd k-contiguous tile would read the
+    // next row's values, possibly non-finite, past K); rows that are not 16-byte aligned are
+    // copied to aligned ones first (one product, and for the 128 x 128 path one of at least
+    // 2^22 multiply-adds: a pass over the operand and a launch, where the general kernel on
+    // such rows takes ~5-10x the direct-to-LDS time).
+    static const bool mid_on = [] {
+        const char* e = std::getenv("DH_GEMM_BF16_MID");   // tuning knob: 0 or 1
+        return !e || std::atoi(e) != 0;
+    }();
     const long long tiles = (long long)((M + 255) / 256) * ((N + 255) / 256) * bt.count;
+    const bool mid = tiles < num_cus();
     const int K32 = K - K % 32;
     const long long a_bytes = 2LL * ((TA ? K : M) + 255) * lda,
                     b_bytes = 2LL * ((TB ? N : K) + 255) * ldb;
-    if (K32 == 0 || tiles < num_cus() || a_bytes >= (1LL << 32) || b_bytes >= (1LL << 32))
+    if (K32 == 0 || (mid && !mid_on) || a_bytes >= (1LL << 32) || b_bytes >= (1LL << 32))
         return launch_general<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
     const bool va = ((uintptr_t)A % 16 == 0) && (lda % 8 == 0) && (bt.sA % 8 == 0);
     const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 8 == 0) && (bt.sB % 8 == 0);
     if (!va || !vb) {
-        if (bt.count > 1) return launch_general<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+        if (bt.count > 1 || (mid && (long long)M * N * K < (1LL << 22)))
+            return launch_general<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
         int la = lda, lb = ldb;
         uint16_t* a2 = va ? nullptr : aligned_copy(A, TA ? K : M, TA ? M : K, lda, la);
         uint16_t* b2 = vb ? nullptr : aligned_copy(B, TB ? N : K, TB ? K : N, ldb, lb);
@@ -966,7 +1136,8 @@ int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, i
         if (b2) dh_free(b2);
         return st;
     }
-    return launch_fast<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
+    return mid ? launch_mid<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt)
+               : launch_fast<TA, TB>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 
 }  // namespace

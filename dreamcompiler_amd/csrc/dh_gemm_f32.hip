@@ -1142,6 +1142,15 @@ __global__ void __launch_bounds__(256) conv_flip_kernel(const float* __restrict_
 }
 
 }  // namespace
+
+int splitk_reduce_launch(const float* part, int S, int M, int N, float beta, float* C, int ldc,
+                         const float* bias, int epi) {
+    size_t blocks = ((size_t)M * N + 255) / 256;
+    if (blocks > (size_t)num_cus() * 8) blocks = (size_t)num_cus() * 8;
+    splitk_reduce<<<(unsigned)blocks, 256, 0, stream()>>>(part, S, M, N, beta, C, ldc, bias, epi);
+    return check_launch("split-K reduce");
+}
+
 }  // namespace dh
 
 using namespace dh;

@@ -549,3 +549,94 @@ def test_bf16_ragged_k_tail_keeps_nonfinite_values_in_their_row():
     A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
     rows = np.where(ok)[0][::97]
     assert maxrel(got[rows], A64[rows] @ B64) <= 1e-5 * np.sqrt(K)
+
+
+# The 128 x 128 direct-to-LDS path: shapes whose 256 x 256 tiles do not make one round of
+# the CUs.  1..5 stages of 32 k (ring fill and drain), K tails, ragged edge tiles, a grid
+# of more than two tiles per CU (3000^2), one-tile and one-row products, and split K (at most
+# half the CUs' worth of tiles and K >= 2048: 784 x 257 x 4096, 512^2 x 8192, 300 x 200 x 2048,
+# 1000 x 700 x 2100, chunks whose last one takes the rest of K); every element against fp64
+# on the bf16-rounded inputs.
+MID = [(2048, 2048, 2048), (128, 128, 32), (256, 384, 64), (129, 255, 96), (300, 200, 128),
+       (1000, 1900, 160), (2000, 1900, 1000), (3000, 3000, 500), (1, 64, 64), (70, 1, 33),
+       (4096, 10, 257), (784, 257, 4096), (512, 512, 8192), (300, 200, 2048), (1000, 700, 2100)]
+
+
+@pytest.mark.parametrize("M,N,K", MID)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_mid_path(M, N, K, ta, tb):
+    rng = np.random.default_rng(M + 5 * N + 9 * K + 11 * ta + 13 * tb)
+    A = bf16_bits(rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32))
+    C0 = rng.standard_normal((M, N), dtype=np.float32)
+    got = gemm(A, B, bool(ta), bool(tb), beta=0.75, C0=C0, dtype="bf16")
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    opA, opB = (A64.T if ta else A64), (B64.T if tb else B64)
+    ref = opA @ opB + 0.75 * C0.astype(np.float64)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+@pytest.mark.parametrize("Bt,M,N,K", [(3, 500, 300, 200), (2, 1024, 1024, 97), (1, 256, 384, 4099)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("relu,row_bias", [(False, False), (True, False), (True, True)])
+def test_bf16_mid_path_batched_epilogue(Bt, M, N, K, ta, tb, relu, row_bias):
+    got, ref = _ex("bf16", ta, tb, Bt, M, N, K, beta=-0.5, bias=True, relu=relu,
+                   seed=Bt + M + K, row_bias=row_bias)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_bf16_mid_path_k_tail_keeps_nonfinite_values_in_their_row():
+    M, N, K = 1000, 900, 300
+    rng = np.random.default_rng(6)
+    Af = rng.standard_normal((M, K), dtype=np.float32)
+    Af[500, K - 1] = np.nan
+    Af[501, 0] = np.inf
+    A = bf16_bits(Af)
+    B = bf16_bits(rng.standard_normal((K, N), dtype=np.float32))
+    got = gemm(A, B, dtype="bf16")
+    bad = np.where(~np.isfinite(got).all(axis=1))[0]
+    assert set(bad.tolist()) == {500, 501}
+    ok = np.isfinite(got).all(axis=1)
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    assert maxrel(got[ok], A64[ok] @ B64) <= 1e-5 * np.sqrt(K)
+
+
+def test_bf16_mid_split_k_is_deterministic():
+    # the partials are added in a fixed order: reruns are bit-identical
+    rng = np.random.default_rng(17)
+    A = bf16_bits(rng.standard_normal((600, 5000), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((5000, 500), dtype=np.float32))
+    first = gemm(A, B, dtype="bf16")
+    for _ in range(3):
+        assert np.array_equal(gemm(A, B, dtype="bf16"), first)
+
+
+_MID_OFF_SCRIPT = r"""
+import sys, numpy as np
+sys.path[:0] = [{tests!r}, {root!r}]
+from _gpu import bf16_bits, bits_to_f32, gemm, maxrel
+for M, N, K in [(2048, 2048, 2048), (129, 255, 96), (1000, 1900, 160)]:
+    for ta, tb in [(0, 0), (0, 1), (1, 0), (1, 1)]:
+        rng = np.random.default_rng(M + N + K + ta + 2 * tb)
+        A = bf16_bits(rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32))
+        B = bf16_bits(rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32))
+        got = gemm(A, B, bool(ta), bool(tb), dtype="bf16")
+        A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+        e = maxrel(got, (A64.T if ta else A64) @ (B64.T if tb else B64))
+        print("general", M, N, K, ta, tb, e, flush=True)
+        assert e <= 1e-5 * np.sqrt(K), e
+"""
+
+
+def test_bf16_mid_shapes_on_the_general_kernel():
+    # DH_GEMM_BF16_MID=0 (read once per process): the same shapes on the register-staged
+    # general kernel, which still serves K < 32 and operands past 4 GB.
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = _MID_OFF_SCRIPT.format(tests=here, root=os.path.dirname(here))
+    r = subprocess.run([sys.executable, "-c", code], env={**os.environ, "DH_GEMM_BF16_MID": "0"},
+                       capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.count("general") == 12, r.stdout
