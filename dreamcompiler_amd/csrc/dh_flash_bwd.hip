@@ -167,8 +167,11 @@ __device__ inline void wait_dma(int ahead) {     // at most `ahead` stages of PE
 //    step of the loop consumes two stages, and at the end the odd-stage waves hand their
 //    partial dK, dV to their partner through LDS, which adds and stores them (a fixed
 //    order: results stay bit-identical run to run).  K and V of the 128 keys stay in LDS;
-//    Q, dO and each stage's LSE*log2(e) and Dvec stream through a 4-stage ring (two
-//    steps).  S = Q K^T and dP = dO V^T come out with lane = key j and register r = query
+//    Q, dO and each step's LSE*log2(e) and Dvec stream through a 4-stage ring (two steps),
+//    all of a step's DMA issued by the even-stage waves so that the odd-stage ones start
+//    computing right after the step barrier (when both waves of a SIMD stalled on their
+//    issue at once, the backward took 1.2-1.6% longer in a same-box A/B).
+//    S = Q K^T and dP = dO V^T come out with lane = key j and register r = query
 //    8 (r / 4) + 4 h + r % 4; P and dS feed dV^T += dO^T P and dK^T += Q^T dS straight from
 //    those registers.
 // ---------------------------------------------------------------------------------
@@ -189,12 +192,13 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
     using R = BwTile<D, KV_KEYS>;                    // resident K, V of the work-group's keys
     constexpr int ND = D / 32, NTK = D / 16;
     constexpr int VEC = 2 * T::TILE;                 // 1 KB of LSE*log2(e), then 1 KB of Dvec
+                                                     // (a step's, in its first stage's slot)
     constexpr int STAGE = VEC + 2048;
     constexpr int KVRES = KV_NSTAGE * STAGE;         // K tile, then V tile, after the ring
     constexpr int PERR = 2 * R::NBLK / KV_WAVES;     // resident blocks per wave
-    constexpr int PER = 4 * T::NBLK / KV_WAVES;      // tile blocks per wave per step
+    constexpr int PER = 4 * T::NBLK / 4;             // tile blocks per even-stage wave per step
     static_assert(PERR >= 1 && PERR * KV_WAVES == 2 * R::NBLK, "resident tiles must split");
-    static_assert(PER >= 1 && PER * KV_WAVES == 4 * T::NBLK, "a step must split over the waves");
+    static_assert(PER >= 1 && PER * 4 == 4 * T::NBLK, "a step must split over the waves");
     static_assert(KV_WAVES * 64 * 32 * ND * 4 / 2 <= KVRES + 2 * R::TILE, "reduction fits LDS");
     extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
@@ -220,14 +224,14 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
     const int s_end = (nst - par + 1) >> 1;
     const int s_first = min((wfirst - par + 1) >> 1, s_end);
 
-    // DMA share per step: tile blocks w + 8 q over (stage in step, tile, block), plus one
-    // vector block (waves w and w + 4 load the same one).
+    // DMA share per step of the even-stage waves w < 4: tile blocks w + 4 q over (stage in
+    // step, tile, block), plus one vector block for waves 0 (LSE) and 1 (Dvec).
     uint32_t dlds[PER], dvoff[PER];
     int dsis[PER];
     bool dq_[PER];
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
-        const int gb = wave + KV_WAVES * q;
+        const int gb = (wave & 3) + 4 * q;
         const int sis = gb / (2 * T::NBLK), rem = gb % (2 * T::NBLK);
         const int tile = rem / T::NBLK, b = rem % T::NBLK;
         dsis[q] = sis;
@@ -235,23 +239,24 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
         dlds[q] = sis * STAGE + tile * T::TILE + b * 1024;
         dvoff[q] = T::dma_voff(b, lane, true);
     }
-    const int vsis = (wave & 3) >> 1;
-    const bool vlse = (wave & 1) == 0;
     auto issue_step = [&](int sp) {
         const uint32_t sb = ring_lds + ((2 * sp) % KV_NSTAGE) * STAGE;
+        if (wave < 4) {
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i0 = qstart + (2 * sp + dsis[q]) * KV_BQ;
-            const u32x4 rs = make_rsrc((dq_[q] ? Q : dO) + base + (size_t)min(i0, S) * D,
-                                       (uint32_t)max(S - i0, 0) * T::ROWB);
-            lds_dma16_buf(dvoff[q], rs, __builtin_amdgcn_readfirstlane(sb + dlds[q]));
+            for (int q = 0; q < PER; ++q) {
+                const int i0 = qstart + (2 * sp + dsis[q]) * KV_BQ;
+                const u32x4 rs = make_rsrc((dq_[q] ? Q : dO) + base + (size_t)min(i0, S) * D,
+                                           (uint32_t)max(S - i0, 0) * T::ROWB);
+                lds_dma16_buf(dvoff[q], rs, __builtin_amdgcn_readfirstlane(sb + dlds[q]));
+            }
         }
-        // 256 floats of LSE*log2(e) or Dvec from the stage's first query
-        const int i0 = qstart + (2 * sp + vsis) * KV_BQ;
-        const u32x4 rv = make_rsrc((vlse ? L2 : Dv) + (size_t)bh * S + min(i0, S),
-                                   (uint32_t)max(S - i0, 0) * 4);
-        lds_dma16_buf(16 * lane, rv,
-                      __builtin_amdgcn_readfirstlane(sb + vsis * STAGE + VEC + (vlse ? 0 : 1024)));
+        // 256 floats of LSE*log2(e) (wave 0) or Dvec (wave 1) from the step's first query
+        if (wave < 2) {
+            const int i0 = qstart + 2 * sp * KV_BQ;
+            const u32x4 rv = make_rsrc((wave == 0 ? L2 : Dv) + (size_t)bh * S + min(i0, S),
+                                       (uint32_t)max(S - i0, 0) * 4);
+            lds_dma16_buf(16 * lane, rv, __builtin_amdgcn_readfirstlane(sb + VEC + 1024 * wave));
+        }
     };
 
     // K and V of the work-group's keys stay in LDS for the whole kernel (loaded first, so
@@ -309,7 +314,8 @@ bwd_dkdv_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __re
     auto compute = [&](int st) {
         const uint8_t* qt = ring + (st % KV_NSTAGE) * STAGE;
         const uint8_t* gt = qt + T::TILE;
-        const float* vec = reinterpret_cast<const float*>(qt + VEC);
+        const float* vec =   // the step's vectors, this stage's 32 queries
+            reinterpret_cast<const float*>(ring + ((st & ~1) % KV_NSTAGE) * STAGE + VEC) + 32 * (st & 1);
         const int i0 = qstart + st * KV_BQ;
         constexpr int EPC = 16 / NTK;                // exponentials per dP chunk
         constexpr int NP = 2 * ND;                   // dV, dK MFMAs per k-step
