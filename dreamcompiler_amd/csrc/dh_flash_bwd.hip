@@ -530,6 +530,13 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
         }
     };
 
+    // The first stages' DMA goes out before the row loads below, so that the two fetches
+    // overlap (the compiler's wait for the rows is a full vmcnt(0): it cannot count the DMA,
+    // so these stages have landed by the loop).
+#pragma unroll
+    for (int st = 0; st < DQ_NSTAGE - 1; ++st)
+        if (st < nst) issue(st);
+
     // Q and dO rows of this lane's query as B operands: Q[i][16t + 8h .. +7].  The same
     // elements of O give the lane half of Dvec_i = dO_i . O_i; the two halves (lanes l and
     // l ^ 32) are added, and -Dvec_i and LSE_i log2(e) are stored for the dK/dV launch.
@@ -584,9 +591,6 @@ bwd_dq_bf16_kernel(int BH, int S, float scale, float sl2, const uint16_t* __rest
         for (int r = 0; r < 16; ++r) dqacc[d][r] = 0.f;
     const int lim = CAUSAL ? min(i, S - 1) : S - 1;   // last key this query sees
 
-#pragma unroll
-    for (int st = 0; st < DQ_NSTAGE - 1; ++st)
-        if (st < nst) issue(st);
     for (int st = 0; st < nst; ++st) {
         wait_dma<PER>(min(nst - 1 - st, DQ_NSTAGE - 2));
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");

@@ -175,19 +175,9 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
     auto ahead_k = [](int st) { return W == 8 ? st + BF_NSTAGE - 1 : st + 2; };
     auto ahead_v = [](int st) { return W == 8 ? st + BF_NSTAGE - 1 : st + 1; };
 
-    // Q fragments (B operand of S^T = K Q^T): lane (i, h) holds Q[i][16t + 8h .. +7].
+    // Q fragments (B operand of S^T = K Q^T): lane (i, h) holds Q[i][16t + 8h .. +7]; loaded
+    // in the prologue below.
     bf16x8 qf[NTK];
-    {
-        const int i = min(r0 + l32, S - 1);
-#pragma unroll
-        for (int t = 0; t < NTK; ++t)
-            qf[t] = __builtin_bit_cast(
-                bf16x8, *reinterpret_cast<const u32x4*>(Qg + (size_t)i * D + 16 * t + 8 * h));
-        // Consume Q here: the compiler's own wait for these loads then sits before the
-        // loop instead of inside it, where it would also drain the prefetched stages.
-#pragma unroll
-        for (int t = 0; t < NTK; ++t) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, qf[t])));
-    }
     // Byte offsets of this lane's fragment reads inside a K / V tile.
     uint32_t kofs[NTK], vofs[ND];
 #pragma unroll
@@ -389,21 +379,32 @@ flash_fwd_bf16_kernel(int BH, int S, float sl2, const uint16_t* __restrict__ Q,
         return overlap(st, cur, nxt);
     };
 
+    // Prologue: the first stages' DMA, then the Q rows, so that the two fetches overlap (Q
+    // comes from HBM; with the Q wait first, a work-group spent both latencies in series).
     if constexpr (W == 8) {
 #pragma unroll
         for (int st = 0; st < BF_NSTAGE - 1; ++st)
             if (st < nst) issue(st, st);
-        // prologue: S(0) and its max
-        if (nst > 2) wait_vmcnt<2 * T::PER>();          // stage 0 landed, 1 and 2 may fly
-        else if (nst == 2) wait_vmcnt<T::PER>();
-        else wait_vmcnt<0>();
     } else {
         static_assert(W == 8 || T::NBLK % 4 == 0, "4 waves: blocks q < PER / 2 are K's");
         issue(0, 0);                                    // K(0), V(0)
 #pragma unroll
         for (int q = 0; q < T::PER / 2; ++q) issue_one(1, 0, q);   // K(1)
-        wait_vmcnt<0>();
     }
+    {   // the Q fragments
+        const int i = min(r0 + l32, S - 1);
+#pragma unroll
+        for (int t = 0; t < NTK; ++t)
+            qf[t] = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4*>(Qg + (size_t)i * D + 16 * t + 8 * h));
+        // Consume Q here: the compiler's own wait for these loads then sits before the
+        // loop instead of inside it, where it would also drain the prefetched stages.
+#pragma unroll
+        for (int t = 0; t < NTK; ++t) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, qf[t])));
+    }
+    // (The compiler's wait for Q above is a full vmcnt(0): it cannot count the DMA, so the
+    // stages issued before the Q loads have landed too.)
+    wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
     f32x16 sa[2], sb[2];
     float mx = 0.f;
