@@ -1100,9 +1100,11 @@ template <bool TA, bool TB>
 int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
            float beta, float* C, int ldc, const Batch& bt) {
     // The direct-to-LDS paths need 16-byte operand rows (aligned bases, leading dimensions
-    // and batch strides in multiples of 8 elements): 256 x 256 tiles when they make at least
-    // one round of the CUs, else 128 x 128 (DH_GEMM_BF16_MID=0 sends those shapes to the
-    // general kernel instead).  Ragged M and N are edge tiles, a K that is not a multiple of
+    // and batch strides in multiples of 8 elements): 256 x 256 tiles when there are more of
+    // them than half the CUs, else 128 x 128 (DH_GEMM_BF16_MID=0 sends those shapes to the
+    // general kernel instead).  Between half a round and a round the 256 tiles, one per CU
+    // with some CUs idle, still beat four times as many 128 tiles (same box: 3840^3 125 against
+    // 158 us, 3072^3 79 against 99 us; 2048 x 4096, 128 tiles, 45-50 us either way).  Ragged M and N are edge tiles, a K that is not a multiple of
     // 32 ends with the kernels' masked tail steps (a DMA'd k-contiguous tile would read the
     // next row's values, possibly non-finite, past K); rows that are not 16-byte aligned are
     // copied to aligned ones first (one product, and for the 128 x 128 path one of at least
@@ -1113,7 +1115,11 @@ int launch(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, i
         return !e || std::atoi(e) != 0;
     }();
     const long long tiles = (long long)((M + 255) / 256) * ((N + 255) / 256) * bt.count;
-    const bool mid = tiles < num_cus();
+    static const int mid_max = [] {   // tuning knob: most 256 x 256 tiles for the 128 path
+        const char* e = std::getenv("DH_GEMM_BF16_MID_MAX_TILES");
+        return e ? std::atoi(e) : -1;   // default: num_cus() / 2
+    }();
+    const bool mid = tiles <= (mid_max >= 0 ? mid_max : num_cus() / 2);
     const int K32 = K - K % 32;
     const long long a_bytes = 2LL * ((TA ? K : M) + 255) * lda,
                     b_bytes = 2LL * ((TB ? N : K) + 255) * ldb;

@@ -601,6 +601,24 @@ def test_bf16_mid_path_k_tail_keeps_nonfinite_values_in_their_row():
     assert maxrel(got[ok], A64[ok] @ B64) <= 1e-5 * np.sqrt(K)
 
 
+# Between half a round and a round of 256 x 256 tiles the fast kernel runs a partial round
+# (144, 224 and 225 tiles here), at the boundary (128 tiles) the 128 x 128 path.
+@pytest.mark.parametrize("M,N,K", [(3000, 3000, 300), (3500, 4000, 96), (3840, 3840, 33),
+                                   (2048, 4096, 160)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_bf16_partial_round_of_256_tiles(M, N, K, ta, tb):
+    rng = np.random.default_rng(M + N + K + ta)
+    A = bf16_bits(rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32))
+    C0 = rng.standard_normal((M, N), dtype=np.float32)
+    got = gemm(A, B, bool(ta), bool(tb), beta=0.5, C0=C0, dtype="bf16")
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    opA, opB = (A64.T if ta else A64), (B64.T if tb else B64)
+    rows = np.sort(np.concatenate([rng.choice(M, 40, replace=False), [0, M - 1]]))
+    assert maxrel(got[rows], opA[rows] @ opB + 0.5 * C0[rows].astype(np.float64)) <= 1e-5 * np.sqrt(K)
+    _rowcol_sums_check(got - 0.5 * C0, opA, opB, 1e-5)
+
+
 def test_bf16_mid_split_k_is_deterministic():
     # the partials are added in a fixed order: reruns are bit-identical
     rng = np.random.default_rng(17)
