@@ -608,12 +608,12 @@ __device__ inline void store_tile(int M, int N, float beta, float* __restrict__ 
     }
 }
 
-// WAVES = 4 (TN, TT): 2 x 2 waves of 128 x 128 (one wave per SIMD, 256 accumulators in
-// AGPRs), reads and DMA issues interleaved op by op.
-// WAVES = 8 (NN, NT): 2 x 4 waves of 128 x 64 (two waves per SIMD, 128 accumulators each, so
-// one wave's MFMAs cover the other's barrier and LDS-read gaps), which reads 1.5x the LDS
-// fragment bytes per matrix-core op.  DEEP8: a k-contiguous A in 64-k double stages on 8
-// waves (the launch's default for NN and NT; off only through the tuning knob).
+// WAVES = 4 (DH_GEMM_BF16_WAVES=4): 2 x 2 waves of 128 x 128 (one wave per SIMD, 256
+// accumulators in AGPRs), reads and DMA issues interleaved op by op.
+// WAVES = 8 (the default): 2 x 4 waves of 128 x 64 (two waves per SIMD, 128 accumulators
+// each, so one wave's MFMAs cover the other's barrier and LDS-read gaps), which reads 1.5x the
+// LDS fragment bytes per matrix-core op.  DEEP8: a k-contiguous A (NN, NT) in 64-k double
+// stages on 8 waves (the default for those; off only through the tuning knob).
 template <bool TA, bool TB, int WAVES, bool DEEP8>
 __global__ void __launch_bounds__(64 * WAVES)
 gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
@@ -967,17 +967,19 @@ gemm_bf16_mid_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int ld
 template <bool TA, bool TB>
 int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t* B, int ldb,
                 float beta, float* C, int ldc, const Batch& bt) {
-    // Default: 8 waves (two per SIMD) with A in 64-k double stages for a k-contiguous A (NN,
-    // NT), 4 waves (one per SIMD) for TN and TT.  Same-box A/B at 8192^3 (ms): NN 0.803 (8
-    // waves, 64-k A) / 0.860 (8 waves, 32-k A) / 0.85-0.87 (4 waves, 64-k A); NT 0.795 / 0.857
-    // / 0.836; TN 0.865 on 8 waves against 0.838 on 4, TT 0.865 against 0.860.  The 32-k
-    // stages fetch half an L2 line per row of a k-contiguous operand (the next stage fetches
-    // the other half again): 40% more L2 requests than the vendor library for the same bytes.
+    // Default: 8 waves (two per SIMD), with A in 64-k double stages when it is k-contiguous
+    // (NN, NT).  Same-box A/B at 8192^3 (ms): NN 0.803 (8 waves, 64-k A) / 0.860 (8 waves, 32-k
+    // A) / 0.85-0.87 (4 waves, 64-k A); NT 0.795 / 0.857 / 0.836.  TN and TT (k-contiguous B
+    // only): within 1-3% of each other on 4 and 8 waves at 8192^3 and 4096^3 (either ahead,
+    // by box), and 8 waves ahead at shorter K: 8192 x 8192 x 1024 TN 176 against 226 us, TT 176
+    // against 195; K = 2048 TN 287 against 323 us.  The 32-k stages fetch half an L2 line per row of a
+    // k-contiguous operand (the next stage fetches the other half again): 40% more L2
+    // requests than the vendor library for the same bytes.
     static const int env_waves = [] {
         const char* e = std::getenv("DH_GEMM_BF16_WAVES");   // tuning knob: 4 or 8
         return e ? (std::atoi(e) == 8 ? 8 : 4) : 0;
     }();
-    const int waves = env_waves ? env_waves : (!TA ? 8 : 4);
+    const int waves = env_waves ? env_waves : 8;
     static const bool deep8 = [] {
         const char* e = std::getenv("DH_GEMM_BF16_DEEP8");   // tuning knob: 0 or 1
         return !e || std::atoi(e) != 0;

@@ -187,10 +187,10 @@ def test_c5_bf16_8192_full_size():
     _rowcol_sums_check(got, A64, B64, 1e-5)
 
 
-# 1..10 stages of 32 k.  Default forms: NN and NT on 8 waves with a k-contiguous A in double
-# stages of 64 k (so odd stage counts, 1, 3, 5, end on half a pair), TN and TT on 4 waves (one
-# per SIMD).  The other forms, reachable through DH_GEMM_BF16_WAVES / DH_GEMM_BF16_DEEP8, are
-# covered by test_bf16_fast_path_knob_variants.
+# 1..10 stages of 32 k.  Default forms: 8 waves, NN and NT with a k-contiguous A in double
+# stages of 64 k (so odd stage counts, 1, 3, 5, end on half a pair), TN and TT in 32-k stages.
+# The other forms, reachable through DH_GEMM_BF16_WAVES / DH_GEMM_BF16_DEEP8, are covered by
+# test_bf16_fast_path_knob_variants.
 @pytest.mark.parametrize("K", [32, 64, 96, 160, 256, 320])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_bf16_tile_aligned_fast_path(K, ta, tb):
@@ -254,8 +254,8 @@ for K in (32, 96, 160, 320):
 
 
 # The fast path's form is chosen once per process from the environment, so each runs in a
-# child process of its own: 8 waves for all four layouts (TN and TT with 64-k A stages too),
-# 4 waves for all four (NN and NT included), and 8 waves with 32-k A stages
+# child process of its own: 8 waves set explicitly (the default), 4 waves for all four layouts
+# (NN and NT with 64-k A stages), and 8 waves with 32-k A stages for NN and NT
 # (DH_GEMM_BF16_DEEP8=0), each over odd and even stage counts.
 @pytest.mark.parametrize("env", [{"DH_GEMM_BF16_WAVES": "8"}, {"DH_GEMM_BF16_WAVES": "4"},
                                  {"DH_GEMM_BF16_DEEP8": "0"}],
