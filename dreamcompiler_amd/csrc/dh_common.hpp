@@ -195,6 +195,18 @@ __device__ inline void wait_vmcnt() {
 }
 
 // ---- XCD-aware tile order --------------------------------------------------------
+// Logical tile index -> (tile row, tile column), walking groups of `group_m` tile-rows.
+__device__ inline void grouped_tile(int logical, int tiles_m, int tiles_n, int group_m, int& tm,
+                                    int& tn) {
+    const int width = group_m * tiles_n;
+    const int group = logical / width;
+    const int first_m = group * group_m;
+    const int gsz = min(tiles_m - first_m, group_m);
+    const int in = logical - group * width;
+    tm = first_m + in % gsz;
+    tn = in / gsz;
+}
+
 // Work-groups are dealt round-robin to the 8 XCDs (block b runs on XCD b % 8).
 // Remap so that each XCD receives a contiguous run of logical tiles, then walk
 // tiles in groups of `group_m` tile-rows so neighbouring tiles on one XCD share
@@ -206,13 +218,7 @@ __device__ inline void xcd_tile_order(int bid, int nblocks, int tiles_m, int til
         const int per = nblocks >> 3;
         logical = (bid & 7) * per + (bid >> 3);
     }
-    const int width = group_m * tiles_n;
-    const int group = logical / width;
-    const int first_m = group * group_m;
-    const int gsz = min(tiles_m - first_m, group_m);
-    const int in = logical - group * width;
-    tm = first_m + in % gsz;
-    tn = in / gsz;
+    grouped_tile(logical, tiles_m, tiles_n, group_m, tm, tn);
 }
 
 // Work-group -> (slice bh, tile rank rr) for BH slices x n_t tiles per slice.  Work-groups are

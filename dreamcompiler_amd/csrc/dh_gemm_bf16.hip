@@ -619,7 +619,7 @@ __global__ void __launch_bounds__(64 * WAVES)
 gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int lda,
                       const uint16_t* __restrict__ B, int ldb, float beta, float* __restrict__ C,
                       int ldc, long long sA, long long sB, long long sC,
-                      const float* __restrict__ bias, int epi) {
+                      const float* __restrict__ bias, int epi, int tile0, int tail) {
     A += blockIdx.y * sA;   // batch member blockIdx.y
     B += blockIdx.y * sB;
     C += blockIdx.y * sC;
@@ -642,7 +642,9 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     // Each XCD's 32 tiles in flight form a 4 x 8 block (4 A panels, 8 B panels).  Same-box
     // A/B at 8192^3 (NN, ms): groups of 4 tile rows 0.862-0.867, 8 rows (8 x 4 blocks)
     // 0.879-0.881, 2: 0.893, 3: 0.889, 5: 0.894, 6: 0.885, 16: 0.903.
-    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 4, tm, tn);
+    // tail: the K chunk blockIdx.y of logical tile tile0 + blockIdx.x (no XCD remap)
+    if (tail) grouped_tile(tile0 + blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
+    else xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 4, tm, tn);
     const int m0 = tm * 256, n0 = tn * 256;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -875,7 +877,42 @@ gemm_bf16_fast_kernel(int M, int N, int K, const uint16_t* __restrict__ A, int l
     }
 
     k_tail<TA, TB, FM, FN>(M, N, K, nk, A, lda, B, ldb, m0 + wm, n0 + wn, lane, acc);
+    if (tail) {   // the tile's fp32 partial, compact: 256 x 256 at C + 65536 blockIdx.x
+        store_tile<FM, FN, 256>(min(M - m0, 256), min(N - n0, 256), 0.f,
+                                C + (size_t)blockIdx.x * 65536, 256, nullptr, 0, 0, 0, wm, wn,
+                                lane, acc);
+        return;
+    }
     store_tile<FM, FN, 256>(M, N, beta, C, ldc, bias, epi, m0, n0, wm, wn, lane, acc);
+}
+
+// The partial last round of a split product (launch_fast): C = beta C + sum_s part[s] (in
+// order, so reruns are bit-identical) + bias, then ReLU, for the R tail tiles (logical tiles
+// tile0 + r), each part[s] tile compact (256 x 256, row stride 256, tile r at 65536 r, chunk s
+// at sstride s).  Work-group (r, 4-row block), 4 columns per thread.
+__global__ void __launch_bounds__(256)
+tail_reduce(const float* __restrict__ part, int S, long long sstride, int tile0, int tiles_m,
+            int tiles_n, int M, int N, float beta, float* __restrict__ C, int ldc,
+            const float* __restrict__ bias, int epi) {
+    const int r = blockIdx.x >> 6, i = 4 * (blockIdx.x & 63) + (threadIdx.x >> 6);
+    const int j = 4 * (threadIdx.x & 63);
+    int tm, tn;
+    grouped_tile(tile0 + r, tiles_m, tiles_n, 4, tm, tn);
+    const int row = tm * 256 + i, col0 = tn * 256 + j;
+    if (row >= M || col0 >= N) return;
+    const float* p = part + (size_t)r * 65536 + i * 256 + j;
+    f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    for (int s = 1; s < S; ++s) v += *reinterpret_cast<const f32x4*>(p + s * sstride);
+    const bool row_bias = bias && (epi & DH_EPI_ROW_BIAS);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int col = col0 + e;
+        if (col >= N) break;
+        float* c = C + (size_t)row * ldc + col;
+        float x = (beta == 0.f ? v[e] : v[e] + beta * *c) + (bias ? bias[row_bias ? row : col] : 0.f);
+        if (epi & DH_EPI_RELU) x = x < 0.f ? 0.f : x;
+        *c = x;
+    }
 }
 
 // ---------------------------------------------------------------------------------
@@ -987,11 +1024,59 @@ int launch_fast(int M, int N, int K, const uint16_t* A, int lda, const uint16_t*
     auto kern = waves == 4 ? gemm_bf16_fast_kernel<TA, TB, 4, false>
               : deep8      ? gemm_bf16_fast_kernel<TA, TB, 8, true>
                            : gemm_bf16_fast_kernel<TA, TB, 8, false>;
+    const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+    const int tiles = tiles_m * tiles_n, cus = num_cus();
+    // One product with K >= 4096 whose last round of tiles fills at most half the CUs: the
+    // full rounds as usual, then the R tiles of the last round split into S chunks of K (a
+    // multiple of 64, the last chunk taking the rest) whose fp32 partials tail_reduce adds in
+    // order with the epilogue: the last round takes about 1/S of a tile's time instead of a
+    // whole one, for two more launches and 8 S R 256^2 bytes of partials.  Same box, µs:
+    // 7000^3 754 -> 701, 4352^3 196 -> 191 (TN 218 -> 204); at K = 1000 and 2048 (4300 x
+    // 4400, 4608 x 4096) the extra launches and partials cost more than they save (83 -> 98,
+    // 107 -> 120), hence the bound on K.
+    static const bool split_tail = [] {
+        const char* e = std::getenv("DH_GEMM_BF16_SPLIT_TAIL");   // tuning knob: 0 or 1
+        return !e || std::atoi(e) != 0;
+    }();
+    const int R = tiles % cus;
+    int S = R > 0 ? cus / R : 0;
+    if (S > K / 256) S = K / 256;
+    if (split_tail && bt.count == 1 && K >= 4096 && tiles > cus && 2 * R <= cus && S >= 2) {
+        const int Kc = K / S / 64 * 64;
+        const long long cstride = 65536LL * R;
+        float* part = static_cast<float*>(dh_malloc((size_t)S * cstride * sizeof(float)));
+        if (part) {
+            const int full = tiles - R;
+            kern<<<dim3(full, 1), 64 * waves, 0, stream()>>>(M, N, K, A, lda, B, ldb, beta, C, ldc,
+                                                            0, 0, 0, bt.bias, bt.epi, 0, 0);
+            int st = check_launch("dh_gemm_bf16(fast)");
+            const long long sA = TA ? (long long)Kc * lda : Kc, sB = TB ? Kc : (long long)Kc * ldb;
+            if (st == DH_OK) {
+                kern<<<dim3(R, S - 1), 64 * waves, 0, stream()>>>(
+                    M, N, Kc, A, lda, B, ldb, 0.f, part, 256, sA, sB, cstride, nullptr, 0, full, 1);
+                st = check_launch("dh_gemm_bf16(fast, split tail)");
+            }
+            if (st == DH_OK) {
+                kern<<<dim3(R, 1), 64 * waves, 0, stream()>>>(
+                    M, N, K - (S - 1) * Kc, A + (S - 1) * sA, lda, B + (S - 1) * sB, ldb, 0.f,
+                    part + (S - 1) * cstride, 256, 0, 0, 0, nullptr, 0, full, 1);
+                st = check_launch("dh_gemm_bf16(fast, split tail)");
+            }
+            if (st == DH_OK) {
+                tail_reduce<<<R * 64, 256, 0, stream()>>>(part, S, cstride, full, tiles_m, tiles_n,
+                                                          M, N, beta, C, ldc, bt.bias, bt.epi);
+                st = check_launch("dh_gemm_bf16(split tail reduce)");
+            }
+            dh_free(part);   // pooled; later users of the buffer are ordered on the stream
+            return st;
+        }
+        // no workspace: the plain grid
+    }
     for (int b0 = 0; b0 < bt.count; b0 += 65535) {   // gridDim.y = batch member
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
-        kern<<<dim3(((M + 255) / 256) * ((N + 255) / 256), nb), 64 * waves, 0, stream()>>>(
+        kern<<<dim3(tiles, nb), 64 * waves, 0, stream()>>>(
             M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB, ldb, beta, C + b0 * bt.sC, ldc, bt.sA,
-            bt.sB, bt.sC, bt.bias, bt.epi);
+            bt.sB, bt.sC, bt.bias, bt.epi, 0, 0);
         DH_TRY(check_launch("dh_gemm_bf16(fast)"));
     }
     return DH_OK;

@@ -619,6 +619,39 @@ def test_bf16_partial_round_of_256_tiles(M, N, K, ta, tb):
     _rowcol_sums_check(got - 0.5 * C0, opA, opB, 1e-5)
 
 
+# More than a round of 256 x 256 tiles with a last round of at most half the CUs and K >= 4096:
+# the full rounds, then the tail tiles split into K chunks (last chunk with the rest, K % 32
+# tails included) reduced in order with the epilogue.  Every element through the row and column
+# sums.
+SPLIT_TAIL = [(4352, 4352, 4352), (4300, 4400, 4100), (4608, 4096, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_TAIL)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_split_tail_round(M, N, K, ta, tb):
+    rng = np.random.default_rng(M + 3 * N + K + 5 * ta + 7 * tb)
+    A = bf16_bits(rng.standard_normal((K, M) if ta else (M, K), dtype=np.float32))
+    B = bf16_bits(rng.standard_normal((N, K) if tb else (K, N), dtype=np.float32))
+    C0 = rng.standard_normal((M, N), dtype=np.float32)
+    got = gemm(A, B, bool(ta), bool(tb), beta=-0.25, C0=C0, dtype="bf16")
+    A64, B64 = bits_to_f32(A).astype(np.float64), bits_to_f32(B).astype(np.float64)
+    opA, opB = (A64.T if ta else A64), (B64.T if tb else B64)
+    rows = np.sort(np.concatenate([rng.choice(M, 48, replace=False), [0, M - 1]]))
+    ref = opA[rows] @ opB - 0.25 * C0[rows].astype(np.float64)
+    assert maxrel(got[rows], ref) <= 1e-5 * np.sqrt(K)
+    _rowcol_sums_check(got + 0.25 * C0, opA, opB, 1e-5)
+
+
+@pytest.mark.parametrize("relu,row_bias", [(False, False), (True, False), (True, True)])
+def test_bf16_split_tail_epilogue_and_reruns(relu, row_bias):
+    got, ref = _ex("bf16", 0, 1, 1, 4300, 4400, 4100, beta=0.5, bias=True, relu=relu,
+                   seed=11, row_bias=row_bias)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(4100)
+    again, _ = _ex("bf16", 0, 1, 1, 4300, 4400, 4100, beta=0.5, bias=True, relu=relu,
+                   seed=11, row_bias=row_bias)
+    assert np.array_equal(got, again)
+
+
 def test_bf16_mid_split_k_is_deterministic():
     # the partials are added in a fixed order: reruns are bit-identical
     rng = np.random.default_rng(17)
