@@ -132,8 +132,11 @@ __global__ void __launch_bounds__(NTHREADS)
 gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
                 const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
                 long long sA, long long sB, long long sC, const float* __restrict__ bias,
-                int epi) {
-    // Batch member blockIdx.y (strides in elements; 0 for a single product).
+                int epi, int k_last) {
+    // Batch member blockIdx.y (strides in elements; 0 for a single product).  In a split-K
+    // launch the members are the chunks of K, and the last one takes the ragged rest, k_last
+    // (= K otherwise).
+    if (blockIdx.y == gridDim.y - 1) K = k_last;
     A += blockIdx.y * sA;
     B += blockIdx.y * sB;
     C += blockIdx.y * sC;
@@ -813,15 +816,62 @@ auto pick_kernel(int M, int N, int K, const float* A, int lda, long long sA, con
                     : gemm_f32_kernel<TA, TB, false, false, TBM, TBN>;
 }
 
+// One grid of the tiled kernel; gridDim.y carries the batch member, in chunks of 65535 (the
+// y limit).
+template <bool TA, bool TB, int TBM, int TBN>
+int launch_grid(int M, int N, int K, const float* A, int lda, const float* B, int ldb,
+                float beta, float* C, int ldc, const Batch& bt) {
+    const int tiles = ((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN);
+    auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, K, A, lda, bt.sA, B, ldb, bt.sB);
+    for (int b0 = 0; b0 < bt.count; b0 += 65535) {
+        const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
+        kern<<<dim3(tiles, nb), NTHREADS, 0, stream()>>>(M, N, K, A + b0 * bt.sA, lda,
+                                                         B + b0 * bt.sB, ldb, beta, C + b0 * bt.sC,
+                                                         ldc, bt.sA, bt.sB, bt.sC, bt.bias, bt.epi, K);
+        DH_TRY(check_launch("dh_gemm_f32"));
+    }
+    return DH_OK;
+}
+
+// One product (bt.count == 1) with K cut into about S chunks (multiples of BK) run as gridDim.y
+// members writing fp32 partials, which splitk_reduce adds in order with the epilogue.
+// DH_ERR_UNSUPPORTED, with nothing launched, when no workspace can be had.
+template <bool TA, bool TB, int TBM, int TBN>
+int launch_split_k(int M, int N, int K, int S, const float* A, int lda, const float* B, int ldb,
+                   float beta, float* C, int ldc, const Batch& bt) {
+    const int tiles = ((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN);
+    hipStream_t s = stream();
+    const int Kc = ((K + S - 1) / S + BK - 1) / BK * BK;   // chunk of K, multiple of BK
+    S = (K + Kc - 1) / Kc;
+    float* part = static_cast<float*>(dh_malloc((size_t)S * M * N * sizeof(float)));
+    if (!part) return DH_ERR_UNSUPPORTED;
+    // chunk j: A columns (or rows, TA) and B rows (or columns, TB) j Kc .. + Kc; the last
+    // chunk K - (S - 1) Kc.  One grid, so the chunks run side by side.  The kernel choice sees
+    // the whole K: 16-byte loads along k only where K is a multiple of 4, so that a ragged last
+    // chunk has no 4-wide group crossing its end.
+    const long long sA = TA ? (long long)Kc * lda : Kc, sB = TB ? Kc : (long long)Kc * ldb;
+    auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, K, A, lda, sA, B, ldb, sB);
+    kern<<<dim3(tiles, S), NTHREADS, 0, s>>>(M, N, Kc, A, lda, B, ldb, 0.f, part, N, sA, sB,
+                                             (long long)M * N, nullptr, 0, K - (S - 1) * Kc);
+    int st = check_launch("dh_gemm_f32(split-K)");
+    if (st == DH_OK) {
+        const int cus = num_cus();
+        size_t blocks = ((size_t)M * N + 255) / 256;
+        if (blocks > (size_t)cus * 8) blocks = (size_t)cus * 8;
+        splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(part, S, M, N, beta, C, ldc, bt.bias, bt.epi);
+        st = check_launch("dh_gemm_f32(split-K reduce)");
+    }
+    dh_free(part);   // pooled; later users of the buffer are ordered on the stream
+    return st;
+}
+
 template <bool TA, bool TB, int TBM, int TBN>
 int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, int ldb,
                  float beta, float* C, int ldc, const Batch& bt) {
-    const int tiles = ((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN);
-    hipStream_t s = stream();
+    const int tm = (M + TBM - 1) / TBM, tn = (N + TBN - 1) / TBN, tiles = tm * tn;
     // Products with few output tiles and a long contraction (the weight gradients dW = dY^T X
     // of a layer, K = the batch; a layer's forward with few output columns) would leave most
-    // CUs idle: split K into S chunks run as gridDim.y members writing fp32 partials, then
-    // reduce them in order.  Where the one-pass grid fills at most half the CUs, S aims at 4
+    // CUs idle: split K.  Where the one-pass grid fills at most half the CUs, S aims at 4
     // work-groups per CU (measured on config 2's layer shapes: 96 tiles with K = 784, 0.088 ->
     // 0.067 ms; 21 tiles with K = 4096, 0.086 -> 0.061 ms; 1 or 2 per CU gain less).
     const int cus = num_cus();
@@ -829,51 +879,58 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
         int S = 4 * cus / tiles;
         S = S > 32 ? 32 : S;
         S = S > K / 128 ? K / 128 : S;
-        const int Kc = ((K + S - 1) / S + BK - 1) / BK * BK;   // chunk of K, multiple of BK
-        S = (K + Kc - 1) / Kc;
-        const int full = K / Kc, tail = K - full * Kc;         // full chunks, last partial one
-        float* part = static_cast<float*>(dh_malloc((size_t)S * M * N * sizeof(float)));
-        if (part) {
-            // chunk j: A columns (or rows, TA) and B rows (or columns, TB) j Kc .. + Kc
-            const long long sA = TA ? (long long)Kc * lda : Kc, sB = TB ? Kc : (long long)Kc * ldb;
-            int st = DH_OK;
-            if (full > 0) {
-                auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, Kc, A, lda, sA, B, ldb, sB);
-                kern<<<dim3(tiles, full), NTHREADS, 0, s>>>(M, N, Kc, A, lda, B, ldb, 0.f, part, N,
-                                                            sA, sB, (long long)M * N, nullptr, 0);
-                st = check_launch("dh_gemm_f32(split-K)");
+        const int st = launch_split_k<TA, TB, TBM, TBN>(M, N, K, S, A, lda, B, ldb, beta, C, ldc, bt);
+        if (st != DH_ERR_UNSUPPORTED) return st;
+        // no workspace: the one-pass grid below
+    }
+    // A partial last round: the matrix cores of a CU are shared by the work-groups it holds,
+    // so a grid of F full rounds of the CUs plus a few tiles runs about F + 1 tiles' time
+    // (3000^3: 576 tiles of 128 on 256 CUs, 2.25 per CU, take 3).  Cut the output into a
+    // part of at most F rounds (whole tile rows, or columns) and a tail strip whose K is
+    // split S ways, so that the strip's S-fold grid fits one round of the CUs: the tail then
+    // takes about 1/S of a tile's time.  Each part applies beta and the epilogue to its own
+    // rows or columns.
+    static const bool split_tail = [] {
+        const char* e = std::getenv("DH_GEMM_F32_SPLIT_TAIL");   // tuning knob: 0 or 1
+        return !e || std::atoi(e) != 0;
+    }();
+    if (split_tail && TBM == 128 && TBN == 128 && bt.count == 1 && K >= 1024 && tiles > cus &&
+        tiles % cus != 0) {
+        const int F = tiles / cus;
+        // tail strip of r tile rows (cut along M) or tile columns (along N)
+        const int rm = tm - F * cus / tn, rn = tn - F * cus / tm;
+        const int Sm = rm > 0 && rm < tm ? cus / (rm * tn) : 0;
+        const int Sn = rn > 0 && rn < tn ? cus / (rn * tm) : 0;
+        int S = Sm >= Sn ? Sm : Sn;
+        S = S > K / 256 ? K / 256 : S;
+        if (S >= 2) {
+            const bool cut_m = Sm >= Sn;
+            const int keep = cut_m ? (tm - rm) * TBM : (tn - rn) * TBN;   // rows / columns kept
+            Batch head = bt, tail = bt;
+            int st;
+            if (cut_m) {
+                st = launch_grid<TA, TB, TBM, TBN>(keep, N, K, A, lda, B, ldb, beta, C, ldc, head);
+                if (st != DH_OK) return st;
+                if (bt.bias && (bt.epi & DH_EPI_ROW_BIAS)) tail.bias = bt.bias + keep;
+                const float* At = TA ? A + keep : A + (size_t)keep * lda;
+                float* Ct = C + (size_t)keep * ldc;
+                st = launch_split_k<TA, TB, TBM, TBN>(M - keep, N, K, S, At, lda, B, ldb, beta, Ct,
+                                                     ldc, tail);
+                if (st != DH_ERR_UNSUPPORTED) return st;
+                return launch_grid<TA, TB, TBM, TBN>(M - keep, N, K, At, lda, B, ldb, beta, Ct, ldc, tail);
             }
-            if (st == DH_OK && tail > 0) {
-                const float* At = A + full * sA;
-                const float* Bt = B + full * sB;
-                auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, tail, At, lda, 0, Bt, ldb, 0);
-                kern<<<dim3(tiles, 1), NTHREADS, 0, s>>>(M, N, tail, At, lda, Bt, ldb, 0.f,
-                                                         part + (size_t)full * M * N, N, 0, 0, 0,
-                                                         nullptr, 0);
-                st = check_launch("dh_gemm_f32(split-K)");
-            }
-            if (st == DH_OK) {
-                size_t blocks = ((size_t)M * N + 255) / 256;
-                if (blocks > (size_t)cus * 8) blocks = (size_t)cus * 8;
-                splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(part, S, M, N, beta, C, ldc,
-                                                               bt.bias, bt.epi);
-                st = check_launch("dh_gemm_f32(split-K reduce)");
-            }
-            dh_free(part);   // pooled; later users of the buffer are ordered on the stream
-            return st;
+            st = launch_grid<TA, TB, TBM, TBN>(M, keep, K, A, lda, B, ldb, beta, C, ldc, head);
+            if (st != DH_OK) return st;
+            if (bt.bias && !(bt.epi & DH_EPI_ROW_BIAS)) tail.bias = bt.bias + keep;
+            const float* Bt = TB ? B + (size_t)keep * ldb : B + keep;
+            float* Ct = C + keep;
+            st = launch_split_k<TA, TB, TBM, TBN>(M, N - keep, K, S, A, lda, Bt, ldb, beta, Ct, ldc,
+                                                 tail);
+            if (st != DH_ERR_UNSUPPORTED) return st;
+            return launch_grid<TA, TB, TBM, TBN>(M, N - keep, K, A, lda, Bt, ldb, beta, Ct, ldc, tail);
         }
-        // no workspace: fall through to the one-pass kernel
     }
-    auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, K, A, lda, bt.sA, B, ldb, bt.sB);
-    // gridDim.y carries the batch member; chunks of 65535 keep it within the y limit.
-    for (int b0 = 0; b0 < bt.count; b0 += 65535) {
-        const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
-        kern<<<dim3(tiles, nb), NTHREADS, 0, s>>>(M, N, K, A + b0 * bt.sA, lda, B + b0 * bt.sB,
-                                                  ldb, beta, C + b0 * bt.sC, ldc, bt.sA, bt.sB,
-                                                  bt.sC, bt.bias, bt.epi);
-        DH_TRY(check_launch("dh_gemm_f32"));
-    }
-    return DH_OK;
+    return launch_grid<TA, TB, TBM, TBN>(M, N, K, A, lda, B, ldb, beta, C, ldc, bt);
 }
 
 // ---- skinny products: an output side of at most 16 (min(M, N) <= 16) ----------------------

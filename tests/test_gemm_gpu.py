@@ -418,6 +418,28 @@ def test_fp32_64x64_two_waves_per_simd(Bt, M, N, K, ta, tb, row_bias):
     assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
 
 
+# A 128 x 128 grid a few tiles past whole rounds of the CUs: the output is cut into whole
+# rounds and a tail strip of tile rows (or columns, the 2000 x 4200 case) whose K is split into
+# chunks with an ordered reduction.  Ragged strips (4100: 132 rows; 4200: 104 columns), K not a
+# multiple of 4 (scalar loads), all layouts, beta and either bias orientation with ReLU.
+SPLIT_TAIL_F32 = [(3000, 3000, 1024), (2000, 4200, 1100), (4100, 4100, 1027)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_TAIL_F32)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("row_bias", [False, True])
+def test_fp32_split_tail(M, N, K, ta, tb, row_bias):
+    got, ref = _ex("f32", ta, tb, 1, M, N, K, beta=0.5, relu=row_bias, row_bias=row_bias,
+                   seed=M + N + K + ta + 2 * tb + row_bias)
+    assert maxrel(got, ref) <= 1e-5 * np.sqrt(K)
+
+
+def test_fp32_split_tail_bit_identical_reruns():
+    a, _ = _ex("f32", 0, 0, 1, 3000, 3000, 1024, seed=5)
+    b, _ = _ex("f32", 0, 0, 1, 3000, 3000, 1024, seed=5)
+    assert np.array_equal(a, b)
+
+
 # Skinny products (a side <= 16): config 2's H W2 (4096 x 10, K 257), dW2 = H^T dY (257 x 10,
 # K 4096, split over work-groups) and dH = dY W2^T (4096 x 257, K 10); M <= 16 (operands
 # swapped, C written transposed); tails of every side; K = 0.
