@@ -906,10 +906,10 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
         if (S >= 2) {
             const bool cut_m = Sm >= Sn;
             const int keep = cut_m ? (tm - rm) * TBM : (tn - rn) * TBN;   // rows / columns kept
-            Batch head = bt, tail = bt;
+            Batch tail = bt;   // the strip's epilogue bias, offset where it runs along the cut
             int st;
             if (cut_m) {
-                st = launch_grid<TA, TB, TBM, TBN>(keep, N, K, A, lda, B, ldb, beta, C, ldc, head);
+                st = launch_grid<TA, TB, TBM, TBN>(keep, N, K, A, lda, B, ldb, beta, C, ldc, bt);
                 if (st != DH_OK) return st;
                 if (bt.bias && (bt.epi & DH_EPI_ROW_BIAS)) tail.bias = bt.bias + keep;
                 const float* At = TA ? A + keep : A + (size_t)keep * lda;
@@ -919,7 +919,7 @@ int launch_tiles(int M, int N, int K, const float* A, int lda, const float* B, i
                 if (st != DH_ERR_UNSUPPORTED) return st;
                 return launch_grid<TA, TB, TBM, TBN>(M - keep, N, K, At, lda, B, ldb, beta, Ct, ldc, tail);
             }
-            st = launch_grid<TA, TB, TBM, TBN>(M, keep, K, A, lda, B, ldb, beta, C, ldc, head);
+            st = launch_grid<TA, TB, TBM, TBN>(M, keep, K, A, lda, B, ldb, beta, C, ldc, bt);
             if (st != DH_OK) return st;
             if (bt.bias && !(bt.epi & DH_EPI_ROW_BIAS)) tail.bias = bt.bias + keep;
             const float* Bt = TB ? B + (size_t)keep * ldb : B + keep;
