@@ -19,7 +19,9 @@
 //   CUs take 4-wave work-groups (128 rows, two per CU) with two-slot K and V rings instead.
 // fp32 kernel (v_mfma_f32_32x32x2_f32): 32 rows per wave, K and V both [key][d] in a
 //   two-stage LDS ring filled through registers; 8 waves (two per SIMD, 256 rows) when that
-//   grid fills the chip (non-causal: 5/8 of it), else 4 (128 rows).
+//   grid fills the chip (non-causal: 5/8 of it), else 4 (128 rows); small grids take
+//   16-row work-groups whose 8 waves split the key range, on v_mfma_f32_16x16x4_f32 with K
+//   and V read straight into registers.
 // Causal work-groups are launched heaviest-first (longest key range) and all
 //   q-tiles of one slice land on the same XCD, which shares that slice's K/V in L2.
 #include <cmath>
@@ -618,179 +620,221 @@ flash_fwd_f32_kernel(int BH, int S, float scale_log2, const float* __restrict__ 
     }
 }
 
-// fp32, small grids (few slices x short sequences, e.g. config 3's 24 slices of 256): the
-// kernel above gives each work-group 128 rows and walks its key stages one after another, so a
-// short problem leaves most CUs idle while a few groups run several stages in series.  Here a
-// work-group owns 32 query rows and its 4 waves take the key stages round-robin (wave w: stages
-// w, w+4, ...), each wave with its own K/V tile in its own LDS region (no work-group barrier in
-// the loop, whose trip count differs per wave); at the end the waves' partial (m, l, O) merge
-// through LDS: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w, M = max_w m_w.
+// fp32, small grids on 16-row work-groups (config 3: 24 slices of 256 rows).  A short problem
+// is a chain of latencies per work-group (Q rows, K/V, the two products, the merge, the
+// stores), so its time is set by the longest chain, not by the matrix cores' throughput.  A
+// work-group owns 16 query rows and its 8 waves take 16- or 32-key chunks round-robin (wave
+// w: chunks w, w + 8, ...), on v_mfma_f32_16x16x4_f32, with K and V read straight from
+// global memory into the operand registers (no LDS staging, no barrier in the loop): the
+// heaviest config-3 work-group runs one 32-key chunk per wave, 64 MFMAs of 2048 flops.
+// MFMA layouts (16 x 16 x 4: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; result
+// register r is D[4 (l / 16) + r][l % 16]); c = l % 16, g = l / 16:
+//  S^T = K Q^T: k-step s pairs K[key][d] with Q[query][d] for d = D/4 g + s (the order of d
+//    inside the contraction is free as long as both operands agree), so a lane loads D/4
+//    consecutive floats of one Q row and of one K row; result register r of key block kb is
+//    the score of key k0 + 16 kb + 4 g + r for query q0 + c.
+//  O^T += V^T P^T: k-step (kb, r) takes key k0 + 16 kb + 4 g + r at lane group g -- exactly
+//    the key whose probability the lane holds in that score register, so P is used in place;
+//    the V operand of d-block e at lane (c, g) is V[that key][D/16 c + e], one vector load of
+//    D/16 floats per key row.  Result register r of d-block e is O^T[D/16 (4 g + r) + e][q0 + c].
+// The row max and sum run over the four lane groups with two lane swaps.  Every chunk a wave
+// processes holds a valid key for each of its rows (chunk starts are multiples of the chunk
+// width at or below the block's first row), so no running max stays at the mask value; waves
+// without a chunk hold m = NEG, l = 0, O = 0 and drop out of the merge (2^(NEG - M) = 0).
+// The merge is spread over all 512 threads: 32 per row, each adding the 8 partials of D/32
+// columns in wave order.
 template <int D>
-struct F32SplitCfg {
-    static constexpr int KEYS = D == 128 ? 32 : 64;        // keys per stage
-    static constexpr int KB = KEYS / 32;                   // 32-key MFMA blocks per stage
-    static constexpr int LS = D + 4;                       // LDS row stride (floats)
-    static constexpr int WAVE_FLOATS = 2 * KEYS * LS;      // K + V tile of one wave
-    static constexpr int MERGE_FLOATS = 32 * (D + 2);      // O rows + m, l of one wave
-    static constexpr int LDS_FLOATS = 4 * (WAVE_FLOATS > MERGE_FLOATS ? WAVE_FLOATS : MERGE_FLOATS);
+struct F32S16Cfg {
+    static constexpr int W = 8;                        // waves per work-group
+    static constexpr int CK = D == 128 ? 16 : 32;      // keys per chunk
+    static constexpr int NKB = CK / 16;                // 16-key blocks per chunk
+    static constexpr int DQ = D / 4;                   // Q / K floats per lane (k-steps)
+    static constexpr int DV = D / 16;                  // V floats per lane per key (d-blocks)
+    static constexpr int RS = D + 4;                   // merge row stride (floats)
+    static constexpr int PART = 16 * RS + 32;          // one wave's O rows, then m[16], l[16]
+    static constexpr int LDS_FLOATS = W * PART;
 };
 
+template <int N>
+__device__ inline void load_floats(const float* __restrict__ p, float (&v)[N]) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < N / 4; ++q) {
+            const f32x4 t = *reinterpret_cast<const f32x4*>(p + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
+        }
+    } else {
+        static_assert(N == 2, "2, or a multiple of 4");
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const f32x2 t = *reinterpret_cast<const f32x2*>(p);
+        v[0] = t[0];
+        v[1] = t[1];
+    }
+}
+
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(NT)
-flash_fwd_f32_split_kernel(int BH, int S, float scale_log2, const float* __restrict__ Q,
-                           const float* __restrict__ K, const float* __restrict__ V,
-                           float* __restrict__ O, float* __restrict__ LSE) {
-    using Cfg = F32SplitCfg<D>;
-    constexpr int ND = D / 32, NDQ = D / 4, KEYS = Cfg::KEYS, LS = Cfg::LS;
+__global__ void __launch_bounds__(64 * F32S16Cfg<D>::W)
+flash_fwd_f32_s16_kernel(int BH, int S, float scale_log2, const float* __restrict__ Q,
+                         const float* __restrict__ K, const float* __restrict__ V,
+                         float* __restrict__ O, float* __restrict__ LSE) {
+    using Cfg = F32S16Cfg<D>;
+    constexpr int W = Cfg::W, CK = Cfg::CK, NKB = Cfg::NKB, DQ = Cfg::DQ, DV = Cfg::DV;
+    constexpr int RS = Cfg::RS, PART = Cfg::PART;
     extern __shared__ __attribute__((aligned(16))) float fsm[];
 
-    const int n_qb = (S + 31) / 32;
+    const int n_qb = (S + 15) / 16;
     const int bh = blockIdx.x % BH;
     const int rr = blockIdx.x / BH;
     const int qb = CAUSAL ? n_qb - 1 - rr : rr;          // longest key range first
-    const int r0 = qb * 32;
+    const int q0 = qb * 16;
     const size_t base = (size_t)bh * S * D;
-    const float* Qg = Q + base;
     const float* Kg = K + base;
     const float* Vg = V + base;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l32 = lane & 31, h = lane >> 5;
-    const int i = r0 + l32;
-    float* const ks = fsm + wave * Cfg::WAVE_FLOATS;
-    float* const vs = ks + KEYS * LS;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int qi = q0 + c;                               // this lane's query row
 
-    float qf[NDQ][2];
+    float qf[DQ];
+    load_floats(Q + base + (size_t)min(qi, S - 1) * D + DQ * g, qf);
+    f32x4 oacc[DV];
 #pragma unroll
-    for (int u = 0; u < NDQ; ++u) {
-        const float* q = Qg + (size_t)i * D + 4 * u + 2 * h;
-        qf[u][0] = i < S ? q[0] : 0.f;
-        qf[u][1] = i < S ? q[1] : 0.f;
-    }
-    f32x16 oacc[ND];
-#pragma unroll
-    for (int d = 0; d < ND; ++d)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[d][r] = 0.f;
+    for (int e = 0; e < DV; ++e) oacc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = NEG, l = 0.f;
 
-    const int kend = CAUSAL ? min(S, r0 + 32) : S;
-    const int nst = (kend + KEYS - 1) / KEYS;
-    for (int st = wave; st < nst; st += 4) {
-        const int j0 = st * KEYS;
-        // this wave's stage into its own LDS region (the previous stage's reads are done)
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int kend = CAUSAL ? min(S, q0 + 16) : S;
+    const int nch = (kend + CK - 1) / CK;
+    // K and V of chunk ch into the operand registers.  K rows past S read row S - 1 (their
+    // scores are masked); V rows come through a buffer resource over the slice, which returns
+    // zeros past it -- no select on the loaded values, so nothing waits for a load before its
+    // use.  The next chunk's K is loaded once the score MFMAs have read kf, its V once the PV
+    // MFMAs have read vf, so each load overlaps the other half of the chunk.
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Vg), 0, 4 * S * D, 0x00020000);
+    float kf[NKB][DQ], vf[NKB][4][DV];
+    auto load_k = [&](int ch) {
 #pragma unroll
-        for (int c = 0; c < KEYS * D / 4 / 64; ++c) {
-            const int f = lane + 64 * c;
-            const int key = f / (D / 4), dq = f % (D / 4);
-            const int j = j0 + key;
-            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            const f32x4 kv = j < S ? *reinterpret_cast<const f32x4*>(Kg + (size_t)j * D + 4 * dq) : z;
-            const f32x4 vv = j < S ? *reinterpret_cast<const f32x4*>(Vg + (size_t)j * D + 4 * dq) : z;
-            *reinterpret_cast<f32x4*>(&ks[key * LS + 4 * dq]) = kv;
-            *reinterpret_cast<f32x4*>(&vs[key * LS + 4 * dq]) = vv;
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // visible to the wave's other lanes
-
-        f32x16 sacc[Cfg::KB];
+        for (int kb = 0; kb < NKB; ++kb)
+            load_floats(Kg + (size_t)min(ch * CK + 16 * kb + c, S - 1) * D + DQ * g, kf[kb]);
+    };
+    auto load_v = [&](int ch) {
 #pragma unroll
-        for (int kb = 0; kb < Cfg::KB; ++kb) {
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t off = 4u * ((uint32_t)(ch * CK + 16 * kb + 4 * g + r) * D + DV * c);
+                // dword loads at consecutive offsets (merged into one wide load): this
+                // toolchain's 64- and 128-bit raw buffer load builtins emit a single dword
 #pragma unroll
-            for (int u = 0; u < NDQ; ++u) {
-                const float* kr = &ks[(32 * kb + l32) * LS + 4 * u + 2 * h];
-                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[0], qf[u][0], sacc[kb], 0, 0, 0);
-                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[1], qf[u][1], sacc[kb], 0, 0, 0);
+                for (int e = 0; e < DV; ++e)
+                    vf[kb][r][e] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rs, off + 4u * e, 0, 0));
             }
-        }
+    };
+    if (wave < nch) {
+        load_k(wave);
+        load_v(wave);
+    }
+    for (int ch = wave; ch < nch; ch += W) {
+        const int k0 = ch * CK;
+        const bool more = ch + W < nch;
+        // two accumulators per key block (even and odd k-steps) halve the dependent chain
+        f32x4 sa[NKB][2];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) sa[kb][0] = sa[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < DQ; ++st)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+                sa[kb][st & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kb][st], qf[st],
+                                                                    sa[kb][st & 1], 0, 0, 0);
+        if (more) load_k(ch + W);
+        float p[NKB][4];
         float mx = NEG;
 #pragma unroll
-        for (int kb = 0; kb < Cfg::KB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int j = j0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                float sc = sacc[kb][r] * scale_log2;
-                if (j >= S || (CAUSAL && j > i)) sc = NEG;
-                sacc[kb][r] = sc;
+            for (int r = 0; r < 4; ++r) {
+                const int j = k0 + 16 * kb + 4 * g + r;
+                float sc = (sa[kb][0][r] + sa[kb][1][r]) * scale_log2;
+                if (j >= S || (CAUSAL && j > qi)) sc = NEG;
+                p[kb][r] = sc;
                 mx = fmaxf(mx, sc);
             }
-        mx = fmaxf(mx, xor32(mx));
+        float lo, hi;
+        halves16(mx, lo, hi);
+        mx = fmaxf(lo, hi);
+        halves32(mx, lo, hi);
+        mx = fmaxf(lo, hi);
         const float m_new = fmaxf(m, mx);
         const float corr = fast_exp2(m - m_new);
         m = m_new;
         float sum = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < Cfg::KB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(sacc[kb][r] - m_new);
-                sacc[kb][r] = p;
-                sum += p;
+            for (int r = 0; r < 4; ++r) {
+                p[kb][r] = fast_exp2(p[kb][r] - m_new);
+                sum += p[kb][r];
             }
-        sum += xor32(sum);
+        halves16(sum, lo, hi);
+        sum = lo + hi;
+        halves32(sum, lo, hi);
+        sum = lo + hi;
         l = l * corr + sum;
 #pragma unroll
-        for (int d = 0; d < ND; ++d)
+        for (int e = 0; e < DV; ++e) oacc[e] *= corr;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[d][r] *= corr;
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int kb = 0; kb < Cfg::KB; ++kb)
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-#pragma unroll
-                for (int d = 0; d < ND; ++d)
-                    oacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * LS + 32 * d + l32],
-                                                                  sacc[kb][r], oacc[d], 0, 0, 0);
-            }
+                for (int e = 0; e < DV; ++e)
+                    oacc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[kb][r][e], p[kb][r], oacc[e],
+                                                                   0, 0, 0);
+        if (more) load_v(ch + W);
     }
 
-    // Merge: every wave parks (m, l, O^T) of its 32 rows; wave 0 combines them.  A wave with
-    // no stage holds m = NEG, l = 0, O = 0 and drops out (2^(NEG - M) = 0).
-    __syncthreads();   // all waves are done with their K/V tiles
-    float* const part = fsm + wave * (32 * (D + 2));   // [32 rows][D] then m[32], l[32]
+    // Merge: each wave parks O^T (lane (c, g): columns D/4 g .. D/4 g + D/4 of row c), m, l.
+    float* const part = fsm + wave * PART;
 #pragma unroll
-    for (int d = 0; d < ND; ++d)
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) part[l32 * D + 32 * d + 8 * (r >> 2) + 4 * h + (r & 3)] = oacc[d][r];
-    if (h == 0) {
-        part[32 * D + l32] = m;
-        part[32 * D + 32 + l32] = l;
+        for (int e = 0; e < DV; ++e) part[c * RS + DV * (4 * g + r) + e] = oacc[e][r];
+    if (g == 0) {
+        part[16 * RS + c] = m;
+        part[16 * RS + 16 + c] = l;
     }
     __syncthreads();
-    if (wave != 0 || i >= S) return;
-    float mw[4], M = NEG;
+    constexpr int TPR = 64 * W / 16;                     // threads per row
+    constexpr int CPT = D / TPR;                         // columns per thread
+    static_assert(CPT >= 1 && D % TPR == 0, "columns per thread");
+    const int row = tid / TPR, col = (tid % TPR) * CPT;
+    const int i = q0 + row;
+    if (i >= S) return;
+    float mw[W], M = NEG;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        mw[w] = fsm[w * (32 * (D + 2)) + 32 * D + l32];
+    for (int w = 0; w < W; ++w) {
+        mw[w] = fsm[w * PART + 16 * RS + row];
         M = fmaxf(M, mw[w]);
     }
-    float sc[4], L = 0.f;
+    float acc[CPT], L = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        sc[w] = fast_exp2(mw[w] - M);
-        L += sc[w] * fsm[w * (32 * (D + 2)) + 32 * D + 32 + l32];
+    for (int e = 0; e < CPT; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        const float sc = fast_exp2(mw[w] - M);
+        L += sc * fsm[w * PART + 16 * RS + 16 + row];
+#pragma unroll
+        for (int e = 0; e < CPT; ++e) acc[e] += sc * fsm[w * PART + row * RS + col + e];
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    float* orow = O + base + (size_t)i * D;
+    float* orow = O + base + (size_t)i * D + col;
 #pragma unroll
-    for (int d = 0; d < ND; ++d)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            f32x4 w4;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int dd = 32 * d + 8 * q + 4 * h + e;
-                float v = 0.f;
-#pragma unroll
-                for (int w = 0; w < 4; ++w) v += sc[w] * fsm[w * (32 * (D + 2)) + l32 * D + dd];
-                w4[e] = v * inv;
-            }
-            *reinterpret_cast<f32x4*>(orow + 32 * d + 8 * q + 4 * h) = w4;
-        }
-    if (h == 0) LSE[(size_t)bh * S + i] = (M + __log2f(L)) * 0.69314718055994531f;
+    for (int e = 0; e < CPT; ++e) orow[e] = acc[e] * inv;
+    if (col == 0) LSE[(size_t)bh * S + i] = (M + __log2f(L)) * 0.69314718055994531f;
 }
 
 template <typename Kern>
@@ -836,15 +880,22 @@ template <int D, bool CAUSAL>
 int launch_f32(int BH, int S, float sl2, const void* Q, const void* K, const void* V, void* O,
                float* LSE) {
     const int grid = BH * ((S + 127) / 128);
-    if (2 * grid < num_cus()) {   // small problem: 32-row work-groups, key stages split over waves
-        auto kern = flash_fwd_f32_split_kernel<D, CAUSAL>;
-        const size_t lds = (size_t)F32SplitCfg<D>::LDS_FLOATS * sizeof(float);
-        static bool done_split = false;
-        DH_TRY(set_lds(kern, lds, done_split));
-        kern<<<BH * ((S + 31) / 32), NT, lds, stream()>>>(BH, S, sl2, (const float*)Q,
-                                                          (const float*)K, (const float*)V,
-                                                          (float*)O, LSE);
-        return check_launch("dh_flash_fwd(f32 split)");
+    // Small problems: 16-row work-groups whose 8 waves split the key range (grids of under
+    // half a round of 128-row tiles, and causal ones of up to a round with S >= 1024, where
+    // the 128-row tiles' uneven key ranges leave most CUs waiting on the longest ones).
+    // Same box, 16-row kernel against the tiled kernels: (16, 2048, 64) causal 120 / 184 us,
+    // (32, 1024, 128) causal 131 / 168, (8, 4096, 128) causal 372 / 620; non-causal (32, 1024,
+    // 64) 120 / 107 and (64, 1024, 64) causal 153 / 154 stay tiled.
+    const int cus = num_cus();
+    if ((long long)S * D * 4 <= INT32_MAX &&   // V's buffer-resource range in bytes
+        (2 * grid < cus || (CAUSAL && grid <= cus && S >= 1024))) {
+        auto kern = flash_fwd_f32_s16_kernel<D, CAUSAL>;
+        const size_t lds = (size_t)F32S16Cfg<D>::LDS_FLOATS * sizeof(float);
+        static bool done_s16 = false;
+        DH_TRY(set_lds(kern, lds, done_s16));
+        kern<<<BH * ((S + 15) / 16), 64 * F32S16Cfg<D>::W, lds, stream()>>>(
+            BH, S, sl2, (const float*)Q, (const float*)K, (const float*)V, (float*)O, LSE);
+        return check_launch("dh_flash_fwd(f32, 16-row)");
     }
     // 256-row tiles on 8 waves when they fill at least one round of the CUs (config 4's
     // shape: 5.48 -> 4.53 ms, same box), else 128-row tiles on 4 waves.

@@ -56,11 +56,31 @@ def test_fp32_fwd_shapes(S, D, causal):
         assert np.allclose(got.reshape(BH, S, D)[:, 0], V.reshape(BH, S, D)[:, 0], atol=1e-6)
 
 
+@pytest.mark.parametrize("BH,S,D", [(2, 1040, 32), (2, 1040, 64), (2, 1040, 128), (1, 17, 128),
+                                    (3, 2000, 64), (8, 2048, 32)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fp32_fwd_small_grid_key_chunks(BH, S, D, causal):
+    # Small grids take 16-row work-groups whose 8 waves split the key range in 16- or 32-key
+    # chunks: S = 1040 and 2000 give each wave several chunks (online rescaling across them,
+    # the next chunk's loads in flight) and a ragged last chunk whose V rows past S read zeros
+    # through the buffer range; S = 17 a single partial chunk; (8, 2048, 32) causal a grid of
+    # half a round of 128-row tiles that takes this kernel because S >= 1024 (non-causal: the
+    # tiled kernel).  fp64 oracle, and for causal grids row 0 is V's row 0.
+    Q, K, V = inputs(BH, S, D, 3000 + S + D + causal, scale=0.5, n=3)
+    got, lse = flash_fwd(Q, K, V, BH, S, D, causal)
+    Q64, K64, V64 = (x.astype(np.float64) for x in (Q, K, V))
+    tol = 1e-5 * np.sqrt(S)
+    assert maxrel(got, O.attention(Q64, K64, V64, BH, S, D, causal)) <= tol
+    assert np.abs(lse - ref_lse(Q, K, BH, S, D, causal)).max() <= tol
+    if causal:
+        assert np.allclose(got.reshape(BH, S, D)[:, 0], V.reshape(BH, S, D)[:, 0], atol=1e-6)
+
+
 @pytest.mark.parametrize("BH,S", [(130, 257), (64, 520), (300, 1), (256, 3)])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 def test_fp32_fwd_wide_grid(BH, S, D, causal):
-    # Grids that fill the chip (the small-grid split kernel covers the 3-slice shapes above):
+    # Grids that fill the chip (the small-grid 16-row kernel covers the 3-slice shapes above):
     # 130 slices x 257 rows take 256-row work-groups on 8 waves (a one-row last tile), 64 x 520
     # causal 128-row work-groups on 4 waves (its 256-row grid, 192, is short of one round of
     # the CUs; non-causal takes 8 waves from 5/8 of a round); many one- and three-row slices
