@@ -188,6 +188,39 @@ __device__ inline uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// N consecutive floats from p (16-byte loads for N a multiple of 4, one 8-byte load for 2;
+// p aligned to match).
+template <int N>
+__device__ inline void load_floats(const float* __restrict__ p, float (&v)[N]) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < N / 4; ++q) {
+            const f32x4 t = *reinterpret_cast<const f32x4*>(p + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
+        }
+    } else {
+        static_assert(N == 2, "2, or a multiple of 4");
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const f32x2 t = *reinterpret_cast<const f32x2*>(p);
+        v[0] = t[0];
+        v[1] = t[1];
+    }
+}
+
+// N consecutive floats at byte offset off of a buffer resource; words past the resource's
+// range read as zero.  Issued as 32-bit loads at consecutive offsets, which the backend merges
+// into one wide load (this toolchain's 64- and 128-bit raw buffer load builtins emit a single
+// dword load).  Offsets are signed ints so that constant parts fold into the instruction's
+// immediate offset (an unsigned sum may wrap, which keeps each load's offset in its own
+// register and the loads unmerged).
+template <int N>
+__device__ inline void buf_load_floats(__amdgpu_buffer_rsrc_t rs, int off, float (&v)[N]) {
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+        v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off + 4 * e, 0, 0));
+}
+
 // Wait until at most N of this wave's vector-memory operations are in flight.
 template <int N>
 __device__ inline void wait_vmcnt() {

@@ -964,6 +964,206 @@ bwd_dq_f32_kernel(int BH, int S, float scale, float sl2, const float* __restrict
         }
 }
 
+// fp32, small grids, D <= 64 (config 3's 24 slices of 256 rows): the kernels above give a
+// work-group of one wave 16 keys (or 32 queries) and walk the other dimension in series, one
+// register-staged LDS stage after another -- at config 3 a 35 us chain each.  Here a work-group
+// owns 16 keys (dK/dV) or 16 queries (dQ) and its 8 waves take 16-query (16-key) chunks of the
+// other dimension round-robin, all operands loaded straight from global memory into the MFMA
+// registers (no LDS staging, no barrier in the loop); the waves' partial sums meet in LDS and
+// are added in wave order (bit-identical reruns).  v_mfma_f32_16x16x4_f32 layouts (lane l
+// supplies A[l % 16][l / 16] and B[l / 16][l % 16]; result register r is D[4 (l / 16) + r]
+// [l % 16]); c = l % 16, g = l / 16, DQ = D / 4, DV = D / 16:
+//  dK/dV: S = Q K^T and dP = dO V^T pair Q[i0 + c][DQ g + u] with K[k0 + c][DQ g + u] at
+//    k-step u (the order of d in the contraction is free as long as both operands agree);
+//    result register r holds query i0 + 4 g + r, key k0 + c.  dV^T += dO^T P and
+//    dK^T += Q^T dS take that query at k-step r, so P and dS feed the products in place; the A
+//    operand of d-block b is dO[query][DV c + b] (Q for dK), read through a buffer resource
+//    that returns zeros for rows past S; result register r' of d-block b is d = DV (4 g + r')
+//    + b for key k0 + c.
+//  dQ: S^T = K Q^T and dP^T = V dO^T (result register r: key k0 + 4 g + r, query q0 + c), then
+//    dQ^T += K^T dS^T with the A operand K[key][DV c + e] of d-block e.
+constexpr int S16_W = 8;
+
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(64 * S16_W)
+bwd_dkdv_f32_s16_kernel(int BH, int S, float scale, float sl2, const float* __restrict__ Q,
+                        const float* __restrict__ K, const float* __restrict__ V,
+                        const float* __restrict__ dO, const float* __restrict__ LSE,
+                        const float* __restrict__ Dv, float* __restrict__ dK,
+                        float* __restrict__ dV, int accumulate, int kv_alias) {
+    constexpr int W = S16_W, DQ = D / 4, DV = D / 16, RS = D + 4, PART = 2 * 16 * RS;
+    extern __shared__ __attribute__((aligned(16))) float fsm[];   // per wave: dK rows, dV rows
+
+    const int bh = blockIdx.x % BH;
+    const int k0 = (blockIdx.x / BH) * 16;
+    const size_t base = (size_t)bh * S * D;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int j = k0 + c;                                  // this lane's key
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(Q + base), 0, 4 * S * D, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(dO + base), 0, 4 * S * D, 0x00020000);
+
+    float kf[DQ], vf[DQ];
+    load_floats(K + base + (size_t)min(j, S - 1) * D + DQ * g, kf);
+    load_floats(V + base + (size_t)min(j, S - 1) * D + DQ * g, vf);
+    f32x4 dk[DV], dv[DV];
+#pragma unroll
+    for (int b = 0; b < DV; ++b) dk[b] = dv[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int qstart = CAUSAL ? k0 : 0;                   // k0 < S: the grid covers S's keys
+    const int nch = (S - qstart + 15) / 16;
+    for (int ch = wave; ch < nch; ch += W) {
+        const int i0 = qstart + 16 * ch;
+        const int ia = min(i0 + c, S - 1);
+        float qa[DQ], ga[DQ], qt[4][DV], gt[4][DV], l2[4], dvr[4];
+        load_floats(Q + base + (size_t)ia * D + DQ * g, qa);
+        load_floats(dO + base + (size_t)ia * D + DQ * g, ga);
+        const int off = 4 * (i0 + 4 * g) * D + 4 * DV * c;   // row i0 + 4 g, this lane's columns
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = i0 + 4 * g + r;
+            buf_load_floats(rq, off + 4 * D * r, qt[r]);
+            buf_load_floats(rg, off + 4 * D * r, gt[r]);
+            const int ir = min(i, S - 1);
+            l2[r] = LSE[(size_t)bh * S + ir] * 1.4426950408889634f;
+            dvr[r] = Dv[(size_t)bh * S + ir];
+        }
+        f32x4 sa[2], pa[2];
+        sa[0] = sa[1] = pa[0] = pa[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < DQ; ++u) {
+            sa[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[u], kf[u], sa[u & 1], 0, 0, 0);
+            pa[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(ga[u], vf[u], pa[u & 1], 0, 0, 0);
+        }
+        float p[4], ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = i0 + 4 * g + r;
+            const bool ok = i < S && j < S && (!CAUSAL || j <= i);
+            p[r] = ok ? fast_exp2((sa[0][r] + sa[1][r]) * sl2 - l2[r]) : 0.f;
+            ds[r] = ok ? p[r] * ((pa[0][r] + pa[1][r]) - dvr[r]) : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int b = 0; b < DV; ++b) {
+                dv[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(gt[r][b], p[r], dv[b], 0, 0, 0);
+                dk[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(qt[r][b], ds[r], dk[b], 0, 0, 0);
+            }
+    }
+
+    float* const part = fsm + wave * PART;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int b = 0; b < DV; ++b) {
+            part[c * RS + DV * (4 * g + r) + b] = dk[b][r];
+            part[16 * RS + c * RS + DV * (4 * g + r) + b] = dv[b][r];
+        }
+    __syncthreads();
+    constexpr int QPR = D / 4;                             // 4-column groups per key row
+    if (tid >= 16 * QPR) return;
+    const int row = tid / QPR, col = 4 * (tid % QPR);
+    const int jj = k0 + row;
+    if (jj >= S) return;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        a += *reinterpret_cast<const f32x4*>(fsm + w * PART + row * RS + col);
+        v += *reinterpret_cast<const f32x4*>(fsm + w * PART + 16 * RS + row * RS + col);
+    }
+    store_dkdv(dK + base + (size_t)jj * D + col, dV + base + (size_t)jj * D + col, a * scale, v,
+               accumulate, accumulate, kv_alias);
+}
+
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(64 * S16_W)
+bwd_dq_f32_s16_kernel(int BH, int S, float scale, float sl2, const float* __restrict__ Q,
+                      const float* __restrict__ K, const float* __restrict__ V,
+                      const float* __restrict__ dO, const float* __restrict__ LSE,
+                      const float* __restrict__ Dv, float* __restrict__ dQ, int accumulate) {
+    constexpr int W = S16_W, DQ = D / 4, DV = D / 16, RS = D + 4, PART = 16 * RS;
+    extern __shared__ __attribute__((aligned(16))) float fsm[];   // per wave: dQ rows
+
+    const int n_qb = (S + 15) / 16;
+    const int bh = blockIdx.x % BH;
+    const int rr = blockIdx.x / BH;
+    const int q0 = (CAUSAL ? n_qb - 1 - rr : rr) * 16;   // longest key range first
+    const size_t base = (size_t)bh * S * D;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int qi = q0 + c;                                 // this lane's query
+    const int qr = min(qi, S - 1);
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(K + base), 0, 4 * S * D, 0x00020000);
+
+    float qf[DQ], gf[DQ];
+    load_floats(Q + base + (size_t)qr * D + DQ * g, qf);
+    load_floats(dO + base + (size_t)qr * D + DQ * g, gf);
+    const float l2 = LSE[(size_t)bh * S + qr] * 1.4426950408889634f;
+    const float dvi = Dv[(size_t)bh * S + qr];
+    f32x4 dq[DV];
+#pragma unroll
+    for (int e = 0; e < DV; ++e) dq[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int kend = CAUSAL ? min(S, q0 + 16) : S;
+    const int nch = (kend + 15) / 16;
+    for (int ch = wave; ch < nch; ch += W) {
+        const int k0 = 16 * ch;
+        const int kr = min(k0 + c, S - 1);
+        float ka[DQ], va[DQ], kt[4][DV];
+        load_floats(K + base + (size_t)kr * D + DQ * g, ka);
+        load_floats(V + base + (size_t)kr * D + DQ * g, va);
+        int off = 4 * (k0 + 4 * g) * D + 4 * DV * c;   // row k0 + 4 g, this lane's columns
+        asm volatile("" : "+v"(off));   // one base register per chunk, constants as immediates
+#pragma unroll
+        for (int r = 0; r < 4; ++r) buf_load_floats(rk, off + 4 * D * r, kt[r]);
+        f32x4 sa[2], pa[2];
+        sa[0] = sa[1] = pa[0] = pa[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < DQ; ++u) {
+            sa[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[u], qf[u], sa[u & 1], 0, 0, 0);
+            pa[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[u], gf[u], pa[u & 1], 0, 0, 0);
+        }
+        float ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = k0 + 4 * g + r;
+            const bool ok = qi < S && key < S && (!CAUSAL || key <= qi);
+            const float p = ok ? fast_exp2((sa[0][r] + sa[1][r]) * sl2 - l2) : 0.f;
+            ds[r] = ok ? p * ((pa[0][r] + pa[1][r]) - dvi) : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int e = 0; e < DV; ++e)
+                dq[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(kt[r][e], ds[r], dq[e], 0, 0, 0);
+    }
+
+    float* const part = fsm + wave * PART;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < DV; ++e) part[c * RS + DV * (4 * g + r) + e] = dq[e][r];
+    __syncthreads();
+    constexpr int QPR = D / 4;
+    if (tid >= 16 * QPR) return;
+    const int row = tid / QPR, col = 4 * (tid % QPR);
+    const int i = q0 + row;
+    if (i >= S) return;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < W; ++w) a += *reinterpret_cast<const f32x4*>(fsm + w * PART + row * RS + col);
+    float* dqr = dQ + base + (size_t)i * D + col;
+    a *= scale;
+    if (accumulate) a += *reinterpret_cast<const f32x4*>(dqr);
+    *reinterpret_cast<f32x4*>(dqr) = a;
+}
+
 // ---------------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------------
@@ -1084,6 +1284,38 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
             int acc, int kv_alias, int acc_q) {
     using Tl = Tile32<D>;
     const float sl2 = scale * 1.4426950408889634f;
+    // Small and mid grids (D <= 64): the 16-key / 16-query kernels, where the tiled kernels'
+    // work-groups walk long serial chains (grids of under a round of 128-row tiles; causal
+    // ones up to a round, or two with S >= 2048, where their uneven key ranges leave CUs
+    // waiting).  Same box, whole backward, these kernels / the tiled ones (us): config 3
+    // 26.8 / 75.8, (2, 1040, 64) 56.8 / 281, (8, 1024, 64) causal 73 / 253, non-causal 110 /
+    // 259, (16, 2048, 64) causal 400 / 556, (64, 512, 64) causal 141 / 161, (32, 2048, 32)
+    // causal 401 / 465; tiled kept: (32, 1024, 32) non-causal 206 / 184, (64, 1024, 64)
+    // causal 429 / 429, (256, 256, 64) causal 182 / 135, (128, 1024, 64) causal 853 / 616.
+    if constexpr (D <= 64) {
+        const long long g128 = (long long)BH * ((S + 127) / 128);
+        const int cus = num_cus();
+        const bool small = CAUSAL ? g128 <= cus || (g128 <= 2LL * cus && S >= 2048) : g128 < cus;
+        // buffer offsets (bytes, up to 16 rows past S) fit an int
+        if (small && (long long)(S + 32) * D * 4 <= INT32_MAX) {
+            auto kdkdv = bwd_dkdv_f32_s16_kernel<D, CAUSAL>;
+            const size_t lds_kv = (size_t)S16_W * 2 * 16 * (D + 4) * sizeof(float);
+            static bool done_kv = false;
+            DH_TRY(set_lds(kdkdv, lds_kv, done_kv));
+            kdkdv<<<BH * ((S + 15) / 16), 64 * S16_W, lds_kv, stream()>>>(
+                BH, S, scale, sl2, (const float*)Q, (const float*)K, (const float*)V,
+                (const float*)dO, LSE, Dv, dK, dV, acc, kv_alias);
+            DH_TRY(check_launch("dh_flash_bwd(dK,dV f32, 16-row)"));
+            auto kdq = bwd_dq_f32_s16_kernel<D, CAUSAL>;
+            const size_t lds_q = (size_t)S16_W * 16 * (D + 4) * sizeof(float);
+            static bool done_q = false;
+            DH_TRY(set_lds(kdq, lds_q, done_q));
+            kdq<<<BH * ((S + 15) / 16), 64 * S16_W, lds_q, stream()>>>(
+                BH, S, scale, sl2, (const float*)Q, (const float*)K, (const float*)V,
+                (const float*)dO, LSE, Dv, dQ, acc_q);
+            return check_launch("dh_flash_bwd(dQ f32, 16-row)");
+        }
+    }
     const size_t lds = 2 * 2 * Tl::ELEMS * sizeof(float);
     // dK/dV: 16 keys per wave (8 waves, 128 keys, when that grid fills the CUs).
     switch (f32_waves(BH, S, 16)) {

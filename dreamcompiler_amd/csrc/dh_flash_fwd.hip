@@ -655,24 +655,6 @@ struct F32S16Cfg {
     static constexpr int LDS_FLOATS = W * PART;
 };
 
-template <int N>
-__device__ inline void load_floats(const float* __restrict__ p, float (&v)[N]) {
-    if constexpr (N % 4 == 0) {
-#pragma unroll
-        for (int q = 0; q < N / 4; ++q) {
-            const f32x4 t = *reinterpret_cast<const f32x4*>(p + 4 * q);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
-        }
-    } else {
-        static_assert(N == 2, "2, or a multiple of 4");
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
-        const f32x2 t = *reinterpret_cast<const f32x2*>(p);
-        v[0] = t[0];
-        v[1] = t[1];
-    }
-}
-
 template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(64 * F32S16Cfg<D>::W)
 flash_fwd_f32_s16_kernel(int BH, int S, float scale_log2, const float* __restrict__ Q,
@@ -723,15 +705,8 @@ flash_fwd_f32_s16_kernel(int BH, int S, float scale_log2, const float* __restric
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t off = 4u * ((uint32_t)(ch * CK + 16 * kb + 4 * g + r) * D + DV * c);
-                // dword loads at consecutive offsets (merged into one wide load): this
-                // toolchain's 64- and 128-bit raw buffer load builtins emit a single dword
-#pragma unroll
-                for (int e = 0; e < DV; ++e)
-                    vf[kb][r][e] = __builtin_bit_cast(
-                        float, __builtin_amdgcn_raw_buffer_load_b32(rs, off + 4u * e, 0, 0));
-            }
+            for (int r = 0; r < 4; ++r)
+                buf_load_floats(rs, 4 * ((ch * CK + 16 * kb + 4 * g + r) * D + DV * c), vf[kb][r]);
     };
     if (wave < nch) {
         load_k(wave);
@@ -887,7 +862,7 @@ int launch_f32(int BH, int S, float sl2, const void* Q, const void* K, const voi
     // (32, 1024, 128) causal 131 / 168, (8, 4096, 128) causal 372 / 620; non-causal (32, 1024,
     // 64) 120 / 107 and (64, 1024, 64) causal 153 / 154 stay tiled.
     const int cus = num_cus();
-    if ((long long)S * D * 4 <= INT32_MAX &&   // V's buffer-resource range in bytes
+    if ((long long)(S + 32) * D * 4 <= INT32_MAX &&   // V's buffer offsets (bytes) fit an int
         (2 * grid < cus || (CAUSAL && grid <= cus && S >= 1024))) {
         auto kern = flash_fwd_f32_s16_kernel<D, CAUSAL>;
         const size_t lds = (size_t)F32S16Cfg<D>::LDS_FLOATS * sizeof(float);
