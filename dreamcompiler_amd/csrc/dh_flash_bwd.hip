@@ -1284,18 +1284,23 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
             int acc, int kv_alias, int acc_q) {
     using Tl = Tile32<D>;
     const float sl2 = scale * 1.4426950408889634f;
-    // Small and mid grids (D <= 64): the 16-key / 16-query kernels, where the tiled kernels'
-    // work-groups walk long serial chains (grids of under a round of 128-row tiles; causal
-    // ones up to a round, or two with S >= 2048, where their uneven key ranges leave CUs
-    // waiting).  Same box, whole backward, these kernels / the tiled ones (us): config 3
-    // 26.8 / 75.8, (2, 1040, 64) 56.8 / 281, (8, 1024, 64) causal 73 / 253, non-causal 110 /
-    // 259, (16, 2048, 64) causal 400 / 556, (64, 512, 64) causal 141 / 161, (32, 2048, 32)
-    // causal 401 / 465; tiled kept: (32, 1024, 32) non-causal 206 / 184, (64, 1024, 64)
-    // causal 429 / 429, (256, 256, 64) causal 182 / 135, (128, 1024, 64) causal 853 / 616.
-    if constexpr (D <= 64) {
+    // Small and mid grids: the 16-key / 16-query kernels, where the tiled kernels' work-groups
+    // walk long serial chains.  D <= 64: grids of under a round of 128-row tiles; causal ones
+    // up to a round, or two with S >= 2048, where their uneven key ranges leave CUs waiting.
+    // D = 128 (the dK/dV kernel at 238 VGPRs, two waves per SIMD): causal grids under a round,
+    // non-causal under half.  Same box, whole backward, these kernels / the tiled ones (us):
+    // config 3 26.8 / 75.8, (2, 1040, 64) 56.8 / 281, (8, 1024, 64) causal 73 / 253,
+    // non-causal 110 / 259, (16, 2048, 64) causal 400 / 556, (64, 512, 64) causal 141 / 161,
+    // (32, 2048, 32) causal 401 / 465, (24, 256, 128) causal 46.7 / 134, (16, 1024, 128)
+    // causal 279 / 420, (8, 512, 128) 79 / 252; tiled kept: (32, 1024, 32) non-causal 206 /
+    // 184, (64, 1024, 64) causal 429 / 429, (256, 256, 64) causal 182 / 135, (32, 1024, 128)
+    // causal 541 / 523, (32, 512, 128) 287 / 231, (128, 256, 128) causal 213 / 168.
+    {
         const long long g128 = (long long)BH * ((S + 127) / 128);
         const int cus = num_cus();
-        const bool small = CAUSAL ? g128 <= cus || (g128 <= 2LL * cus && S >= 2048) : g128 < cus;
+        const bool small = D <= 64 ? (CAUSAL ? g128 <= cus || (g128 <= 2LL * cus && S >= 2048)
+                                             : g128 < cus)
+                                   : (CAUSAL ? g128 < cus : 2 * g128 < cus);
         // buffer offsets (bytes, up to 16 rows past S) fit an int
         if (small && (long long)(S + 32) * D * 4 <= INT32_MAX) {
             auto kdkdv = bwd_dkdv_f32_s16_kernel<D, CAUSAL>;

@@ -94,7 +94,8 @@ def test_fp32_fwd_wide_grid(BH, S, D, causal):
     assert np.abs(lse - ref_lse(Q, K, BH, S, D, causal)).max() <= tol
 
 
-@pytest.mark.parametrize("BH,S", [(130, 257), (64, 520), (300, 2), (256, 3), (64, 256), (32, 256)])
+@pytest.mark.parametrize("BH,S", [(130, 257), (64, 520), (300, 2), (256, 3), (64, 256), (32, 256),
+                                  (200, 20)])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 def test_fp32_bwd_wide_grid(BH, S, D, causal):
@@ -102,8 +103,9 @@ def test_fp32_bwd_wide_grid(BH, S, D, causal):
     # one-row last tile), 64 x 520 on 128-query tiles (4 waves), many two- and three-row
     # slices the 8-wave launch with one mostly padding stage; 64 x 256 and 32 x 256 at
     # D = 128 the smaller work-groups of both launches (dK/dV on 4 and 2 waves, dQ on 2 and 1),
-    # as grids short of a round take them (at D <= 64 those grids, and causal 256 x 3, take
-    # the small-grid 16-row kernels).  The whole tensor meets the
+    # as grids short of a round take them (except where the small-grid 16-row kernels do:
+    # 64 x 256 and 32 x 256 at D <= 64, causal ones at D = 128, and causal 256 x 3 at D <= 64);
+    # 200 x 20 non-causal at D = 128 the 1-wave work-groups of both.  The whole tensor meets the
     # normwise bar; each slice, so that a misplaced tile cannot hide behind the others,
     # meets it relative to the size of the terms it sums (for two keys dQ_1 is
     # scale P10 P11 (dP10 - dP11)(K0 - K1), which cancellation can make far smaller than
@@ -209,9 +211,10 @@ def test_fp32_bwd(S, D, causal):
 
 @pytest.mark.parametrize("BH,S,D,causal", [(2, 1040, 32, True), (2, 1040, 64, False),
                                            (3, 600, 64, True), (16, 300, 32, False),
-                                           (20, 2048, 32, True)])
+                                           (20, 2048, 32, True), (2, 1040, 128, False),
+                                           (4, 600, 128, True)])
 def test_fp32_bwd_small_grid_chunks(BH, S, D, causal):
-    # D <= 64 grids short of a round of 128-row tiles take the 16-key (dK/dV) and 16-query
+    # Grids short of a round of 128-row tiles take the 16-key (dK/dV) and 16-query
     # (dQ) work-groups whose 8 waves split the other dimension in 16-row chunks: several
     # chunks per wave, ragged last chunks (operand rows past S read as zeros through the
     # buffer range), and (20, 2048, 32) causal, which takes them because S >= 2048 with up to
@@ -295,13 +298,14 @@ def _aliased_bwd(Q, K, V, O_, dO, LSE, BH, S, D, causal, dtype, pattern, accumul
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("pattern", ["qqq", "qkk"])
 @pytest.mark.parametrize("accumulate", [False, True])
-@pytest.mark.parametrize("D", [64, 128])
-def test_bwd_aliased_gradient_buffers(dtype, pattern, accumulate, D):
+@pytest.mark.parametrize("BH,S,D", [(3, 200, 64), (128, 256, 128)])
+def test_bwd_aliased_gradient_buffers(dtype, pattern, accumulate, BH, S, D):
     """attention(q, q, q) and attention(q, kv, kv): one tensor's gradient buffer is passed as
     two or three of dQ, dK, dV and must receive the sum of the gradients aimed at it (the
-    reference adds each input's gradient in turn, autograd.inc:693-728).  fp32 at D = 64 takes
-    the small-grid 16-row kernels, at D = 128 the tiled ones."""
-    BH, S, causal = 3, 200, True
+    reference adds each input's gradient in turn, autograd.inc:693-728).  fp32: 3 x 200 takes
+    the small-grid 16-row kernels, 128 x 256 at D = 128 (a round of 128-row tiles) the tiled
+    ones."""
+    causal = True
     x, kv, G, i0, i1 = inputs(BH, S, D, 91 + accumulate + 2 * (pattern == "qkk"), n=5)
     if dtype == "bf16":
         x, kv, G = bf16_bits(x), bf16_bits(kv), bf16_bits(G)
