@@ -856,14 +856,16 @@ int launch_f32(int BH, int S, float sl2, const void* Q, const void* K, const voi
                float* LSE) {
     const int grid = BH * ((S + 127) / 128);
     // Small problems: 16-row work-groups whose 8 waves split the key range (grids of under
-    // half a round of 128-row tiles, and causal ones of up to a round with S >= 1024, where
-    // the 128-row tiles' uneven key ranges leave most CUs waiting on the longest ones).
-    // Same box, 16-row kernel against the tiled kernels: (16, 2048, 64) causal 120 / 184 us,
-    // (32, 1024, 128) causal 131 / 168, (8, 4096, 128) causal 372 / 620; non-causal (32, 1024,
-    // 64) 120 / 107 and (64, 1024, 64) causal 153 / 154 stay tiled.
+    // half a round of 128-row tiles; causal ones under a round, or of one round with S >= 1024,
+    // where the 128-row tiles' uneven key ranges leave most CUs waiting on the longest ones).
+    // Same box, 16-row kernel against the tiled kernels (us): causal (16, 2048, 64) 120 / 184,
+    // (32, 1024, 128) 131 / 168, (8, 4096, 128) 372 / 620, (64, 256, 64) 18.0 / 29.4,
+    // (32, 768, 64) 47.6 / 73.7, (40, 512, 128) 54.5 / 88.7; kept tiled: (128, 256, 64) causal
+    // 35 / 31, non-causal (32, 1024, 64) 120 / 107, (100, 256, 64) 38.5 / 32.8, and (64, 1024,
+    // 64) causal 153 / 154.
     const int cus = num_cus();
     if ((long long)(S + 32) * D * 4 <= INT32_MAX &&   // V's buffer offsets (bytes) fit an int
-        (2 * grid < cus || (CAUSAL && grid <= cus && S >= 1024))) {
+        (2 * grid < cus || (CAUSAL && (grid < cus || (grid == cus && S >= 1024))))) {
         auto kern = flash_fwd_f32_s16_kernel<D, CAUSAL>;
         const size_t lds = (size_t)F32S16Cfg<D>::LDS_FLOATS * sizeof(float);
         static bool done_s16 = false;

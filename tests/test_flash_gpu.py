@@ -57,15 +57,16 @@ def test_fp32_fwd_shapes(S, D, causal):
 
 
 @pytest.mark.parametrize("BH,S,D", [(2, 1040, 32), (2, 1040, 64), (2, 1040, 128), (1, 17, 128),
-                                    (3, 2000, 64), (8, 2048, 32)])
+                                    (3, 2000, 64), (8, 2048, 32), (40, 512, 128), (96, 256, 64)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_fp32_fwd_small_grid_key_chunks(BH, S, D, causal):
     # Small grids take 16-row work-groups whose 8 waves split the key range in 16- or 32-key
     # chunks: S = 1040 and 2000 give each wave several chunks (online rescaling across them,
     # the next chunk's loads in flight) and a ragged last chunk whose V rows past S read zeros
-    # through the buffer range; S = 17 a single partial chunk; (8, 2048, 32) causal a grid of
-    # half a round of 128-row tiles that takes this kernel because S >= 1024 (non-causal: the
-    # tiled kernel).  fp64 oracle, and for causal grids row 0 is V's row 0.
+    # through the buffer range; S = 17 a single partial chunk; (8, 2048, 32), (40, 512, 128) and
+    # (96, 256, 64) grids of half to three quarters of a round of 128-row tiles, which take
+    # this kernel when causal (non-causal: the tiled kernels).  fp64 oracle, and for causal
+    # grids row 0 is V's row 0.
     Q, K, V = inputs(BH, S, D, 3000 + S + D + causal, scale=0.5, n=3)
     got, lse = flash_fwd(Q, K, V, BH, S, D, causal)
     Q64, K64, V64 = (x.astype(np.float64) for x in (Q, K, V))
