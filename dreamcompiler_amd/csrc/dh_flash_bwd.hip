@@ -8,6 +8,8 @@
 //   1. Dvec_i = dO_i . O_i                                   (one pass over O, dO)
 //   2. per key tile:   dV += P^T dO,  dK += scale * dS^T Q    (dS = P o (dP - Dvec))
 //   3. per query tile: dQ += scale * dS K                     (S and dP recomputed)
+// or, at D = 128 over at least 64 slices, launch 2 also stores scale * dS and dQ is one batched
+// GEMM per 128-row query tile on it.
 // bf16, two: the per-query-tile launch runs first and forms Dvec_i (and LSE_i log2 e) from
 // the dO row it holds anyway and the O row, stores -Dvec_i and LSE_i log2 e, and the
 // per-key-tile launch reads them.
@@ -737,14 +739,15 @@ struct Tile32 {
 template <int D, int W>
 constexpr int dkdv_f32_wpe() { return W == 8 ? (D == 128 ? 2 : 4) : W == 4 ? 2 : 1; }
 
-template <int D, bool CAUSAL, int W>
+template <int D, bool CAUSAL, int W, bool DS = false>
 __global__ void __launch_bounds__(64 * W)
 __attribute__((amdgpu_waves_per_eu(dkdv_f32_wpe<D, W>(), dkdv_f32_wpe<D, W>())))
 bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restrict__ Q,
                        const float* __restrict__ K, const float* __restrict__ V,
                        const float* __restrict__ dO, const float* __restrict__ LSE,
                        const float* __restrict__ Dv, float* __restrict__ dK,
-                       float* __restrict__ dV, int accumulate, int kv_alias) {
+                       float* __restrict__ dV, int accumulate, int kv_alias,
+                       float* __restrict__ dS_out, long long ds_slice) {
     using Tl = Tile32<D, 64 * W>;
     constexpr int NB = D / 16, NDQ = D / 4, QB = RB / 16;
     extern __shared__ __attribute__((aligned(16))) float fsm[];
@@ -804,7 +807,27 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
         const bool more = st + 1 < nst;
         if (more) fetch(st + 1);
         const int i0 = qstart + st * RB;
-        if (!(CAUSAL && i0 + RB - 1 < k0)) {
+        // DS (128-key work-groups only): scale dS[i][j] into dS_out's rows that the dQ product reads,
+        // row i of 128-row tile t = i / 128 at t (t + 1) 8192 + (i - 128 t)(t + 1) 128 (causal:
+        // keys up to the tile's end) or i 128 T (all T tiles of keys)
+        auto ds_at = [&](int i) -> float* {
+            const int t = i >> 7;
+            const long long off = CAUSAL ? 8192LL * t * (t + 1) + (long long)(i - 128 * t) * (t + 1) * 128
+                                         : (long long)i * (((S + 127) >> 7) << 7);
+            return dS_out + bh * ds_slice + off + j;
+        };
+        if (CAUSAL && i0 + RB - 1 < k0) {
+            // no key of this wave is visible to these queries: their dS entries are zeros
+            if (DS) {
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = i0 + 16 * qb + 4 * g + r;
+                        if (i < S) *ds_at(i) = 0.f;
+                    }
+            }
+        } else {
             const float* qs = fsm + cur * 2 * Tl::ELEMS;
             const float* gs = qs + Tl::ELEMS;
             f32x4 s[QB], dp[QB];
@@ -828,6 +851,7 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
                     const bool ok = i < S && j < S && (!CAUSAL || j <= i);
                     p[qb][r] = ok ? fast_exp2(s[qb][r] * sl2 - s_lse[cur][il]) : 0.f;
                     ds[qb][r] = p[qb][r] * (dp[qb][r] - s_dv[cur][il]);
+                    if (DS && i < S) *ds_at(i) = ds[qb][r] * scale;
                 }
             // dV^T[d][j] += sum_i dO[i][d] P[i][j], d = 16 b + (row of the result)
 #pragma unroll
@@ -1244,16 +1268,17 @@ int run_bf16(int BH, int S, float scale, const void* Q, const void* K, const voi
     return DH_OK;
 }
 
-template <int D, bool CAUSAL, int W>
+template <int D, bool CAUSAL, int W, bool DS = false>
 int launch_dkdv_f32(int BH, int S, float scale, float sl2, const void* Q, const void* K,
                     const void* V, const void* dO, const float* LSE, const float* Dv, float* dK,
-                    float* dV, int acc, int kv_alias, size_t lds) {
-    auto kern = bwd_dkdv_f32_kernel<D, CAUSAL, W>;
+                    float* dV, int acc, int kv_alias, size_t lds, float* dS_out = nullptr,
+                    long long ds_slice = 0) {
+    auto kern = bwd_dkdv_f32_kernel<D, CAUSAL, W, DS>;
     static bool done = false;
     DH_TRY(set_lds(kern, lds, done));
     kern<<<BH * ((S + 16 * W - 1) / (16 * W)), 64 * W, lds, stream()>>>(
         BH, S, scale, sl2, (const float*)Q, (const float*)K, (const float*)V, (const float*)dO,
-        LSE, Dv, dK, dV, acc, kv_alias);
+        LSE, Dv, dK, dV, acc, kv_alias, dS_out, ds_slice);
     return check_launch("dh_flash_bwd(dK,dV f32)");
 }
 
@@ -1281,7 +1306,7 @@ inline int f32_waves(int BH, int S, int rows) {
 template <int D, bool CAUSAL>
 int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void* V,
             const void* dO, const float* LSE, const float* Dv, float* dQ, float* dK, float* dV,
-            int acc, int kv_alias, int acc_q) {
+            int acc, int kv_alias, int acc_q, int allow_ds) {
     using Tl = Tile32<D>;
     const float sl2 = scale * 1.4426950408889634f;
     // Small and mid grids: the 16-key / 16-query kernels, where the tiled kernels' work-groups
@@ -1322,6 +1347,44 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
         }
     }
     const size_t lds = 2 * 2 * Tl::ELEMS * sizeof(float);
+    // D = 128 grids of 128-key dK/dV work-groups over at least 64 slices: that launch also
+    // stores scale dS (fp32) for every query row and the keys up to the end of its 128-row tile
+    // (causal) or all keys, and dQ becomes one batched GEMM per 128-row tile, dQ_tile (+)=
+    // (scale dS_tile) K -- one S^2 D product instead of the dQ launch's three (S and dP
+    // recomputed, then dS K).  Scratch: BH 128^2 T (T + 1) / 2 floats causal, BH (128 T)^2 not
+    // (T = ceil(S / 128)), from the pool; without it, or beyond 8 GB, the dQ launch below.  The
+    // dS traffic does not shrink with D, and each per-tile GEMM needs the slices to fill the
+    // CUs, hence the bounds.  Same box, whole backward: config 4's shape 16.85 -> 13.55 ms,
+    // (64, 2048, 128) causal 2.23 -> 1.77 ms, (64, 1024, 128) 1.05 -> 0.88 ms; but (32, 4096,
+    // 128) causal 4.13 -> 8.03 ms (128 tiles per GEMM), (64, 1024, 64) causal 0.43 -> 0.66 ms.
+    if constexpr (D == 128) {
+        static const int ds_knob = [] {
+            const char* e = std::getenv("DH_FLASH_BWD_F32_DS");   // tuning knob: 0 or 1
+            return e ? std::atoi(e) : 1;
+        }();
+        if (allow_ds && ds_knob && BH >= 64 && f32_waves(BH, S, 16) == 8) {
+            const long long T = (S + 127) / 128;
+            const long long slice = CAUSAL ? 8192LL * T * (T + 1) : 16384LL * T * T;
+            constexpr long long DS_CAP = 8LL << 30;
+            const long long bytes = slice * BH * (long long)sizeof(float);
+            float* dS = bytes <= DS_CAP ? static_cast<float*>(dh_malloc((size_t)bytes)) : nullptr;
+            if (dS) {
+                int st = launch_dkdv_f32<D, CAUSAL, 8, true>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv,
+                                                             dK, dV, acc, kv_alias, lds, dS, slice);
+                for (int t = 0; st == DH_OK && t < T; ++t) {
+                    const int rows = S - 128 * t < 128 ? S - 128 * t : 128;
+                    const int len = CAUSAL ? (int)(128 * (t + 1)) : (int)(128 * T);
+                    const int kk = len < S ? len : S;
+                    const long long aoff = CAUSAL ? 8192LL * t * (t + 1) : (long long)128 * t * len;
+                    st = dh_gemm_f32_ex(0, 0, rows, D, kk, dS + aoff, len, slice, (const float*)K, D,
+                                        (long long)S * D, acc_q ? 1.f : 0.f, dQ + (size_t)128 * t * D,
+                                        D, (long long)S * D, BH, nullptr, 0);
+                }
+                dh_free(dS);   // pooled; later users of the buffer are ordered on the stream
+                return st;
+            }
+        }
+    }
     // dK/dV: 16 keys per wave (8 waves, 128 keys, when that grid fills the CUs).
     switch (f32_waves(BH, S, 16)) {
     case 8: DH_TRY((launch_dkdv_f32<D, CAUSAL, 8>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv, dK, dV, acc, kv_alias, lds))); break;
@@ -1355,7 +1418,7 @@ int run_dvec(int rows, const void* O, const void* dO, float* Dv) {
 template <int D>
 int dispatch(int dtype, int causal, int BH, int S, float scale, const void* Q, const void* K,
              const void* V, const void* O, const void* dO, const float* LSE, float* Dv,
-             float* dQ, float* dK, float* dV, int acc, int kv_alias, int acc_q) {
+             float* dQ, float* dK, float* dV, int acc, int kv_alias, int acc_q, int allow_ds) {
     const int rows = BH * S;
     if (dtype == DH_BF16) {
         float* L2 = Dv + rows;                       // second half of the scratch
@@ -1363,8 +1426,8 @@ int dispatch(int dtype, int causal, int BH, int S, float scale, const void* Q, c
                       : run_bf16<D, false>(BH, S, scale, Q, K, V, O, dO, LSE, L2, Dv, dQ, dK, dV, acc);
     }
     DH_TRY((run_dvec<float, D>(rows, O, dO, Dv)));
-    return causal ? run_f32<D, true>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc, kv_alias, acc_q)
-                  : run_f32<D, false>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc, kv_alias, acc_q);
+    return causal ? run_f32<D, true>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc, kv_alias, acc_q, allow_ds)
+                  : run_f32<D, false>(BH, S, scale, Q, K, V, dO, LSE, Dv, dQ, dK, dV, acc, kv_alias, acc_q, allow_ds);
 }
 
 }  // namespace
@@ -1407,17 +1470,17 @@ int check_bwd_args(int dtype, int BH, int S, int D, const void* Q, const void* K
 // dV accumulates onto what that launch stored; bf16: the other way round (run_bf16).
 int run_bwd(int dtype, int BH, int S, int D, float scale, int causal, const void* Q,
             const void* K, const void* V, const void* O, const void* dO, const float* LSE,
-            float* dQ, float* dK, float* dV, int accumulate, float* Dv) {
+            float* dQ, float* dK, float* dV, int accumulate, float* Dv, int allow_ds) {
     const int kv_alias = dK == dV;
     const int acc_q = accumulate || dQ == dK || dQ == dV;
     if (D == 128)
         return dispatch<128>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV,
-                             accumulate, kv_alias, acc_q);
+                             accumulate, kv_alias, acc_q, allow_ds);
     if (D == 64)
         return dispatch<64>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV,
-                            accumulate, kv_alias, acc_q);
+                            accumulate, kv_alias, acc_q, allow_ds);
     return dispatch<32>(dtype, causal, BH, S, scale, Q, K, V, O, dO, LSE, Dv, dQ, dK, dV,
-                        accumulate, kv_alias, acc_q);
+                        accumulate, kv_alias, acc_q, allow_ds);
 }
 
 }  // namespace
@@ -1435,7 +1498,7 @@ extern "C" int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int ca
     float* Dv = (float*)dh_malloc((size_t)BH * S * sizeof(float) * (dtype == DH_BF16 ? 2 : 1));
     if (!Dv) return DH_ERR_OOM;
     const int st = run_bwd(dtype, BH, S, D, scale, causal, Q, K, V, O, dO, LSE, dQ, dK, dV,
-                           accumulate, Dv);
+                           accumulate, Dv, 1);
     dh_free(Dv);
     return st;
 }
@@ -1494,6 +1557,7 @@ extern "C" int dh_flash_bwd_noalloc(int dtype, int BH, int S, int D, float scale
     DH_TRY(scratch_address(&Dv));
     // Every Dvec / LSE*log2(e) entry the later launches read is written earlier in this call
     // (by the Dvec launch, or for bf16 by the dQ launch), so nothing is cleared.
+    // (no pool memory here: the fp32 dQ launch recomputes dS instead of storing it)
     return run_bwd(dtype, BH, S, D, scale, causal, Q, K, V, O, dO, LSE, dQ, dK, dV, accumulate,
-                   Dv);
+                   Dv, 0);
 }

@@ -1,7 +1,8 @@
 """dh_flash_bwd_noalloc (the flash backward over a fixed device array, for callers that cannot
 allocate) against dh_flash_bwd on the same inputs: bit-identical outputs, fp32 and bf16, on
 two calls in a row with the second one smaller, so stale scratch contents from the first call
-cannot leak into the second.  Also the size limit, the shared-buffer (aliased) cases, and a
+cannot leak into the second; at a shape where dh_flash_bwd forms the fp32 dQ from a stored dS
+(D = 128, 64 slices), equal to fp32 rounding.  Also the size limit, the shared-buffer (aliased) cases, and a
 call recorded under HIP stream capture and replayed as a graph."""
 import ctypes
 
@@ -60,6 +61,19 @@ def test_noalloc_matches_pool_version_on_two_calls(dtype):
         got = _run_noalloc(*args, BH, S, D, causal, dtype, init=init, accumulate=True)
         for w, g in zip(want, got):
             assert np.array_equal(w, g), (BH, S, D, dtype, "accumulate")
+
+
+def test_noalloc_fp32_where_the_pool_version_stores_ds():
+    # D = 128 over 64 slices: dh_flash_bwd writes scale dS to pool memory and forms dQ as a
+    # GEMM on it; the no-alloc entry point recomputes dS in its dQ launch.  dK and dV come from
+    # the same launch either way (bit-identical); dQ agrees to the fp32 bound.
+    BH, S, D = 64, 512, 128
+    args = _case(BH, S, D, True, "f32", 4)
+    want = flash_bwd(*args, BH, S, D, True, dtype="f32")
+    got = _run_noalloc(*args, BH, S, D, True, "f32")
+    assert np.array_equal(want[1], got[1]) and np.array_equal(want[2], got[2])
+    err = np.abs(want[0] - got[0]).max() / np.abs(want[0]).max()
+    assert err <= 1e-5 * np.sqrt(S), err
 
 
 def test_noalloc_rejects_sizes_beyond_its_scratch():
