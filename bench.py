@@ -20,7 +20,7 @@ synchronisation on both sides.  ms_per_step is the mean launch duration.  Every 
 inputs are staged in HBM before the first one is timed, and the workloads run back to back
 (fp32 GEMM 4096^3 first, then the headline), so none but the first starts from an idle chip.
 The two PCIe-inclusive runtime steps (config 2 and config 4 through the Dream builtins on
-host fp64 tensors) run last, after 10 s of idle.
+host fp64 tensors) run last, after 20 s of idle.
 """
 import argparse
 import json
@@ -916,10 +916,11 @@ def main():
         # gap except the first, the fp32 GEMM, which takes the transient.  The other
         # workloads follow in the same way (all inputs together take a few GB of HBM).
         # The two runtime steps (host fp64 tensors, PCIe copies inside the time) come last,
-        # after 10 s of idle: right after the fp32 flash backward at config 4's shape the
-        # platform's power management leaves device-to-host copies at half speed for seconds
-        # (config-2 step 2.3 ms, then 1.7 / 1.6 / 1.4 ms after 1 / 3 / 10 s idle; its kernels
-        # unchanged, rocprofv3 copy trace 62 -> 135 us per copy).
+        # after 20 s of idle: after heavy GPU work the platform's power management leaves
+        # device-to-host copies slow for seconds (config-2 step 2.3 ms right after the fp32
+        # flash backward at config 4's shape, then 1.7 / 1.6 / 1.4 ms after 1 / 3 / 10 s of
+        # idle; its kernels unchanged, rocprofv3 copy trace 62 -> 135 us per copy).  Timed
+        # first instead, they left the bf16 GEMM's 5-launch protocol 2% slower.
         order = NORTH_STAR_ORDER + [n for n in WORKLOADS if n not in NORTH_STAR_ORDER]
         staged = {n: prepare(n) for n in order}
         hip.sync()
@@ -928,7 +929,7 @@ def main():
         head = metrics.pop(args.workload)
         metrics["mlp_c2"] = mlp_metrics(max(5, args.steps), 3)
         hip.sync()
-        time.sleep(10.0)
+        time.sleep(20.0)
         metrics["runtime_mlp_c2_step"] = runtime_mlp_metrics()
         metrics["runtime_flash_c4_step"] = runtime_flash_c4_metrics()
 
