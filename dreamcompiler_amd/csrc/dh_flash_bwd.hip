@@ -797,6 +797,26 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
             s_dv[buf][tid] = pre_dv;
         }
     };
+    // DS (128-key work-groups): scale dS of each stage goes to an LDS tile [RB queries][128
+    // keys] (two, alternating by stage), and the work-group writes the previous stage's tile
+    // out as whole 512-byte row pieces: row i of 128-row tile t lies at t (t + 1) 8192 +
+    // (i - 128 t)(t + 1) 128 of the slice (causal: keys up to the tile's end) or at i 128 T
+    // (all T tiles of keys), and this work-group's keys are the 128 from kbase.
+    constexpr int DSS = 128 + 4;                                    // LDS tile row stride
+    float* const dst = fsm + 4 * Tl::ELEMS;                         // [2][RB][DSS] with DS
+    auto flush = [&](int stp) {
+        static_assert(!DS || W == 8, "dS tiles need 128-key work-groups");
+        const int row = tid >> 4, c0 = 8 * (tid & 15);              // 32 rows x 16 x 8 keys
+        const int i = qstart + stp * RB + row;
+        if (i >= S) return;
+        const int t = i >> 7;
+        const long long off = CAUSAL ? 8192LL * t * (t + 1) + (long long)(i - 128 * t) * (t + 1) * 128
+                                     : (long long)i * (((S + 127) >> 7) << 7);
+        const float* src = dst + (stp & 1) * RB * DSS + row * DSS + c0;
+        float* out = dS_out + bh * ds_slice + off + kbase + c0;
+        *reinterpret_cast<f32x4*>(out) = *reinterpret_cast<const f32x4*>(src);
+        *reinterpret_cast<f32x4*>(out + 4) = *reinterpret_cast<const f32x4*>(src + 4);
+    };
     if (nst > 0) {
         fetch(0);
         store(0);
@@ -806,26 +826,18 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
         const int cur = st & 1;
         const bool more = st + 1 < nst;
         if (more) fetch(st + 1);
+        // the previous stage's tile, complete since the barrier that ended that stage; the
+        // next write to its buffer comes after this stage's barrier
+        if (DS && st > 0) flush(st - 1);
         const int i0 = qstart + st * RB;
-        // DS (128-key work-groups only): scale dS[i][j] into dS_out's rows that the dQ product reads,
-        // row i of 128-row tile t = i / 128 at t (t + 1) 8192 + (i - 128 t)(t + 1) 128 (causal:
-        // keys up to the tile's end) or i 128 T (all T tiles of keys)
-        auto ds_at = [&](int i) -> float* {
-            const int t = i >> 7;
-            const long long off = CAUSAL ? 8192LL * t * (t + 1) + (long long)(i - 128 * t) * (t + 1) * 128
-                                         : (long long)i * (((S + 127) >> 7) << 7);
-            return dS_out + bh * ds_slice + off + j;
-        };
         if (CAUSAL && i0 + RB - 1 < k0) {
             // no key of this wave is visible to these queries: their dS entries are zeros
             if (DS) {
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int i = i0 + 16 * qb + 4 * g + r;
-                        if (i < S) *ds_at(i) = 0.f;
-                    }
+                    for (int r = 0; r < 4; ++r)
+                        dst[cur * RB * DSS + (16 * qb + 4 * g + r) * DSS + 16 * wave + l16] = 0.f;
             }
         } else {
             const float* qs = fsm + cur * 2 * Tl::ELEMS;
@@ -851,7 +863,7 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
                     const bool ok = i < S && j < S && (!CAUSAL || j <= i);
                     p[qb][r] = ok ? fast_exp2(s[qb][r] * sl2 - s_lse[cur][il]) : 0.f;
                     ds[qb][r] = p[qb][r] * (dp[qb][r] - s_dv[cur][il]);
-                    if (DS && i < S) *ds_at(i) = ds[qb][r] * scale;
+                    if (DS) dst[cur * RB * DSS + il * DSS + 16 * wave + l16] = ds[qb][r] * scale;
                 }
             // dV^T[d][j] += sum_i dO[i][d] P[i][j], d = 16 b + (row of the result)
 #pragma unroll
@@ -871,6 +883,7 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
         if (more) store(cur ^ 1);
         __syncthreads();
     }
+    if (DS && nst > 0) flush(nst - 1);
     if (j >= S) return;
     float* dkr = dK + base + (size_t)j * D;
     float* dvr = dV + base + (size_t)j * D;
@@ -1369,8 +1382,9 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
             const long long bytes = slice * BH * (long long)sizeof(float);
             float* dS = bytes <= DS_CAP ? static_cast<float*>(dh_malloc((size_t)bytes)) : nullptr;
             if (dS) {
+                const size_t lds_ds = lds + (size_t)2 * RB * (128 + 4) * sizeof(float);
                 int st = launch_dkdv_f32<D, CAUSAL, 8, true>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv,
-                                                             dK, dV, acc, kv_alias, lds, dS, slice);
+                                                             dK, dV, acc, kv_alias, lds_ds, dS, slice);
                 for (int t = 0; st == DH_OK && t < T; ++t) {
                     const int rows = S - 128 * t < 128 ? S - 128 * t : 128;
                     const int len = CAUSAL ? (int)(128 * (t + 1)) : (int)(128 * T);
