@@ -8,8 +8,8 @@
 //   1. Dvec_i = dO_i . O_i                                   (one pass over O, dO)
 //   2. per key tile:   dV += P^T dO,  dK += scale * dS^T Q    (dS = P o (dP - Dvec))
 //   3. per query tile: dQ += scale * dS K                     (S and dP recomputed)
-// or, at D = 128 over at least 64 slices, launch 2 also stores scale * dS and dQ is one batched
-// GEMM per 128-row query tile on it.
+// or, at D = 128 where launch 2's 128-key work-groups fill the CUs, launch 2 also stores
+// scale * dS and dQ is one GEMM launch over every 128-row query tile on it.
 // bf16, two: the per-query-tile launch runs first and forms Dvec_i (and LSE_i log2 e) from
 // the dO row it holds anyway and the O row, stores -Dvec_i and LSE_i log2 e, and the
 // per-key-tile launch reads them.
@@ -1360,22 +1360,24 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
         }
     }
     const size_t lds = 2 * 2 * Tl::ELEMS * sizeof(float);
-    // D = 128 grids of 128-key dK/dV work-groups over at least 64 slices: that launch also
-    // stores scale dS (fp32) for every query row and the keys up to the end of its 128-row tile
-    // (causal) or all keys, and dQ becomes one batched GEMM per 128-row tile, dQ_tile (+)=
-    // (scale dS_tile) K -- one S^2 D product instead of the dQ launch's three (S and dP
-    // recomputed, then dS K).  Scratch: BH 128^2 T (T + 1) / 2 floats causal, BH (128 T)^2 not
-    // (T = ceil(S / 128)), from the pool; without it, or beyond 8 GB, the dQ launch below.  The
-    // dS traffic does not shrink with D, and each per-tile GEMM needs the slices to fill the
-    // CUs, hence the bounds.  Same box, whole backward: config 4's shape 16.85 -> 13.55 ms,
-    // (64, 2048, 128) causal 2.23 -> 1.77 ms, (64, 1024, 128) 1.05 -> 0.88 ms; but (32, 4096,
-    // 128) causal 4.13 -> 8.03 ms (128 tiles per GEMM), (64, 1024, 64) causal 0.43 -> 0.66 ms.
+    // D = 128 grids of at least a round of 128-key dK/dV work-groups: that launch also stores
+    // scale dS (fp32) for every query row and the keys up to the end of its 128-row tile
+    // (causal) or all keys, and dQ_tile (+)= (scale dS_tile) K for every 128-row tile of every
+    // slice is one GEMM launch (flash_dq_from_ds_f32, heaviest tiles first) -- one S^2 D product
+    // instead of the dQ launch's three (S and dP recomputed, then dS K).  Scratch: BH 128^2 T
+    // (T + 1) / 2 floats causal, BH (128 T)^2 not (T = ceil(S / 128)), from the pool; without
+    // it, or beyond 8 GB, the dQ launch below.  The dS traffic does not shrink with D, hence
+    // D = 128 only ((64, 1024, 64) causal 0.43 -> 0.66 ms with one GEMM launch per tile).
+    // Same box, whole backward, recomputing dQ launch -> stored dS: config 4's shape 16.85 ->
+    // 12.5-12.7 ms, (64, 2048, 128) causal 2.23 -> 1.68 ms, (64, 1024, 128) 1.05 -> 0.85 ms,
+    // (32, 4096, 128) causal 4.14 -> 3.11 ms, (8, 4096, 128) non-causal 2.05 -> 1.54 ms,
+    // (1, 32768, 128) causal 15.9 -> 11.7 ms.
     if constexpr (D == 128) {
         static const int ds_knob = [] {
             const char* e = std::getenv("DH_FLASH_BWD_F32_DS");   // tuning knob: 0 or 1
             return e ? std::atoi(e) : 1;
         }();
-        if (allow_ds && ds_knob && BH >= 64 && f32_waves(BH, S, 16) == 8) {
+        if (allow_ds && ds_knob && f32_waves(BH, S, 16) == 8) {
             const long long T = (S + 127) / 128;
             const long long slice = CAUSAL ? 8192LL * T * (T + 1) : 16384LL * T * T;
             constexpr long long DS_CAP = 8LL << 30;
@@ -1385,15 +1387,9 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
                 const size_t lds_ds = lds + (size_t)2 * RB * (128 + 4) * sizeof(float);
                 int st = launch_dkdv_f32<D, CAUSAL, 8, true>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv,
                                                              dK, dV, acc, kv_alias, lds_ds, dS, slice);
-                for (int t = 0; st == DH_OK && t < T; ++t) {
-                    const int rows = S - 128 * t < 128 ? S - 128 * t : 128;
-                    const int len = CAUSAL ? (int)(128 * (t + 1)) : (int)(128 * T);
-                    const int kk = len < S ? len : S;
-                    const long long aoff = CAUSAL ? 8192LL * t * (t + 1) : (long long)128 * t * len;
-                    st = dh_gemm_f32_ex(0, 0, rows, D, kk, dS + aoff, len, slice, (const float*)K, D,
-                                        (long long)S * D, acc_q ? 1.f : 0.f, dQ + (size_t)128 * t * D,
-                                        D, (long long)S * D, BH, nullptr, 0);
-                }
+                if (st == DH_OK)
+                    st = flash_dq_from_ds_f32(BH, S, CAUSAL, dS, slice, (const float*)K,
+                                              acc_q ? 1.f : 0.f, dQ);
                 dh_free(dS);   // pooled; later users of the buffer are ordered on the stream
                 return st;
             }

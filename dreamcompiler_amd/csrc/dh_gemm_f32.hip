@@ -125,21 +125,15 @@ struct Slice {
     }
 };
 
-// Work-group tile TBM x TBN (128 x 128, or 64 x 256 / 256 x 64 for products with M or N at
-// most 64); the 4 waves tile it in 64 x 64 sub-tiles.
-template <bool TA, bool TB, bool VA, bool VB, int TBM, int TBN>
-__global__ void __launch_bounds__(NTHREADS)
-gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
-                const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
-                long long sA, long long sB, long long sC, const float* __restrict__ bias,
-                int epi, int k_last) {
-    // Batch member blockIdx.y (strides in elements; 0 for a single product).  In a split-K
-    // launch the members are the chunks of K, and the last one takes the ragged rest, k_last
-    // (= K otherwise).
-    if (blockIdx.y == gridDim.y - 1) K = k_last;
-    A += blockIdx.y * sA;
-    B += blockIdx.y * sB;
-    C += blockIdx.y * sC;
+// One work-group tile TBM x TBN of C (128 x 128, or 64 x 256 / 256 x 64 for products with M
+// or N at most 64) at the origin tile_of(m0, n0) sets; the 4 waves tile it in 64 x 64
+// sub-tiles.
+template <bool TA, bool TB, bool VA, bool VB, int TBM, int TBN, typename TileOf>
+__device__ __forceinline__ void gemm_f32_tile(int M, int N, int K, const float* __restrict__ A,
+                                              int lda, const float* __restrict__ B, int ldb,
+                                              float beta, float* __restrict__ C, int ldc,
+                                              const float* __restrict__ bias, int epi,
+                                              TileOf tile_of) {
     constexpr int LDS_A = TBM + 4, LDS_B = TBN + 4;   // padded k-major row strides (floats)
     // Wave sub-tile WT x WT: 64 (2 x 2 MFMA blocks) for the 128 x 128 / 64 x 256 / 256 x 64
     // tiles, 32 (one block) for 64 x 64 tiles.
@@ -149,10 +143,8 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     __shared__ __attribute__((aligned(16))) float As[2][BK * LDS_A];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDS_B];
 
-    const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
-    int tm, tn;
-    xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
-    const int m0 = tm * TBM, n0 = tn * TBN;
+    int m0, n0;
+    tile_of(m0, n0);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, h = lane >> 5;
@@ -249,6 +241,52 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
                 }
             }
         }
+}
+
+template <bool TA, bool TB, bool VA, bool VB, int TBM, int TBN>
+__global__ void __launch_bounds__(NTHREADS)
+gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
+                const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
+                long long sA, long long sB, long long sC, const float* __restrict__ bias,
+                int epi, int k_last) {
+    // Batch member blockIdx.y (strides in elements; 0 for a single product).  In a split-K
+    // launch the members are the chunks of K, and the last one takes the ragged rest, k_last
+    // (= K otherwise).
+    if (blockIdx.y == gridDim.y - 1) K = k_last;
+    A += blockIdx.y * sA;
+    B += blockIdx.y * sB;
+    C += blockIdx.y * sC;
+    gemm_f32_tile<TA, TB, VA, VB, TBM, TBN>(M, N, K, A, lda, B, ldb, beta, C, ldc, bias, epi,
+                                            [&](int& m0, int& n0) {
+        const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
+        int tm, tn;
+        xcd_tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, 8, tm, tn);
+        m0 = tm * TBM;
+        n0 = tn * TBN;
+    });
+}
+
+// dQ of the fp32 flash backward from stored scale*dS (one launch for all row tiles): work-group
+// b owns query tile t = T - 1 - b / BH (heaviest first) of slice bh = b % BH and forms
+// dQ[bh][128 t .. +rows][0..128) (+)= dS_t K[bh][0..kk), where dS_t (rows x kk, row stride len)
+// starts at dS + bh slice + off: causal len = 128 (t + 1), off = 8192 t (t + 1) (tile t's rows
+// hold the keys up to the tile's end); otherwise len = 128 T, off = 128 t len; kk = min(len,
+// S).  Consecutive work-groups take consecutive slices, so with BH a multiple of 8 each XCD
+// reads the K rows of its own slices.  Head dimension 128 (the tile width).
+template <bool VA, bool VB>
+__global__ void __launch_bounds__(NTHREADS)
+flash_dq_from_ds_kernel(int BH, int S, int T, int causal, const float* __restrict__ dS,
+                        long long slice, const float* __restrict__ Kr, float beta,
+                        float* __restrict__ dQ) {
+    const int b = blockIdx.x, t = T - 1 - b / BH, bh = b % BH;
+    const int rows = S - 128 * t < 128 ? S - 128 * t : 128;
+    const int len = causal ? 128 * (t + 1) : 128 * T;
+    const int kk = len < S ? len : S;
+    const long long off = causal ? 8192LL * t * (t + 1) : 128LL * t * len;
+    const size_t sd = (size_t)bh * S * 128;
+    gemm_f32_tile<false, false, VA, VB, 128, 128>(rows, 128, kk, dS + bh * slice + off, len,
+                                                  Kr + sd, 128, beta, dQ + sd + (size_t)128 * t * 128,
+                                                  128, nullptr, 0, [](int& m0, int& n0) { m0 = n0 = 0; });
 }
 
 // 64 x 64 tiles with two waves per SIMD: for grids of about one work-group per CU (config 1's
@@ -1206,6 +1244,20 @@ int splitk_reduce_launch(const float* part, int S, int M, int N, float beta, flo
     if (blocks > (size_t)num_cus() * 8) blocks = (size_t)num_cus() * 8;
     splitk_reduce<<<(unsigned)blocks, 256, 0, stream()>>>(part, S, M, N, beta, C, ldc, bias, epi);
     return check_launch("split-K reduce");
+}
+
+int flash_dq_from_ds_f32(int BH, int S, int causal, const float* dS, long long slice,
+                         const float* K, float beta, float* dQ) {
+    const int T = (S + 127) / 128;
+    // 16-byte loads of dS rows need every tile's K extent (a multiple of 128, or S) to be a
+    // multiple of 4; K rows (128 floats) need an aligned base
+    const bool va = S % 4 == 0, vb = (uintptr_t)K % 16 == 0;
+    auto kern = va && vb ? flash_dq_from_ds_kernel<true, true>
+              : va       ? flash_dq_from_ds_kernel<true, false>
+              : vb       ? flash_dq_from_ds_kernel<false, true>
+                         : flash_dq_from_ds_kernel<false, false>;
+    kern<<<(unsigned)(T * BH), NTHREADS, 0, stream()>>>(BH, S, T, causal, dS, slice, K, beta, dQ);
+    return check_launch("flash backward dQ from dS");
 }
 
 }  // namespace dh

@@ -124,6 +124,25 @@ def test_fp32_bwd_wide_grid(BH, S, D, causal):
         assert err[worst] <= tol * m[worst].max(), (name, worst)
 
 
+@pytest.mark.parametrize("BH,S,causal", [(8, 4096, True), (16, 2048, False), (13, 2558, True)])
+def test_fp32_bwd_stored_ds_few_slices(BH, S, causal):
+    """D = 128 grids of a round of 128-key dK/dV work-groups over few, long slices: that
+    launch stores scale dS and dQ comes from one GEMM launch over all T = ceil(S / 128) query
+    tiles of every slice, heaviest first -- 32, 16 and 20 tiles here, so tile t's dS rows
+    (keys up to 128 (t + 1) causal, all 128 T otherwise) sit far into each slice's scratch;
+    S = 2558 leaves a ragged last tile and rows whose length is not a multiple of 4 (the
+    GEMM's scalar-load form).  Every slice of all three gradients against the fp64 oracle."""
+    D = 128
+    Q, K, V, G = inputs(BH, S, D, 9100 + S + causal)
+    Of, lse = flash_fwd(Q, K, V, BH, S, D, causal)
+    grads = flash_bwd(Q, K, V, Of, G, lse, BH, S, D, causal)
+    refs = _bwd_ref(Q, K, V, G, BH, S, D, causal)
+    tol = 1e-5 * np.sqrt(S)
+    for name, g, r in zip("QKV", grads, refs):
+        for b in range(BH):
+            assert maxrel(g.reshape(BH, S, D)[b], r.reshape(BH, S, D)[b]) <= tol, (name, b)
+
+
 @pytest.mark.parametrize("S", [1, 64, 100, 257, 520])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
