@@ -784,7 +784,7 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
         tg.fetch(dO + base, r0, S, tid);
         if (tid < RB) {
             const int row = r0 + tid;
-            pre_lse = row < S ? LSE[(size_t)bh * S + row] * 1.4426950408889634f : 0.f;
+            pre_lse = row < S ? LSE[(size_t)bh * S + row] : 0.f;   // scaled in store()
             pre_dv = row < S ? Dv[(size_t)bh * S + row] : 0.f;
         }
     };
@@ -793,7 +793,9 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
         tq.store(sb, tid);
         tg.store(sb + Tl::ELEMS, tid);
         if (tid < RB) {
-            s_lse[buf][tid] = pre_lse;
+            // the log2(e) scaling here rather than at the load, so that no instruction waits
+            // for the load (and, in order, for the Q/dO loads before it) until this store
+            s_lse[buf][tid] = pre_lse * 1.4426950408889634f;
             s_dv[buf][tid] = pre_dv;
         }
     };
@@ -822,6 +824,12 @@ bwd_dkdv_f32_kernel(int BH, int S, float scale, float sl2, const float* __restri
         store(0);
         __syncthreads();
     }
+    // K and V (kf, vf) have landed on every path into the stage loop.  store(0)'s wait covers
+    // them only where a stage exists, and without this wait the compiler's wait insertion
+    // cannot tell them from the loop's own loads: it made each stage's first MFMA wait for the
+    // next stage's prefetch.  The builtin (vmcnt(0), expcnt and lgkmcnt untouched), unlike
+    // inline assembly, is seen by that pass.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     for (int st = 0; st < nst; ++st) {
         const int cur = st & 1;
         const bool more = st + 1 < nst;
