@@ -1372,9 +1372,13 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
     // scale dS (fp32) for every query row and the keys up to the end of its 128-row tile
     // (causal) or all keys, and dQ_tile (+)= (scale dS_tile) K for every 128-row tile of every
     // slice is one GEMM launch (flash_dq_from_ds_f32, heaviest tiles first) -- one S^2 D product
-    // instead of the dQ launch's three (S and dP recomputed, then dS K).  Scratch: BH 128^2 T
-    // (T + 1) / 2 floats causal, BH (128 T)^2 not (T = ceil(S / 128)), from the pool; without
-    // it, or beyond 8 GB, the dQ launch below.  The dS traffic does not shrink with D, hence
+    // instead of the dQ launch's three (S and dP recomputed, then dS K).  Scratch: 128^2 T
+    // (T + 1) / 2 floats per slice causal, (128 T)^2 not (T = ceil(S / 128)), from the pool, at
+    // most 8 GB: beyond that the slices run in equal chunks (each dK/dV launch and its dQ launch
+    // over one chunk, the scratch reused), each chunk still a round of 128-key tiles; without
+    // the memory, or where a chunk would be smaller, the dQ launch below.  Per slice the work
+    // is the same whichever chunk holds it, so results do not depend on the chunking.  The dS
+    // traffic does not shrink with D, hence
     // D = 128 only ((64, 1024, 64) causal 0.43 -> 0.66 ms with one GEMM launch per tile).
     // Same box, whole backward, recomputing dQ launch -> stored dS: config 4's shape 16.85 ->
     // 12.5-12.7 ms, (64, 2048, 128) causal 2.23 -> 1.68 ms, (64, 1024, 128) 1.05 -> 0.85 ms,
@@ -1385,19 +1389,36 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
             const char* e = std::getenv("DH_FLASH_BWD_F32_DS");   // tuning knob: 0 or 1
             return e ? std::atoi(e) : 1;
         }();
+        static const long long ds_cap = [] {
+            const char* e = std::getenv("DH_FLASH_BWD_F32_DS_CAP");   // tuning knob: bytes
+            return e ? std::atoll(e) : 8LL << 30;
+        }();
         if (allow_ds && ds_knob && f32_waves(BH, S, 16) == 8) {
             const long long T = (S + 127) / 128;
             const long long slice = CAUSAL ? 8192LL * T * (T + 1) : 16384LL * T * T;
-            constexpr long long DS_CAP = 8LL << 30;
-            const long long bytes = slice * BH * (long long)sizeof(float);
-            float* dS = bytes <= DS_CAP ? static_cast<float*>(dh_malloc((size_t)bytes)) : nullptr;
+            // nch chunks of BH / nch or one more slices (at most `per`, the cap's worth)
+            const long long per = ds_cap / (slice * (long long)sizeof(float));
+            const int nch = per > 0 ? (int)((BH + per - 1) / per) : 0;
+            const int small = nch > 0 ? BH / nch : 0, big = nch > 0 ? (BH + nch - 1) / nch : 0;
+            float* dS = nch > 0 && (long long)small * T >= num_cus()
+                            ? static_cast<float*>(dh_malloc((size_t)(slice * big) * sizeof(float)))
+                            : nullptr;
             if (dS) {
                 const size_t lds_ds = lds + (size_t)2 * RB * (128 + 4) * sizeof(float);
-                int st = launch_dkdv_f32<D, CAUSAL, 8, true>(BH, S, scale, sl2, Q, K, V, dO, LSE, Dv,
-                                                             dK, dV, acc, kv_alias, lds_ds, dS, slice);
-                if (st == DH_OK)
-                    st = flash_dq_from_ds_f32(BH, S, CAUSAL, dS, slice, (const float*)K,
-                                              acc_q ? 1.f : 0.f, dQ);
+                int st = DH_OK;
+                for (int c = 0, b0 = 0; st == DH_OK && c < nch; ++c) {
+                    const int nb = small + (c < BH % nch ? 1 : 0);
+                    const size_t eo = (size_t)b0 * S * D, ro = (size_t)b0 * S;
+                    const float* Kc = (const float*)K + eo;
+                    st = launch_dkdv_f32<D, CAUSAL, 8, true>(
+                        nb, S, scale, sl2, (const float*)Q + eo, Kc, (const float*)V + eo,
+                        (const float*)dO + eo, LSE + ro, Dv + ro, dK + eo, dV + eo, acc, kv_alias,
+                        lds_ds, dS, slice);
+                    if (st == DH_OK)
+                        st = flash_dq_from_ds_f32(nb, S, CAUSAL, dS, slice, Kc, acc_q ? 1.f : 0.f,
+                                                  dQ + eo);
+                    b0 += nb;
+                }
                 dh_free(dS);   // pooled; later users of the buffer are ordered on the stream
                 return st;
             }

@@ -143,6 +143,57 @@ def test_fp32_bwd_stored_ds_few_slices(BH, S, causal):
             assert maxrel(g.reshape(BH, S, D)[b], r.reshape(BH, S, D)[b]) <= tol, (name, b)
 
 
+_CHUNK_SCRIPT = r"""
+import hashlib, sys
+sys.path.insert(0, {tests!r})
+sys.path.insert(0, {root!r})
+import numpy as np
+from _gpu import flash_bwd, flash_fwd
+for BH, S, causal in ((512, 128, True), (600, 100, False), (384, 200, True), (769, 64, True)):
+    rng = np.random.default_rng(BH + S)
+    Q, K, V, G = (rng.standard_normal((BH, S * 128)).astype(np.float32) for _ in range(4))
+    O, lse = flash_fwd(Q, K, V, BH, S, 128, causal)
+    init = [rng.standard_normal((BH, S * 128)).astype(np.float32) for _ in range(3)]
+    for acc in (False, True):
+        g = flash_bwd(Q, K, V, O, G, lse, BH, S, 128, causal, accumulate=acc,
+                      init=init if acc else None)
+        print(BH, S, int(causal), int(acc), *(hashlib.sha1(x.tobytes()).hexdigest()[:16] for x in g),
+              flush=True)
+"""
+
+
+def test_fp32_bwd_stored_ds_slice_chunks():
+    """The stored-dS backward in chunks of slices, as a scratch cap below the whole run forces
+    (the cap is read once per process, so each setting runs in a child process): with a 24 MB
+    cap these shapes split into 2 equal, 2 equal, 3 equal and 3 unequal chunks (257, 256, 256),
+    each a round of 128-key tiles.  Every slice does the same work in any chunk, so dQ, dK and
+    dV, plain and accumulated, are bit-identical to the one-chunk run.  With the stored dS off,
+    dK and dV are again identical (the same dK/dV arithmetic) while dQ, recomputed by the other
+    launch, differs in rounding -- which shows the chunked runs took the stored-dS path."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = _CHUNK_SCRIPT.format(tests=here, root=os.path.dirname(here))
+
+    def run(env):
+        r = subprocess.run([sys.executable, "-c", code], env={**os.environ, **env},
+                           capture_output=True, text=True, timeout=110)
+        assert r.returncode == 0, r.stdout + r.stderr
+        lines = r.stdout.split("\n")
+        lines = [l.split() for l in lines if l.strip()]
+        assert len(lines) == 8, r.stdout
+        return lines
+
+    one = run({})
+    chunked = run({"DH_FLASH_BWD_F32_DS_CAP": str(24 << 20)})
+    off = run({"DH_FLASH_BWD_F32_DS": "0"})
+    assert chunked == one
+    for a, b in zip(one, off):
+        assert a[:4] == b[:4] and a[5:] == b[5:], (a, b)   # dK, dV
+        assert a[4] != b[4], a                              # dQ
+
+
 @pytest.mark.parametrize("S", [1, 64, 100, 257, 520])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
