@@ -18,10 +18,10 @@ int num_cus();
 // of M x N (part[s] at part + s M N), added in a fixed order; defined in dh_gemm_f32.hip.
 int splitk_reduce_launch(const float* part, int S, int M, int N, float beta, float* C, int ldc,
                          const float* bias, int epi);
-// The fp32 flash backward's dQ (head dimension 128) from stored scale*dS, every 128-row query
-// tile of every slice in one launch: dQ[bh][tile t] = beta dQ + dS_t K[bh] (dS_t's layout in
-// flash_dq_from_ds_kernel); defined in dh_gemm_f32.hip.
-int flash_dq_from_ds_f32(int BH, int S, int causal, const float* dS, long long slice,
+// The fp32 flash backward's dQ (head dimension D = 128 or 64) from stored scale*dS, every
+// 128-row query tile of every slice in one launch: dQ[bh][tile t] = beta dQ + dS_t K[bh]
+// (dS_t's layout in flash_dq_from_ds_kernel); defined in dh_gemm_f32.hip.
+int flash_dq_from_ds_f32(int BH, int S, int D, int causal, const float* dS, long long slice,
                          const float* K, float beta, float* dQ);
 
 #define DH_TRY(expr)                      \

@@ -8,7 +8,7 @@
 //   1. Dvec_i = dO_i . O_i                                   (one pass over O, dO)
 //   2. per key tile:   dV += P^T dO,  dK += scale * dS^T Q    (dS = P o (dP - Dvec))
 //   3. per query tile: dQ += scale * dS K                     (S and dP recomputed)
-// or, at D = 128 where launch 2's 128-key work-groups fill the CUs, launch 2 also stores
+// or, at D = 128 and 64 where launch 2's 128-key work-groups fill the CUs, launch 2 also stores
 // scale * dS and dQ is one GEMM launch over every 128-row query tile on it.
 // bf16, two: the per-query-tile launch runs first and forms Dvec_i (and LSE_i log2 e) from
 // the dO row it holds anyway and the O row, stores -Dvec_i and LSE_i log2 e, and the
@@ -1368,7 +1368,7 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
         }
     }
     const size_t lds = 2 * 2 * Tl::ELEMS * sizeof(float);
-    // D = 128 grids of at least a round of 128-key dK/dV work-groups: that launch also stores
+    // D = 128 and 64 grids of at least a round of 128-key dK/dV work-groups: that launch stores
     // scale dS (fp32) for every query row and the keys up to the end of its 128-row tile
     // (causal) or all keys, and dQ_tile (+)= (scale dS_tile) K for every 128-row tile of every
     // slice is one GEMM launch (flash_dq_from_ds_f32, heaviest tiles first) -- one S^2 D product
@@ -1378,13 +1378,13 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
     // over one chunk, the scratch reused), each chunk still a round of 128-key tiles; without
     // the memory, or where a chunk would be smaller, the dQ launch below.  Per slice the work
     // is the same whichever chunk holds it, so results do not depend on the chunking.  The dS
-    // traffic does not shrink with D, hence
-    // D = 128 only ((64, 1024, 64) causal 0.43 -> 0.66 ms with one GEMM launch per tile).
+    // traffic does not shrink with D while the products do, so D = 32 keeps the dQ launch.
     // Same box, whole backward, recomputing dQ launch -> stored dS: config 4's shape 16.85 ->
     // 12.5-12.7 ms, (64, 2048, 128) causal 2.23 -> 1.68 ms, (64, 1024, 128) 1.05 -> 0.85 ms,
     // (32, 4096, 128) causal 4.14 -> 3.11 ms, (8, 4096, 128) non-causal 2.05 -> 1.54 ms,
-    // (1, 32768, 128) causal 15.9 -> 11.7 ms.
-    if constexpr (D == 128) {
+    // (1, 32768, 128) causal 15.9 -> 11.7 ms; (128, 2048, 64) causal 2.31 -> 1.95 ms,
+    // (64, 1024, 64) causal 0.44 -> 0.32 ms, (128, 1024, 64) 1.09 -> 0.93 ms.
+    if constexpr (D == 128 || D == 64) {
         static const int ds_knob = [] {
             const char* e = std::getenv("DH_FLASH_BWD_F32_DS");   // tuning knob: 0 or 1
             return e ? std::atoi(e) : 1;
@@ -1415,8 +1415,8 @@ int run_f32(int BH, int S, float scale, const void* Q, const void* K, const void
                         (const float*)dO + eo, LSE + ro, Dv + ro, dK + eo, dV + eo, acc, kv_alias,
                         lds_ds, dS, slice);
                     if (st == DH_OK)
-                        st = flash_dq_from_ds_f32(nb, S, CAUSAL, dS, slice, Kc, acc_q ? 1.f : 0.f,
-                                                  dQ + eo);
+                        st = flash_dq_from_ds_f32(nb, S, D, CAUSAL, dS, slice, Kc,
+                                                  acc_q ? 1.f : 0.f, dQ + eo);
                     b0 += nb;
                 }
                 dh_free(dS);   // pooled; later users of the buffer are ordered on the stream

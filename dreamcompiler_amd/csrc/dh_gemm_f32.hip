@@ -266,27 +266,32 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
     });
 }
 
-// dQ of the fp32 flash backward from stored scale*dS (one launch for all row tiles): work-group
-// b owns query tile t = T - 1 - b / BH (heaviest first) of slice bh = b % BH and forms
-// dQ[bh][128 t .. +rows][0..128) (+)= dS_t K[bh][0..kk), where dS_t (rows x kk, row stride len)
-// starts at dS + bh slice + off: causal len = 128 (t + 1), off = 8192 t (t + 1) (tile t's rows
-// hold the keys up to the tile's end); otherwise len = 128 T, off = 128 t len; kk = min(len,
-// S).  Consecutive work-groups take consecutive slices, so with BH a multiple of 8 each XCD
-// reads the K rows of its own slices.  Head dimension 128 (the tile width).
-template <bool VA, bool VB>
+// dQ of the fp32 flash backward from stored scale*dS (one launch for all row tiles), head
+// dimension D = 128 or 64: query tile t of slice bh is dQ[bh][128 t .. +rows][0..D) (+)= dS_t
+// K[bh][0..kk), where dS_t (rows x kk, row stride len) starts at dS + bh slice + off: causal
+// len = 128 (t + 1), off = 8192 t (t + 1) (tile t's rows hold the keys up to the tile's end);
+// otherwise len = 128 T, off = 128 t len; kk = min(len, S).  A work-group takes a TM x D block
+// of it (TM = 128 at D = 128; two 64 x 64 blocks per tile at D = 64); the tiles go heaviest
+// first, and consecutive work-groups take consecutive slices, so with BH a multiple of 8 each
+// XCD reads the K rows of its own slices.
+template <bool VA, bool VB, int D>
 __global__ void __launch_bounds__(NTHREADS)
 flash_dq_from_ds_kernel(int BH, int S, int T, int causal, const float* __restrict__ dS,
                         long long slice, const float* __restrict__ Kr, float beta,
                         float* __restrict__ dQ) {
-    const int b = blockIdx.x, t = T - 1 - b / BH, bh = b % BH;
-    const int rows = S - 128 * t < 128 ? S - 128 * t : 128;
+    constexpr int TM = D == 128 ? 128 : 64, R = 128 / TM;   // R row blocks per query tile
+    const int bh = blockIdx.x % BH, q = blockIdx.x / BH;
+    const int t = T - 1 - q / R, r = q % R;
+    const int rows = (S - 128 * t < 128 ? S - 128 * t : 128) - TM * r;
+    if (rows <= 0) return;   // the second block of a short last tile
     const int len = causal ? 128 * (t + 1) : 128 * T;
     const int kk = len < S ? len : S;
-    const long long off = causal ? 8192LL * t * (t + 1) : 128LL * t * len;
-    const size_t sd = (size_t)bh * S * 128;
-    gemm_f32_tile<false, false, VA, VB, 128, 128>(rows, 128, kk, dS + bh * slice + off, len,
-                                                  Kr + sd, 128, beta, dQ + sd + (size_t)128 * t * 128,
-                                                  128, nullptr, 0, [](int& m0, int& n0) { m0 = n0 = 0; });
+    const long long off = (causal ? 8192LL * t * (t + 1) : 128LL * t * len) + (long long)TM * r * len;
+    const size_t sd = (size_t)bh * S * D;
+    gemm_f32_tile<false, false, VA, VB, TM, D>(rows < TM ? rows : TM, D, kk, dS + bh * slice + off,
+                                               len, Kr + sd, D, beta,
+                                               dQ + sd + (size_t)(128 * t + TM * r) * D, D, nullptr, 0,
+                                               [](int& m0, int& n0) { m0 = n0 = 0; });
 }
 
 // 64 x 64 tiles with two waves per SIMD: for grids of about one work-group per CU (config 1's
@@ -1246,18 +1251,27 @@ int splitk_reduce_launch(const float* part, int S, int M, int N, float beta, flo
     return check_launch("split-K reduce");
 }
 
-int flash_dq_from_ds_f32(int BH, int S, int causal, const float* dS, long long slice,
-                         const float* K, float beta, float* dQ) {
+template <int D>
+int launch_dq_from_ds(int BH, int S, int causal, const float* dS, long long slice, const float* K,
+                      float beta, float* dQ) {
     const int T = (S + 127) / 128;
     // 16-byte loads of dS rows need every tile's K extent (a multiple of 128, or S) to be a
-    // multiple of 4; K rows (128 floats) need an aligned base
+    // multiple of 4; K rows (D floats) need an aligned base
     const bool va = S % 4 == 0, vb = (uintptr_t)K % 16 == 0;
-    auto kern = va && vb ? flash_dq_from_ds_kernel<true, true>
-              : va       ? flash_dq_from_ds_kernel<true, false>
-              : vb       ? flash_dq_from_ds_kernel<false, true>
-                         : flash_dq_from_ds_kernel<false, false>;
-    kern<<<(unsigned)(T * BH), NTHREADS, 0, stream()>>>(BH, S, T, causal, dS, slice, K, beta, dQ);
+    auto kern = va && vb ? flash_dq_from_ds_kernel<true, true, D>
+              : va       ? flash_dq_from_ds_kernel<true, false, D>
+              : vb       ? flash_dq_from_ds_kernel<false, true, D>
+                         : flash_dq_from_ds_kernel<false, false, D>;
+    kern<<<(unsigned)(T * BH * (D == 128 ? 1 : 2)), NTHREADS, 0, stream()>>>(BH, S, T, causal, dS,
+                                                                            slice, K, beta, dQ);
     return check_launch("flash backward dQ from dS");
+}
+
+int flash_dq_from_ds_f32(int BH, int S, int D, int causal, const float* dS, long long slice,
+                         const float* K, float beta, float* dQ) {
+    if (D == 128) return launch_dq_from_ds<128>(BH, S, causal, dS, slice, K, beta, dQ);
+    if (D == 64) return launch_dq_from_ds<64>(BH, S, causal, dS, slice, K, beta, dQ);
+    return set_error(DH_ERR_INVALID, "flash backward dQ from dS: head dimension %d", D);
 }
 
 }  // namespace dh

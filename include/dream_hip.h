@@ -214,7 +214,7 @@ int dh_flash_bwd(int dtype, int BH, int S, int D, float scale, int causal,
 /* dh_flash_bwd without any allocation.  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, serving loops, harnesses
  * that forbid hipMalloc).  Same arguments and errors as dh_flash_bwd, and the same results bit
- * for bit, except fp32 at D = 128 with BH*ceil(S/128) at least the GPU's CU count, where
+ * for bit, except fp32 at D = 64 or 128 with BH*ceil(S/128) at least the GPU's CU count, where
  * dh_flash_bwd forms dQ from a stored dS in pool memory and this one recomputes it (equal to
  * fp32 rounding); the scratch is a fixed 8 MB device array per GPU (held until the process ends), so BH*S must be at most
  * 1048576 rows, else DH_ERR_INVALID.  Every call on one GPU shares that array: calls that

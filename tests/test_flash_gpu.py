@@ -124,15 +124,17 @@ def test_fp32_bwd_wide_grid(BH, S, D, causal):
         assert err[worst] <= tol * m[worst].max(), (name, worst)
 
 
-@pytest.mark.parametrize("BH,S,causal", [(8, 4096, True), (16, 2048, False), (13, 2558, True)])
-def test_fp32_bwd_stored_ds_few_slices(BH, S, causal):
-    """D = 128 grids of a round of 128-key dK/dV work-groups over few, long slices: that
-    launch stores scale dS and dQ comes from one GEMM launch over all T = ceil(S / 128) query
-    tiles of every slice, heaviest first -- 32, 16 and 20 tiles here, so tile t's dS rows
-    (keys up to 128 (t + 1) causal, all 128 T otherwise) sit far into each slice's scratch;
-    S = 2558 leaves a ragged last tile and rows whose length is not a multiple of 4 (the
-    GEMM's scalar-load form).  Every slice of all three gradients against the fp64 oracle."""
-    D = 128
+@pytest.mark.parametrize("BH,S,D,causal", [(8, 4096, 128, True), (16, 2048, 128, False),
+                                           (13, 2558, 128, True), (24, 1500, 64, True),
+                                           (20, 1700, 64, False)])
+def test_fp32_bwd_stored_ds_few_slices(BH, S, D, causal):
+    """Grids of a round of 128-key dK/dV work-groups over few, long slices: that launch
+    stores scale dS and dQ comes from one GEMM launch over all T = ceil(S / 128) query tiles of
+    every slice, heaviest first -- 32, 16, 20, 12 and 14 tiles here, so tile t's dS rows (keys
+    up to 128 (t + 1) causal, all 128 T otherwise) sit far into each slice's scratch; S = 2558,
+    1500 and 1700 leave a ragged last tile (at D = 64 the GEMM's second 64-row block of it is
+    short or empty), and S = 2558 rows whose length is not a multiple of 4 (the GEMM's
+    scalar-load form).  Every slice of all three gradients against the fp64 oracle."""
     Q, K, V, G = inputs(BH, S, D, 9100 + S + causal)
     Of, lse = flash_fwd(Q, K, V, BH, S, D, causal)
     grads = flash_bwd(Q, K, V, Of, G, lse, BH, S, D, causal)

@@ -2,7 +2,7 @@
 allocate) against dh_flash_bwd on the same inputs: bit-identical outputs, fp32 and bf16, on
 two calls in a row with the second one smaller, so stale scratch contents from the first call
 cannot leak into the second; at shapes where dh_flash_bwd forms the fp32 dQ from a stored dS
-(D = 128 over at least a round of 128-key tiles), equal to fp32 rounding.  Also the size limit,
+(D = 64 or 128 over at least a round of 128-key tiles), equal to fp32 rounding.  Also the size limit,
 the shared-buffer (aliased) cases, and a call recorded under HIP stream capture and replayed as
 a graph."""
 import ctypes
@@ -64,13 +64,14 @@ def test_noalloc_matches_pool_version_on_two_calls(dtype):
             assert np.array_equal(w, g), (BH, S, D, dtype, "accumulate")
 
 
-@pytest.mark.parametrize("BH,S,causal", [(64, 512, True), (4, 8192, True), (8, 4096, False)])
-def test_noalloc_fp32_where_the_pool_version_stores_ds(BH, S, causal):
-    # D = 128 over at least a round of 128-key tiles: dh_flash_bwd writes scale dS to pool
-    # memory and forms dQ as a GEMM on it; the no-alloc entry point recomputes dS in its dQ
-    # launch.  dK and dV come from the same launch either way (bit-identical); dQ agrees to
-    # the fp32 bound.
-    D = 128
+@pytest.mark.parametrize("BH,S,D,causal", [(64, 512, 128, True), (4, 8192, 128, True),
+                                           (8, 4096, 128, False), (64, 1024, 64, False),
+                                           (48, 1500, 64, True)])
+def test_noalloc_fp32_where_the_pool_version_stores_ds(BH, S, D, causal):
+    # D = 128 or 64 over at least a round of 128-key tiles: dh_flash_bwd writes scale dS to
+    # pool memory and forms dQ as a GEMM on it; the no-alloc entry point recomputes dS in its
+    # dQ launch.  dK and dV come from the same arithmetic either way (bit-identical); dQ agrees
+    # to the fp32 bound.
     args = _case(BH, S, D, causal, "f32", 4)
     want = flash_bwd(*args, BH, S, D, causal, dtype="f32")
     got = _run_noalloc(*args, BH, S, D, causal, "f32")
