@@ -527,6 +527,12 @@ flash_fwd_f32_kernel(int BH, int S, float scale_log2, const float* __restrict__ 
         stage.store(kbuf, vbuf, tid);
         __syncthreads();
     }
+    // The Q rows (qf) have landed on every path into the stage loop.  store(0)'s wait covers
+    // them only where a stage exists; without this wait the compiler's wait insertion cannot
+    // tell them from the loop's own loads and made each stage's first MFMA wait for the next
+    // stage's prefetch.  The builtin (vmcnt(0), expcnt and lgkmcnt untouched), unlike inline
+    // assembly, is seen by that pass.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     for (int st = 0; st < nst; ++st) {
         const int cur = st & 1;
         const bool more = st + 1 < nst;
