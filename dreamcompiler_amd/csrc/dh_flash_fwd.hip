@@ -451,16 +451,20 @@ struct F32Stage {
     static constexpr int CH = BN * D / 4 / THREADS;   // float4 chunks per thread per tensor
     f32x4 k[CH], v[CH];
 
+    // The stage's base (uniform) plus a 32-bit unsigned offset per thread: scalar-base loads
+    // instead of a 64-bit address per thread kept across stages.
     __device__ void fetch(const float* __restrict__ Kg, const float* __restrict__ Vg, int j0,
                           int S, int tid) {
+        const float* ks = Kg + (size_t)j0 * D;
+        const float* vs = Vg + (size_t)j0 * D;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int f = tid + c * THREADS;
             const int key = f / (D / 4), dq = f % (D / 4);
-            const int j = j0 + key;
+            const uint32_t o = key * D + 4 * dq;
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            k[c] = j < S ? *reinterpret_cast<const f32x4*>(Kg + (size_t)j * D + 4 * dq) : z;
-            v[c] = j < S ? *reinterpret_cast<const f32x4*>(Vg + (size_t)j * D + 4 * dq) : z;
+            k[c] = j0 + key < S ? *reinterpret_cast<const f32x4*>(ks + o) : z;
+            v[c] = j0 + key < S ? *reinterpret_cast<const f32x4*>(vs + o) : z;
         }
     }
     __device__ void store(float* ks, float* vs, int tid) const {
