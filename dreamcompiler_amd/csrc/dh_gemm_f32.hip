@@ -243,15 +243,16 @@ __device__ __forceinline__ void gemm_f32_tile(int M, int N, int K, const float* 
         }
 }
 
+// The kernel body: batch member blockIdx.y (strides in elements; 0 for a single product).  In
+// a split-K launch the members are the chunks of K, and the last one takes the ragged rest,
+// k_last (= K otherwise).
 template <bool TA, bool TB, bool VA, bool VB, int TBM, int TBN>
-__global__ void __launch_bounds__(NTHREADS)
-gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
-                const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
-                long long sA, long long sB, long long sC, const float* __restrict__ bias,
-                int epi, int k_last) {
-    // Batch member blockIdx.y (strides in elements; 0 for a single product).  In a split-K
-    // launch the members are the chunks of K, and the last one takes the ragged rest, k_last
-    // (= K otherwise).
+__device__ __forceinline__ void gemm_f32_grid_tile(int M, int N, int K, const float* __restrict__ A,
+                                                   int lda, const float* __restrict__ B, int ldb,
+                                                   float beta, float* __restrict__ C, int ldc,
+                                                   long long sA, long long sB, long long sC,
+                                                   const float* __restrict__ bias, int epi,
+                                                   int k_last) {
     if (blockIdx.y == gridDim.y - 1) K = k_last;
     A += blockIdx.y * sA;
     B += blockIdx.y * sB;
@@ -264,6 +265,33 @@ gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
         m0 = tm * TBM;
         n0 = tn * TBN;
     });
+}
+
+template <bool TA, bool TB, bool VA, bool VB, int TBM, int TBN>
+__global__ void __launch_bounds__(NTHREADS)
+gemm_f32_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
+                const float* __restrict__ B, int ldb, float beta, float* __restrict__ C, int ldc,
+                long long sA, long long sB, long long sC, const float* __restrict__ bias,
+                int epi, int k_last) {
+    gemm_f32_grid_tile<TA, TB, VA, VB, TBM, TBN>(M, N, K, A, lda, B, ldb, beta, C, ldc, sA, sB, sC,
+                                                bias, epi, k_last);
+}
+
+// The 128 x 128 tile held to four waves per SIMD (at most 128 registers a lane: the
+// accumulators move to arch VGPRs), so that four work-groups share a CU where the default form
+// fits three (94 VGPRs + 64 accumulation registers).  For grids of at least four tiles per CU:
+// same box, fp32 4096^3 NN 1.080 -> 1.055 ms, TN 1.094-1.099 -> 1.062-1.066, 8192 x 8192 x 2048
+// 1-3% faster; with fewer tiles per CU the default form is faster (2048^3, one per CU: 175 ->
+// 184 us; 3000^3 NN 520 -> 535-543 us).
+template <bool TA, bool TB, bool VA, bool VB>
+__global__ void __launch_bounds__(NTHREADS)
+__attribute__((amdgpu_waves_per_eu(4, 4)))
+gemm_f32_occ4_kernel(int M, int N, int K, const float* __restrict__ A, int lda,
+                     const float* __restrict__ B, int ldb, float beta, float* __restrict__ C,
+                     int ldc, long long sA, long long sB, long long sC,
+                     const float* __restrict__ bias, int epi, int k_last) {
+    gemm_f32_grid_tile<TA, TB, VA, VB, 128, 128>(M, N, K, A, lda, B, ldb, beta, C, ldc, sA, sB, sC,
+                                                bias, epi, k_last);
 }
 
 // dQ of the fp32 flash backward from stored scale*dS (one launch for all row tiles), head
@@ -845,14 +873,23 @@ int launch_wgrad(int N, int Cout, int P, int R, const float* dY, const float* X,
     return st;
 }
 
+// wgs: work-groups of a one-pass grid (0 for split-K launches), which takes the four-wave 128 x
+// 128 form from four per CU.
 template <bool TA, bool TB, int TBM, int TBN>
 auto pick_kernel(int M, int N, int K, const float* A, int lda, long long sA, const float* B,
-                 int ldb, long long sB) {
+                 int ldb, long long sB, long long wgs = 0) {
     // 128-bit loads need 16-byte aligned bases, leading dimensions and batch strides divisible
     // by 4, and a contiguous extent (K, or M / N for the transposed storage) divisible by 4.
     const int ca = TA ? M : K, cb = TB ? K : N;
     const bool va = ((uintptr_t)A % 16 == 0) && (lda % 4 == 0) && (sA % 4 == 0) && (ca % 4 == 0);
     const bool vb = ((uintptr_t)B % 16 == 0) && (ldb % 4 == 0) && (sB % 4 == 0) && (cb % 4 == 0);
+    if constexpr (TBM == 128 && TBN == 128) {
+        static const bool occ4 = [] {
+            const char* e = std::getenv("DH_GEMM_F32_OCC4");   // tuning knob: 0 or 1
+            return !e || std::atoi(e) != 0;
+        }();
+        if (occ4 && va && vb && wgs >= 4LL * num_cus()) return gemm_f32_occ4_kernel<TA, TB, true, true>;
+    }
     return va && vb ? gemm_f32_kernel<TA, TB, true, true, TBM, TBN>
          : va       ? gemm_f32_kernel<TA, TB, true, false, TBM, TBN>
          : vb       ? gemm_f32_kernel<TA, TB, false, true, TBM, TBN>
@@ -865,7 +902,8 @@ template <bool TA, bool TB, int TBM, int TBN>
 int launch_grid(int M, int N, int K, const float* A, int lda, const float* B, int ldb,
                 float beta, float* C, int ldc, const Batch& bt) {
     const int tiles = ((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN);
-    auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, K, A, lda, bt.sA, B, ldb, bt.sB);
+    auto kern = pick_kernel<TA, TB, TBM, TBN>(M, N, K, A, lda, bt.sA, B, ldb, bt.sB,
+                                              (long long)tiles * bt.count);
     for (int b0 = 0; b0 < bt.count; b0 += 65535) {
         const int nb = bt.count - b0 < 65535 ? bt.count - b0 : 65535;
         kern<<<dim3(tiles, nb), NTHREADS, 0, stream()>>>(M, N, K, A + b0 * bt.sA, lda,

@@ -271,6 +271,42 @@ def test_bf16_fast_path_knob_variants(env):
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.count("variant") == 16, r.stdout
 
+_OCC4_SCRIPT = r"""
+import hashlib, sys
+sys.path[:0] = [{tests!r}, {root!r}]
+from test_gemm_gpu import _ex
+for ta, tb in [(0, 0), (0, 1), (1, 0), (1, 1)]:
+    got, _ = _ex("f32", ta, tb, 1, 4096, 4096, 520, beta=0.5, bias=True, relu=True, seed=ta + 2 * tb)
+    print("single", ta, tb, hashlib.sha1(got.tobytes()).hexdigest()[:16], flush=True)
+got, _ = _ex("f32", 0, 0, 40, 512, 640, 300, beta=0.0, bias=True, seed=7)
+print("batched", hashlib.sha1(got.tobytes()).hexdigest()[:16], flush=True)
+"""
+
+
+def test_fp32_four_wave_form_is_bit_identical():
+    """One-pass fp32 grids of at least four 128 x 128 tiles per CU take the four-wave form of
+    the tile kernel (same tile body, held to 128 registers so that four work-groups share a
+    CU).  Every layout at 4096 x 4096 (1024 tiles) with beta, bias and ReLU, and a batched grid
+    (40 x 20 tiles), against the default form (DH_GEMM_F32_OCC4=0), bit for bit: the
+    arithmetic and its order are the same.  The switch is read once per process, so each form
+    runs in a child process."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = _OCC4_SCRIPT.format(tests=here, root=os.path.dirname(here))
+
+    def run(env):
+        r = subprocess.run([sys.executable, "-c", code], env={**os.environ, **env},
+                           capture_output=True, text=True, timeout=110)
+        assert r.returncode == 0, r.stdout + r.stderr
+        lines = [l for l in r.stdout.split("\n") if l.strip()]
+        assert len(lines) == 5, r.stdout
+        return lines
+
+    assert run({}) == run({"DH_GEMM_F32_OCC4": "0"})
+
+
 def _ex(dtype, ta, tb, Bt, M, N, K, beta=0.0, bias=True, relu=False, share=None, seed=0,
         row_bias=False):
     """Run dh_gemm_*_ex on random inputs; returns (got, ref) as (Bt, M, N) arrays."""
