@@ -705,15 +705,18 @@ struct Tile32 {
     static constexpr int CH = RB * D / 4;           // float4 chunks per tile
     f32x4 v[(CH + THREADS - 1) / THREADS];
     // The stage's base (uniform) plus a 32-bit unsigned offset per thread, so that the loads
-    // can take the scalar-base form instead of a 64-bit address per thread kept across stages.
+    // take the scalar-base form instead of a 64-bit address per thread kept across stages (the
+    // empty asm keeps the compiler from hoisting base + offset out of the stage loop as one).
     __device__ void fetch(const float* __restrict__ g, int r0, int S, int tid) {
         const float* gs = g + (size_t)r0 * D;
 #pragma unroll
         for (int c = 0; c < (CH + THREADS - 1) / THREADS; ++c) {
             const int f = tid + c * THREADS;
             const int row = f / (D / 4), dq = f % (D / 4);
+            uint32_t ob = 4u * (row * D + 4 * dq);   // bytes
+            asm volatile("" : "+v"(ob));
             v[c] = (f < CH && r0 + row < S)
-                       ? *reinterpret_cast<const f32x4*>(gs + (uint32_t)(row * D + 4 * dq))
+                       ? *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(gs) + ob)
                        : f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
